@@ -1,0 +1,226 @@
+"""Benchmark: MoE FFN tokens/s of the Qwen3-30B-A3B-shaped MoE stack on one MI355X.
+
+Workload (the single 30B-A3B MoE layer, decode, Q8_0 experts, F16 router, repeated over the model's
+48 MoE layers): one step runs the whole MoE block - router, top-8, permutation, gate/up GEMV +
+SwiGLU, down GEMV, weighted combine, residual - of each of 48 layers for T tokens (T = 1 by default;
+T = 8 is reported alongside). Every layer has its own HBM copy of the expert table (48 x 642 MB =
+30.8 GB, so the 256 MB last-level cache cannot serve repeats), its own F16 router weights and its
+own N(0, 1) hnorm rows. Weights are random-init and synthetic (seeded); one layer's expert bytes are
+generated and uploaded into each layer's slots.
+
+The timed region replays one captured HIP graph per step on torch's current stream, bracketed by
+synchronize; value = T * steps / seconds (tokens/s through all 48 MoE layers).
+
+Roofline: the dominant kernel is gate_up (two thirds of the bytes). Its average duration is measured
+with HIP events recorded around each of its launches on the launch stream (the library's stage
+timing, over `--steps` eager steps), and its algorithmic bytes per launch are the distinct experts'
+gate+up bytes plus activations in and SwiGLU rows out.
+
+cpu_baseline: the oracle (a C restatement of ggml's CPU algorithm: Q8_0 activations, int8 block
+dots, OpenMP) runs the same layer on the host cores for a bounded sample of layer passes.
+"""
+import argparse
+import json
+import os
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+H, F, E, K, N_LAYER = 2048, 768, 128, 8, 48
+Q8_0 = 8
+HBM_PEAK_GBS = 8000.0
+
+
+def parse():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--tokens", type=int, default=1)
+    ap.add_argument("--layers", type=int, default=N_LAYER)
+    ap.add_argument("--no-graph", action="store_true")
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    return ap.parse_args()
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+class Stack:
+    """Resident pool of the 30B-A3B MoE layers plus per-layer inputs on the device."""
+
+    def __init__(self, torch, L, n_layer, t_max, seed=0):
+        from localstack_amd import synth
+        self.torch = torch
+        self.n_layer = n_layer
+        rng = np.random.default_rng(seed)
+        t0 = time.time()
+        self.up = synth.experts(rng, Q8_0, E, F, H)
+        self.gate = synth.experts(rng, Q8_0, E, F, H)
+        self.down = synth.experts(rng, Q8_0, E, H, F)
+        log(f"[bench] generated one layer of Q8_0 experts ({3 * self.up.nbytes / 1e9:.2f} GB) in {time.time() - t0:.1f}s")
+        t0 = time.time()
+        types = (Q8_0,) * 3
+        self.store = L.ExpertStore(n_layer, H, F, E, K, t_max, [(types, self.up, self.gate, self.down)] * n_layer)
+        log(f"[bench] resident pool: {self.store.total_bytes() / 1e9:.1f} GB in HBM, built in {time.time() - t0:.1f}s")
+        dev = torch.device("cuda:0")
+        d = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to(dev)
+        self.routers = [d(synth.router_f16(rng, E, H)) for _ in range(n_layer)]
+        self.routers_host = None
+        self.rng = rng
+        self.dev = dev
+        self.t_max = t_max
+
+    def inputs(self, T, seed):
+        from localstack_amd import synth
+        torch = self.torch
+        rng = np.random.default_rng(seed)
+        d = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to(self.dev)
+        self.T = T
+        self.x = [d(synth.activations(rng, T, H)) for _ in range(self.n_layer)]
+        self.resid = [d(synth.activations(rng, T, H)) for _ in range(self.n_layer)]
+        self.out = [torch.zeros((T, H), dtype=torch.float32, device=self.dev) for _ in range(self.n_layer)]
+        self.ids = [torch.zeros((T, K), dtype=torch.int32, device=self.dev) for _ in range(self.n_layer)]
+        self.w = [torch.zeros((T, K), dtype=torch.float32, device=self.dev) for _ in range(self.n_layer)]
+
+    def step(self):
+        for l in range(self.n_layer):
+            self.store.block(l, self.x[l], self.routers[l], 1, self.resid[l], self.out[l], self.ids[l], self.w[l])
+
+
+def time_steps(torch, fn, steps, warmup):
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize()
+    s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    s.record()
+    for _ in range(steps):
+        fn()
+    e.record()
+    torch.cuda.synchronize()
+    return s.elapsed_time(e) / steps
+
+
+def measure(torch, st, T, steps, warmup, use_graph):
+    st.inputs(T, seed=1000 + T)
+    graph = None
+    if use_graph:
+        st.step()
+        torch.cuda.synchronize()
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            st.step()
+        fn = graph.replay
+    else:
+        fn = st.step
+    ms = time_steps(torch, fn, steps, warmup)
+    st.store.check()
+    # stage timing (eager, events around every launch on the launch stream)
+    st.store.set_timing(True)
+    n_eager = max(2, min(steps, 10))
+    for _ in range(n_eager):
+        st.step()
+    stage_ms, launches = st.store.timing()
+    st.store.set_timing(False)
+    ids = [i.cpu().numpy() for i in st.ids]
+    distinct = np.array([len(np.unique(a)) for a in ids], np.float64)
+    gu_bytes = distinct.mean() * 2 * 1671168 + T * (H + H // 32 * 8) + T * K * F * 4
+    dn_bytes = distinct.mean() * 1671168 + T * K * (F * 4 + H * 4) + T * H * 8
+    rt_bytes = E * H * 2 + T * H * 4
+    avg = [stage_ms[i] / max(1, launches[i]) for i in range(3)]
+    res = dict(T=T, ms_per_step=ms, tok_s=T * 1000.0 / ms, graph=use_graph,
+               stage_avg_us={"prologue": avg[0] * 1e3, "gate_up": avg[1] * 1e3, "down": avg[2] * 1e3},
+               stage_launches=launches, distinct_experts_per_layer=float(distinct.mean()),
+               bytes_per_layer=float(gu_bytes + dn_bytes + rt_bytes),
+               gate_up_bytes=float(gu_bytes))
+    res["layer_gbs"] = res["bytes_per_layer"] * st.n_layer / (ms * 1e-3) / 1e9
+    res["gate_up_gbs"] = gu_bytes / (avg[1] * 1e-3) / 1e9
+    return res, graph
+
+
+def cpu_baseline(st, T, seconds):
+    """Times the oracle on this host over whole layer passes of the same workload."""
+    import oracle
+    from localstack_amd import synth
+    rng = np.random.default_rng(7)
+    gate_inp = synth.router_f16(rng, E, H)
+    x = synth.activations(rng, T, H)
+    resid = synth.activations(rng, T, H)
+    up, gate, down = (a.reshape(E, -1) for a in (st.up, st.gate, st.down))
+    cores = len(os.sched_getaffinity(0))
+    os.environ.setdefault("OMP_NUM_THREADS", str(cores))
+    n = 0
+    t0 = time.time()
+    while True:
+        ids, w, _, _ = oracle.router(x, gate_inp, 1, K)
+        oracle.moe_ffn(x, ids, w, resid, up, gate, down, (Q8_0,) * 3, F, n_threads=cores)
+        n += 1
+        el = time.time() - t0
+        if el >= seconds or n >= 2000:
+            break
+    per_layer = el / n
+    return dict(value=T / (per_layer * N_LAYER), unit="tok/s", cores=cores, kind="port",
+                sample=f"{n} passes of one Qwen3-30B-A3B MoE layer (router + Q8_0 experts, T={T}) by the oracle "
+                       f"(C restatement of ggml's CPU algorithm, OpenMP {cores} threads), scaled to 48 layers; "
+                       f"{per_layer * 1e3:.2f} ms per layer")
+
+
+def main():
+    a = parse()
+    if a.gpus != 1:
+        print(f"bench.py runs on one GPU only (asked for {a.gpus}); the multi-GPU expert-parallel path is not built.",
+              file=sys.stderr)
+        sys.exit(2)
+    import torch
+    import localstack_amd as L
+    L.lib()
+    st = Stack(torch, L, a.layers, t_max=max(8, a.tokens))
+    main_res, g = measure(torch, st, a.tokens, a.steps, a.warmup, not a.no_graph)
+    del g
+    log(f"[bench] T={a.tokens}: {json.dumps(main_res)}")
+    extra = None
+    if a.tokens == 1:
+        extra, g = measure(torch, st, 8, a.steps, a.warmup, not a.no_graph)
+        del g
+        log(f"[bench] T=8: {json.dumps(extra)}")
+    cpu = None if a.no_cpu else cpu_baseline(st, a.tokens, a.cpu_seconds)
+    gu_avg_s = main_res["stage_avg_us"]["gate_up"] * 1e-6
+    achieved = main_res["gate_up_bytes"] / gu_avg_s / 1e9
+    line = {
+        "metric": "MoE FFN tok/s + % of HBM roofline (decode) / MFMA peak (prefill), 30B-A3B",
+        "value": main_res["tok_s"],
+        "unit": "tok/s",
+        "n_gpus": 1,
+        "steps": a.steps,
+        "warmup": a.warmup,
+        "ms_per_step": main_res["ms_per_step"],
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "int8",
+        "data": "synthetic",
+        "config": {"workload": f"Qwen3-30B-A3B MoE FFN x {a.layers} layers, decode T={a.tokens}, Q8_0 experts, "
+                               f"F16 router", "n_layer": a.layers, "tokens": a.tokens, "n_embd": H, "n_ff_exp": F,
+                   "n_expert": E, "top_k": K, "expert_type": "Q8_0", "hip_graph": main_res["graph"]},
+        "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": achieved / HBM_PEAK_GBS, "traffic": None, "kernel": "gate_up",
+                     "kernel_avg_us": main_res["stage_avg_us"]["gate_up"],
+                     "bytes_per_launch": main_res["gate_up_bytes"]},
+        "stack_gbs": main_res["layer_gbs"],
+        "stage_avg_us": main_res["stage_avg_us"],
+        "t8": None if extra is None else {"tok_s": extra["tok_s"], "ms_per_step": extra["ms_per_step"],
+                                          "stack_gbs": extra["layer_gbs"], "stage_avg_us": extra["stage_avg_us"],
+                                          "distinct_experts_per_layer": extra["distinct_experts_per_layer"]},
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

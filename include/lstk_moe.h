@@ -1,0 +1,170 @@
+/* lstk_moe.h - C ABI of the MI355X (gfx950) Qwen3-MoE expert-FFN library.
+ *
+ * The library replaces the MoE block of localstack's qwen3 forward pass:
+ *   router()     src/qwen3.cpp:175-192  (gate matmul, softmax, top-k, renormalised weights)
+ *   moe_apply()  src/qwen3.cpp:197-214  (gate/up/down mul_mat_id, SwiGLU, weighted k-sum)
+ *   residual add src/qwen3.cpp:250 (resident graph) and :287 (streaming segment)
+ * and the expert pool that feeds it:
+ *   ExpertStore  src/expert_store.h:113-131, src/expert_store.cpp:106-295
+ *
+ * Conventions (mirroring the reference's `bool f(..., std::string &err)`):
+ *   - every call returns 0 on success and a negative LSTK_E_* code on failure;
+ *     lstk_last_error() returns the message of the last failure on the calling thread;
+ *   - device pointers and streams are owned by the caller; `stream` is a hipStream_t
+ *     (NULL = the default stream);
+ *   - a pool and its scratch are used from one host thread and one stream at a time, like the
+ *     reference Engine (src/engine.h:65); calls that overlap on one pool race.
+ * Tensor layouts are row-major C order: hnorm/resid/out are [n_tokens][n_embd] f32,
+ * ids/slots are [n_tokens][n_expert_used] int32, weights are [n_tokens][n_expert_used] f32.
+ */
+#ifndef LSTK_MOE_H
+#define LSTK_MOE_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define LSTK_ABI_VERSION 1
+
+/* ggml tensor type ids used on this path (ggml.h enum ggml_type). */
+#define LSTK_TYPE_F32 0
+#define LSTK_TYPE_F16 1
+#define LSTK_TYPE_Q8_0 8
+#define LSTK_TYPE_Q4_K 12
+
+/* Error codes. */
+#define LSTK_OK 0
+#define LSTK_E_INVALID (-1)   /* bad argument or shape */
+#define LSTK_E_NOMEM (-2)     /* host or device allocation failed */
+#define LSTK_E_EXHAUSTED (-3) /* pool exhausted (src/expert_store.cpp:261-266) */
+#define LSTK_E_DEVICE (-4)    /* a HIP call failed */
+#define LSTK_E_IO (-5)        /* a host-tier copy failed; the slot is marked empty */
+#define LSTK_E_BADID (-6)     /* a device kernel saw an expert/slot id out of range */
+
+typedef void *lstk_stream_t; /* a hipStream_t */
+typedef struct lstk_pool lstk_pool;
+
+/* Model shape: the MoE part of Qwen3HParams (src/qwen3.h:22-46) plus the largest step size
+ * (EngineParams::n_batch, src/engine.h:33) that sizes the pool's scratch. */
+typedef struct lstk_moe_dims {
+    int32_t n_layer;
+    int32_t n_embd;        /* h */
+    int32_t n_ff_exp;      /* f */
+    int32_t n_expert;      /* E */
+    int32_t n_expert_used; /* k */
+    int32_t n_batch;       /* max tokens per call */
+} lstk_moe_dims;
+
+/* One layer's stacked expert tensors as they sit in a GGUF file: expert e of a matrix starts at
+ * host_x + e * expert_stride (GgufTensorInfo::expert_stride, src/gguf_model.h:28).
+ * up/gate are [n_expert][n_ff_exp rows][n_embd cols], down is [n_expert][n_embd rows][n_ff_exp cols],
+ * each row a run of Q8_0 (34 B / 32 values) or Q4_K (144 B / 256 values) blocks.
+ * Replaces ExpertLayerInfo (src/expert_store.h:32-36), with host memory in place of a file offset. */
+typedef struct lstk_expert_layer {
+    int32_t type_up, type_gate, type_down;
+    const void *host_up, *host_gate, *host_down;
+} lstk_expert_layer;
+
+/* ExpertStoreStats (src/expert_store.h:70-77). */
+typedef struct lstk_pool_stats_t {
+    uint64_t hits;
+    uint64_t misses;
+    uint64_t bytes_read; /* bytes copied host tier -> HBM */
+    uint64_t acquires;
+    double wait_ms;      /* host time spent inside acquire() */
+} lstk_pool_stats_t;
+
+/* Pool flags. */
+#define LSTK_POOL_STREAMING 1 /* slots < experts: misses are copied from the pinned host tier */
+#define LSTK_POOL_DRY 2       /* bookkeeping only: no device memory, no HIP calls (CPU tests) */
+
+const char *lstk_last_error(void);
+int lstk_abi_version(void);
+
+/* Creates the expert pool on the current HIP device.
+ * Resident (flags without LSTK_POOL_STREAMING): every expert of every layer is uploaded to HBM once
+ * and slot s of a layer holds expert s; acquire() is the identity.
+ * Streaming: ExpertStore::init semantics (src/expert_store.cpp:106-198): layers are grouped by their
+ * (up, gate, down) type triple, each group gets pool_bytes * n_layers_in_group / n_layer, shards hold
+ * at most 1024 slots and at least min_slots; the full expert table is copied once into pinned host
+ * memory (the host tier, standing in for the GGUF file) and misses are served from it with
+ * hipMemcpyAsync on the pool's side stream.
+ * The layers' host pointers are only read during this call. */
+int lstk_pool_create(const lstk_moe_dims *dims, const lstk_expert_layer *layers, size_t pool_bytes,
+                     uint32_t min_slots, uint32_t flags, lstk_pool **out);
+void lstk_pool_destroy(lstk_pool *pool);
+
+/* ExpertStore::acquire (src/expert_store.cpp:232-286): makes `n` experts of `layer` resident and
+ * writes their slot numbers to `slots` (host arrays), pinning them until lstk_pool_release_all().
+ * Hits pin; misses evict the LRU head and queue the three matrix copies on the side stream; `stream`
+ * (the compute stream) is made to wait for those copies, so the host never blocks on them.
+ * Fails with LSTK_E_EXHAUSTED when the layer needs more slots than its shard has. */
+int lstk_pool_acquire(lstk_pool *pool, int layer, const int32_t *experts, int n, int32_t *slots,
+                      lstk_stream_t stream);
+/* ExpertStore::release_all (src/expert_store.cpp:289-295). Slots released here are not overwritten
+ * before the work already queued on `stream` has finished with them. */
+int lstk_pool_release_all(lstk_pool *pool, lstk_stream_t stream);
+int lstk_pool_stats(const lstk_pool *pool, lstk_pool_stats_t *out);
+size_t lstk_pool_total_bytes(const lstk_pool *pool);   /* ExpertStore::total_bytes */
+uint32_t lstk_pool_total_slots(const lstk_pool *pool); /* ExpertStore::total_slots */
+/* Slots of the shard serving `layer` (ExpertPool::n_slots via pool_for, src/expert_store.h:120). */
+int lstk_pool_layer_slots(const lstk_pool *pool, int layer);
+/* ExpertStore::describe (src/expert_store.cpp:309-319); writes a NUL-terminated string. */
+int lstk_pool_describe(const lstk_pool *pool, char *buf, size_t len);
+
+/* router() (src/qwen3.cpp:175-192) on the device: logits = gate_inp . hnorm (F16 weights take
+ * fp16-rounded activations as ggml's CPU mul_mat does), softmax over the n_expert logits, top-k in
+ * descending order (ties to the lower expert id), weights = p / max(sum p, 2^-14).
+ * d_gate_inp is [n_expert][n_embd] of gate_type (LSTK_TYPE_F16 or LSTK_TYPE_F32). */
+int lstk_moe_route(lstk_pool *pool, int layer, const float *d_hnorm, int n_tokens, const void *d_gate_inp,
+                   int gate_type, int32_t *d_ids, float *d_weights, lstk_stream_t stream);
+
+/* moe_apply() + the residual add (src/qwen3.cpp:197-214 and :250 / :287) on the device:
+ * out[t] = resid[t] + sum_{j=0..k-1} weights[t][j] * down_s(swiglu(gate_s(x_t), up_s(x_t))),
+ * s = d_slots[t][j], summed left to right in j. x_t is quantized to the activation type ggml pairs with
+ * the weight type (Q8_0 for Q8_0, Q8_K for Q4_K), and so is the SwiGLU output before down.
+ * d_slots holds slot numbers from lstk_pool_acquire (streaming) or expert ids (resident).
+ * d_out may alias d_resid. */
+int lstk_moe_ffn(lstk_pool *pool, int layer, const float *d_hnorm, const int32_t *d_slots, const float *d_weights,
+                 const float *d_resid, float *d_out, int n_tokens, lstk_stream_t stream);
+
+/* The whole MoE block of a resident layer in one call (router + experts + residual), with the
+ * router's last block also building the token->expert permutation, so no host round trip is
+ * needed. d_ids / d_weights receive the routing (for traces, src/engine.cpp:301-316); they may not
+ * be NULL. Valid for resident pools only. */
+int lstk_moe_block(lstk_pool *pool, int layer, const float *d_hnorm, const void *d_gate_inp, int gate_type,
+                   const float *d_resid, float *d_out, int32_t *d_ids, float *d_weights, int n_tokens,
+                   lstk_stream_t stream);
+
+/* Waits for `stream` and reports LSTK_E_BADID if a kernel has seen an id out of range since the
+ * last check (the id is clamped on the device so no access leaves the pool). */
+int lstk_pool_check(lstk_pool *pool, lstk_stream_t stream);
+
+/* Per-stage kernel timing with HIP events recorded on the compute stream around each launch.
+ * stage: 0 = prologue (router / quantize / permute), 1 = gate+up+SwiGLU, 2 = down+combine.
+ * lstk_pool_timing syncs the events recorded so far and returns the summed milliseconds and the
+ * launch count of each stage; it resets the counters. */
+int lstk_pool_set_timing(lstk_pool *pool, int enable);
+int lstk_pool_timing(lstk_pool *pool, double ms[3], int64_t launches[3]);
+
+/* Host-side repacking between GGUF expert bytes and the pool's HBM layout (one expert matrix of
+ * `rows` x `cols`). The pool layout is [cols/256][C][rows][16 B]: each 256-value super-block row is
+ * split into C 16-byte chunks (Q8_0: 8 fp16 scales + 16 chunks of int8; Q4_K: {d, dmin, scales}
+ * + 8 chunks of 4-bit pairs) and the chunks of neighbouring rows are adjacent, so a wavefront reading
+ * one chunk of 64 rows issues one coalesced 1 KiB load. Sizes are unchanged. */
+size_t lstk_matrix_bytes(int type, int rows, int cols);
+int lstk_repack_matrix(int type, int rows, int cols, const void *gguf, void *packed);
+int lstk_unpack_matrix(int type, int rows, int cols, const void *packed, void *gguf);
+
+/* Test hook for the failure path the reference leaves silent (a failed pread is only logged,
+ * src/expert_store.cpp:62-66): the next n host-tier copies fail, the acquire returns LSTK_E_IO and
+ * the slots involved are unmapped. */
+int lstk_pool_debug_fail_copies(lstk_pool *pool, int n);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

@@ -1,0 +1,250 @@
+"""localstack_amd - MI355X (gfx950) Qwen3-MoE expert-FFN path behind a C ABI.
+
+The shared library liblstk_moe.so (built by localstack_amd/build.py from csrc/) holds the HIP
+kernels, the HBM expert pool and the C ABI declared in include/lstk_moe.h. This module is a thin
+ctypes view of that ABI that mirrors the reference's interface for the path:
+
+  ExpertStore          src/expert_store.h:113-131 (init / acquire / release_all / stats / describe)
+  ExpertStore.route    router()    src/qwen3.cpp:175-192
+  ExpertStore.ffn      moe_apply() src/qwen3.cpp:197-214 plus the residual add (:250 / :287)
+  ExpertStore.block    the resident MoE block of qwen3_build_graph (src/qwen3.cpp:239-250)
+
+Device buffers are torch tensors on a ROCm device (or raw integer device pointers); torch is used
+only to own device memory and streams. There is no CPU fallback: every compute call runs the HIP
+kernels, and a missing library raises.
+"""
+import ctypes
+import os
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "liblstk_moe.so")
+
+TYPE_F32, TYPE_F16, TYPE_Q8_0, TYPE_Q4_K = 0, 1, 8, 12
+POOL_STREAMING, POOL_DRY = 1, 2
+E_INVALID, E_NOMEM, E_EXHAUSTED, E_DEVICE, E_IO, E_BADID = -1, -2, -3, -4, -5, -6
+
+
+class LstkError(RuntimeError):
+    def __init__(self, code, msg):
+        super().__init__(msg)
+        self.code = code
+
+
+class MoeDims(ctypes.Structure):
+    _fields_ = [("n_layer", ctypes.c_int32), ("n_embd", ctypes.c_int32), ("n_ff_exp", ctypes.c_int32),
+                ("n_expert", ctypes.c_int32), ("n_expert_used", ctypes.c_int32), ("n_batch", ctypes.c_int32)]
+
+
+class ExpertLayer(ctypes.Structure):
+    _fields_ = [("type_up", ctypes.c_int32), ("type_gate", ctypes.c_int32), ("type_down", ctypes.c_int32),
+                ("host_up", ctypes.c_void_p), ("host_gate", ctypes.c_void_p), ("host_down", ctypes.c_void_p)]
+
+
+class PoolStats(ctypes.Structure):
+    _fields_ = [("hits", ctypes.c_uint64), ("misses", ctypes.c_uint64), ("bytes_read", ctypes.c_uint64),
+                ("acquires", ctypes.c_uint64), ("wait_ms", ctypes.c_double)]
+
+
+# name -> (restype, argtypes); every function declared in include/lstk_moe.h
+_P, _I, _SZ = ctypes.c_void_p, ctypes.c_int, ctypes.c_size_t
+SIGNATURES = {
+    "lstk_last_error": (ctypes.c_char_p, []),
+    "lstk_abi_version": (_I, []),
+    "lstk_pool_create": (_I, [ctypes.POINTER(MoeDims), _P, _SZ, ctypes.c_uint32, ctypes.c_uint32, ctypes.POINTER(_P)]),
+    "lstk_pool_destroy": (None, [_P]),
+    "lstk_pool_acquire": (_I, [_P, _I, _P, _I, _P, _P]),
+    "lstk_pool_release_all": (_I, [_P, _P]),
+    "lstk_pool_stats": (_I, [_P, ctypes.POINTER(PoolStats)]),
+    "lstk_pool_total_bytes": (_SZ, [_P]),
+    "lstk_pool_total_slots": (ctypes.c_uint32, [_P]),
+    "lstk_pool_layer_slots": (_I, [_P, _I]),
+    "lstk_pool_describe": (_I, [_P, ctypes.c_char_p, _SZ]),
+    "lstk_moe_route": (_I, [_P, _I, _P, _I, _P, _I, _P, _P, _P]),
+    "lstk_moe_ffn": (_I, [_P, _I, _P, _P, _P, _P, _P, _I, _P]),
+    "lstk_moe_block": (_I, [_P, _I, _P, _P, _I, _P, _P, _P, _P, _I, _P]),
+    "lstk_pool_check": (_I, [_P, _P]),
+    "lstk_pool_set_timing": (_I, [_P, _I]),
+    "lstk_pool_timing": (_I, [_P, ctypes.POINTER(ctypes.c_double), ctypes.POINTER(ctypes.c_int64)]),
+    "lstk_matrix_bytes": (_SZ, [_I, _I, _I]),
+    "lstk_repack_matrix": (_I, [_I, _I, _I, _P, _P]),
+    "lstk_unpack_matrix": (_I, [_I, _I, _I, _P, _P]),
+    "lstk_pool_debug_fail_copies": (_I, [_P, _I]),
+}
+
+_lib = None
+
+
+def lib():
+    """Loads liblstk_moe.so; raises if it has not been built (there is no fallback)."""
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise ImportError(f"{LIB_PATH} is missing: build it with `python localstack_amd/build.py`")
+        # torch ships its own HIP runtime (SONAME libamdhip64.so.7). Loading it first makes the
+        # library's libamdhip64.so.7 dependency bind to that same runtime, so the library and torch
+        # share one device context and torch's streams are valid handles for the library.
+        try:
+            import torch  # noqa: F401
+        except ImportError:
+            pass
+        L = ctypes.CDLL(LIB_PATH)
+        for name, (res, args) in SIGNATURES.items():
+            fn = getattr(L, name)
+            fn.restype = res
+            fn.argtypes = args
+        _lib = L
+    return _lib
+
+
+def _check(rc):
+    if rc != 0:
+        raise LstkError(rc, lib().lstk_last_error().decode())
+    return rc
+
+
+def _ptr(x):
+    """Device/host pointer of a torch tensor, numpy array or integer."""
+    if x is None:
+        return None
+    if isinstance(x, int):
+        return x
+    if hasattr(x, "data_ptr"):
+        return x.data_ptr()
+    if isinstance(x, np.ndarray):
+        return x.ctypes.data
+    raise TypeError(f"cannot take the address of {type(x)}")
+
+
+def _stream(stream):
+    if stream is None:
+        try:
+            import torch
+            if torch.cuda.is_available():
+                return torch.cuda.current_stream().cuda_stream
+        except ImportError:
+            pass
+        return None
+    if isinstance(stream, int):
+        return stream
+    return stream.cuda_stream
+
+
+def matrix_bytes(type_, rows, cols):
+    return lib().lstk_matrix_bytes(type_, rows, cols)
+
+
+def repack_matrix(type_, rows, cols, gguf):
+    gguf = np.ascontiguousarray(gguf, dtype=np.uint8)
+    out = np.empty(matrix_bytes(type_, rows, cols), np.uint8)
+    _check(lib().lstk_repack_matrix(type_, rows, cols, gguf.ctypes.data, out.ctypes.data))
+    return out
+
+
+def unpack_matrix(type_, rows, cols, packed):
+    packed = np.ascontiguousarray(packed, dtype=np.uint8)
+    out = np.empty(matrix_bytes(type_, rows, cols), np.uint8)
+    _check(lib().lstk_unpack_matrix(type_, rows, cols, packed.ctypes.data, out.ctypes.data))
+    return out
+
+
+class ExpertStore:
+    """The HBM expert pool (ExpertStore, src/expert_store.h:113-131) and the MoE calls that read it.
+
+    layers: one (types, up, gate, down) per layer; types = (type_up, type_gate, type_down), and
+    up/gate/down are the layer's stacked expert tensors as GGUF bytes (numpy uint8, expert-major).
+    """
+
+    def __init__(self, n_layer, n_embd, n_ff_exp, n_expert, n_expert_used, n_batch, layers, pool_bytes=0,
+                 min_slots=0, streaming=False, dry=False):
+        self.dims = MoeDims(n_layer, n_embd, n_ff_exp, n_expert, n_expert_used, n_batch)
+        arr = (ExpertLayer * n_layer)()
+        self._keep = []
+        for l, (types, up, gate, down) in enumerate(layers):
+            ptrs = []
+            for a in (up, gate, down):
+                if a is None:
+                    ptrs.append(None)
+                else:
+                    a = np.ascontiguousarray(a)
+                    self._keep.append(a)
+                    ptrs.append(a.ctypes.data)
+            arr[l] = ExpertLayer(types[0], types[1], types[2], *ptrs)
+        flags = (POOL_STREAMING if streaming else 0) | (POOL_DRY if dry else 0)
+        h = ctypes.c_void_p()
+        _check(lib().lstk_pool_create(ctypes.byref(self.dims), ctypes.cast(arr, ctypes.c_void_p), int(pool_bytes),
+                                      int(min_slots), flags, ctypes.byref(h)))
+        self._h = h
+        self._keep = None  # the pool copied what it needs
+
+    def close(self):
+        if getattr(self, "_h", None):
+            lib().lstk_pool_destroy(self._h)
+            self._h = None
+
+    def __del__(self):
+        self.close()
+
+    # -- ExpertStore bookkeeping ------------------------------------------------------------
+    def acquire(self, layer, experts, stream=None):
+        e = np.ascontiguousarray(experts, dtype=np.int32).ravel()
+        slots = np.zeros(e.size, np.int32)
+        _check(lib().lstk_pool_acquire(self._h, layer, e.ctypes.data, e.size, slots.ctypes.data, _stream(stream)))
+        return slots.reshape(np.shape(experts))
+
+    def release_all(self, stream=None):
+        _check(lib().lstk_pool_release_all(self._h, _stream(stream)))
+
+    def stats(self):
+        s = PoolStats()
+        _check(lib().lstk_pool_stats(self._h, ctypes.byref(s)))
+        return dict(hits=s.hits, misses=s.misses, bytes_read=s.bytes_read, acquires=s.acquires, wait_ms=s.wait_ms)
+
+    def total_bytes(self):
+        return lib().lstk_pool_total_bytes(self._h)
+
+    def total_slots(self):
+        return lib().lstk_pool_total_slots(self._h)
+
+    def layer_slots(self, layer):
+        n = lib().lstk_pool_layer_slots(self._h, layer)
+        if n < 0:
+            _check(n)
+        return n
+
+    def describe(self):
+        buf = ctypes.create_string_buffer(1 << 16)
+        _check(lib().lstk_pool_describe(self._h, buf, len(buf)))
+        return buf.value.decode()
+
+    def debug_fail_copies(self, n):
+        _check(lib().lstk_pool_debug_fail_copies(self._h, n))
+
+    # -- compute ----------------------------------------------------------------------------
+    def route(self, layer, hnorm, gate_inp, gate_type, ids, weights, n_tokens=None, stream=None):
+        T = hnorm.shape[0] if n_tokens is None else n_tokens
+        _check(lib().lstk_moe_route(self._h, layer, _ptr(hnorm), T, _ptr(gate_inp), gate_type, _ptr(ids), _ptr(weights),
+                                    _stream(stream)))
+
+    def ffn(self, layer, hnorm, slots, weights, resid, out, n_tokens=None, stream=None):
+        T = hnorm.shape[0] if n_tokens is None else n_tokens
+        _check(lib().lstk_moe_ffn(self._h, layer, _ptr(hnorm), _ptr(slots), _ptr(weights), _ptr(resid), _ptr(out), T,
+                                  _stream(stream)))
+
+    def block(self, layer, hnorm, gate_inp, gate_type, resid, out, ids, weights, n_tokens=None, stream=None):
+        T = hnorm.shape[0] if n_tokens is None else n_tokens
+        _check(lib().lstk_moe_block(self._h, layer, _ptr(hnorm), _ptr(gate_inp), gate_type, _ptr(resid), _ptr(out),
+                                    _ptr(ids), _ptr(weights), T, _stream(stream)))
+
+    def check(self, stream=None):
+        _check(lib().lstk_pool_check(self._h, _stream(stream)))
+
+    def set_timing(self, on):
+        _check(lib().lstk_pool_set_timing(self._h, 1 if on else 0))
+
+    def timing(self):
+        ms = (ctypes.c_double * 3)()
+        n = (ctypes.c_int64 * 3)()
+        _check(lib().lstk_pool_timing(self._h, ms, n))
+        return list(ms), list(n)

@@ -1,0 +1,49 @@
+"""Builds localstack_amd/liblstk_moe.so (gfx950) with hipcc, in place.
+
+The library is the product: the HIP kernels (csrc/kernels.hip), the HBM expert pool and the C ABI
+(csrc/pool.cpp, include/lstk_moe.h) and the host repacker (csrc/repack.cpp).
+"""
+import os
+import shutil
+import subprocess
+import sys
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+ROOT = os.path.dirname(HERE)
+CSRC = os.path.join(HERE, "csrc")
+LIB = os.path.join(HERE, "liblstk_moe.so")
+SOURCES = ["kernels.hip", "pool.cpp", "repack.cpp"]
+ARCH = os.environ.get("LSTK_OFFLOAD_ARCH", "gfx950")
+
+
+def hipcc():
+    for c in (os.environ.get("HIPCC"), "/opt/rocm/bin/hipcc", shutil.which("hipcc")):
+        if c and os.path.exists(c):
+            return c
+    raise RuntimeError("hipcc not found")
+
+
+def build(verbose=False):
+    """Compiles every source for gfx950 and links the shared library; always rebuilds."""
+    tmp = LIB + ".tmp"
+    cmd = [hipcc(), "-x", "hip", f"--offload-arch={ARCH}", "-O3", "-std=c++20", "-fPIC", "-shared",
+           # packed-FP32 instructions off for all device code
+           "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+           "-Wall", "-Wno-unused-function", "-I", os.path.join(ROOT, "include"),
+           "-o", tmp] + [os.path.join(CSRC, s) for s in SOURCES] + ["-lpthread"]
+    if verbose:
+        print(" ".join(cmd), flush=True)
+    r = subprocess.run(cmd, capture_output=True, text=True)
+    out = "\n".join(l for l in (r.stdout + r.stderr).splitlines()
+                    if "packed-fp32-ops' is not a recognized feature" not in l)
+    if r.returncode != 0:
+        sys.stderr.write(out + "\n")
+        raise RuntimeError("hipcc failed")
+    if out.strip() and verbose:
+        print(out)
+    os.replace(tmp, LIB)
+    return LIB
+
+
+if __name__ == "__main__":
+    print(build(verbose=True))

@@ -1,0 +1,816 @@
+// pool.cpp - the HBM expert pool and the C ABI of the MoE path (include/lstk_moe.h).
+//
+// lstk_pool plays the part of the reference's ExpertStore (src/expert_store.h:113-149,
+// src/expert_store.cpp:106-295) on MI355X:
+//   - resident pools hold every expert of every layer in HBM (288 GB holds a 235B-A22B-shaped
+//     Q4_K expert table whole), slot s of a layer = expert s;
+//   - streaming pools keep the reference's slot bookkeeping exactly (type-triple classes, shards of
+//     at most 1024 slots, pin counts, intrusive LRU, hits/misses/bytes_read/acquires stats), with the
+//     GGUF file replaced by a pinned host tier and pread() by hipMemcpyAsync on a side stream that the
+//     compute stream waits on through an event, so acquire() never blocks the host on a copy;
+//   - a copy that fails unmaps its slot and fails the acquire (the reference only logs a short read,
+//     src/expert_store.cpp:62-66, and leaves the slot holding garbage).
+// It also owns the per-call device scratch (quantized activations, logits, permutation, SwiGLU rows,
+// per-pair outputs, arrival counters) sized for dims.n_batch tokens.
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <array>
+#include <chrono>
+#include <cstdio>
+#include <cstring>
+#include <map>
+#include <string>
+#include <thread>
+#include <tuple>
+#include <vector>
+
+#include "../../include/lstk_moe.h"
+#include "formats.h"
+#include "kernels.h"
+
+namespace lstk {
+int repack_matrix(int type, int rows, int cols, const void *gguf, void *packed);
+int unpack_matrix(int type, int rows, int cols, const void *packed, void *gguf);
+}  // namespace lstk
+
+namespace {
+
+thread_local std::string g_err;
+
+int fail(int code, const std::string &msg) {
+    g_err = msg;
+    return code;
+}
+
+int hip_fail(hipError_t e, const char *what) {
+    return fail(LSTK_E_DEVICE, std::string(what) + ": " + hipGetErrorString(e));
+}
+
+constexpr uint32_t kMaxSlotsPerShard = 1024; // kMaxSlotsPerPool, src/expert_store.h:80
+
+const char *type_name(int t) {
+    switch (t) {
+        case lstk::kTypeQ8_0: return "q8_0";
+        case lstk::kTypeQ4_K: return "q4_K";
+        case lstk::kTypeF16: return "f16";
+        case lstk::kTypeF32: return "f32";
+        default: return "?";
+    }
+}
+
+// One pool shard (ExpertPool, src/expert_store.h:83-110).
+struct Shard {
+    int tu = 0, tg = 0, td = 0;
+    size_t up_bytes = 0, gate_bytes = 0, down_bytes = 0, slab = 0;
+    uint32_t n_slots = 0;
+    std::vector<int> layers;
+    uint8_t *d_up = nullptr, *d_gate = nullptr, *d_down = nullptr;
+    std::vector<int32_t> owner_layer, owner_expert, refcount, prev, next;
+    int32_t lru_head = -1, lru_tail = -1;
+    uint32_t n_in_lru = 0;
+};
+
+void lru_push_tail(Shard &p, int32_t s) {
+    p.prev[s] = p.lru_tail;
+    p.next[s] = -1;
+    if (p.lru_tail >= 0) p.next[p.lru_tail] = s;
+    p.lru_tail = s;
+    if (p.lru_head < 0) p.lru_head = s;
+    p.n_in_lru++;
+}
+
+void lru_unlink(Shard &p, int32_t s) {
+    const int32_t a = p.prev[s], b = p.next[s];
+    if (a >= 0) p.next[a] = b;
+    else p.lru_head = b;
+    if (b >= 0) p.prev[b] = a;
+    else p.lru_tail = a;
+    p.prev[s] = p.next[s] = -1;
+    p.n_in_lru--;
+}
+
+int32_t lru_pop_head(Shard &p) {
+    const int32_t s = p.lru_head;
+    if (s < 0) return -1;
+    lru_unlink(p, s);
+    return s;
+}
+
+struct TimedLaunch {
+    hipEvent_t start, end;
+};
+
+}  // namespace
+
+struct lstk_pool {
+    lstk_moe_dims dims{};
+    bool streaming = false, dry = false;
+    int device = 0;
+    std::vector<Shard> shards;
+    std::vector<int> layer_shard;
+    std::vector<std::array<int, 3>> types;
+    std::vector<int32_t> slot_of; // streaming: [layer * n_expert + expert] -> slot or -1
+    std::vector<std::pair<int, int32_t>> pinned;
+    // streaming host tier: per layer, the layer's experts in pool layout, in pinned memory
+    uint8_t *tier = nullptr;
+    std::vector<std::array<uint8_t *, 3>> tier_of;
+    hipStream_t side = nullptr;
+    hipEvent_t copy_done = nullptr, release_ev = nullptr;
+    int fail_copies = 0;
+    lstk_pool_stats_t stats{};
+    // scratch
+    void *scratch = nullptr;
+    lstk::ActBuf xq{};
+    float *logits = nullptr, *act = nullptr, *Y = nullptr;
+    lstk::PermBuf pb{};
+    unsigned *route_counter = nullptr, *down_counters = nullptr;
+    int32_t *err = nullptr;
+    int n_bins_max = 0;
+    // timing
+    bool timing = false;
+    std::vector<TimedLaunch> launched[3];
+    double ms[3] = {0, 0, 0};
+    int64_t launches[3] = {0, 0, 0};
+};
+
+namespace {
+
+size_t align_up(size_t x, size_t a) { return (x + a - 1) / a * a; }
+
+int alloc_scratch(lstk_pool *P) {
+    const lstk_moe_dims &d = P->dims;
+    const size_t nb = (size_t) P->n_bins_max, T = (size_t) d.n_batch, k = (size_t) d.n_expert_used;
+    const size_t h = (size_t) d.n_embd, f = (size_t) d.n_ff_exp, E = (size_t) d.n_expert;
+    size_t off = 0;
+    auto take = [&](size_t bytes) {
+        const size_t o = off;
+        off = align_up(off + bytes, 256);
+        return o;
+    };
+    const size_t o_qs = take(T * h), o_d = take(T * (h / 32) * 4), o_bs = take(T * (h / 32) * 4);
+    const size_t o_logits = take(T * E * 4);
+    const size_t o_counts = take(nb * 4), o_offsets = take((nb + 1) * 4), o_active = take(nb * 4);
+    const size_t o_nactive = take(16), o_perm = take(T * k * 4);
+    const size_t o_act = take(T * k * f * 4), o_Y = take(T * k * h * 4);
+    const size_t o_rc = take(64), o_dc = take((h / 64) * 4 + 64), o_err = take(64);
+    hipError_t e = hipMalloc(&P->scratch, off);
+    if (e != hipSuccess) return hip_fail(e, "hipMalloc(scratch)");
+    e = hipMemset(P->scratch, 0, off);
+    if (e != hipSuccess) return hip_fail(e, "hipMemset(scratch)");
+    uint8_t *b = static_cast<uint8_t *>(P->scratch);
+    P->xq.qs = reinterpret_cast<int8_t *>(b + o_qs);
+    P->xq.d = reinterpret_cast<float *>(b + o_d);
+    P->xq.bs = reinterpret_cast<int32_t *>(b + o_bs);
+    P->logits = reinterpret_cast<float *>(b + o_logits);
+    P->pb.counts = reinterpret_cast<int32_t *>(b + o_counts);
+    P->pb.offsets = reinterpret_cast<int32_t *>(b + o_offsets);
+    P->pb.active = reinterpret_cast<int32_t *>(b + o_active);
+    P->pb.n_active = reinterpret_cast<int32_t *>(b + o_nactive);
+    P->pb.perm = reinterpret_cast<int32_t *>(b + o_perm);
+    P->act = reinterpret_cast<float *>(b + o_act);
+    P->Y = reinterpret_cast<float *>(b + o_Y);
+    P->route_counter = reinterpret_cast<unsigned *>(b + o_rc);
+    P->down_counters = reinterpret_cast<unsigned *>(b + o_dc);
+    P->err = reinterpret_cast<int32_t *>(b + o_err);
+    return LSTK_OK;
+}
+
+// Repacks `n_expert` GGUF expert matrices (expert-major) into dst (host memory, pool layout),
+// experts spread over host threads.
+int repack_experts(int type, int rows, int cols, int n_expert, const void *src, uint8_t *dst) {
+    const size_t bytes = lstk::matrix_bytes(type, rows, cols);
+    const int n_threads = (int) std::min<unsigned>(16, std::max(1u, std::thread::hardware_concurrency()));
+    std::vector<int> rcs(n_threads, LSTK_OK);
+    auto work = [&](int i) {
+        for (int e = i; e < n_expert; e += n_threads) {
+            const int rc = lstk::repack_matrix(type, rows, cols, static_cast<const uint8_t *>(src) + (size_t) e * bytes,
+                                               dst + (size_t) e * bytes);
+            if (rc != LSTK_OK) rcs[i] = rc;
+        }
+    };
+    std::vector<std::thread> pool;
+    for (int i = 1; i < n_threads; i++) pool.emplace_back(work, i);
+    work(0);
+    for (std::thread &t : pool) t.join();
+    for (int rc : rcs)
+        if (rc != LSTK_OK) return fail(rc, "repack failed");
+    return LSTK_OK;
+}
+
+void destroy(lstk_pool *P) {
+    if (!P) return;
+    if (!P->dry) {
+        for (Shard &s : P->shards) {
+            if (s.d_up) (void) hipFree(s.d_up);
+            if (s.d_gate) (void) hipFree(s.d_gate);
+            if (s.d_down) (void) hipFree(s.d_down);
+        }
+        if (P->tier) (void) hipHostFree(P->tier);
+        if (P->scratch) (void) hipFree(P->scratch);
+        if (P->copy_done) (void) hipEventDestroy(P->copy_done);
+        if (P->release_ev) (void) hipEventDestroy(P->release_ev);
+        if (P->side) (void) hipStreamDestroy(P->side);
+        for (auto &v : P->launched)
+            for (TimedLaunch &t : v) {
+                (void) hipEventDestroy(t.start);
+                (void) hipEventDestroy(t.end);
+            }
+    }
+    delete P;
+}
+
+// ExpertStore::init (src/expert_store.cpp:116-150): shard layout of a streaming pool.
+int plan_streaming(lstk_pool *P, size_t pool_bytes, uint32_t min_slots) {
+    const lstk_moe_dims &d = P->dims;
+    if (min_slots > kMaxSlotsPerShard)
+        return fail(LSTK_E_INVALID, "expert pool floor of " + std::to_string(min_slots) + " slots exceeds the limit of " +
+                                        std::to_string(kMaxSlotsPerShard) + " experts per shard");
+    std::map<std::tuple<int, int, int>, std::vector<int>> classes;
+    for (int l = 0; l < d.n_layer; l++)
+        classes[std::make_tuple(P->types[l][0], P->types[l][1], P->types[l][2])].push_back(l);
+    for (auto &[key, ls] : classes) {
+        const auto [tu, tg, td] = key;
+        const size_t ub = lstk::matrix_bytes(tu, d.n_ff_exp, d.n_embd), gb = lstk::matrix_bytes(tg, d.n_ff_exp, d.n_embd);
+        const size_t db = lstk::matrix_bytes(td, d.n_embd, d.n_ff_exp);
+        const size_t slab = ub + gb + db;
+        const size_t want = std::max<size_t>(min_slots, pool_bytes * ls.size() / (size_t) d.n_layer / slab);
+        const size_t n_shards = (want + kMaxSlotsPerShard - 1) / kMaxSlotsPerShard;
+        const size_t per = (ls.size() + n_shards - 1) / n_shards;
+        for (size_t i = 0; i < ls.size(); i += per) {
+            Shard p;
+            p.tu = tu;
+            p.tg = tg;
+            p.td = td;
+            p.up_bytes = ub;
+            p.gate_bytes = gb;
+            p.down_bytes = db;
+            p.slab = slab;
+            p.layers.assign(ls.begin() + (long) i, ls.begin() + (long) std::min(i + per, ls.size()));
+            const size_t share = pool_bytes * p.layers.size() / (size_t) d.n_layer;
+            p.n_slots = (uint32_t) std::min<size_t>(kMaxSlotsPerShard, std::max<size_t>(min_slots, share / slab));
+            for (int l : p.layers) P->layer_shard[l] = (int) P->shards.size();
+            p.owner_layer.assign(p.n_slots, -1);
+            p.owner_expert.assign(p.n_slots, -1);
+            p.refcount.assign(p.n_slots, 0);
+            p.prev.assign(p.n_slots, -1);
+            p.next.assign(p.n_slots, -1);
+            for (uint32_t s = 0; s < p.n_slots; s++) lru_push_tail(p, (int32_t) s);
+            P->shards.push_back(std::move(p));
+        }
+    }
+    return LSTK_OK;
+}
+
+int create(const lstk_moe_dims *dims, const lstk_expert_layer *layers, size_t pool_bytes, uint32_t min_slots,
+           uint32_t flags, lstk_pool **out) {
+    if (!dims || !layers || !out) return fail(LSTK_E_INVALID, "null argument");
+    *out = nullptr;
+    const lstk_moe_dims &d = *dims;
+    if (d.n_layer < 1 || d.n_batch < 1) return fail(LSTK_E_INVALID, "n_layer and n_batch must be >= 1");
+    lstk_pool *P = new lstk_pool();
+    P->dims = d;
+    P->streaming = (flags & LSTK_POOL_STREAMING) != 0;
+    P->dry = (flags & LSTK_POOL_DRY) != 0;
+    P->layer_shard.assign(d.n_layer, -1);
+    P->types.resize(d.n_layer);
+    for (int l = 0; l < d.n_layer; l++) {
+        const lstk_expert_layer &L = layers[l];
+        P->types[l] = {L.type_up, L.type_gate, L.type_down};
+        for (int t : P->types[l])
+            if (!lstk::supported_weight_type(t)) {
+                destroy(P);
+                return fail(LSTK_E_INVALID, "layer " + std::to_string(l) + ": unsupported expert type " + std::to_string(t) +
+                                                " (supported: 8 = Q8_0, 12 = Q4_K)");
+            }
+        if (L.type_up != L.type_gate) {
+            destroy(P);
+            return fail(LSTK_E_INVALID, "layer " + std::to_string(l) + ": gate and up experts must share a quant type");
+        }
+        if (!P->dry && (!L.host_up || !L.host_gate || !L.host_down)) {
+            destroy(P);
+            return fail(LSTK_E_INVALID, "layer " + std::to_string(l) + ": missing expert bytes");
+        }
+    }
+    int rc;
+    if (P->streaming) {
+        rc = plan_streaming(P, pool_bytes, min_slots);
+        if (rc != LSTK_OK) {
+            destroy(P);
+            return rc;
+        }
+        P->slot_of.assign((size_t) d.n_layer * d.n_expert, -1);
+    } else {
+        for (int l = 0; l < d.n_layer; l++) {
+            Shard p;
+            p.tu = P->types[l][0];
+            p.tg = P->types[l][1];
+            p.td = P->types[l][2];
+            p.up_bytes = lstk::matrix_bytes(p.tu, d.n_ff_exp, d.n_embd);
+            p.gate_bytes = lstk::matrix_bytes(p.tg, d.n_ff_exp, d.n_embd);
+            p.down_bytes = lstk::matrix_bytes(p.td, d.n_embd, d.n_ff_exp);
+            p.slab = p.up_bytes + p.gate_bytes + p.down_bytes;
+            p.n_slots = (uint32_t) d.n_expert;
+            p.layers = {l};
+            P->layer_shard[l] = (int) P->shards.size();
+            P->shards.push_back(std::move(p));
+        }
+    }
+    for (const Shard &s : P->shards) P->n_bins_max = std::max(P->n_bins_max, (int) s.n_slots);
+    const char *bad = lstk::check_shapes(d.n_embd, d.n_ff_exp, d.n_expert, d.n_expert_used, P->n_bins_max);
+    if (bad[0]) {
+        destroy(P);
+        return fail(LSTK_E_INVALID, bad);
+    }
+    if (P->dry) {
+        *out = P;
+        return LSTK_OK;
+    }
+    hipError_t e = hipGetDevice(&P->device);
+    if (e != hipSuccess) {
+        destroy(P);
+        return hip_fail(e, "hipGetDevice");
+    }
+    // HBM slots
+    for (Shard &s : P->shards) {
+        if ((e = hipMalloc(&s.d_up, s.up_bytes * s.n_slots)) != hipSuccess ||
+            (e = hipMalloc(&s.d_gate, s.gate_bytes * s.n_slots)) != hipSuccess ||
+            (e = hipMalloc(&s.d_down, s.down_bytes * s.n_slots)) != hipSuccess) {
+            destroy(P);
+            return fail(LSTK_E_NOMEM, std::string("cannot allocate expert pool memory: ") + hipGetErrorString(e));
+        }
+    }
+    const int h = d.n_embd, f = d.n_ff_exp, E = d.n_expert;
+    if (P->streaming) {
+        // pinned host tier with every layer's experts in pool layout (the stand-in for the GGUF file)
+        size_t total = 0;
+        for (int l = 0; l < d.n_layer; l++) total += (size_t) E * P->shards[P->layer_shard[l]].slab;
+        if ((e = hipHostMalloc((void **) &P->tier, total, hipHostMallocDefault)) != hipSuccess) {
+            destroy(P);
+            return fail(LSTK_E_NOMEM, std::string("cannot allocate the pinned host tier: ") + hipGetErrorString(e));
+        }
+        size_t off = 0;
+        P->tier_of.resize(d.n_layer);
+        for (int l = 0; l < d.n_layer; l++) {
+            const Shard &s = P->shards[P->layer_shard[l]];
+            uint8_t *u = P->tier + off, *g = u + (size_t) E * s.up_bytes, *dn = g + (size_t) E * s.gate_bytes;
+            P->tier_of[l] = {u, g, dn};
+            off += (size_t) E * s.slab;
+            if ((rc = repack_experts(s.tu, f, h, E, layers[l].host_up, u)) != LSTK_OK ||
+                (rc = repack_experts(s.tg, f, h, E, layers[l].host_gate, g)) != LSTK_OK ||
+                (rc = repack_experts(s.td, h, f, E, layers[l].host_down, dn)) != LSTK_OK) {
+                destroy(P);
+                return rc;
+            }
+        }
+        if ((e = hipStreamCreateWithFlags(&P->side, hipStreamNonBlocking)) != hipSuccess ||
+            (e = hipEventCreateWithFlags(&P->copy_done, hipEventDisableTiming)) != hipSuccess ||
+            (e = hipEventCreateWithFlags(&P->release_ev, hipEventDisableTiming)) != hipSuccess) {
+            destroy(P);
+            return hip_fail(e, "side stream / events");
+        }
+    } else {
+        // resident: repack each layer's experts on the host and upload them once
+        size_t maxb = 0;
+        for (const Shard &s : P->shards) maxb = std::max({maxb, s.up_bytes, s.gate_bytes, s.down_bytes});
+        std::vector<uint8_t> staging((size_t) E * maxb);
+        for (int l = 0; l < d.n_layer; l++) {
+            Shard &s = P->shards[P->layer_shard[l]];
+            const struct {
+                int type, rows, cols;
+                const void *src;
+                uint8_t *dst;
+                size_t bytes;
+            } mats[3] = {{s.tu, f, h, layers[l].host_up, s.d_up, s.up_bytes},
+                         {s.tg, f, h, layers[l].host_gate, s.d_gate, s.gate_bytes},
+                         {s.td, h, f, layers[l].host_down, s.d_down, s.down_bytes}};
+            for (const auto &m : mats) {
+                if ((rc = repack_experts(m.type, m.rows, m.cols, E, m.src, staging.data())) != LSTK_OK) {
+                    destroy(P);
+                    return rc;
+                }
+                if ((e = hipMemcpy(m.dst, staging.data(), (size_t) E * m.bytes, hipMemcpyHostToDevice)) != hipSuccess) {
+                    destroy(P);
+                    return hip_fail(e, "hipMemcpy(experts)");
+                }
+            }
+        }
+    }
+    if ((rc = alloc_scratch(P)) != LSTK_OK) {
+        destroy(P);
+        return rc;
+    }
+    *out = P;
+    return LSTK_OK;
+}
+
+// Issues the three host-tier -> HBM copies of a miss on the side stream.
+int copy_in(lstk_pool *P, int layer, const Shard &s, int32_t slot, int32_t expert) {
+    if (P->fail_copies > 0) {
+        P->fail_copies--;
+        return fail(LSTK_E_IO, "expert copy failed (injected) for layer " + std::to_string(layer) + " expert " +
+                                   std::to_string(expert));
+    }
+    if (P->dry) return LSTK_OK;
+    const auto &t = P->tier_of[layer];
+    const size_t b[3] = {s.up_bytes, s.gate_bytes, s.down_bytes};
+    uint8_t *dst[3] = {s.d_up, s.d_gate, s.d_down};
+    for (int m = 0; m < 3; m++) {
+        const hipError_t e = hipMemcpyAsync(dst[m] + (size_t) slot * b[m], t[m] + (size_t) expert * b[m], b[m],
+                                            hipMemcpyHostToDevice, P->side);
+        if (e != hipSuccess)
+            return fail(LSTK_E_IO, std::string("expert copy failed for layer ") + std::to_string(layer) + ": " +
+                                       hipGetErrorString(e));
+    }
+    return LSTK_OK;
+}
+
+// ExpertStore::acquire (src/expert_store.cpp:232-286). As in the reference, a miss records its slot
+// in slot_of at once, so a repeat of the expert later in the same call counts as a hit.
+int acquire(lstk_pool *P, int layer, const int32_t *experts, int n, int32_t *slots, hipStream_t stream) {
+    const lstk_moe_dims &d = P->dims;
+    if (layer < 0 || layer >= d.n_layer || n < 0 || (n > 0 && (!experts || !slots)))
+        return fail(LSTK_E_INVALID, "acquire: bad arguments");
+    for (int i = 0; i < n; i++)
+        if (experts[i] < 0 || experts[i] >= d.n_expert)
+            return fail(LSTK_E_INVALID, "acquire: expert id " + std::to_string(experts[i]) + " out of range");
+    const auto t0 = std::chrono::steady_clock::now();
+    P->stats.acquires++;
+    if (!P->streaming) {
+        for (int i = 0; i < n; i++) slots[i] = experts[i];
+        P->stats.hits += (uint64_t) n;
+        P->stats.wait_ms += std::chrono::duration<double, std::milli>(std::chrono::steady_clock::now() - t0).count();
+        return LSTK_OK;
+    }
+    const int sh = P->layer_shard[layer];
+    Shard &p = P->shards[sh];
+    std::vector<std::pair<int32_t, int32_t>> misses; // (slot, expert)
+    int rc = LSTK_OK;
+    for (int i = 0; i < n; i++) {
+        const int32_t e = experts[i];
+        int32_t &ref = P->slot_of[(size_t) layer * d.n_expert + e];
+        if (ref >= 0) {
+            const int32_t s = ref;
+            if (p.refcount[s] == 0) lru_unlink(p, s);
+            p.refcount[s]++;
+            P->pinned.push_back({sh, s});
+            slots[i] = s;
+            P->stats.hits++;
+            continue;
+        }
+        const int32_t s = lru_pop_head(p);
+        if (s < 0) {
+            rc = fail(LSTK_E_EXHAUSTED, "expert pool exhausted: layer " + std::to_string(layer) + " needs more than " +
+                                            std::to_string(p.n_slots) + " slots at once; raise the pool size or lower n_batch");
+            break;
+        }
+        if (p.owner_layer[s] >= 0) P->slot_of[(size_t) p.owner_layer[s] * d.n_expert + p.owner_expert[s]] = -1;
+        p.owner_layer[s] = layer;
+        p.owner_expert[s] = e;
+        ref = s;
+        p.refcount[s] = 1;
+        P->pinned.push_back({sh, s});
+        slots[i] = s;
+        misses.push_back({s, e});
+        P->stats.misses++;
+        P->stats.bytes_read += p.slab;
+    }
+    if (!misses.empty()) {
+        hipError_t e = hipSuccess;
+        // a slot released by earlier compute may only be overwritten once that compute has finished
+        if (!P->dry) e = hipStreamWaitEvent(P->side, P->release_ev, 0);
+        if (e != hipSuccess) rc = hip_fail(e, "hipStreamWaitEvent(side)");
+        for (const auto &[s, ex] : misses) {
+            const int crc = copy_in(P, layer, p, s, ex);
+            if (crc != LSTK_OK) {
+                // the slot holds no valid expert: unmap it rather than serve garbage
+                P->slot_of[(size_t) layer * d.n_expert + ex] = -1;
+                p.owner_layer[s] = -1;
+                p.owner_expert[s] = -1;
+                rc = crc;
+            }
+        }
+        if (!P->dry) {
+            if ((e = hipEventRecord(P->copy_done, P->side)) != hipSuccess ||
+                (e = hipStreamWaitEvent(stream, P->copy_done, 0)) != hipSuccess)
+                rc = hip_fail(e, "copy event");
+        }
+    }
+    P->stats.wait_ms += std::chrono::duration<double, std::milli>(std::chrono::steady_clock::now() - t0).count();
+    return rc;
+}
+
+int release_all(lstk_pool *P, hipStream_t stream) {
+    for (const auto &[sh, s] : P->pinned) {
+        Shard &p = P->shards[sh];
+        if (--p.refcount[s] == 0) lru_push_tail(p, s);
+    }
+    P->pinned.clear();
+    if (P->streaming && !P->dry) {
+        const hipError_t e = hipEventRecord(P->release_ev, stream);
+        if (e != hipSuccess) return hip_fail(e, "hipEventRecord(release)");
+    }
+    return LSTK_OK;
+}
+
+// Records events around a launch when timing is on.
+template <typename F>
+hipError_t timed(lstk_pool *P, int stage, hipStream_t st, F &&launch) {
+    if (!P->timing) return launch();
+    TimedLaunch t{};
+    hipError_t e;
+    if ((e = hipEventCreate(&t.start)) != hipSuccess) return e;
+    if ((e = hipEventCreate(&t.end)) != hipSuccess) return e;
+    if ((e = hipEventRecord(t.start, st)) != hipSuccess) return e;
+    const hipError_t le = launch();
+    if ((e = hipEventRecord(t.end, st)) != hipSuccess) return e;
+    P->launched[stage].push_back(t);
+    return le;
+}
+
+bool aligned(const void *p, size_t a) { return (reinterpret_cast<uintptr_t>(p) % a) == 0; }
+
+int check_call(lstk_pool *P, int layer, int T) {
+    if (!P) return fail(LSTK_E_INVALID, "null pool");
+    if (P->dry) return fail(LSTK_E_INVALID, "a dry pool has no device memory");
+    if (layer < 0 || layer >= P->dims.n_layer) return fail(LSTK_E_INVALID, "layer out of range");
+    if (T < 0 || T > P->dims.n_batch)
+        return fail(LSTK_E_INVALID, "n_tokens " + std::to_string(T) + " outside [0, n_batch = " +
+                                        std::to_string(P->dims.n_batch) + "]");
+    return LSTK_OK;
+}
+
+int run_experts(lstk_pool *P, int layer, const float *d_hnorm, const float *d_weights, const float *d_resid, float *d_out,
+                int T, hipStream_t st, const lstk::PrologueParams *pro_in, const int32_t *d_bins) {
+    const lstk_moe_dims &d = P->dims;
+    const Shard &s = P->shards[P->layer_shard[layer]];
+    lstk::PrologueParams pro{};
+    if (pro_in) pro = *pro_in;
+    pro.hnorm = d_hnorm;
+    pro.T = T;
+    pro.h = d.n_embd;
+    pro.k = d.n_expert_used;
+    pro.qtype = s.tu;
+    pro.xq = P->xq;
+    pro.do_perm = 1;
+    pro.bins = d_bins;
+    pro.n_bins = (int) s.n_slots;
+    pro.pb = P->pb;
+    pro.err = P->err;
+    pro.counter = P->route_counter;
+    hipError_t e = timed(P, 0, st, [&] { return lstk::launch_prologue(pro, st); });
+    if (e != hipSuccess) return hip_fail(e, "prologue launch");
+    const int max_active = std::min<int>((int) s.n_slots, T * d.n_expert_used);
+    lstk::GateUpParams gu{};
+    gu.w_gate = s.d_gate;
+    gu.w_up = s.d_up;
+    gu.stride_gate = s.gate_bytes;
+    gu.stride_up = s.up_bytes;
+    gu.type = s.tu;
+    gu.f = d.n_ff_exp;
+    gu.h = d.n_embd;
+    gu.k = d.n_expert_used;
+    gu.xq = P->xq;
+    gu.pb = P->pb;
+    gu.max_active = max_active;
+    gu.act = P->act;
+    e = timed(P, 1, st, [&] { return lstk::launch_gate_up(gu, st); });
+    if (e != hipSuccess) return hip_fail(e, "gate_up launch");
+    lstk::DownParams dn{};
+    dn.w_down = s.d_down;
+    dn.stride_down = s.down_bytes;
+    dn.type = s.td;
+    dn.h = d.n_embd;
+    dn.f = d.n_ff_exp;
+    dn.k = d.n_expert_used;
+    dn.T = T;
+    dn.act = P->act;
+    dn.weights = d_weights;
+    dn.pb = P->pb;
+    dn.max_active = max_active;
+    dn.Y = P->Y;
+    dn.resid = d_resid;
+    dn.out = d_out;
+    dn.counters = P->down_counters;
+    e = timed(P, 2, st, [&] { return lstk::launch_down(dn, st); });
+    if (e != hipSuccess) return hip_fail(e, "down launch");
+    return LSTK_OK;
+}
+
+int check_router_args(const void *d_gate_inp, int gate_type) {
+    if (gate_type != lstk::kTypeF16 && gate_type != lstk::kTypeF32)
+        return fail(LSTK_E_INVALID, "gate_inp type must be F16 (1) or F32 (0)");
+    if (!d_gate_inp || !aligned(d_gate_inp, gate_type == lstk::kTypeF16 ? 8 : 16))
+        return fail(LSTK_E_INVALID, "gate_inp must be non-null and 8 (F16) / 16 (F32) byte aligned");
+    return LSTK_OK;
+}
+
+int check_act(const float *p, const char *name) {
+    if (!p || !aligned(p, 16)) return fail(LSTK_E_INVALID, std::string(name) + " must be non-null and 16-byte aligned");
+    return LSTK_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+const char *lstk_last_error(void) { return g_err.c_str(); }
+int lstk_abi_version(void) { return LSTK_ABI_VERSION; }
+
+int lstk_pool_create(const lstk_moe_dims *dims, const lstk_expert_layer *layers, size_t pool_bytes, uint32_t min_slots,
+                     uint32_t flags, lstk_pool **out) {
+    try {
+        return create(dims, layers, pool_bytes, min_slots, flags, out);
+    } catch (const std::exception &ex) {
+        return fail(LSTK_E_NOMEM, std::string("lstk_pool_create: ") + ex.what());
+    }
+}
+
+void lstk_pool_destroy(lstk_pool *pool) { destroy(pool); }
+
+int lstk_pool_acquire(lstk_pool *pool, int layer, const int32_t *experts, int n, int32_t *slots, lstk_stream_t stream) {
+    if (!pool) return fail(LSTK_E_INVALID, "null pool");
+    return acquire(pool, layer, experts, n, slots, static_cast<hipStream_t>(stream));
+}
+
+int lstk_pool_release_all(lstk_pool *pool, lstk_stream_t stream) {
+    if (!pool) return fail(LSTK_E_INVALID, "null pool");
+    return release_all(pool, static_cast<hipStream_t>(stream));
+}
+
+int lstk_pool_stats(const lstk_pool *pool, lstk_pool_stats_t *out) {
+    if (!pool || !out) return fail(LSTK_E_INVALID, "null argument");
+    *out = pool->stats;
+    return LSTK_OK;
+}
+
+size_t lstk_pool_total_bytes(const lstk_pool *pool) {
+    size_t t = 0;
+    if (pool)
+        for (const Shard &s : pool->shards) t += s.slab * s.n_slots;
+    return t;
+}
+
+uint32_t lstk_pool_total_slots(const lstk_pool *pool) {
+    uint32_t t = 0;
+    if (pool)
+        for (const Shard &s : pool->shards) t += s.n_slots;
+    return t;
+}
+
+int lstk_pool_layer_slots(const lstk_pool *pool, int layer) {
+    if (!pool || layer < 0 || layer >= pool->dims.n_layer) return fail(LSTK_E_INVALID, "bad layer");
+    return (int) pool->shards[pool->layer_shard[layer]].n_slots;
+}
+
+int lstk_pool_describe(const lstk_pool *pool, char *buf, size_t len) {
+    if (!pool || !buf || len == 0) return fail(LSTK_E_INVALID, "null argument");
+    std::string s;
+    char line[256];
+    for (const Shard &p : pool->shards) {
+        snprintf(line, sizeof(line), "  pool %s/%s/%s: %zu layers, %u slots x %.2f MiB = %.2f GiB\n", type_name(p.tu),
+                 type_name(p.tg), type_name(p.td), p.layers.size(), p.n_slots, p.slab / 1048576.0,
+                 p.slab * (double) p.n_slots / 1073741824.0);
+        s += line;
+    }
+    snprintf(buf, len, "%s", s.c_str());
+    return LSTK_OK;
+}
+
+int lstk_moe_route(lstk_pool *pool, int layer, const float *d_hnorm, int n_tokens, const void *d_gate_inp, int gate_type,
+                   int32_t *d_ids, float *d_weights, lstk_stream_t stream) {
+    int rc;
+    if ((rc = check_call(pool, layer, n_tokens)) != LSTK_OK) return rc;
+    if (n_tokens == 0) return LSTK_OK;
+    if ((rc = check_router_args(d_gate_inp, gate_type)) != LSTK_OK || (rc = check_act(d_hnorm, "hnorm")) != LSTK_OK) return rc;
+    if (!d_ids || !d_weights) return fail(LSTK_E_INVALID, "ids and weights must be non-null");
+    hipStream_t st = static_cast<hipStream_t>(stream);
+    lstk::PrologueParams pro{};
+    pro.hnorm = d_hnorm;
+    pro.T = n_tokens;
+    pro.h = pool->dims.n_embd;
+    pro.k = pool->dims.n_expert_used;
+    pro.do_route = 1;
+    pro.gate_inp = d_gate_inp;
+    pro.gate_type = gate_type;
+    pro.E = pool->dims.n_expert;
+    pro.logits = pool->logits;
+    pro.ids = d_ids;
+    pro.weights = d_weights;
+    pro.qtype = 0;
+    pro.do_perm = 0;
+    pro.n_bins = pool->n_bins_max;
+    pro.err = pool->err;
+    pro.counter = pool->route_counter;
+    const hipError_t e = timed(pool, 0, st, [&] { return lstk::launch_prologue(pro, st); });
+    if (e != hipSuccess) return hip_fail(e, "route launch");
+    return LSTK_OK;
+}
+
+int lstk_moe_ffn(lstk_pool *pool, int layer, const float *d_hnorm, const int32_t *d_slots, const float *d_weights,
+                 const float *d_resid, float *d_out, int n_tokens, lstk_stream_t stream) {
+    int rc;
+    if ((rc = check_call(pool, layer, n_tokens)) != LSTK_OK) return rc;
+    if (n_tokens == 0) return LSTK_OK;
+    if ((rc = check_act(d_hnorm, "hnorm")) != LSTK_OK || (rc = check_act(d_resid, "resid")) != LSTK_OK ||
+        (rc = check_act(d_out, "out")) != LSTK_OK)
+        return rc;
+    if (!d_slots || !d_weights) return fail(LSTK_E_INVALID, "slots and weights must be non-null");
+    return run_experts(pool, layer, d_hnorm, d_weights, d_resid, d_out, n_tokens, static_cast<hipStream_t>(stream), nullptr,
+                       d_slots);
+}
+
+int lstk_moe_block(lstk_pool *pool, int layer, const float *d_hnorm, const void *d_gate_inp, int gate_type,
+                   const float *d_resid, float *d_out, int32_t *d_ids, float *d_weights, int n_tokens,
+                   lstk_stream_t stream) {
+    int rc;
+    if ((rc = check_call(pool, layer, n_tokens)) != LSTK_OK) return rc;
+    if (pool->streaming) return fail(LSTK_E_INVALID, "lstk_moe_block needs a resident pool; use route + acquire + ffn");
+    if (n_tokens == 0) return LSTK_OK;
+    if ((rc = check_router_args(d_gate_inp, gate_type)) != LSTK_OK || (rc = check_act(d_hnorm, "hnorm")) != LSTK_OK ||
+        (rc = check_act(d_resid, "resid")) != LSTK_OK || (rc = check_act(d_out, "out")) != LSTK_OK)
+        return rc;
+    if (!d_ids || !d_weights) return fail(LSTK_E_INVALID, "ids and weights must be non-null");
+    lstk::PrologueParams pro{};
+    pro.do_route = 1;
+    pro.gate_inp = d_gate_inp;
+    pro.gate_type = gate_type;
+    pro.E = pool->dims.n_expert;
+    pro.logits = pool->logits;
+    pro.ids = d_ids;
+    pro.weights = d_weights;
+    return run_experts(pool, layer, d_hnorm, d_weights, d_resid, d_out, n_tokens, static_cast<hipStream_t>(stream), &pro,
+                       d_ids);
+}
+
+int lstk_pool_check(lstk_pool *pool, lstk_stream_t stream) {
+    if (!pool) return fail(LSTK_E_INVALID, "null pool");
+    if (pool->dry) return LSTK_OK;
+    hipError_t e = hipStreamSynchronize(static_cast<hipStream_t>(stream));
+    if (e != hipSuccess) return hip_fail(e, "hipStreamSynchronize");
+    int32_t flag = 0;
+    if ((e = hipMemcpy(&flag, pool->err, sizeof(flag), hipMemcpyDeviceToHost)) != hipSuccess) return hip_fail(e, "read error flag");
+    if (flag) {
+        const int32_t zero = 0;
+        if ((e = hipMemcpy(pool->err, &zero, sizeof(zero), hipMemcpyHostToDevice)) != hipSuccess) return hip_fail(e, "clear error flag");
+        std::string msg = "a kernel saw";
+        if (flag & 1) msg += " an expert/slot id out of range (clamped)";
+        if (flag & 2) msg += std::string(flag & 1 ? " and" : "") + " an expert repeated within one token";
+        return fail(LSTK_E_BADID, msg);
+    }
+    return LSTK_OK;
+}
+
+int lstk_pool_set_timing(lstk_pool *pool, int enable) {
+    if (!pool) return fail(LSTK_E_INVALID, "null pool");
+    pool->timing = enable != 0;
+    return LSTK_OK;
+}
+
+int lstk_pool_timing(lstk_pool *pool, double ms[3], int64_t launches[3]) {
+    if (!pool || !ms || !launches) return fail(LSTK_E_INVALID, "null argument");
+    for (int s = 0; s < 3; s++) {
+        for (TimedLaunch &t : pool->launched[s]) {
+            hipError_t e = hipEventSynchronize(t.end);
+            if (e != hipSuccess) return hip_fail(e, "hipEventSynchronize");
+            float v = 0.0f;
+            if ((e = hipEventElapsedTime(&v, t.start, t.end)) != hipSuccess) return hip_fail(e, "hipEventElapsedTime");
+            pool->ms[s] += v;
+            pool->launches[s]++;
+            (void) hipEventDestroy(t.start);
+            (void) hipEventDestroy(t.end);
+        }
+        pool->launched[s].clear();
+        ms[s] = pool->ms[s];
+        launches[s] = pool->launches[s];
+        pool->ms[s] = 0.0;
+        pool->launches[s] = 0;
+    }
+    return LSTK_OK;
+}
+
+size_t lstk_matrix_bytes(int type, int rows, int cols) {
+    if (!lstk::supported_weight_type(type) || rows <= 0 || cols <= 0 || cols % lstk::kSuper) return 0;
+    return lstk::matrix_bytes(type, rows, cols);
+}
+
+int lstk_repack_matrix(int type, int rows, int cols, const void *gguf, void *packed) {
+    if (!gguf || !packed) return fail(LSTK_E_INVALID, "null argument");
+    const int rc = lstk::repack_matrix(type, rows, cols, gguf, packed);
+    return rc == LSTK_OK ? rc : fail(rc, "unsupported type or shape");
+}
+
+int lstk_unpack_matrix(int type, int rows, int cols, const void *packed, void *gguf) {
+    if (!gguf || !packed) return fail(LSTK_E_INVALID, "null argument");
+    const int rc = lstk::unpack_matrix(type, rows, cols, packed, gguf);
+    return rc == LSTK_OK ? rc : fail(rc, "unsupported type or shape");
+}
+
+// Test hook: makes the next n host-tier copies fail, to exercise the LSTK_E_IO path.
+int lstk_pool_debug_fail_copies(lstk_pool *pool, int n) {
+    if (!pool) return fail(LSTK_E_INVALID, "null pool");
+    pool->fail_copies = n;
+    return LSTK_OK;
+}
+
+}  // extern "C"

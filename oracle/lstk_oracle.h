@@ -1,0 +1,115 @@
+/* lstk_oracle.h - CPU oracle for the Qwen3-MoE expert-FFN path.
+ *
+ * TEST INFRASTRUCTURE ONLY. Only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg
+ * may load this library, and only as the checker (or the timed CPU baseline). The product path
+ * (localstack_amd/) never links or calls it.
+ *
+ * It restates, in plain C, what localstack's MoE block computes when ggml runs it on the CPU:
+ *   router()      src/qwen3.cpp:175-192
+ *   moe_apply()   src/qwen3.cpp:197-214, residual add :250 / :287
+ *   ExpertStore   src/expert_store.cpp:106-295 (slot bookkeeping only, no I/O)
+ * ggml itself (llama.cpp submodule pinned at 23b0202a189c44a54625aadcb37a946dd1d6278d,
+ * docs/llama_cpp_commit.txt:1) is not present, so its kernels are restated from its published
+ * algorithm: Q8_0/Q4_K/Q8_K block formats, quantize_row_q8_0 (x86 AVX path: id = 127/amax,
+ * round-half-even), quantize_row_q8_K_ref, ggml_vec_dot_q8_0_q8_0, ggml_vec_dot_q4_K_q8_K,
+ * ggml_vec_dot_f16 (activations rounded to fp16), soft_max (double-precision sum), argsort
+ * (descending), sum_rows (double), swiglu (x / (1 + expf(-x)) * g).
+ *
+ * What no check in this repository can pin (the reference's arithmetic lives in an absent library):
+ *   - ggml's SIMD reduction order inside each dot product (the oracle uses the fixed orders
+ *     documented per function; router logits use the 64-lane order the GPU kernel uses);
+ *   - ggml's SIMD expf / silu approximations (the oracle calls libm expf);
+ *   - std::sort's order among exactly equal probabilities (the oracle breaks ties to the lower id).
+ * Every other function is pinned by the tests listed in tests/test_oracle_*.py.
+ */
+#ifndef LSTK_ORACLE_H
+#define LSTK_ORACLE_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define OR_QK8_0 32
+#define OR_QK_K 256
+
+typedef struct {
+    uint16_t d; /* fp16 */
+    int8_t qs[OR_QK8_0];
+} or_block_q8_0; /* 34 bytes */
+
+typedef struct {
+    uint16_t d;    /* fp16 super-block scale for the 6-bit sub-block scales */
+    uint16_t dmin; /* fp16 super-block scale for the 6-bit sub-block mins */
+    uint8_t scales[12];
+    uint8_t qs[OR_QK_K / 2];
+} or_block_q4_K; /* 144 bytes */
+
+typedef struct {
+    float d;
+    int8_t qs[OR_QK_K];
+    int16_t bsums[OR_QK_K / 16];
+} or_block_q8_K; /* 292 bytes */
+
+/* ---- fp16 ---- */
+uint16_t or_fp32_to_fp16(float f); /* round to nearest even, like F16C / numpy */
+float or_fp16_to_fp32(uint16_t h);
+
+/* ---- block formats ---- */
+size_t or_row_bytes(int type, int n); /* bytes of one row of n values (types 0, 1, 8, 12, 15) */
+void or_quantize_q8_0_ref(const float *x, int n, void *out); /* quantize_row_q8_0_ref: roundf, id = 1/d */
+void or_quantize_q8_0_act(const float *x, int n, void *out); /* x86 quantize_row_q8_0: RNE, id = 127/amax */
+void or_quantize_q8_K(const float *x, int n, void *out);     /* quantize_row_q8_K_ref */
+void or_dequant_q8_0(const void *in, int n, float *y);
+void or_dequant_q4_K(const void *in, int n, float *y);
+void or_dequant_q8_K(const void *in, int n, float *y);
+void or_q4_K_scale_min(int j, const uint8_t *scales, uint8_t *sc, uint8_t *m); /* get_scale_min_k4 */
+float or_vec_dot_q8_0_q8_0(int n, const void *w, const void *x);
+float or_vec_dot_q4_K_q8_K(int n, const void *w, const void *x);
+
+/* ---- router (src/qwen3.cpp:175-192) ----
+ * hnorm [T][h] f32; gate_inp [E][h] of gate_type (0 = F32, 1 = F16).
+ * Outputs ids [T][k], weights [T][k]; logits / probs [T][E] are optional (may be NULL). */
+void or_router_logits(const float *hnorm, int T, int h, const void *gate_inp, int gate_type, int E, float *logits);
+void or_router(const float *hnorm, int T, int h, const void *gate_inp, int gate_type, int E, int k, int32_t *ids,
+               float *weights, float *logits, float *probs);
+
+/* ---- token -> expert permutation (grouping of ggml's CPU mul_mat_id) ----
+ * bins [T*k] in [0, n_bins). counts [n_bins], offsets [n_bins + 1] (exclusive scan),
+ * perm [T*k]: position -> pair index (t*k + j), pairs of one bin in token-major order,
+ * active [n_bins]: bins with count > 0 in ascending order; returns the number of active bins. */
+int or_permute(const int32_t *bins, int T, int k, int n_bins, int32_t *counts, int32_t *offsets, int32_t *perm,
+               int32_t *active);
+
+/* ---- expert FFN + combine + residual (src/qwen3.cpp:197-214, :250) ----
+ * Weights in GGUF layout: slot s of a matrix starts at base + s * stride (bytes).
+ * up/gate are [f rows][h cols], down is [h rows][f cols]. out may alias resid.
+ * y_out (optional, [T][k][h]) receives each pair's weighted expert output. */
+void or_moe_ffn(const float *hnorm, int T, int h, int f, int k, const int32_t *slots, const float *weights,
+                const float *resid, const void *up, const void *gate, const void *down, size_t stride_up,
+                size_t stride_gate, size_t stride_down, int type_up, int type_gate, int type_down, float *out,
+                float *y_out, int n_threads);
+
+/* ---- ExpertStore slot bookkeeping (src/expert_store.cpp:106-295) ---- */
+typedef struct or_pool or_pool;
+/* types / strides: [n_layer][3] = (up, gate, down). Returns NULL and fills err on failure. */
+or_pool *or_pool_create(int n_layer, int n_expert, const int32_t *types, const uint64_t *strides, uint64_t pool_bytes,
+                        uint32_t min_slots, char *err, size_t err_len);
+void or_pool_destroy(or_pool *p);
+int or_pool_acquire(or_pool *p, int layer, const int32_t *experts, int n, int32_t *slots, char *err, size_t err_len);
+void or_pool_release_all(or_pool *p);
+void or_pool_stats(const or_pool *p, uint64_t out[4]); /* hits, misses, bytes_read, acquires */
+int or_pool_n_shards(const or_pool *p);
+int or_pool_shard_of_layer(const or_pool *p, int layer);
+int or_pool_shard_slots(const or_pool *p, int shard);
+/* slot owner (layer, expert) or (-1, -1); returns the refcount. */
+int or_pool_slot_owner(const or_pool *p, int shard, int slot, int32_t *layer, int32_t *expert);
+/* LRU order of a shard, head (evicted next) first; returns the count written. */
+int or_pool_lru(const or_pool *p, int shard, int32_t *out, int cap);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

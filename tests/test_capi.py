@@ -1,0 +1,91 @@
+"""The C ABI library: it loads, exports every symbol include/lstk_moe.h declares, validates its
+inputs, and its host repacker round-trips GGUF bytes (no GPU: no compute call is made)."""
+import ctypes
+import os
+import re
+
+import numpy as np
+import pytest
+
+from localstack_amd import synth
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+
+
+def declared_functions():
+    src = open(os.path.join(ROOT, "include", "lstk_moe.h")).read()
+    src = re.sub(r"/\*.*?\*/", "", src, flags=re.S)
+    return sorted(set(re.findall(r"\b(lstk_[a-z_0-9]+)\s*\(", src)))
+
+
+def test_exports_every_declared_symbol(lstk):
+    names = declared_functions()
+    assert len(names) >= 20
+    raw = ctypes.CDLL(lstk.LIB_PATH)
+    for n in names:
+        assert hasattr(raw, n), n
+    assert set(names) == set(lstk.SIGNATURES), set(names) ^ set(lstk.SIGNATURES)
+    assert lstk.lib().lstk_abi_version() == 1
+
+
+@pytest.mark.parametrize("wtype,rows,cols", [(8, 768, 2048), (8, 2048, 768), (12, 768, 2048), (12, 256, 512), (8, 3, 256)])
+def test_repack_roundtrip_and_layout(lstk, wtype, rows, cols):
+    rng = np.random.default_rng(rows + cols + wtype)
+    g = synth.experts(rng, wtype, 1, rows, cols)
+    assert g.size == lstk.matrix_bytes(wtype, rows, cols)
+    p = lstk.repack_matrix(wtype, rows, cols, g)
+    assert np.array_equal(lstk.unpack_matrix(wtype, rows, cols, p), g)
+    assert not np.array_equal(p, g) or rows == 1
+    # chunk (sb, c, r) of the pool layout sits at ((sb * C + c) * rows + r) * 16
+    C = 17 if wtype == 8 else 9
+    sbb = C * 16
+    r, sb = rows - 1, cols // 256 - 1
+    row = g[r * (cols // 256) * sbb:(r + 1) * (cols // 256) * sbb]
+    blk = row[sb * sbb:(sb + 1) * sbb]
+    at = lambda c: p[((sb * C + c) * rows + r) * 16:((sb * C + c) * rows + r) * 16 + 16]
+    if wtype == 12:
+        for c in range(9):
+            assert np.array_equal(at(c), blk[16 * c:16 * c + 16])
+    else:
+        b = blk.reshape(8, 34)
+        assert np.array_equal(at(0), b[:, 0:2].reshape(-1))
+        for i in range(8):
+            assert np.array_equal(at(1 + 2 * i), b[i, 2:18]) and np.array_equal(at(2 + 2 * i), b[i, 18:34])
+
+
+def test_rejects_bad_shapes_and_types(lstk):
+    Q8 = (8, 8, 8)
+    cases = [
+        (dict(n_embd=300), "n_embd"),
+        (dict(n_ff_exp=100), "n_ff_exp"),
+        (dict(n_embd=8192), "4096"),
+        (dict(n_expert=300), "n_expert"),
+        (dict(n_expert_used=9), "n_expert_used"),
+        (dict(types=(2, 2, 2)), "unsupported expert type"),
+        (dict(types=(8, 12, 8)), "share a quant type"),
+    ]
+    for over, msg in cases:
+        a = dict(n_layer=2, n_embd=256, n_ff_exp=512, n_expert=8, n_expert_used=2, n_batch=4, types=Q8)
+        a.update(over)
+        t = a.pop("types")
+        with pytest.raises(lstk.LstkError, match=msg) as ei:
+            lstk.ExpertStore(a["n_layer"], a["n_embd"], a["n_ff_exp"], a["n_expert"], a["n_expert_used"], a["n_batch"],
+                             [(t, None, None, None)] * a["n_layer"], dry=True)
+        assert ei.value.code == lstk.E_INVALID
+
+
+def test_dry_pool_refuses_compute(lstk):
+    p = lstk.ExpertStore(1, 256, 512, 8, 2, 4, [((8, 8, 8), None, None, None)], dry=True)
+    with pytest.raises(lstk.LstkError, match="dry pool"):
+        p.ffn(0, 16, 16, 16, 16, 16, n_tokens=1, stream=0)
+    with pytest.raises(lstk.LstkError, match="dry pool"):
+        p.block(0, 16, 16, 1, 16, 16, 16, 16, n_tokens=1, stream=0)
+
+
+def test_missing_library_fails_loudly(tmp_path, monkeypatch):
+    import importlib
+    import localstack_amd
+    monkeypatch.setattr(localstack_amd, "_lib", None)
+    monkeypatch.setattr(localstack_amd, "LIB_PATH", str(tmp_path / "missing.so"))
+    with pytest.raises(ImportError, match="missing"):
+        localstack_amd.lib()
