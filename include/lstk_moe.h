@@ -131,10 +131,10 @@ int lstk_moe_route(lstk_pool *pool, int layer, const float *d_hnorm, int n_token
 int lstk_moe_ffn(lstk_pool *pool, int layer, const float *d_hnorm, const int32_t *d_slots, const float *d_weights,
                  const float *d_resid, float *d_out, int n_tokens, lstk_stream_t stream);
 
-/* The whole MoE block of a resident layer in one call (router + experts + residual), with the
- * router's last block also building the token->expert permutation, so no host round trip is
- * needed. d_ids / d_weights receive the routing (for traces, src/engine.cpp:301-316); they may not
- * be NULL. Valid for resident pools only. */
+/* The whole MoE block of a resident layer in one call (router + experts + residual) with no host
+ * round trip: up to 16 tokens the gate/up kernel runs the top-k itself from the router logits.
+ * d_ids / d_weights receive the routing (for traces, src/engine.cpp:301-316); they may not be NULL.
+ * Valid for resident pools only. */
 int lstk_moe_block(lstk_pool *pool, int layer, const float *d_hnorm, const void *d_gate_inp, int gate_type,
                    const float *d_resid, float *d_out, int32_t *d_ids, float *d_weights, int n_tokens,
                    lstk_stream_t stream);
@@ -143,12 +143,15 @@ int lstk_moe_block(lstk_pool *pool, int layer, const float *d_hnorm, const void 
  * last check (the id is clamped on the device so no access leaves the pool). */
 int lstk_pool_check(lstk_pool *pool, lstk_stream_t stream);
 
-/* Per-stage kernel timing with HIP events recorded on the compute stream around each launch.
- * stage: 0 = prologue (router / quantize / permute), 1 = gate+up+SwiGLU, 2 = down+combine.
- * lstk_pool_timing syncs the events recorded so far and returns the summed milliseconds and the
- * launch count of each stage; it resets the counters. */
+/* Per-stage kernel timing: with timing on, every launch records its own start and stop timestamps
+ * into HIP events (hipExtLaunchKernel), the interval a kernel trace reports.
+ * stage: 0 = router logits + activation quantization (+ the top-k kernel above 16 tokens),
+ * 1 = gate + up + SwiGLU, 2 = down + router weight, 3 = combine + residual.
+ * lstk_pool_timing waits for the launches recorded so far and returns the summed milliseconds and
+ * the launch count of each stage; it resets the counters. Timing is for eager launches (not inside
+ * a captured graph). */
 int lstk_pool_set_timing(lstk_pool *pool, int enable);
-int lstk_pool_timing(lstk_pool *pool, double ms[3], int64_t launches[3]);
+int lstk_pool_timing(lstk_pool *pool, double ms[4], int64_t launches[4]);
 
 /* Host-side repacking between GGUF expert bytes and the pool's HBM layout (one expert matrix of
  * `rows` x `cols`). The pool layout is [cols/256][C][rows][16 B]: each 256-value super-block row is

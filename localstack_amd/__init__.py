@@ -244,7 +244,8 @@ class ExpertStore:
         _check(lib().lstk_pool_set_timing(self._h, 1 if on else 0))
 
     def timing(self):
-        ms = (ctypes.c_double * 3)()
-        n = (ctypes.c_int64 * 3)()
+        """(ms, launches) per stage: router (+ top-k), gate_up, down, combine."""
+        ms = (ctypes.c_double * 4)()
+        n = (ctypes.c_int64 * 4)()
         _check(lib().lstk_pool_timing(self._h, ms, n))
         return list(ms), list(n)

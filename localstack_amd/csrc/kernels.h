@@ -8,77 +8,93 @@
 
 namespace lstk {
 
-// Quantized activations: qs [T][K] int8, d [T][K/32] f32 (the scale of the 32-value group; Q8_K's
-// per-256 scale is repeated 8 times), bs [T][K/32] int32 (sum of the group's int8 values, Q8_K only).
+// Quantized activations: qs [rows][K] int8, d [rows][K/32] f32 (the scale of each 32-value group;
+// Q8_K's per-256 scale is repeated 8 times), bs [rows][K/32] int32 (group sums, Q8_K only).
 struct ActBuf {
     int8_t *qs;
     float *d;
     int32_t *bs;
 };
 
-// Token -> bin permutation: counts [n_bins], offsets [n_bins + 1], active [n_bins] (bins with
-// count > 0, ascending), n_active [1], perm [T*k] (position -> pair index t*k + j).
-struct PermBuf {
-    int32_t *counts;
-    int32_t *offsets;
-    int32_t *active;
-    int32_t *n_active;
-    int32_t *perm;
+// When non-null, a launch records its own start/stop timestamps into these events
+// (hipExtLaunchKernel), i.e. the same interval a kernel trace reports.
+struct LaunchTiming {
+    hipEvent_t start = nullptr, stop = nullptr;
 };
 
-struct PrologueParams {
+// Router logits and activation quantization (fully parallel, no cross-work-group step).
+struct RouteParams {
     const float *hnorm;
-    int T, h, k;
-    // router
+    int T, h;
     int do_route;
     const void *gate_inp;
     int gate_type;
     int E;
-    float *logits;
+    float *logits; // [T][E]
+    int qtype;     // 0: none, 8: Q8_0 rows, 12: Q8_K rows (for Q4_K weights)
+    ActBuf xq;
+};
+
+// softmax + top-k + renormalisation from logits, one wavefront per token.
+struct TopkParams {
+    const float *logits;
+    int T, E, k;
     int32_t *ids;
     float *weights;
-    // activation quantization (qtype 0 = none, 8 = Q8_0, 12 = Q8_K for Q4_K weights)
-    int qtype;
-    ActBuf xq;
-    // permutation (bins = ids when routing)
-    int do_perm;
-    const int32_t *bins;
-    int n_bins;
-    PermBuf pb;
+};
+
+// How a work-group of the expert kernels finds its expert and that expert's (token, slot) pairs.
+// route = 1 (gate_up only): the work-group computes the top-k of every token from `logits` itself;
+// work-group (0, 0) stores ids / weights. route = 0: ids come from `ids`.
+struct GroupParams {
+    int T, k, n_bins;
+    int route;
+    const int32_t *ids;
+    const float *logits;
+    int E;
+    int32_t *ids_out;
+    float *weights_out;
     int32_t *err;
-    unsigned *counter;
 };
 
 struct GateUpParams {
+    GroupParams gp;
     const uint8_t *w_gate, *w_up;
     size_t stride_gate, stride_up; // bytes per slot
     int type;                      // weight type of gate and up
-    int f, h, k;
+    int f, h;
     ActBuf xq;
-    PermBuf pb;
     int max_active;
-    float *act; // [T*k][f], rows in permuted order
+    float *act; // [T*k][f] SwiGLU rows by pair index t*k + j
 };
 
 struct DownParams {
+    GroupParams gp;
     const uint8_t *w_down;
     size_t stride_down;
     int type;
-    int h, f, k, T;
+    int h, f;
     const float *act;
-    const float *weights; // [T*k] router weights
-    PermBuf pb;
+    const float *weights; // [T*k]
     int max_active;
-    float *Y;             // [T*k][h] weighted expert outputs by pair index
+    float *Y; // [T*k][h] weighted expert outputs by pair index
+};
+
+struct CombineParams {
+    const float *Y;
     const float *resid;
     float *out;
-    unsigned *counters;   // [h / 64], zero between calls
+    int T, k, h;
 };
 
 // Checks the shapes the kernels assume; returns an empty string when they hold.
-const char *check_shapes(int h, int f, int E, int k, int n_bins);
-hipError_t launch_prologue(const PrologueParams &p, hipStream_t s);
-hipError_t launch_gate_up(const GateUpParams &p, hipStream_t s);
-hipError_t launch_down(const DownParams &p, hipStream_t s);
+const char *check_shapes(int h, int f, int E, int k, int n_bins, int n_batch);
+// Largest n_tokens for which gate_up computes the top-k itself.
+int decode_route_max_tokens();
+hipError_t launch_route(const RouteParams &p, hipStream_t s, const LaunchTiming *t);
+hipError_t launch_topk(const TopkParams &p, hipStream_t s, const LaunchTiming *t);
+hipError_t launch_gate_up(const GateUpParams &p, hipStream_t s, const LaunchTiming *t);
+hipError_t launch_down(const DownParams &p, hipStream_t s, const LaunchTiming *t);
+hipError_t launch_combine(const CombineParams &p, hipStream_t s, const LaunchTiming *t);
 
 }  // namespace lstk

@@ -1,20 +1,21 @@
 // kernels.hip - gfx950 (CDNA4) kernels of the Qwen3-MoE expert-FFN path.
 //
-// One MoE block = three launches on the caller's stream:
-//   prologue  router logits (one wavefront per expert, all tokens of a tile), activation
-//             quantization (Q8_0 or Q8_K rows of hnorm), and in the last work-group to finish:
-//             softmax + top-k + renormalisation per token (one wavefront per token) and the stable
-//             token->expert permutation. Replaces src/qwen3.cpp:178-189 and ggml's mul_mat_id
-//             grouping. The "last work-group" is found with one atomic per work-group: nobody waits.
-//   gate_up   per active expert and 16-row block: gate and up rows dequantized in registers from
-//             coalesced 16-byte chunks, int8 dot products (v_dot4_i32_i8) against the quantized
-//             activations of every token routed to the expert, fused SwiGLU (src/qwen3.cpp:201-203).
-//   down      per active expert and 64-row block: the SwiGLU rows re-quantized in LDS, down rows
-//             from registers, each pair's output scaled by its router weight (src/qwen3.cpp:204-205);
-//             the last expert to finish a row block sums the k outputs of every token in slot order
-//             and adds the residual (src/qwen3.cpp:206-212, :250).
-// Decode is HBM-bound: every weight byte is read once per step, with all of a thread's loads issued
-// before any arithmetic.
+// A MoE block is four or five launches on the caller's stream, none of which waits on another
+// work-group (cross-work-group arrival counters cost ~60 ns of serialized L2 write-back per
+// work-group on this part):
+//   route     router logits (a wavefront per expert, all tokens of a tile; src/qwen3.cpp:178) and
+//             the Q8_0 / Q8_K quantization of hnorm rows, in one grid.
+//   topk      (n_tokens > 16) softmax + top-k + renormalisation, a wavefront per token
+//             (src/qwen3.cpp:179-189).
+//   gate_up   per active expert and row block: gate and up rows held in registers, loaded as
+//             coalesced 16-byte chunks before anything else; v_dot4_i32_i8 against the quantized
+//             activations of every token routed to the expert; fused SwiGLU (src/qwen3.cpp:201-203).
+//             Each work-group derives its expert and token list from the routing itself (for
+//             n_tokens <= 16 it also runs the top-k), replacing ggml's mul_mat_id grouping.
+//   down      per active expert and 64-row block: the SwiGLU rows re-quantized in LDS, down rows from
+//             registers, each pair's output times its router weight (src/qwen3.cpp:204-205).
+//   combine   out = resid + sum_j y_j, left to right in the slot index j (src/qwen3.cpp:206-212, :250).
+#include <hip/hip_ext.h>
 #include <hip/hip_fp16.h>
 #include <hip/hip_runtime.h>
 
@@ -34,15 +35,68 @@ constexpr int kRouteEPW = 2;      // experts per wavefront in the router tile
 constexpr int kRouteEG = 8;       // experts per router work-group (4 wavefronts x 2)
 constexpr int kRouteMaxNG = 16;   // n_embd <= 4096: 16 groups of 256 per lane
 constexpr int kMaxEPL = 4;        // n_expert <= 256: 4 logits per lane in the top-k
-constexpr int kGuRows = 16;       // rows of gate (and of up) per gate_up work-group
 constexpr int kDnRows = 64;       // rows per down work-group
 constexpr int kTC = 8;            // tokens staged per pass
 constexpr int kMaxG = 8;          // K-groups per work-group
 constexpr int kMaxK = 64;         // n_expert_used <= 64 (one lane per selected expert)
 constexpr int kMaxBins = 4096;
+constexpr int kMaxPairs = 8192;   // n_batch * n_expert_used
+constexpr int kDecodeRouteT = 16; // gate_up runs the top-k itself up to this many tokens
 
 __device__ __forceinline__ float h2f(unsigned h) { return __half2float(__ushort_as_half((unsigned short) (h & 0xffffu))); }
 __device__ __forceinline__ float round_f16(float x) { return __half2float(__float2half_rn(x)); }
+
+// ------------------------------------------------------------------------------------------------
+// wavefront reductions without LDS: DPP within 16-lane rows, readlane across rows
+// ------------------------------------------------------------------------------------------------
+
+template <int CTRL>
+__device__ __forceinline__ float dpp_f(float v) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xF, 0xF, false));
+}
+template <int CTRL>
+__device__ __forceinline__ double dpp_d(double v) {
+    const unsigned long long u = __builtin_bit_cast(unsigned long long, v);
+    const int lo = __builtin_amdgcn_update_dpp(0, (int) (u & 0xffffffffu), CTRL, 0xF, 0xF, false);
+    const int hi = __builtin_amdgcn_update_dpp(0, (int) (u >> 32), CTRL, 0xF, 0xF, false);
+    return __builtin_bit_cast(double, ((unsigned long long) (unsigned) hi << 32) | (unsigned) lo);
+}
+__device__ __forceinline__ float readlane_f(float v, int l) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), l));
+}
+__device__ __forceinline__ double readlane_d(double v, int l) {
+    const unsigned long long u = __builtin_bit_cast(unsigned long long, v);
+    const unsigned lo = (unsigned) __builtin_amdgcn_readlane((int) (u & 0xffffffffu), l);
+    const unsigned hi = (unsigned) __builtin_amdgcn_readlane((int) (u >> 32), l);
+    return __builtin_bit_cast(double, ((unsigned long long) hi << 32) | lo);
+}
+
+// Sum over the 64 lanes as a pairwise tree: lanes l and l^1, then quads, octets, halves of rows,
+// rows (0+1, 2+3) and the two row pairs. IEEE addition is commutative, so every lane of a level
+// holds the same partial; the oracle evaluates the same tree. Result uniform.
+__device__ __forceinline__ float wave_sum_tree(float v) {
+    v = v + dpp_f<0xB1>(v);   // quad_perm [1,0,3,2]
+    v = v + dpp_f<0x4E>(v);   // quad_perm [2,3,0,1]
+    v = v + dpp_f<0x141>(v);  // row_half_mirror: the other quad of the octet
+    v = v + dpp_f<0x140>(v);  // row_mirror: the other octet of the row
+    return (readlane_f(v, 0) + readlane_f(v, 16)) + (readlane_f(v, 32) + readlane_f(v, 48));
+}
+
+__device__ __forceinline__ double wave_sum_d(double v) {
+    v = v + dpp_d<0xB1>(v);
+    v = v + dpp_d<0x4E>(v);
+    v = v + dpp_d<0x141>(v);
+    v = v + dpp_d<0x140>(v);
+    return (readlane_d(v, 0) + readlane_d(v, 16)) + (readlane_d(v, 32) + readlane_d(v, 48));
+}
+
+__device__ __forceinline__ float wave_max(float v) {
+    v = fmaxf(v, dpp_f<0xB1>(v));
+    v = fmaxf(v, dpp_f<0x4E>(v));
+    v = fmaxf(v, dpp_f<0x141>(v));
+    v = fmaxf(v, dpp_f<0x140>(v));
+    return fmaxf(fmaxf(readlane_f(v, 0), readlane_f(v, 16)), fmaxf(readlane_f(v, 32), readlane_f(v, 48)));
+}
 
 // ------------------------------------------------------------------------------------------------
 // router logits
@@ -50,16 +104,43 @@ __device__ __forceinline__ float round_f16(float x) { return __half2float(__floa
 
 // Dot products of a tile of tokens with kRouteEG experts. Lane l of a wavefront owns elements
 // 256 g + 4 l + q (g ascending, then q) and accumulates them with fmaf from 0; the 64 partials are
-// combined with a butterfly. The oracle evaluates the same expression in the same order, so the
+// summed by wave_sum_tree. The oracle evaluates the same expression in the same order, so the
 // logits agree bit for bit and so does the top-k. F16 weights see fp16-rounded activations, as
 // ggml's CPU mul_mat converts src1 to the F16 vec_dot_type (src/qwen3.cpp:178).
-template <int GT>
-__device__ void route_tile(const PrologueParams &P, int b, float *xs, int tt) {
+// The wavefront's two weight rows are loaded before the activations are staged.
+template <int GT, int NG>
+__device__ __forceinline__ void route_tile(const RouteParams &P, int b, float *xs, int tt) {
     const int n_eg = (P.E + kRouteEG - 1) / kRouteEG;
     const int tile = b / n_eg, eg = b - tile * n_eg;
     const int t0 = tile * tt;
     const int nt = min(tt, P.T - t0);
-    const int h = P.h, ng = h / 256;
+    constexpr int h = NG * 256;
+    const int wave = threadIdx.x / kWave, lane = threadIdx.x % kWave;
+    float w[kRouteEPW][NG][4];
+    // every load unconditional and unrolled, so all of them are in flight before the first use
+#pragma unroll
+    for (int ee = 0; ee < kRouteEPW; ee++) {
+        const int e = min(eg * kRouteEG + wave * kRouteEPW + ee, P.E - 1);
+#pragma unroll
+        for (int g = 0; g < NG; g++) {
+            {
+                const size_t i = (size_t) e * h + 256 * g + 4 * lane;
+                if (GT == kTypeF16) {
+                    const uint2 raw = *reinterpret_cast<const uint2 *>(static_cast<const unsigned short *>(P.gate_inp) + i);
+                    w[ee][g][0] = h2f(raw.x);
+                    w[ee][g][1] = h2f(raw.x >> 16);
+                    w[ee][g][2] = h2f(raw.y);
+                    w[ee][g][3] = h2f(raw.y >> 16);
+                } else {
+                    const float4 raw = *reinterpret_cast<const float4 *>(static_cast<const float *>(P.gate_inp) + i);
+                    w[ee][g][0] = raw.x;
+                    w[ee][g][1] = raw.y;
+                    w[ee][g][2] = raw.z;
+                    w[ee][g][3] = raw.w;
+                }
+            }
+        }
+    }
     const float4 *src = reinterpret_cast<const float4 *>(P.hnorm + (size_t) t0 * h);
     float4 *dst = reinterpret_cast<float4 *>(xs);
     for (int i = threadIdx.x; i < nt * h / 4; i += blockDim.x) {
@@ -73,45 +154,28 @@ __device__ void route_tile(const PrologueParams &P, int b, float *xs, int tt) {
         dst[i] = v;
     }
     __syncthreads();
-    const int wave = threadIdx.x / kWave, lane = threadIdx.x % kWave;
-    for (int ee = 0; ee < kRouteEPW; ee++) {
-        const int e = eg * kRouteEG + wave * kRouteEPW + ee;
-        if (e >= P.E) break;
-        float w[kRouteMaxNG][4];
+    for (int t = 0; t < nt; t++) {
+        float acc[kRouteEPW];
 #pragma unroll
-        for (int g = 0; g < kRouteMaxNG; g++) {
-            if (g < ng) {
-                const size_t i = (size_t) e * h + 256 * g + 4 * lane;
-                if (GT == kTypeF16) {
-                    const uint2 raw = *reinterpret_cast<const uint2 *>(static_cast<const unsigned short *>(P.gate_inp) + i);
-                    w[g][0] = h2f(raw.x);
-                    w[g][1] = h2f(raw.x >> 16);
-                    w[g][2] = h2f(raw.y);
-                    w[g][3] = h2f(raw.y >> 16);
-                } else {
-                    const float4 raw = *reinterpret_cast<const float4 *>(static_cast<const float *>(P.gate_inp) + i);
-                    w[g][0] = raw.x;
-                    w[g][1] = raw.y;
-                    w[g][2] = raw.z;
-                    w[g][3] = raw.w;
+        for (int ee = 0; ee < kRouteEPW; ee++) acc[ee] = 0.0f;
+#pragma unroll
+        for (int g = 0; g < NG; g++) {
+            {
+                const float4 x = *reinterpret_cast<const float4 *>(xs + (size_t) t * h + 256 * g + 4 * lane);
+#pragma unroll
+                for (int ee = 0; ee < kRouteEPW; ee++) {
+                    acc[ee] = fmaf(x.x, w[ee][g][0], acc[ee]);
+                    acc[ee] = fmaf(x.y, w[ee][g][1], acc[ee]);
+                    acc[ee] = fmaf(x.z, w[ee][g][2], acc[ee]);
+                    acc[ee] = fmaf(x.w, w[ee][g][3], acc[ee]);
                 }
             }
         }
-        for (int t = 0; t < nt; t++) {
-            float acc = 0.0f;
 #pragma unroll
-            for (int g = 0; g < kRouteMaxNG; g++) {
-                if (g < ng) {
-                    const float4 x = *reinterpret_cast<const float4 *>(xs + (size_t) t * h + 256 * g + 4 * lane);
-                    acc = fmaf(x.x, w[g][0], acc);
-                    acc = fmaf(x.y, w[g][1], acc);
-                    acc = fmaf(x.z, w[g][2], acc);
-                    acc = fmaf(x.w, w[g][3], acc);
-                }
-            }
-#pragma unroll
-            for (int s = 32; s >= 1; s >>= 1) acc = acc + __shfl_xor(acc, s);
-            if (lane == 0) P.logits[(size_t) (t0 + t) * P.E + e] = acc;
+        for (int ee = 0; ee < kRouteEPW; ee++) {
+            const int e = eg * kRouteEG + wave * kRouteEPW + ee;
+            const float sum = wave_sum_tree(acc[ee]);
+            if (lane == 0 && e < P.E) P.logits[(size_t) (t0 + t) * P.E + e] = sum;
         }
     }
 }
@@ -126,7 +190,7 @@ __device__ void route_tile(const PrologueParams &P, int b, float *xs, int tt) {
 // q = min(127, rne(iscale x)), d = 1/iscale; groups of 32 threads; bs = sums of 32-value groups.
 // Every thread runs the shuffles; threads past the end contribute zeros and write nothing.
 template <int QT>
-__device__ void quantize_row(const float *__restrict__ x, int n, int8_t *qs, float *d, int32_t *bs) {
+__device__ __forceinline__ void quantize_row(const float *__restrict__ x, int n, int8_t *qs, float *d, int32_t *bs) {
     for (int base = 0; base < n; base += blockDim.x * 8) {
         const int i0 = base + threadIdx.x * 8;
         const bool on = i0 < n;
@@ -146,13 +210,14 @@ __device__ void quantize_row(const float *__restrict__ x, int n, int8_t *qs, flo
             float amax = 0.0f;
 #pragma unroll
             for (int j = 0; j < 8; j++) amax = fmaxf(amax, fabsf(v[j]));
-            amax = fmaxf(amax, __shfl_xor(amax, 1));
-            amax = fmaxf(amax, __shfl_xor(amax, 2));
+            amax = fmaxf(amax, dpp_f<0xB1>(amax)); // the 4 threads of a 32-value block
+            amax = fmaxf(amax, dpp_f<0x4E>(amax));
             dd = round_f16(__fdiv_rn(amax, 127.0f));
             const float id = amax != 0.0f ? __fdiv_rn(127.0f, amax) : 0.0f;
 #pragma unroll
             for (int j = 0; j < 8; j++) q[j] = (int) rintf(v[j] * id);
         } else {
+            // (|x|, x, index) of the first largest |x|: 32 threads per 256-value block
             float amax = 0.0f, mx = 0.0f;
             int idx = INT_MAX;
 #pragma unroll
@@ -164,17 +229,28 @@ __device__ void quantize_row(const float *__restrict__ x, int n, int8_t *qs, flo
                     idx = i0 + j;
                 }
             }
-#pragma unroll
-            for (int s = 16; s >= 1; s >>= 1) {
-                const float oa = __shfl_xor(amax, s);
-                const float om = __shfl_xor(mx, s);
-                const int oi = __shfl_xor(idx, s);
+            auto take = [&](float oa, float om, int oi) {
                 if (oa > amax || (oa == amax && oi < idx)) {
                     amax = oa;
                     mx = om;
                     idx = oi;
                 }
-            }
+            };
+            take(dpp_f<0xB1>(amax), dpp_f<0xB1>(mx), __builtin_amdgcn_update_dpp(0, idx, 0xB1, 0xF, 0xF, false));
+            take(dpp_f<0x4E>(amax), dpp_f<0x4E>(mx), __builtin_amdgcn_update_dpp(0, idx, 0x4E, 0xF, 0xF, false));
+            take(dpp_f<0x141>(amax), dpp_f<0x141>(mx), __builtin_amdgcn_update_dpp(0, idx, 0x141, 0xF, 0xF, false));
+            take(dpp_f<0x140>(amax), dpp_f<0x140>(mx), __builtin_amdgcn_update_dpp(0, idx, 0x140, 0xF, 0xF, false));
+            // rows 0+1 form the block of lanes 0-31, rows 2+3 the block of lanes 32-63
+            const int lane = threadIdx.x % kWave;
+            const int r0 = lane < 32 ? 0 : 32;
+            const float a0 = readlane_f(amax, 0), a1 = readlane_f(amax, 16), a2 = readlane_f(amax, 32), a3 = readlane_f(amax, 48);
+            const float m0 = readlane_f(mx, 0), m1 = readlane_f(mx, 16), m2 = readlane_f(mx, 32), m3 = readlane_f(mx, 48);
+            const int x0 = __builtin_amdgcn_readlane(idx, 0), x1 = __builtin_amdgcn_readlane(idx, 16);
+            const int x2 = __builtin_amdgcn_readlane(idx, 32), x3 = __builtin_amdgcn_readlane(idx, 48);
+            amax = r0 ? a2 : a0;
+            mx = r0 ? m2 : m0;
+            idx = r0 ? x2 : x0;
+            take(r0 ? a3 : a1, r0 ? m3 : m1, r0 ? x3 : x1);
             if (amax == 0.0f) {
                 dd = 0.0f;
 #pragma unroll
@@ -189,8 +265,8 @@ __device__ void quantize_row(const float *__restrict__ x, int n, int8_t *qs, flo
         int s = 0;
 #pragma unroll
         for (int j = 0; j < 8; j++) s += q[j];
-        s += __shfl_xor(s, 1);
-        s += __shfl_xor(s, 2);
+        s += __builtin_amdgcn_update_dpp(0, s, 0xB1, 0xF, 0xF, false);
+        s += __builtin_amdgcn_update_dpp(0, s, 0x4E, 0xF, 0xF, false);
         if (on) {
             uint2 packed;
             packed.x = (unsigned) (q[0] & 0xff) | ((unsigned) (q[1] & 0xff) << 8) | ((unsigned) (q[2] & 0xff) << 16) |
@@ -210,216 +286,343 @@ __device__ void quantize_row(const float *__restrict__ x, int n, int8_t *qs, flo
 // softmax / top-k / renormalisation (router(), src/qwen3.cpp:179-189)
 // ------------------------------------------------------------------------------------------------
 
-// One wavefront per token. Selection is made on the logits (softmax is monotone), largest first,
-// ties to the lower expert id; p = expf(l - max) * (float)(1 / sum) with the sum in double; the k
-// selected p are summed in selection order in double, clamped to >= 2^-14 and divided out.
-__device__ void route_finalize(const PrologueParams &P) {
-    const int lane = threadIdx.x % kWave, wave = threadIdx.x / kWave, nw = blockDim.x / kWave;
-    const int E = P.E, k = P.k;
-    for (int t = wave; t < P.T; t += nw) {
-        float l[kMaxEPL], p[kMaxEPL];
-        bool taken[kMaxEPL];
-        float m = -INFINITY;
+// Barrier among the wavefronts cooperating on one token: the whole block, or one wavefront (whose
+// lanes already run in lock step; only its LDS traffic has to land).
+__device__ __forceinline__ void group_barrier(int nsplit) {
+    if (nsplit > 1) __syncthreads();
+    else asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+}
+
+// Order key of a logit: monotone in the value (-0 and +0 equal), ties broken towards the lower
+// expert id, unique per expert.
+__device__ __forceinline__ unsigned long long order_key(float v, int e) {
+    unsigned u = __float_as_uint(v);
+    if (v == 0.0f) u = 0u;
+    u = (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+    return ((unsigned long long) u << 8) | (unsigned) (255 - e);
+}
+
+// One token's softmax / top-k / renormalisation, everything in parallel. The rank of an expert is
+// the number of experts with a larger logit, or an equal logit and a lower id, so the selection is
+// largest first with ties to the lower expert id, as the oracle's sequential argmax. Ranks are
+// counted with f32 compares against the row broadcast from LDS, split over `nsplit` wavefronts
+// (partial counts summed in LDS); exact ties are rare and take a second, 64-bit-key pass.
+// p = expf(l - max) * (float)(1 / sum) with the sum in double; the k selected p are summed in rank
+// order in double, clamped to >= 2^-14 and divided out. The expert of rank j is written to ids[j],
+// its weight to weights[j].
+// Called by the `nsplit` wavefronts [w0, w0 + nsplit) of the block with part = wave - w0.
+// s_l: >= E floats, s_rank: >= nsplit * 64 * EPL ints, s_p: >= k floats, all LDS shared by the group.
+template <int EPL>
+__device__ __forceinline__ void topk_token(const float *__restrict__ l_row, int E, int k, int part, int nsplit, float *s_l,
+                           int *s_rank, float *s_p, int16_t *ids16, int32_t *ids32, float *weights, int32_t *ids32_b,
+                           float *weights_b) {
+    const int lane = threadIdx.x % kWave;
+    float l[EPL];
+    bool valid[EPL];
 #pragma unroll
-        for (int i = 0; i < kMaxEPL; i++) {
-            const int e = lane + kWave * i;
-            l[i] = e < E ? P.logits[(size_t) t * E + e] : -INFINITY;
-            m = fmaxf(m, l[i]);
-            taken[i] = false;
+    for (int i = 0; i < EPL; i++) {
+        const int e = lane + kWave * i;
+        valid[i] = e < E;
+        l[i] = l_row[min(e, E - 1)]; // unconditional: all loads in flight together
+    }
+#pragma unroll
+    for (int i = 0; i < EPL; i++)
+        if (!valid[i]) l[i] = -INFINITY;
+    if (part == 0) {
+        // the row, padded with -inf to 4 * 64 entries so the rank loop needs no remainder
+#pragma unroll
+        for (int i = 0; i < kMaxEPL; i++) s_l[lane + kWave * i] = i < EPL ? l[i] : -INFINITY;
+    }
+    group_barrier(nsplit);
+    // partial ranks over this wavefront's share of the row, 32 values per batch of LDS reads
+    const int per = (((E + nsplit - 1) / nsplit) + 31) & ~31;
+    const int a0 = part * per, a1 = min(((E + 31) & ~31), a0 + per);
+    int r[EPL];
+#pragma unroll
+    for (int i = 0; i < EPL; i++) r[i] = 0;
+    for (int e2 = a0; e2 < a1; e2 += 32) {
+        float4 v[8];
+#pragma unroll
+        for (int u = 0; u < 8; u++) v[u] = *reinterpret_cast<const float4 *>(s_l + e2 + 4 * u);
+#pragma unroll
+        for (int u = 0; u < 8; u++) {
+#pragma unroll
+            for (int i = 0; i < EPL; i++)
+                r[i] += (v[u].x > l[i]) + (v[u].y > l[i]) + (v[u].z > l[i]) + (v[u].w > l[i]);
         }
+    }
 #pragma unroll
-        for (int s = 32; s >= 1; s >>= 1) m = fmaxf(m, __shfl_xor(m, s));
-        double sum = 0.0;
+    for (int i = 0; i < EPL; i++) s_rank[(part * EPL + i) * kWave + lane] = r[i];
+    group_barrier(nsplit);
+    if (part != 0) return;
+    int rank[EPL];
 #pragma unroll
-        for (int i = 0; i < kMaxEPL; i++) {
-            const int e = lane + kWave * i;
-            p[i] = e < E ? expf(l[i] - m) : 0.0f;
-            sum += (double) p[i];
-        }
+    for (int i = 0; i < EPL; i++) {
+        rank[i] = 0;
+        for (int q = 0; q < nsplit; q++) rank[i] += s_rank[(q * EPL + i) * kWave + lane];
+    }
+    // exact ties: an expert with an equal logit and a lower id ranks first
+    bool tie = false;
 #pragma unroll
-        for (int s = 32; s >= 1; s >>= 1) sum += __shfl_xor(sum, s);
-        const float inv = (float) (1.0 / sum);
+    for (int i = 0; i < EPL; i++) tie |= valid[i] && rank[i] < k;
+    {
+        unsigned long long seen = 0ull; // bit r set once some selected expert has rank r
+        // ranks are distinct exactly when there is no tie among the experts that reach rank < k
+        unsigned long long mine = 0ull;
 #pragma unroll
-        for (int i = 0; i < kMaxEPL; i++) p[i] = p[i] * inv;
-        int my_id = 0;
-        for (int j = 0; j < k; j++) {
-            float bv = -INFINITY;
-            int bi = INT_MAX;
+        for (int i = 0; i < EPL; i++)
+            if (valid[i] && rank[i] < k) mine |= 1ull << rank[i];
+        int cnt = 0;
 #pragma unroll
-            for (int i = 0; i < kMaxEPL; i++) {
-                const int e = lane + kWave * i;
-                if (e < E && !taken[i] && (bi == INT_MAX || l[i] > bv)) {
-                    bv = l[i];
-                    bi = e;
+        for (int i = 0; i < EPL; i++) cnt += __popcll(__ballot(valid[i] && rank[i] < k));
+        // OR of every lane's bits via DPP and readlane
+        unsigned lo = (unsigned) mine, hi = (unsigned) (mine >> 32);
+        lo |= __builtin_amdgcn_update_dpp(0, (int) lo, 0xB1, 0xF, 0xF, false);
+        hi |= __builtin_amdgcn_update_dpp(0, (int) hi, 0xB1, 0xF, 0xF, false);
+        lo |= __builtin_amdgcn_update_dpp(0, (int) lo, 0x4E, 0xF, 0xF, false);
+        hi |= __builtin_amdgcn_update_dpp(0, (int) hi, 0x4E, 0xF, 0xF, false);
+        lo |= __builtin_amdgcn_update_dpp(0, (int) lo, 0x141, 0xF, 0xF, false);
+        hi |= __builtin_amdgcn_update_dpp(0, (int) hi, 0x141, 0xF, 0xF, false);
+        lo |= __builtin_amdgcn_update_dpp(0, (int) lo, 0x140, 0xF, 0xF, false);
+        hi |= __builtin_amdgcn_update_dpp(0, (int) hi, 0x140, 0xF, 0xF, false);
+        lo = (unsigned) __builtin_amdgcn_readlane((int) lo, 0) | (unsigned) __builtin_amdgcn_readlane((int) lo, 16) |
+             (unsigned) __builtin_amdgcn_readlane((int) lo, 32) | (unsigned) __builtin_amdgcn_readlane((int) lo, 48);
+        hi = (unsigned) __builtin_amdgcn_readlane((int) hi, 0) | (unsigned) __builtin_amdgcn_readlane((int) hi, 16) |
+             (unsigned) __builtin_amdgcn_readlane((int) hi, 32) | (unsigned) __builtin_amdgcn_readlane((int) hi, 48);
+        seen = ((unsigned long long) hi << 32) | lo;
+        const unsigned long long want = k >= 64 ? ~0ull : ((1ull << k) - 1ull);
+        tie = !(cnt == k && seen == want);
+    }
+    if (tie) {
+        // rare: recount with the id tie-break over the whole row
+#pragma unroll
+        for (int i = 0; i < EPL; i++) rank[i] = 0;
+        for (int e2 = 0; e2 < E; e2 += 4) {
+            const float4 v = *reinterpret_cast<const float4 *>(s_l + e2);
+            const float vv[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+            for (int u = 0; u < 4; u++) {
+#pragma unroll
+                for (int i = 0; i < EPL; i++) {
+                    const int e = lane + kWave * i;
+                    rank[i] += (vv[u] > l[i]) || (vv[u] == l[i] && e2 + u < e);
                 }
             }
-#pragma unroll
-            for (int s = 32; s >= 1; s >>= 1) {
-                const float ov = __shfl_xor(bv, s);
-                const int oi = __shfl_xor(bi, s);
-                if (oi != INT_MAX && (bi == INT_MAX || ov > bv || (ov == bv && oi < bi))) {
-                    bv = ov;
-                    bi = oi;
-                }
-            }
-            if ((bi & (kWave - 1)) == lane) {
-#pragma unroll
-                for (int i = 0; i < kMaxEPL; i++)
-                    if ((bi >> 6) == i) taken[i] = true;
-            }
-            if (lane == j) my_id = bi;
         }
-        float my_p = 0.0f;
+    }
+    // softmax over the row
+    float m = -INFINITY;
 #pragma unroll
-        for (int i = 0; i < kMaxEPL; i++) {
-            const float v = __shfl(p[i], my_id & (kWave - 1));
-            if ((my_id >> 6) == i) my_p = v;
-        }
-        double ss = 0.0;
-        for (int j = 0; j < k; j++) ss += (double) __shfl(my_p, j);
-        const float sf = fmaxf((float) ss, 6.103515625e-5f);
-        if (lane < k) {
-            P.ids[(size_t) t * k + lane] = my_id;
-            P.weights[(size_t) t * k + lane] = __fdiv_rn(my_p, sf);
+    for (int i = 0; i < EPL; i++) m = fmaxf(m, l[i]);
+    m = wave_max(m);
+    float p[EPL];
+    double s = 0.0;
+#pragma unroll
+    for (int i = 0; i < EPL; i++) {
+        p[i] = valid[i] ? expf(l[i] - m) : 0.0f;
+        s += (double) p[i];
+    }
+    const float inv = (float) (1.0 / wave_sum_d(s));
+#pragma unroll
+    for (int i = 0; i < EPL; i++) {
+        p[i] = p[i] * inv;
+        if (valid[i] && rank[i] < k) s_p[rank[i]] = p[i];
+    }
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    double ss = 0.0;
+    for (int j = 0; j < k; j++) ss += (double) s_p[j];
+    const float sf = fmaxf((float) ss, 6.103515625e-5f);
+#pragma unroll
+    for (int i = 0; i < EPL; i++) {
+        if (valid[i] && rank[i] < k) {
+            const int e = lane + kWave * i;
+            const float w = __fdiv_rn(p[i], sf);
+            if (ids16) ids16[rank[i]] = (int16_t) e;
+            if (ids32) ids32[rank[i]] = e;
+            if (weights) weights[rank[i]] = w;
+            if (ids32_b) ids32_b[rank[i]] = e;
+            if (weights_b) weights_b[rank[i]] = w;
         }
     }
 }
 
-// ------------------------------------------------------------------------------------------------
-// permutation
-// ------------------------------------------------------------------------------------------------
-
-__device__ int block_exclusive_scan(int v, int *tmp, int *total) {
-    const int lane = threadIdx.x & (kWave - 1), wave = threadIdx.x / kWave, nw = blockDim.x / kWave;
-    int x = v;
-#pragma unroll
-    for (int s = 1; s < kWave; s <<= 1) {
-        const int y = __shfl_up(x, s);
-        if (lane >= s) x += y;
-    }
-    if (lane == kWave - 1) tmp[wave] = x;
-    __syncthreads();
-    int wbase = 0, tot = 0;
-    for (int w = 0; w < nw; w++) {
-        const int tw = tmp[w];
-        if (w < wave) wbase += tw;
-        tot += tw;
-    }
-    __syncthreads();
-    *total = tot;
-    return wbase + x - v;
-}
-
-// Stable counting sort of the T*k (t, j) pairs by bin: histogram and scan in LDS, then 32 tokens
-// at a time, each pair's rank among the chunk's earlier tokens is a popcount of a per-bin bitmask.
-// Ids out of range are clamped and flagged in *err (bit 0); a bin repeated within one token is
-// flagged (bit 1). perm is cleared first so every position read later names a valid pair.
-__device__ void permute(const PrologueParams &P, int *lds) {
-    const int nb = P.n_bins, k = P.k, np = P.T * k;
-    const int tid = threadIdx.x, bd = blockDim.x;
-    int *cnt = lds;
-    int *cur = lds + nb;
-    unsigned *bm = reinterpret_cast<unsigned *>(lds + 2 * nb);
-    int *tmp = lds + 3 * nb;
-    for (int b = tid; b < nb; b += bd) cnt[b] = 0;
-    for (int p = tid; p < np; p += bd) P.pb.perm[p] = 0;
-    __syncthreads();
-    for (int p = tid; p < np; p += bd) {
-        int b = P.bins[p];
-        if (b < 0 || b >= nb) {
-            atomicOr(P.err, 1);
-            b = min(max(b, 0), nb - 1);
+// Top-k of T tokens by the block's wavefronts: one wavefront per token, or all wavefronts on one
+// token when there are fewer tokens than wavefronts. The block must call this uniformly.
+__device__ __forceinline__ void topk_block(const float *__restrict__ logits, int T, int E, int k, unsigned char *lds, int16_t *ids16,
+                           int32_t *ids32, float *weights, int32_t *ids32_b, float *weights_b) {
+    const int wave = threadIdx.x / kWave, nw = blockDim.x / kWave;
+    const int nsplit = T < nw ? nw : 1;
+    const int epl = (E + kWave - 1) / kWave;
+    // one row per wavefront (or one shared row when they split a token); the rank partials of all
+    // wavefronts: nw * kMaxEPL * 64 ints in either mode
+    float *s_l = reinterpret_cast<float *>(lds);                             // [nw][256]
+    int *s_rank = reinterpret_cast<int *>(lds + (size_t) nw * 256 * 4);       // [nw * kMaxEPL * 64]
+    float *s_p = reinterpret_cast<float *>(s_rank + (size_t) nw * kMaxEPL * kWave); // [nw][kMaxK]
+    for (int t0 = 0; t0 < T; t0 += (nsplit > 1 ? 1 : nw)) {
+        const int t = nsplit > 1 ? t0 : t0 + wave;
+        const int part = nsplit > 1 ? wave : 0;
+        const int slot = nsplit > 1 ? 0 : wave; // LDS set of this token's group
+        if (t < T) {
+            const size_t o = (size_t) t * k;
+            float *sl = s_l + slot * 256;
+            int *sr = s_rank + (size_t) slot * kMaxEPL * kWave;
+            float *sp = s_p + slot * kMaxK;
+            const float *lr = logits + (size_t) t * E;
+            int16_t *a = ids16 ? ids16 + o : nullptr;
+            int32_t *b = ids32 ? ids32 + o : nullptr;
+            float *c = weights ? weights + o : nullptr;
+            int32_t *d = ids32_b ? ids32_b + o : nullptr;
+            float *f = weights_b ? weights_b + o : nullptr;
+            if (epl == 1) topk_token<1>(lr, E, k, part, nsplit, sl, sr, sp, a, b, c, d, f);
+            else if (epl == 2) topk_token<2>(lr, E, k, part, nsplit, sl, sr, sp, a, b, c, d, f);
+            else topk_token<4>(lr, E, k, part, nsplit, sl, sr, sp, a, b, c, d, f);
         }
-        atomicAdd(&cnt[b], 1);
-    }
-    __syncthreads();
-    const int per = (nb + bd - 1) / bd;
-    const int b0 = min(nb, tid * per), b1 = min(nb, b0 + per);
-    int s = 0, a = 0;
-    for (int b = b0; b < b1; b++) {
-        s += cnt[b];
-        a += cnt[b] > 0;
-    }
-    int tot, tota;
-    int so = block_exclusive_scan(s, tmp, &tot);
-    int ao = block_exclusive_scan(a, tmp, &tota);
-    for (int b = b0; b < b1; b++) {
-        P.pb.counts[b] = cnt[b];
-        P.pb.offsets[b] = so;
-        cur[b] = so;
-        so += cnt[b];
-        if (cnt[b] > 0) P.pb.active[ao++] = b;
-    }
-    if (tid == 0) {
-        P.pb.offsets[nb] = tot;
-        *P.pb.n_active = tota;
-    }
-    __syncthreads();
-    constexpr int kPairsPerThread = 32 * kMaxK / kBlock;
-    for (int t0 = 0; t0 < P.T; t0 += 32) {
-        const int npc = min(32, P.T - t0) * k;
-        for (int b = tid; b < nb; b += bd) bm[b] = 0u;
-        __syncthreads();
-        int myb[kPairsPerThread];
-#pragma unroll
-        for (int q = 0; q < kPairsPerThread; q++) {
-            const int pc = tid + q * bd;
-            myb[q] = 0;
-            if (pc < npc) {
-                int b = P.bins[t0 * k + pc];
-                b = min(max(b, 0), nb - 1);
-                myb[q] = b;
-                const unsigned bit = 1u << (pc / k);
-                if (atomicOr(&bm[b], bit) & bit) atomicOr(P.err, 2);
-            }
-        }
-        __syncthreads();
-#pragma unroll
-        for (int q = 0; q < kPairsPerThread; q++) {
-            const int pc = tid + q * bd;
-            if (pc < npc) {
-                const int b = myb[q];
-                const int pos = cur[b] + __popc(bm[b] & ((1u << (pc / k)) - 1u));
-                P.pb.perm[pos] = t0 * k + pc;
-            }
-        }
-        __syncthreads();
-        for (int b = tid; b < nb; b += bd) cur[b] += __popc(bm[b]);
-        __syncthreads();
+        if (nsplit > 1) __syncthreads();
     }
 }
 
-// ------------------------------------------------------------------------------------------------
-// prologue kernel
-// ------------------------------------------------------------------------------------------------
+__device__ __host__ inline size_t topk_lds_bytes(int nw) {
+    return (size_t) nw * 256 * 4 + (size_t) nw * kMaxEPL * kWave * 4 + (size_t) nw * kMaxK * 4;
+}
 
-template <int GT, int QT>
-__global__ __launch_bounds__(kBlock) void prologue_kernel(PrologueParams P, int n_route_wg, int n_quant_wg, int route_tt) {
+template <int GT, int NG>
+__global__ __launch_bounds__(kBlock) void route_kernel(RouteParams P, int n_route_wg, int n_quant_wg, int route_tt) {
     extern __shared__ __align__(16) float lds[];
-    __shared__ int is_last;
     const int b = blockIdx.x;
     if (b < n_route_wg) {
-        route_tile<GT>(P, b, lds, route_tt);
-    } else if (QT != 0) {
+        route_tile<GT, NG>(P, b, lds, route_tt);
+    } else if (P.qtype != 0) {
         const int h = P.h;
-        for (int t = b - n_route_wg; t < P.T; t += n_quant_wg)
-            quantize_row<QT>(P.hnorm + (size_t) t * h, h, P.xq.qs + (size_t) t * h, P.xq.d + (size_t) t * (h / 32),
-                             P.xq.bs + (size_t) t * (h / 32));
+        for (int t = b - n_route_wg; t < P.T; t += n_quant_wg) {
+            if (P.qtype == kTypeQ8_0)
+                quantize_row<kTypeQ8_0>(P.hnorm + (size_t) t * h, h, P.xq.qs + (size_t) t * h, P.xq.d + (size_t) t * (h / 32),
+                                        P.xq.bs + (size_t) t * (h / 32));
+            else
+                quantize_row<kTypeQ4_K>(P.hnorm + (size_t) t * h, h, P.xq.qs + (size_t) t * h, P.xq.d + (size_t) t * (h / 32),
+                                        P.xq.bs + (size_t) t * (h / 32));
+        }
     }
-    // arrival: the last work-group to get here sees every other work-group's writes
-    __threadfence();
-    __syncthreads();
-    if (threadIdx.x == 0) is_last = atomicAdd(P.counter, 1u) == gridDim.x - 1;
-    __syncthreads();
-    if (!is_last) return;
-    __threadfence();
-    if (P.do_route) route_finalize(P);
-    if (P.do_perm) {
-        __threadfence();
-        __syncthreads();
-        permute(P, reinterpret_cast<int *>(lds));
+}
+
+__global__ __launch_bounds__(kBlock) void topk_kernel(TopkParams P) {
+    __shared__ __align__(16) unsigned char lds[(kBlock / kWave) * 256 * 4 + (kBlock / kWave) * kMaxEPL * kWave * 4 +
+                                               (kBlock / kWave) * kMaxK * 4];
+    const int t0 = blockIdx.x * (kBlock / kWave);
+    const int nt = min(kBlock / kWave, P.T - t0);
+    topk_block(P.logits + (size_t) t0 * P.E, nt, P.E, P.k, lds, nullptr, P.ids + (size_t) t0 * P.k,
+               P.weights + (size_t) t0 * P.k, nullptr, nullptr);
+}
+
+// ------------------------------------------------------------------------------------------------
+// per-work-group grouping: which expert, which pairs
+// ------------------------------------------------------------------------------------------------
+
+// LDS layout of the grouping step, in front of each expert kernel's own LDS.
+struct GroupLds {
+    unsigned char *scratch; // top-k scratch (route mode), topk_lds_bytes(4)
+    int16_t *ids;   // [T*k] bins
+    float *w;       // [T*k] router weights (route mode only)
+    unsigned *bm;   // [n_bins / 32] bins in use
+    int *list;      // [T] this work-group's pairs, ascending
+    int *misc;      // [0] = expert or -1, [1] = number of pairs
+};
+
+constexpr size_t kTopkLds = (size_t) (kBlock / kWave) * 256 * 4 + (size_t) (kBlock / kWave) * kMaxEPL * kWave * 4 +
+                            (size_t) (kBlock / kWave) * kMaxK * 4;
+
+// The top-k scratch and the weights exist only when the work-group routes (route = 1).
+__device__ __host__ inline size_t group_lds_bytes(int T, int k, int n_bins, int route) {
+    const size_t np = (size_t) T * k;
+    return (route ? kTopkLds + np * 4 : 0) + ((np * 2 + 15) / 16) * 16 + ((size_t) (n_bins + 31) / 32) * 4 +
+           (size_t) T * 4 + 64;
+}
+
+__device__ __forceinline__ GroupLds group_lds(unsigned char *base, int T, int k, int n_bins, int route) {
+    const size_t np = (size_t) T * k;
+    GroupLds g{};
+    if (route) {
+        g.scratch = base;
+        base += kTopkLds;
+        g.w = reinterpret_cast<float *>(base);
+        base += np * 4;
     }
-    if (threadIdx.x == 0) atomicExch(P.counter, 0u);
+    g.ids = reinterpret_cast<int16_t *>(base);
+    base += ((np * 2 + 15) / 16) * 16;
+    g.bm = reinterpret_cast<unsigned *>(base);
+    base += ((size_t) (n_bins + 31) / 32) * 4;
+    g.list = reinterpret_cast<int *>(base);
+    base += (size_t) T * 4;
+    g.misc = reinterpret_cast<int *>(base);
+    return g;
+}
+
+// Every work-group derives the same grouping from the same routing: the active bins in ascending
+// order (the order ggml's CPU mul_mat_id walks experts), work-group y takes the y-th active bin, and
+// its pairs (t, j) in token-major order. Bins out of range are clamped and flagged in *err.
+// Returns false when this work-group has no bin (y >= number of active bins).
+template <bool ROUTE>
+__device__ __forceinline__ bool group_pairs(const GroupParams &P, GroupLds g) {
+    const int tid = threadIdx.x, bd = blockDim.x;
+    const int lane = tid % kWave, wave = tid / kWave;
+    const int k = P.k, np = P.T * k, nb = P.n_bins, nwords = (nb + 31) / 32;
+    if (ROUTE) {
+        const bool first = blockIdx.x == 0 && blockIdx.y == 0;
+        topk_block(P.logits, P.T, P.E, k, g.scratch, g.ids, nullptr, g.w, first ? P.ids_out : nullptr,
+                   first ? P.weights_out : nullptr);
+    } else {
+        for (int p = tid; p < np; p += bd) {
+            int b = P.ids[p];
+            if (b < 0 || b >= nb) {
+                if (blockIdx.x == 0 && blockIdx.y == 0) atomicOr(P.err, 1);
+                b = min(max(b, 0), nb - 1);
+            }
+            g.ids[p] = (int16_t) b;
+        }
+    }
+    for (int w = tid; w < nwords; w += bd) g.bm[w] = 0u;
+    __syncthreads();
+    for (int p = tid; p < np; p += bd) {
+        const int b = g.ids[p];
+        atomicOr(&g.bm[b >> 5], 1u << (b & 31));
+    }
+    __syncthreads();
+    if (wave == 0) {
+        // the y-th bin in use, 64 bins per ballot
+        const int y = blockIdx.y;
+        int e = -1, cum = 0;
+        for (int base = 0; base < nb && e < 0; base += kWave) {
+            const int b = base + lane;
+            const bool used = b < nb && ((g.bm[b >> 5] >> (b & 31)) & 1u);
+            unsigned long long mk = __ballot(used);
+            const int c = __popcll(mk);
+            if (y < cum + c) {
+                for (int r = y - cum; r > 0; r--) mk &= mk - 1ull;
+                e = base + __ffsll((long long) mk) - 1;
+            }
+            cum += c;
+        }
+        int n = 0;
+        if (e >= 0) {
+            for (int base = 0; base < np; base += kWave) {
+                const int p = base + lane;
+                const bool hit = p < np && g.ids[p] == e;
+                const unsigned long long mk = __ballot(hit);
+                const int rank = __popcll(mk & ((1ull << lane) - 1ull));
+                if (hit && n + rank < P.T) g.list[n + rank] = p;
+                n += __popcll(mk);
+            }
+            if (n > P.T) {
+                if (lane == 0) atomicOr(P.err, 2);
+                n = P.T;
+            }
+        }
+        if (lane == 0) {
+            g.misc[0] = e;
+            g.misc[1] = n;
+        }
+    }
+    __syncthreads();
+    return g.misc[0] >= 0;
 }
 
 // ------------------------------------------------------------------------------------------------
@@ -537,23 +740,25 @@ __device__ __forceinline__ float dot_sb(const uint4 (&w)[chunks_of(WT)], const i
 // gate + up + SwiGLU
 // ------------------------------------------------------------------------------------------------
 
-// Work-group (row block, active expert): thread (g, m, r) holds super-blocks g, g + G, ... of row r
-// of gate (m = 0) or up (m = 1) in registers, loaded before anything else. Tokens of the expert are
-// staged 8 at a time in LDS; partial dots are reduced over g in ascending order, then
-// act = silu(gate) * up is written to the token's row in permuted order.
-template <int WT, int S>
+// Work-group (row block, y): rows = 128 / G per matrix, thread (g, m, r) holds super-blocks
+// g, g + G, ... of row r of gate (m = 0) or up (m = 1) in registers, loaded before anything else.
+// The y-th active expert's tokens are staged 8 at a time in LDS; partial dots are reduced over g in
+// ascending order, then act[pair] = silu(gate) * up.
+template <int WT, int S, bool ROUTE>
 __global__ __launch_bounds__(kBlock) void gate_up_kernel(GateUpParams P) {
     constexpr int C = chunks_of(WT);
     extern __shared__ __align__(16) unsigned char smem[];
-    const int n_active = *P.pb.n_active;
-    const int ai = blockIdx.y;
-    if (ai >= n_active) return;
-    const int e = P.pb.active[ai];
-    const int G = blockDim.x / (2 * kGuRows);
+    const int G = P.h / 256 / S;
+    const int RW = 128 / G;
     const int tid = threadIdx.x;
-    const int r = tid % kGuRows, m = (tid / kGuRows) & 1, g = tid / (2 * kGuRows);
-    const int f = P.f, h = P.h, k = P.k;
-    const int row = blockIdx.x * kGuRows + r;
+    const int r = tid % RW, m = (tid / RW) & 1, g = tid / (2 * RW);
+    const int f = P.f, h = P.h, k = P.gp.k;
+    const int row = blockIdx.x * RW + r;
+    GroupLds gl = group_lds(smem, P.gp.T, k, P.gp.n_bins, ROUTE);
+    unsigned char *work = smem + group_lds_bytes(P.gp.T, k, P.gp.n_bins, ROUTE);
+    work = reinterpret_cast<unsigned char *>((reinterpret_cast<uintptr_t>(work) + 15) & ~uintptr_t(15));
+    if (!group_pairs<ROUTE>(P.gp, gl)) return;
+    const int e = gl.misc[0], cnt = gl.misc[1];
     const uint8_t *base = m ? P.w_up + (size_t) e * P.stride_up : P.w_gate + (size_t) e * P.stride_gate;
     uint4 w[S][C];
 #pragma unroll
@@ -563,15 +768,14 @@ __global__ __launch_bounds__(kBlock) void gate_up_kernel(GateUpParams P) {
         for (int c = 0; c < C; c++) w[s][c] = *reinterpret_cast<const uint4 *>(base + chunk_offset(C, f, sb, c, row));
     }
     const int h32 = h / 32;
-    int8_t *xs = reinterpret_cast<int8_t *>(smem);
-    float *xd = reinterpret_cast<float *>(smem + (size_t) kTC * h);
+    int8_t *xs = reinterpret_cast<int8_t *>(work);
+    float *xd = reinterpret_cast<float *>(work + (size_t) kTC * h);
     int *xb = reinterpret_cast<int *>(xd + kTC * h32);
     float *red = reinterpret_cast<float *>(xb + kTC * h32);
-    const int cnt = P.pb.counts[e], off = P.pb.offsets[e];
     for (int c0 = 0; c0 < cnt; c0 += kTC) {
         const int nt = min(kTC, cnt - c0);
         for (int tc = 0; tc < nt; tc++) {
-            const int t = P.pb.perm[off + c0 + tc] / k;
+            const int t = gl.list[c0 + tc] / k;
             const int4 *src = reinterpret_cast<const int4 *>(P.xq.qs + (size_t) t * h);
             int4 *dst = reinterpret_cast<int4 *>(xs + (size_t) tc * h);
             for (int i = tid; i < h / 16; i += blockDim.x) dst[i] = src[i];
@@ -588,26 +792,34 @@ __global__ __launch_bounds__(kBlock) void gate_up_kernel(GateUpParams P) {
                 const int sb = g + s * G;
                 acc = dot_sb<WT>(w[s], xs + (size_t) tc * h + sb * 256, xd + tc * h32 + sb * 8, xb + tc * h32 + sb * 8, acc);
             }
-            red[((tc * G + g) * 2 + m) * kGuRows + r] = acc;
+            red[((tc * G + g) * 2 + m) * RW + r] = acc;
         }
         __syncthreads();
-        for (int idx = tid; idx < nt * kGuRows; idx += blockDim.x) {
-            const int tc = idx / kGuRows, rr = idx % kGuRows;
-            float gs = red[((tc * G) * 2 + 0) * kGuRows + rr];
-            float us = red[((tc * G) * 2 + 1) * kGuRows + rr];
-            for (int gg = 1; gg < G; gg++) {
-                gs += red[((tc * G + gg) * 2 + 0) * kGuRows + rr];
-                us += red[((tc * G + gg) * 2 + 1) * kGuRows + rr];
+        for (int idx = tid; idx < nt * RW; idx += blockDim.x) {
+            const int tc = idx / RW, rr = idx % RW;
+            float gv[kMaxG], uv[kMaxG];
+#pragma unroll
+            for (int gg = 0; gg < kMaxG; gg++) {
+                gv[gg] = gg < G ? red[((tc * G + gg) * 2 + 0) * RW + rr] : 0.0f;
+                uv[gg] = gg < G ? red[((tc * G + gg) * 2 + 1) * RW + rr] : 0.0f;
+            }
+            float gs = gv[0], us = uv[0];
+#pragma unroll
+            for (int gg = 1; gg < kMaxG; gg++) {
+                if (gg < G) {
+                    gs += gv[gg];
+                    us += uv[gg];
+                }
             }
             const float a = (gs / (1.0f + expf(-gs))) * us;
-            P.act[(size_t) (off + c0 + tc) * f + blockIdx.x * kGuRows + rr] = a;
+            P.act[(size_t) gl.list[c0 + tc] * f + blockIdx.x * RW + rr] = a;
         }
         __syncthreads();
     }
 }
 
 // ------------------------------------------------------------------------------------------------
-// down + router weight + combine + residual
+// down + router weight
 // ------------------------------------------------------------------------------------------------
 
 template <int WT, int S>
@@ -615,15 +827,15 @@ __global__ __launch_bounds__(kDnRows * kMaxG) void down_kernel(DownParams P) {
     constexpr int C = chunks_of(WT);
     constexpr int QT = WT == kTypeQ4_K ? kTypeQ4_K : kTypeQ8_0;
     extern __shared__ __align__(16) unsigned char smem[];
-    __shared__ int is_last;
-    const int n_active = *P.pb.n_active;
-    const int ai = blockIdx.y, rb = blockIdx.x;
-    if (ai >= n_active) return;
-    const int e = P.pb.active[ai];
     const int G = blockDim.x / kDnRows;
     const int tid = threadIdx.x, r = tid % kDnRows, g = tid / kDnRows;
-    const int h = P.h, f = P.f, k = P.k;
-    const int row = rb * kDnRows + r;
+    const int h = P.h, f = P.f;
+    const int row = blockIdx.x * kDnRows + r;
+    GroupLds gl = group_lds(smem, P.gp.T, P.gp.k, P.gp.n_bins, 0);
+    unsigned char *work = smem + group_lds_bytes(P.gp.T, P.gp.k, P.gp.n_bins, 0);
+    work = reinterpret_cast<unsigned char *>((reinterpret_cast<uintptr_t>(work) + 15) & ~uintptr_t(15));
+    if (!group_pairs<false>(P.gp, gl)) return;
+    const int e = gl.misc[0], cnt = gl.misc[1];
     const uint8_t *base = P.w_down + (size_t) e * P.stride_down;
     uint4 w[S][C];
 #pragma unroll
@@ -633,15 +845,14 @@ __global__ __launch_bounds__(kDnRows * kMaxG) void down_kernel(DownParams P) {
         for (int c = 0; c < C; c++) w[s][c] = *reinterpret_cast<const uint4 *>(base + chunk_offset(C, h, sb, c, row));
     }
     const int f32 = f / 32;
-    int8_t *xs = reinterpret_cast<int8_t *>(smem);
-    float *xd = reinterpret_cast<float *>(smem + (size_t) kTC * f);
+    int8_t *xs = reinterpret_cast<int8_t *>(work);
+    float *xd = reinterpret_cast<float *>(work + (size_t) kTC * f);
     int *xb = reinterpret_cast<int *>(xd + kTC * f32);
     float *red = reinterpret_cast<float *>(xb + kTC * f32);
-    const int cnt = P.pb.counts[e], off = P.pb.offsets[e];
     for (int c0 = 0; c0 < cnt; c0 += kTC) {
         const int nt = min(kTC, cnt - c0);
         for (int tc = 0; tc < nt; tc++)
-            quantize_row<QT>(P.act + (size_t) (off + c0 + tc) * f, f, xs + (size_t) tc * f, xd + tc * f32, xb + tc * f32);
+            quantize_row<QT>(P.act + (size_t) gl.list[c0 + tc] * f, f, xs + (size_t) tc * f, xd + tc * f32, xb + tc * f32);
         __syncthreads();
         for (int tc = 0; tc < nt; tc++) {
             float acc = 0.0f;
@@ -655,35 +866,65 @@ __global__ __launch_bounds__(kDnRows * kMaxG) void down_kernel(DownParams P) {
         __syncthreads();
         for (int idx = tid; idx < nt * kDnRows; idx += blockDim.x) {
             const int tc = idx / kDnRows, rr = idx % kDnRows;
-            float ds = red[(tc * G) * kDnRows + rr];
-            for (int gg = 1; gg < G; gg++) ds += red[(tc * G + gg) * kDnRows + rr];
-            const int p = P.pb.perm[off + c0 + tc];
-            P.Y[(size_t) p * h + rb * kDnRows + rr] = ds * P.weights[p];
+            float dv[kMaxG];
+#pragma unroll
+            for (int gg = 0; gg < kMaxG; gg++) dv[gg] = gg < G ? red[(tc * G + gg) * kDnRows + rr] : 0.0f;
+            float ds = dv[0];
+#pragma unroll
+            for (int gg = 1; gg < kMaxG; gg++)
+                if (gg < G) ds += dv[gg];
+            const int p = gl.list[c0 + tc];
+            P.Y[(size_t) p * h + blockIdx.x * kDnRows + rr] = ds * P.weights[p];
         }
         __syncthreads();
     }
-    // arrival: the last active expert of this row block combines the k outputs of every token
-    __threadfence();
-    __syncthreads();
-    if (tid == 0) is_last = atomicAdd(&P.counters[rb], 1u) == (unsigned) (n_active - 1);
-    __syncthreads();
-    if (!is_last) return;
-    __threadfence();
-    for (int idx = tid; idx < P.T * kDnRows; idx += blockDim.x) {
-        const int t = idx / kDnRows, rr = idx % kDnRows;
-        const int rw = rb * kDnRows + rr;
-        const float *y = P.Y + (size_t) t * k * h + rw;
-        float acc = y[0];
-        for (int j = 1; j < k; j++) acc = acc + y[(size_t) j * h];
-        P.out[(size_t) t * h + rw] = acc + P.resid[(size_t) t * h + rw];
-    }
-    if (tid == 0) atomicExch(&P.counters[rb], 0u);
     (void) row;
+}
+
+// ------------------------------------------------------------------------------------------------
+// combine + residual
+// ------------------------------------------------------------------------------------------------
+
+__global__ __launch_bounds__(kBlock) void combine_kernel(CombineParams P) {
+    const int h4 = P.h / 4;
+    const int idx = blockIdx.x * kBlock + threadIdx.x;
+    if (idx >= P.T * h4) return;
+    const int t = idx / h4, c = idx - t * h4;
+    const float4 *y = reinterpret_cast<const float4 *>(P.Y) + (size_t) t * P.k * h4 + c;
+    const float4 rs = reinterpret_cast<const float4 *>(P.resid)[idx];
+    float4 acc = y[0];
+    // slots in batches of 8 loads issued together, summed left to right
+    for (int j0 = 1; j0 < P.k; j0 += 8) {
+        float4 v[8];
+#pragma unroll
+        for (int u = 0; u < 8; u++) v[u] = y[(size_t) min(j0 + u, P.k - 1) * h4];
+#pragma unroll
+        for (int u = 0; u < 8; u++) {
+            if (j0 + u < P.k) {
+                acc.x = acc.x + v[u].x;
+                acc.y = acc.y + v[u].y;
+                acc.z = acc.z + v[u].z;
+                acc.w = acc.w + v[u].w;
+            }
+        }
+    }
+    acc.x = acc.x + rs.x;
+    acc.y = acc.y + rs.y;
+    acc.z = acc.z + rs.z;
+    acc.w = acc.w + rs.w;
+    reinterpret_cast<float4 *>(P.out)[idx] = acc;
 }
 
 // ------------------------------------------------------------------------------------------------
 // host side
 // ------------------------------------------------------------------------------------------------
+
+template <typename K, typename... A>
+hipError_t launch(K kernel, dim3 grid, dim3 block, size_t lds, hipStream_t st, const LaunchTiming *tm, A... args) {
+    if (tm && tm->start) hipExtLaunchKernelGGL(kernel, grid, block, (uint32_t) lds, st, tm->start, tm->stop, 0, args...);
+    else hipLaunchKernelGGL(kernel, grid, block, lds, st, args...);
+    return hipGetLastError();
+}
 
 // Super-blocks per thread S and K-groups G for nsb super-blocks: the smallest S <= 2 dividing nsb
 // with nsb / S <= 8 (S = 3 would need more than 256 VGPRs and spill).
@@ -698,90 +939,124 @@ bool pick_split(int nsb, int *S, int *G) {
     return false;
 }
 
+// gate_up additionally needs 128 % G == 0 (rows per work-group = 128 / G).
+bool pick_split_gate_up(int nsb, int *S, int *G) { return pick_split(nsb, S, G) && 128 % *G == 0; }
+
 int route_tile_tokens(int h) { return std::max(1, std::min(8, 32768 / (h * 4))); }
 
-template <int GT, int QT>
-hipError_t launch_prologue_t(const PrologueParams &P, hipStream_t st) {
-    int n_route = 0, tt = 0;
+size_t align16(size_t x) { return (x + 15) / 16 * 16; }
+
+template <int GT, int NG>
+hipError_t launch_route_t(const RouteParams &P, hipStream_t st, const LaunchTiming *tm) {
+    int n_route = 0, tt = 1;
     if (P.do_route) {
         tt = route_tile_tokens(P.h);
         n_route = ((P.T + tt - 1) / tt) * ((P.E + kRouteEG - 1) / kRouteEG);
     }
-    const int n_quant = QT ? std::min(P.T, 256) : 0;
-    int grid = n_route + n_quant;
-    if (grid == 0) grid = 1;
-    size_t lds = 0;
-    if (P.do_route) lds = std::max(lds, (size_t) tt * P.h * 4);
-    if (P.do_perm) lds = std::max(lds, (size_t) (3 * P.n_bins + 16) * 4);
-    if (lds == 0) lds = 16;
-    hipLaunchKernelGGL((prologue_kernel<GT, QT>), dim3(grid), dim3(kBlock), lds, st, P, n_route, n_quant, tt);
-    return hipGetLastError();
+    const int n_quant = P.qtype ? std::min(P.T, 256) : 0;
+    const int grid = std::max(1, n_route + n_quant);
+    const size_t lds = P.do_route ? (size_t) tt * P.h * 4 : 16;
+    return launch(route_kernel<GT, NG>, dim3(grid), dim3(kBlock), lds, st, tm, P, n_route, n_quant, tt);
+}
+
+template <int GT>
+hipError_t launch_route_g(const RouteParams &P, hipStream_t st, const LaunchTiming *tm) {
+    switch (P.h / 256) {
+        case 1: return launch_route_t<GT, 1>(P, st, tm);
+        case 2: return launch_route_t<GT, 2>(P, st, tm);
+        case 4: return launch_route_t<GT, 4>(P, st, tm);
+        case 8: return launch_route_t<GT, 8>(P, st, tm);
+        case 12: return launch_route_t<GT, 12>(P, st, tm);
+        default: return launch_route_t<GT, 16>(P, st, tm);
+    }
 }
 
 template <int WT, int S>
-hipError_t launch_gate_up_t(const GateUpParams &P, int G, hipStream_t st) {
-    const int h32 = P.h / 32;
-    const size_t lds = (size_t) kTC * P.h + (size_t) 2 * kTC * h32 * 4 + (size_t) kTC * G * 2 * kGuRows * 4;
-    hipLaunchKernelGGL((gate_up_kernel<WT, S>), dim3(P.f / kGuRows, P.max_active), dim3(2 * kGuRows * G), lds, st, P);
-    return hipGetLastError();
+hipError_t launch_gate_up_t(const GateUpParams &P, int G, hipStream_t st, const LaunchTiming *tm) {
+    const int h32 = P.h / 32, RW = 128 / G;
+    const size_t lds = align16(group_lds_bytes(P.gp.T, P.gp.k, P.gp.n_bins, P.gp.route)) + 16 + (size_t) kTC * P.h +
+                       (size_t) 2 * kTC * h32 * 4 + (size_t) kTC * G * 2 * RW * 4;
+    if (P.gp.route)
+        return launch(gate_up_kernel<WT, S, true>, dim3(P.f / RW, P.max_active), dim3(2 * RW * G), lds, st, tm, P);
+    return launch(gate_up_kernel<WT, S, false>, dim3(P.f / RW, P.max_active), dim3(2 * RW * G), lds, st, tm, P);
 }
 
 template <int WT, int S>
-hipError_t launch_down_t(const DownParams &P, int G, hipStream_t st) {
+hipError_t launch_down_t(const DownParams &P, int G, hipStream_t st, const LaunchTiming *tm) {
     const int f32 = P.f / 32;
-    const size_t lds = (size_t) kTC * P.f + (size_t) 2 * kTC * f32 * 4 + (size_t) kTC * G * kDnRows * 4;
-    hipLaunchKernelGGL((down_kernel<WT, S>), dim3(P.h / kDnRows, P.max_active), dim3(kDnRows * G), lds, st, P);
-    return hipGetLastError();
+    const size_t lds = align16(group_lds_bytes(P.gp.T, P.gp.k, P.gp.n_bins, 0)) + 16 + (size_t) kTC * P.f +
+                       (size_t) 2 * kTC * f32 * 4 + (size_t) kTC * G * kDnRows * 4;
+    return launch(down_kernel<WT, S>, dim3(P.h / kDnRows, P.max_active), dim3(kDnRows * G), lds, st, tm, P);
 }
 
 }  // namespace
 
-const char *check_shapes(int h, int f, int E, int k, int n_bins) {
+int decode_route_max_tokens() { return kDecodeRouteT; }
+
+const char *check_shapes(int h, int f, int E, int k, int n_bins, int n_batch) {
     int S, G;
     if (h <= 0 || h % 256 != 0) return "n_embd must be a positive multiple of 256";
     if (h > 256 * kRouteMaxNG) return "n_embd above 4096 is not supported by the router kernel";
+    {
+        const int ng = h / 256;
+        if (ng != 1 && ng != 2 && ng != 4 && ng != 8 && ng != 12 && ng != 16)
+            return "n_embd must be 256, 512, 1024, 2048, 3072 or 4096";
+    }
     if (f <= 0 || f % 256 != 0) return "n_ff_exp must be a positive multiple of 256";
     if (E < 1 || E > kWave * kMaxEPL) return "n_expert must be in [1, 256]";
     if (k < 1 || k > E || k > kMaxK) return "n_expert_used must be in [1, min(n_expert, 64)]";
     if (n_bins < 1 || n_bins > kMaxBins) return "slot count must be in [1, 4096]";
-    if (!pick_split(h / 256, &S, &G)) return "n_embd / 256 has no split into <= 8 groups of <= 2 super-blocks";
+    if (n_batch < 1 || (long) n_batch * k > kMaxPairs) return "n_batch * n_expert_used must be in [1, 8192]";
+    if (!pick_split_gate_up(h / 256, &S, &G)) return "n_embd / 256 must split into 1, 2, 4 or 8 groups of <= 2 super-blocks";
     if (!pick_split(f / 256, &S, &G)) return "n_ff_exp / 256 has no split into <= 8 groups of <= 2 super-blocks";
+    pick_split_gate_up(h / 256, &S, &G);
+    if (f % (128 / G) != 0) return "n_ff_exp must be a multiple of the gate/up row block";
+    // LDS: grouping + staging must fit in 64 KiB
+    const size_t work = 16 + (size_t) kTC * h + (size_t) 2 * kTC * (h / 32) * 4 + (size_t) kTC * G * 2 * (128 / G) * 4;
+    const size_t gu_route = align16(group_lds_bytes(std::min(n_batch, kDecodeRouteT), k, n_bins, 1)) + work;
+    const size_t gu = align16(group_lds_bytes(n_batch, k, n_bins, 0)) + work;
+    if (gu > 65536 || gu_route > 65536) return "n_batch * n_expert_used too large for the gate/up work-group's LDS";
     return "";
 }
 
-hipError_t launch_prologue(const PrologueParams &P, hipStream_t st) {
+hipError_t launch_route(const RouteParams &P, hipStream_t st, const LaunchTiming *tm) {
     if (P.T <= 0) return hipSuccess;
     const int gt = P.do_route ? P.gate_type : kTypeF16;
-    if (gt == kTypeF16) {
-        if (P.qtype == kTypeQ8_0) return launch_prologue_t<kTypeF16, kTypeQ8_0>(P, st);
-        if (P.qtype == kTypeQ4_K) return launch_prologue_t<kTypeF16, kTypeQ4_K>(P, st);
-        return launch_prologue_t<kTypeF16, 0>(P, st);
-    }
-    if (P.qtype == kTypeQ8_0) return launch_prologue_t<kTypeF32, kTypeQ8_0>(P, st);
-    if (P.qtype == kTypeQ4_K) return launch_prologue_t<kTypeF32, kTypeQ4_K>(P, st);
-    return launch_prologue_t<kTypeF32, 0>(P, st);
+    return gt == kTypeF16 ? launch_route_g<kTypeF16>(P, st, tm) : launch_route_g<kTypeF32>(P, st, tm);
 }
 
-hipError_t launch_gate_up(const GateUpParams &P, hipStream_t st) {
+hipError_t launch_topk(const TopkParams &P, hipStream_t st, const LaunchTiming *tm) {
+    if (P.T <= 0) return hipSuccess;
+    const int per = kBlock / kWave;
+    return launch(topk_kernel, dim3((P.T + per - 1) / per), dim3(kBlock), 0, st, tm, P);
+}
+
+hipError_t launch_gate_up(const GateUpParams &P, hipStream_t st, const LaunchTiming *tm) {
     int S, G;
-    if (P.max_active <= 0 || !pick_split(P.h / 256, &S, &G)) return hipSuccess;
+    if (P.max_active <= 0 || !pick_split_gate_up(P.h / 256, &S, &G)) return hipSuccess;
     if (P.type == kTypeQ8_0) {
-        if (S == 1) return launch_gate_up_t<kTypeQ8_0, 1>(P, G, st);
-        return launch_gate_up_t<kTypeQ8_0, 2>(P, G, st);
+        if (S == 1) return launch_gate_up_t<kTypeQ8_0, 1>(P, G, st, tm);
+        return launch_gate_up_t<kTypeQ8_0, 2>(P, G, st, tm);
     }
-    if (S == 1) return launch_gate_up_t<kTypeQ4_K, 1>(P, G, st);
-    return launch_gate_up_t<kTypeQ4_K, 2>(P, G, st);
+    if (S == 1) return launch_gate_up_t<kTypeQ4_K, 1>(P, G, st, tm);
+    return launch_gate_up_t<kTypeQ4_K, 2>(P, G, st, tm);
 }
 
-hipError_t launch_down(const DownParams &P, hipStream_t st) {
+hipError_t launch_down(const DownParams &P, hipStream_t st, const LaunchTiming *tm) {
     int S, G;
     if (P.max_active <= 0 || !pick_split(P.f / 256, &S, &G)) return hipSuccess;
     if (P.type == kTypeQ8_0) {
-        if (S == 1) return launch_down_t<kTypeQ8_0, 1>(P, G, st);
-        return launch_down_t<kTypeQ8_0, 2>(P, G, st);
+        if (S == 1) return launch_down_t<kTypeQ8_0, 1>(P, G, st, tm);
+        return launch_down_t<kTypeQ8_0, 2>(P, G, st, tm);
     }
-    if (S == 1) return launch_down_t<kTypeQ4_K, 1>(P, G, st);
-    return launch_down_t<kTypeQ4_K, 2>(P, G, st);
+    if (S == 1) return launch_down_t<kTypeQ4_K, 1>(P, G, st, tm);
+    return launch_down_t<kTypeQ4_K, 2>(P, G, st, tm);
+}
+
+hipError_t launch_combine(const CombineParams &P, hipStream_t st, const LaunchTiming *tm) {
+    if (P.T <= 0) return hipSuccess;
+    const int n = P.T * (P.h / 4);
+    return launch(combine_kernel, dim3((n + kBlock - 1) / kBlock), dim3(kBlock), 0, st, tm, P);
 }
 
 }  // namespace lstk

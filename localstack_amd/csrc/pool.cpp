@@ -101,6 +101,8 @@ struct TimedLaunch {
     hipEvent_t start, end;
 };
 
+constexpr int kStages = 4; // router (+ top-k), gate_up, down, combine
+
 }  // namespace
 
 struct lstk_pool {
@@ -123,15 +125,13 @@ struct lstk_pool {
     void *scratch = nullptr;
     lstk::ActBuf xq{};
     float *logits = nullptr, *act = nullptr, *Y = nullptr;
-    lstk::PermBuf pb{};
-    unsigned *route_counter = nullptr, *down_counters = nullptr;
     int32_t *err = nullptr;
     int n_bins_max = 0;
     // timing
     bool timing = false;
-    std::vector<TimedLaunch> launched[3];
-    double ms[3] = {0, 0, 0};
-    int64_t launches[3] = {0, 0, 0};
+    std::vector<TimedLaunch> launched[kStages];
+    double ms[kStages] = {};
+    int64_t launches[kStages] = {};
 };
 
 namespace {
@@ -150,10 +150,9 @@ int alloc_scratch(lstk_pool *P) {
     };
     const size_t o_qs = take(T * h), o_d = take(T * (h / 32) * 4), o_bs = take(T * (h / 32) * 4);
     const size_t o_logits = take(T * E * 4);
-    const size_t o_counts = take(nb * 4), o_offsets = take((nb + 1) * 4), o_active = take(nb * 4);
-    const size_t o_nactive = take(16), o_perm = take(T * k * 4);
     const size_t o_act = take(T * k * f * 4), o_Y = take(T * k * h * 4);
-    const size_t o_rc = take(64), o_dc = take((h / 64) * 4 + 64), o_err = take(64);
+    const size_t o_err = take(64);
+    (void) nb;
     hipError_t e = hipMalloc(&P->scratch, off);
     if (e != hipSuccess) return hip_fail(e, "hipMalloc(scratch)");
     e = hipMemset(P->scratch, 0, off);
@@ -163,15 +162,8 @@ int alloc_scratch(lstk_pool *P) {
     P->xq.d = reinterpret_cast<float *>(b + o_d);
     P->xq.bs = reinterpret_cast<int32_t *>(b + o_bs);
     P->logits = reinterpret_cast<float *>(b + o_logits);
-    P->pb.counts = reinterpret_cast<int32_t *>(b + o_counts);
-    P->pb.offsets = reinterpret_cast<int32_t *>(b + o_offsets);
-    P->pb.active = reinterpret_cast<int32_t *>(b + o_active);
-    P->pb.n_active = reinterpret_cast<int32_t *>(b + o_nactive);
-    P->pb.perm = reinterpret_cast<int32_t *>(b + o_perm);
     P->act = reinterpret_cast<float *>(b + o_act);
     P->Y = reinterpret_cast<float *>(b + o_Y);
-    P->route_counter = reinterpret_cast<unsigned *>(b + o_rc);
-    P->down_counters = reinterpret_cast<unsigned *>(b + o_dc);
     P->err = reinterpret_cast<int32_t *>(b + o_err);
     return LSTK_OK;
 }
@@ -317,7 +309,7 @@ int create(const lstk_moe_dims *dims, const lstk_expert_layer *layers, size_t po
         }
     }
     for (const Shard &s : P->shards) P->n_bins_max = std::max(P->n_bins_max, (int) s.n_slots);
-    const char *bad = lstk::check_shapes(d.n_embd, d.n_ff_exp, d.n_expert, d.n_expert_used, P->n_bins_max);
+    const char *bad = lstk::check_shapes(d.n_embd, d.n_ff_exp, d.n_expert, d.n_expert_used, P->n_bins_max, d.n_batch);
     if (bad[0]) {
         destroy(P);
         return fail(LSTK_E_INVALID, bad);
@@ -513,17 +505,18 @@ int release_all(lstk_pool *P, hipStream_t stream) {
     return LSTK_OK;
 }
 
-// Records events around a launch when timing is on.
+// Runs one launch; with timing on, the launch records its own start/stop timestamps.
 template <typename F>
-hipError_t timed(lstk_pool *P, int stage, hipStream_t st, F &&launch) {
-    if (!P->timing) return launch();
+hipError_t timed(lstk_pool *P, int stage, F &&launch) {
+    if (!P->timing) return launch(nullptr);
     TimedLaunch t{};
     hipError_t e;
     if ((e = hipEventCreate(&t.start)) != hipSuccess) return e;
     if ((e = hipEventCreate(&t.end)) != hipSuccess) return e;
-    if ((e = hipEventRecord(t.start, st)) != hipSuccess) return e;
-    const hipError_t le = launch();
-    if ((e = hipEventRecord(t.end, st)) != hipSuccess) return e;
+    lstk::LaunchTiming tm;
+    tm.start = t.start;
+    tm.stop = t.end;
+    const hipError_t le = launch(&tm);
     P->launched[stage].push_back(t);
     return le;
 }
@@ -540,28 +533,47 @@ int check_call(lstk_pool *P, int layer, int T) {
     return LSTK_OK;
 }
 
-int run_experts(lstk_pool *P, int layer, const float *d_hnorm, const float *d_weights, const float *d_resid, float *d_out,
-                int T, hipStream_t st, const lstk::PrologueParams *pro_in, const int32_t *d_bins) {
+// Router (optional) + experts + combine of one layer. mode 0: ffn with caller slots / weights;
+// mode 1: resident block, routing from gate_inp, ids / weights written to d_ids / d_weights.
+int run_block(lstk_pool *P, int layer, int mode, const float *d_hnorm, const void *d_gate_inp, int gate_type,
+              const int32_t *d_slots, int32_t *d_ids, float *d_weights, const float *d_resid, float *d_out, int T,
+              hipStream_t st) {
     const lstk_moe_dims &d = P->dims;
     const Shard &s = P->shards[P->layer_shard[layer]];
-    lstk::PrologueParams pro{};
-    if (pro_in) pro = *pro_in;
-    pro.hnorm = d_hnorm;
-    pro.T = T;
-    pro.h = d.n_embd;
-    pro.k = d.n_expert_used;
-    pro.qtype = s.tu;
-    pro.xq = P->xq;
-    pro.do_perm = 1;
-    pro.bins = d_bins;
-    pro.n_bins = (int) s.n_slots;
-    pro.pb = P->pb;
-    pro.err = P->err;
-    pro.counter = P->route_counter;
-    hipError_t e = timed(P, 0, st, [&] { return lstk::launch_prologue(pro, st); });
-    if (e != hipSuccess) return hip_fail(e, "prologue launch");
-    const int max_active = std::min<int>((int) s.n_slots, T * d.n_expert_used);
+    const int k = d.n_expert_used;
+    lstk::RouteParams rp{};
+    rp.hnorm = d_hnorm;
+    rp.T = T;
+    rp.h = d.n_embd;
+    rp.do_route = mode == 1;
+    rp.gate_inp = d_gate_inp;
+    rp.gate_type = gate_type;
+    rp.E = d.n_expert;
+    rp.logits = P->logits;
+    rp.qtype = s.tu;
+    rp.xq = P->xq;
+    hipError_t e = timed(P, 0, [&](const lstk::LaunchTiming *tm) { return lstk::launch_route(rp, st, tm); });
+    if (e != hipSuccess) return hip_fail(e, "route launch");
+    const bool fused_topk = mode == 1 && T <= lstk::decode_route_max_tokens();
+    if (mode == 1 && !fused_topk) {
+        lstk::TopkParams tp{P->logits, T, d.n_expert, k, d_ids, d_weights};
+        e = timed(P, 0, [&](const lstk::LaunchTiming *tm) { return lstk::launch_topk(tp, st, tm); });
+        if (e != hipSuccess) return hip_fail(e, "topk launch");
+    }
+    lstk::GroupParams gp{};
+    gp.T = T;
+    gp.k = k;
+    gp.n_bins = (int) s.n_slots;
+    gp.route = fused_topk ? 1 : 0;
+    gp.ids = mode == 1 ? d_ids : d_slots;
+    gp.logits = P->logits;
+    gp.E = d.n_expert;
+    gp.ids_out = d_ids;
+    gp.weights_out = d_weights;
+    gp.err = P->err;
+    const int max_active = std::min<int>((int) s.n_slots, T * k);
     lstk::GateUpParams gu{};
+    gu.gp = gp;
     gu.w_gate = s.d_gate;
     gu.w_up = s.d_up;
     gu.stride_gate = s.gate_bytes;
@@ -569,31 +581,28 @@ int run_experts(lstk_pool *P, int layer, const float *d_hnorm, const float *d_we
     gu.type = s.tu;
     gu.f = d.n_ff_exp;
     gu.h = d.n_embd;
-    gu.k = d.n_expert_used;
     gu.xq = P->xq;
-    gu.pb = P->pb;
     gu.max_active = max_active;
     gu.act = P->act;
-    e = timed(P, 1, st, [&] { return lstk::launch_gate_up(gu, st); });
+    e = timed(P, 1, [&](const lstk::LaunchTiming *tm) { return lstk::launch_gate_up(gu, st, tm); });
     if (e != hipSuccess) return hip_fail(e, "gate_up launch");
     lstk::DownParams dn{};
+    dn.gp = gp;
+    dn.gp.route = 0;
     dn.w_down = s.d_down;
     dn.stride_down = s.down_bytes;
     dn.type = s.td;
     dn.h = d.n_embd;
     dn.f = d.n_ff_exp;
-    dn.k = d.n_expert_used;
-    dn.T = T;
     dn.act = P->act;
     dn.weights = d_weights;
-    dn.pb = P->pb;
     dn.max_active = max_active;
     dn.Y = P->Y;
-    dn.resid = d_resid;
-    dn.out = d_out;
-    dn.counters = P->down_counters;
-    e = timed(P, 2, st, [&] { return lstk::launch_down(dn, st); });
+    e = timed(P, 2, [&](const lstk::LaunchTiming *tm) { return lstk::launch_down(dn, st, tm); });
     if (e != hipSuccess) return hip_fail(e, "down launch");
+    lstk::CombineParams cp{P->Y, d_resid, d_out, T, k, d.n_embd};
+    e = timed(P, 3, [&](const lstk::LaunchTiming *tm) { return lstk::launch_combine(cp, st, tm); });
+    if (e != hipSuccess) return hip_fail(e, "combine launch");
     return LSTK_OK;
 }
 
@@ -685,25 +694,21 @@ int lstk_moe_route(lstk_pool *pool, int layer, const float *d_hnorm, int n_token
     if ((rc = check_router_args(d_gate_inp, gate_type)) != LSTK_OK || (rc = check_act(d_hnorm, "hnorm")) != LSTK_OK) return rc;
     if (!d_ids || !d_weights) return fail(LSTK_E_INVALID, "ids and weights must be non-null");
     hipStream_t st = static_cast<hipStream_t>(stream);
-    lstk::PrologueParams pro{};
-    pro.hnorm = d_hnorm;
-    pro.T = n_tokens;
-    pro.h = pool->dims.n_embd;
-    pro.k = pool->dims.n_expert_used;
-    pro.do_route = 1;
-    pro.gate_inp = d_gate_inp;
-    pro.gate_type = gate_type;
-    pro.E = pool->dims.n_expert;
-    pro.logits = pool->logits;
-    pro.ids = d_ids;
-    pro.weights = d_weights;
-    pro.qtype = 0;
-    pro.do_perm = 0;
-    pro.n_bins = pool->n_bins_max;
-    pro.err = pool->err;
-    pro.counter = pool->route_counter;
-    const hipError_t e = timed(pool, 0, st, [&] { return lstk::launch_prologue(pro, st); });
+    lstk::RouteParams rp{};
+    rp.hnorm = d_hnorm;
+    rp.T = n_tokens;
+    rp.h = pool->dims.n_embd;
+    rp.do_route = 1;
+    rp.gate_inp = d_gate_inp;
+    rp.gate_type = gate_type;
+    rp.E = pool->dims.n_expert;
+    rp.logits = pool->logits;
+    rp.qtype = 0;
+    hipError_t e = timed(pool, 0, [&](const lstk::LaunchTiming *tm) { return lstk::launch_route(rp, st, tm); });
     if (e != hipSuccess) return hip_fail(e, "route launch");
+    lstk::TopkParams tp{pool->logits, n_tokens, pool->dims.n_expert, pool->dims.n_expert_used, d_ids, d_weights};
+    e = timed(pool, 0, [&](const lstk::LaunchTiming *tm) { return lstk::launch_topk(tp, st, tm); });
+    if (e != hipSuccess) return hip_fail(e, "topk launch");
     return LSTK_OK;
 }
 
@@ -716,8 +721,8 @@ int lstk_moe_ffn(lstk_pool *pool, int layer, const float *d_hnorm, const int32_t
         (rc = check_act(d_out, "out")) != LSTK_OK)
         return rc;
     if (!d_slots || !d_weights) return fail(LSTK_E_INVALID, "slots and weights must be non-null");
-    return run_experts(pool, layer, d_hnorm, d_weights, d_resid, d_out, n_tokens, static_cast<hipStream_t>(stream), nullptr,
-                       d_slots);
+    return run_block(pool, layer, 0, d_hnorm, nullptr, 0, d_slots, nullptr, const_cast<float *>(d_weights), d_resid, d_out,
+                     n_tokens, static_cast<hipStream_t>(stream));
 }
 
 int lstk_moe_block(lstk_pool *pool, int layer, const float *d_hnorm, const void *d_gate_inp, int gate_type,
@@ -731,16 +736,8 @@ int lstk_moe_block(lstk_pool *pool, int layer, const float *d_hnorm, const void 
         (rc = check_act(d_resid, "resid")) != LSTK_OK || (rc = check_act(d_out, "out")) != LSTK_OK)
         return rc;
     if (!d_ids || !d_weights) return fail(LSTK_E_INVALID, "ids and weights must be non-null");
-    lstk::PrologueParams pro{};
-    pro.do_route = 1;
-    pro.gate_inp = d_gate_inp;
-    pro.gate_type = gate_type;
-    pro.E = pool->dims.n_expert;
-    pro.logits = pool->logits;
-    pro.ids = d_ids;
-    pro.weights = d_weights;
-    return run_experts(pool, layer, d_hnorm, d_weights, d_resid, d_out, n_tokens, static_cast<hipStream_t>(stream), &pro,
-                       d_ids);
+    return run_block(pool, layer, 1, d_hnorm, d_gate_inp, gate_type, nullptr, d_ids, d_weights, d_resid, d_out, n_tokens,
+                     static_cast<hipStream_t>(stream));
 }
 
 int lstk_pool_check(lstk_pool *pool, lstk_stream_t stream) {
@@ -767,9 +764,9 @@ int lstk_pool_set_timing(lstk_pool *pool, int enable) {
     return LSTK_OK;
 }
 
-int lstk_pool_timing(lstk_pool *pool, double ms[3], int64_t launches[3]) {
+int lstk_pool_timing(lstk_pool *pool, double ms[4], int64_t launches[4]) {
     if (!pool || !ms || !launches) return fail(LSTK_E_INVALID, "null argument");
-    for (int s = 0; s < 3; s++) {
+    for (int s = 0; s < kStages; s++) {
         for (TimedLaunch &t : pool->launched[s]) {
             hipError_t e = hipEventSynchronize(t.end);
             if (e != hipSuccess) return hip_fail(e, "hipEventSynchronize");

@@ -248,7 +248,8 @@ float or_vec_dot_q4_K_q8_K(int n, const void *w, const void *x) {
  * the activations to fp16 first (vec_dot_type F16) and accumulates the exact fp16*fp16 products in
  * f32. ggml's SIMD summation order is unpinned; the order used here, shared bit for bit with the
  * device kernel, is: 64 lane partials, lane l owning elements 256c + 4l + q (c ascending, then
- * q = 0..3), each accumulated with fmaf from 0, then a butterfly p[l] += p[l ^ s] for s = 32..1. */
+ * q = 0..3), each accumulated with fmaf from 0, then a pairwise tree p[l] + p[l ^ s] for
+ * s = 1, 2, 4, 8, 16, 32 (neighbouring lanes first). */
 static float router_dot(const float *x, const void *w, int type, int h) {
     float p[64], t[64];
     const uint16_t *wh = (const uint16_t *) w;
@@ -264,7 +265,7 @@ static float router_dot(const float *x, const void *w, int type, int h) {
         }
         p[l] = acc;
     }
-    for (int s = 32; s >= 1; s >>= 1) {
+    for (int s = 1; s <= 32; s <<= 1) {
         for (int l = 0; l < 64; l++) t[l] = p[l] + p[l ^ s];
         memcpy(p, t, sizeof(p));
     }
