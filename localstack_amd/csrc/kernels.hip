@@ -41,7 +41,8 @@ constexpr int kMaxG = 8;          // K-groups per work-group
 constexpr int kMaxK = 64;         // n_expert_used <= 64 (one lane per selected expert)
 constexpr int kMaxBins = 4096;
 constexpr int kMaxPairs = 8192;   // n_batch * n_expert_used
-constexpr int kDecodeRouteT = 16; // gate_up runs the top-k itself up to this many tokens
+typedef int xvec __attribute__((ext_vector_type(4))); // 16 bytes of int8 activations
+constexpr int kDecodeRouteT = 1;  // gate_up runs the top-k itself for a single token
 
 __device__ __forceinline__ float h2f(unsigned h) { return __half2float(__ushort_as_half((unsigned short) (h & 0xffffu))); }
 __device__ __forceinline__ float round_f16(float x) { return __half2float(__float2half_rn(x)); }
@@ -313,12 +314,9 @@ __device__ __forceinline__ unsigned long long order_key(float v, int e) {
 // Called by the `nsplit` wavefronts [w0, w0 + nsplit) of the block with part = wave - w0.
 // s_l: >= E floats, s_rank: >= nsplit * 64 * EPL ints, s_p: >= k floats, all LDS shared by the group.
 template <int EPL>
-__device__ __forceinline__ void topk_token(const float *__restrict__ l_row, int E, int k, int part, int nsplit, float *s_l,
-                           int *s_rank, float *s_p, int16_t *ids16, int32_t *ids32, float *weights, int32_t *ids32_b,
-                           float *weights_b) {
+__device__ __forceinline__ bool rank_token(const float *__restrict__ l_row, int E, int k, int part, int nsplit, float *s_l,
+                                           int *s_rank, float (&l)[EPL], bool (&valid)[EPL], int (&rank)[EPL]) {
     const int lane = threadIdx.x % kWave;
-    float l[EPL];
-    bool valid[EPL];
 #pragma unroll
     for (int i = 0; i < EPL; i++) {
         const int e = lane + kWave * i;
@@ -354,8 +352,7 @@ __device__ __forceinline__ void topk_token(const float *__restrict__ l_row, int 
 #pragma unroll
     for (int i = 0; i < EPL; i++) s_rank[(part * EPL + i) * kWave + lane] = r[i];
     group_barrier(nsplit);
-    if (part != 0) return;
-    int rank[EPL];
+    if (part != 0) return false;
 #pragma unroll
     for (int i = 0; i < EPL; i++) {
         rank[i] = 0;
@@ -410,6 +407,15 @@ __device__ __forceinline__ void topk_token(const float *__restrict__ l_row, int 
             }
         }
     }
+    return true;
+}
+
+// Softmax, renormalisation and output of one token whose ranks rank_token found (part 0 only).
+template <int EPL>
+__device__ __forceinline__ void weights_token(int k, const float (&l)[EPL], const bool (&valid)[EPL], const int (&rank)[EPL],
+                                              float *s_p, int16_t *ids16, int32_t *ids32, float *weights, int32_t *ids32_b,
+                                              float *weights_b) {
+    const int lane = threadIdx.x % kWave;
     // softmax over the row
     float m = -INFINITY;
 #pragma unroll
@@ -444,6 +450,18 @@ __device__ __forceinline__ void topk_token(const float *__restrict__ l_row, int 
             if (weights_b) weights_b[rank[i]] = w;
         }
     }
+}
+
+
+template <int EPL>
+__device__ __forceinline__ void topk_token(const float *__restrict__ l_row, int E, int k, int part, int nsplit, float *s_l,
+                                           int *s_rank, float *s_p, int16_t *ids16, int32_t *ids32, float *weights,
+                                           int32_t *ids32_b, float *weights_b) {
+    float l[EPL];
+    bool valid[EPL];
+    int rank[EPL];
+    if (rank_token<EPL>(l_row, E, k, part, nsplit, s_l, s_rank, l, valid, rank))
+        weights_token<EPL>(k, l, valid, rank, s_p, ids16, ids32, weights, ids32_b, weights_b);
 }
 
 // Top-k of T tokens by the block's wavefronts: one wavefront per token, or all wavefronts on one
@@ -556,6 +574,45 @@ __device__ __forceinline__ GroupLds group_lds(unsigned char *base, int T, int k,
     return g;
 }
 
+// Single-token routing inside an expert work-group (route mode): exact ranks of the token's row
+// by all wavefronts, the block's expert = the y-th selected expert by ascending id, its pair index
+// = t * k + rank = rank. Returns false when y >= k.
+template <int EPL>
+__device__ __forceinline__ bool route_one(const GroupParams &P, GroupLds g) {
+    const int lane = threadIdx.x % kWave, wave = threadIdx.x / kWave, nw = blockDim.x / kWave;
+    float *s_l = reinterpret_cast<float *>(g.scratch);
+    int *s_rank = reinterpret_cast<int *>(g.scratch + (size_t) nw * 256 * 4);
+    float *s_p = reinterpret_cast<float *>(s_rank + (size_t) nw * kMaxEPL * kWave);
+    float l[EPL];
+    bool valid[EPL];
+    int rank[EPL];
+    if (rank_token<EPL>(P.logits, P.E, P.k, wave, nw, s_l, s_rank, l, valid, rank)) {
+        if (blockIdx.x == 0 && blockIdx.y == 0)
+            weights_token<EPL>(P.k, l, valid, rank, s_p, nullptr, nullptr, nullptr, P.ids_out, P.weights_out);
+        const int y = blockIdx.y;
+        int e = -1, j = 0, cum = 0;
+#pragma unroll
+        for (int i = 0; i < EPL; i++) {
+            unsigned long long mk = __ballot(valid[i] && rank[i] < P.k);
+            const int c = __popcll(mk);
+            if (y >= cum && y < cum + c) {
+                for (int r = y - cum; r > 0; r--) mk &= mk - 1ull;
+                const int src = __ffsll((long long) mk) - 1;
+                e = src + kWave * i;
+                j = __builtin_amdgcn_readlane(rank[i], src);
+            }
+            cum += c;
+        }
+        if (lane == 0) {
+            g.misc[0] = e;
+            g.misc[1] = e >= 0 ? 1 : 0;
+            g.list[0] = j;
+        }
+    }
+    __syncthreads();
+    return g.misc[0] >= 0;
+}
+
 // Every work-group derives the same grouping from the same routing: the active bins in ascending
 // order (the order ggml's CPU mul_mat_id walks experts), work-group y takes the y-th active bin, and
 // its pairs (t, j) in token-major order. Bins out of range are clamped and flagged in *err.
@@ -566,9 +623,15 @@ __device__ __forceinline__ bool group_pairs(const GroupParams &P, GroupLds g) {
     const int lane = tid % kWave, wave = tid / kWave;
     const int k = P.k, np = P.T * k, nb = P.n_bins, nwords = (nb + 31) / 32;
     if (ROUTE) {
-        const bool first = blockIdx.x == 0 && blockIdx.y == 0;
-        topk_block(P.logits, P.T, P.E, k, g.scratch, g.ids, nullptr, g.w, first ? P.ids_out : nullptr,
-                   first ? P.weights_out : nullptr);
+        // route mode serves a single token: every wavefront helps rank its row, then the
+        // selected experts are a ballot away (ascending id = the work-group order); only
+        // work-group (0, 0) runs the softmax and stores ids / weights for the caller and down
+        const int epl = (P.E + kWave - 1) / kWave;
+        bool ok;
+        if (epl == 1) ok = route_one<1>(P, g);
+        else if (epl == 2) ok = route_one<2>(P, g);
+        else ok = route_one<4>(P, g);
+        return ok;
     } else {
         for (int p = tid; p < np; p += bd) {
             int b = P.ids[p];
@@ -760,6 +823,29 @@ __global__ __launch_bounds__(kBlock) void gate_up_kernel(GateUpParams P) {
     if (!group_pairs<ROUTE>(P.gp, gl)) return;
     const int e = gl.misc[0], cnt = gl.misc[1];
     const uint8_t *base = m ? P.w_up + (size_t) e * P.stride_up : P.w_gate + (size_t) e * P.stride_gate;
+    const int h32 = h / 32, h16 = h / 16;
+    // The first kXr * blockDim 16-byte pieces of the first chunk's activations are loaded into
+    // registers before the weight loads are issued (a single token of up to 8192 values), so the
+    // LDS staging below waits for them only; the rest of a chunk is staged from global memory.
+    constexpr int kXr = 2;
+    const int nt0 = min(kTC, cnt);
+    const int n16 = nt0 * h16, n32 = nt0 * h32;
+    const int bd = blockDim.x;
+    xvec xr[kXr];
+    float dr;
+    int br;
+#pragma unroll
+    for (int u = 0; u < kXr; u++) {
+        const int idx = min(tid + u * bd, n16 - 1);
+        const int t = gl.list[idx / h16] / k;
+        xr[u] = reinterpret_cast<const xvec *>(P.xq.qs + (size_t) t * h)[idx % h16];
+    }
+    {
+        const int idx = min(tid, n32 - 1);
+        const size_t o = (size_t) (gl.list[idx / h32] / k) * h32 + idx % h32;
+        dr = P.xq.d[o];
+        br = WT == kTypeQ4_K ? P.xq.bs[o] : 0;
+    }
     uint4 w[S][C];
 #pragma unroll
     for (int s = 0; s < S; s++) {
@@ -767,21 +853,38 @@ __global__ __launch_bounds__(kBlock) void gate_up_kernel(GateUpParams P) {
 #pragma unroll
         for (int c = 0; c < C; c++) w[s][c] = *reinterpret_cast<const uint4 *>(base + chunk_offset(C, f, sb, c, row));
     }
-    const int h32 = h / 32;
     int8_t *xs = reinterpret_cast<int8_t *>(work);
     float *xd = reinterpret_cast<float *>(work + (size_t) kTC * h);
     int *xb = reinterpret_cast<int *>(xd + kTC * h32);
     float *red = reinterpret_cast<float *>(xb + kTC * h32);
+#pragma unroll
+    for (int u = 0; u < kXr; u++) {
+        const int idx = tid + u * bd;
+        if (idx < n16) reinterpret_cast<xvec *>(xs)[idx] = xr[u];
+    }
+    for (int idx = tid + kXr * bd; idx < n16; idx += bd)
+        reinterpret_cast<xvec *>(xs)[idx] = reinterpret_cast<const xvec *>(P.xq.qs + (size_t) (gl.list[idx / h16] / k) * h)[idx % h16];
+    if (tid < n32) {
+        xd[tid] = dr;
+        if (WT == kTypeQ4_K) xb[tid] = br;
+    }
+    for (int idx = tid + bd; idx < n32; idx += bd) {
+        const size_t o = (size_t) (gl.list[idx / h32] / k) * h32 + idx % h32;
+        xd[idx] = P.xq.d[o];
+        if (WT == kTypeQ4_K) xb[idx] = P.xq.bs[o];
+    }
     for (int c0 = 0; c0 < cnt; c0 += kTC) {
         const int nt = min(kTC, cnt - c0);
-        for (int tc = 0; tc < nt; tc++) {
-            const int t = gl.list[c0 + tc] / k;
-            const int4 *src = reinterpret_cast<const int4 *>(P.xq.qs + (size_t) t * h);
-            int4 *dst = reinterpret_cast<int4 *>(xs + (size_t) tc * h);
-            for (int i = tid; i < h / 16; i += blockDim.x) dst[i] = src[i];
-            for (int i = tid; i < h32; i += blockDim.x) {
-                xd[tc * h32 + i] = P.xq.d[(size_t) t * h32 + i];
-                if (WT == kTypeQ4_K) xb[tc * h32 + i] = P.xq.bs[(size_t) t * h32 + i];
+        if (c0 > 0) { // later chunks (more than 8 tokens on one expert) are staged here
+            for (int tc = 0; tc < nt; tc++) {
+                const int t = gl.list[c0 + tc] / k;
+                const int4 *src = reinterpret_cast<const int4 *>(P.xq.qs + (size_t) t * h);
+                int4 *dst = reinterpret_cast<int4 *>(xs + (size_t) tc * h);
+                for (int i = tid; i < h16; i += blockDim.x) dst[i] = src[i];
+                for (int i = tid; i < h32; i += blockDim.x) {
+                    xd[tc * h32 + i] = P.xq.d[(size_t) t * h32 + i];
+                    if (WT == kTypeQ4_K) xb[tc * h32 + i] = P.xq.bs[(size_t) t * h32 + i];
+                }
             }
         }
         __syncthreads();

@@ -217,16 +217,19 @@ def test_bad_ids_are_reported_not_faulted(orc, lstk, dev):
 
 
 def test_stage_timing_counts_launches(orc, lstk, dev):
+    """Stage 0 is one launch for a single token (gate_up ranks the experts itself) and two (router
+    + top-k kernel) for a batch; every other stage is one launch per block call."""
     import torch
     cfg, _, routers, store = model("tiny")
-    T = 4
-    x = to_dev(synth.activations(np.random.default_rng(6), T, cfg["h"]), dev)
-    ids = torch.zeros((T, 2), dtype=torch.int32, device=dev)
-    w = torch.zeros((T, 2), device=dev)
-    out = torch.zeros((T, cfg["h"]), device=dev)
+    gate = to_dev(routers[0], dev)
     store.set_timing(True)
-    for _ in range(3):
-        store.block(0, x, to_dev(routers[0], dev), 1, out, out, ids, w)
+    for T, reps in ((1, 3), (4, 1)):
+        x = to_dev(synth.activations(np.random.default_rng(6), T, cfg["h"]), dev)
+        ids = torch.zeros((T, 2), dtype=torch.int32, device=dev)
+        w = torch.zeros((T, 2), device=dev)
+        out = torch.zeros((T, cfg["h"]), device=dev)
+        for _ in range(reps):
+            store.block(0, x, gate, 1, out, out, ids, w)
     ms, n = store.timing()
     store.set_timing(False)
-    assert n == [3, 3, 3, 3] and all(m > 0 for m in ms)
+    assert n == [3 + 2, 4, 4, 4] and all(m > 0 for m in ms)
