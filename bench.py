@@ -16,6 +16,11 @@ with HIP events recorded around each of its launches on the launch stream (the l
 timing, over `--steps` eager steps), and its algorithmic bytes per launch are the distinct experts'
 gate+up bytes plus activations in and SwiGLU rows out.
 
+prefill: the same layer with Q4_K experts as a 512-token prefill with a Zipf(1.1)-skewed router
+(the grouped MFMA path), over 8 layer copies; reported beside the decode line with its own
+roofline (algorithmic flops per second against the int8 MFMA peak, and expert bytes per second
+against HBM).
+
 cpu_baseline: the oracle (a C restatement of ggml's CPU algorithm: Q8_0 activations, int8 block
 dots, OpenMP) runs the same layer on the host cores for a bounded sample of layer passes, each with
 new hnorm rows (so new experts).
@@ -33,7 +38,9 @@ sys.path.insert(0, ROOT)
 
 H, F, E, K, N_LAYER = 2048, 768, 128, 8, 48
 Q8_0 = 8
+Q4_K = 12
 HBM_PEAK_GBS = 8000.0
+INT8_PEAK_TOPS = 5000.0  # dense MFMA int8, MI355X
 
 
 def parse():
@@ -46,6 +53,8 @@ def parse():
     ap.add_argument("--no-graph", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--no-prefill", action="store_true")
+    ap.add_argument("--prefill-layers", type=int, default=8)
     return ap.parse_args()
 
 
@@ -146,7 +155,61 @@ def measure(torch, st, T, steps, warmup, use_graph):
     return res, graph
 
 
-def cpu_baseline(st, T, seconds):
+def prefill_leg(torch, L, n_layer, T, steps, warmup):
+    """The 30B-A3B MoE layer with Q4_K experts as a 512-token prefill with a Zipf(1.1)-skewed router:
+    n_layer layer copies (340 MB of experts each, so replays rotate through more than the 256 MB
+    last-level cache), one captured HIP graph of the n_layer MoE blocks per step."""
+    from localstack_amd import synth
+    rng = np.random.default_rng(11)
+    t0 = time.time()
+    up, gate, down = (synth.experts(rng, Q4_K, E, F, H), synth.experts(rng, Q4_K, E, F, H),
+                      synth.experts(rng, Q4_K, E, H, F))
+    store = L.ExpertStore(n_layer, H, F, E, K, T, [((Q4_K,) * 3, up, gate, down)] * n_layer)
+    log(f"[bench] prefill pool: {store.total_bytes() / 1e9:.2f} GB of Q4_K experts, built in {time.time() - t0:.1f}s")
+    dev = torch.device("cuda:0")
+    d = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to(dev)
+    routers = [d(synth.zipf_router_f16(rng, E, H)) for _ in range(n_layer)]
+    xs = [d(synth.activations(rng, T, H, bias_unit=True)) for _ in range(n_layer)]
+    resid = [d(synth.activations(rng, T, H)) for _ in range(n_layer)]
+    out = [torch.zeros((T, H), dtype=torch.float32, device=dev) for _ in range(n_layer)]
+    ids = [torch.zeros((T, K), dtype=torch.int32, device=dev) for _ in range(n_layer)]
+    w = [torch.zeros((T, K), dtype=torch.float32, device=dev) for _ in range(n_layer)]
+
+    def step():
+        for l in range(n_layer):
+            store.block(l, xs[l], routers[l], 1, resid[l], out[l], ids[l], w[l])
+
+    step()
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        step()
+    ms = time_steps(torch, graph.replay, steps, warmup)
+    store.check()
+    store.set_timing(True)
+    for _ in range(max(2, min(steps, 10))):
+        step()
+    stage_ms, launches = store.timing()
+    store.set_timing(False)
+    # stage 0 = route + top-k + permute (3 launches per block), 1 = gate_up, 2 = act quant + down, 3 = combine
+    per_block = [stage_ms[i] / max(1, launches[i] // (1 if i in (1, 3) else (3 if i == 0 else 2))) for i in range(4)]
+    counts = [np.bincount(i.cpu().numpy().ravel(), minlength=E) for i in ids]
+    active = float(np.mean([np.count_nonzero(c) for c in counts]))
+    flops = 2.0 * T * K * 3 * H * F
+    flops_gu = 2.0 * T * K * 2 * H * F
+    wbytes = active * 3 * 884736
+    layer_s = ms * 1e-3 / n_layer
+    gu_s = per_block[1] * 1e-3
+    del graph
+    return dict(T=T, n_layer=n_layer, ms_per_step=ms, tok_s=T * n_layer / (ms * 1e-3), layer_us=layer_s * 1e6,
+                stage_us_per_block={"route_topk_permute": per_block[0] * 1e3, "gate_up": per_block[1] * 1e3,
+                                    "quant_down": per_block[2] * 1e3, "combine": per_block[3] * 1e3},
+                active_experts=active, max_tokens_per_expert=int(max(c.max() for c in counts)),
+                layer_tflops=flops / layer_s / 1e12, layer_hbm_gbs=wbytes / layer_s / 1e9,
+                gate_up_tflops=flops_gu / gu_s / 1e12)
+
+
+def cpu_baseline(T, seconds):
     """Times the oracle on this host over whole layer passes of the same workload."""
     import oracle
     from localstack_amd import synth
@@ -156,7 +219,8 @@ def cpu_baseline(st, T, seconds):
     # is streamed from DRAM rather than replayed from the host's last-level cache
     xs = [synth.activations(rng, T, H) for _ in range(64)]
     resid = synth.activations(rng, T, H)
-    up, gate, down = (a.reshape(E, -1) for a in (st.up, st.gate, st.down))
+    up, gate, down = (synth.experts(rng, Q8_0, E, F, H).reshape(E, -1), synth.experts(rng, Q8_0, E, F, H).reshape(E, -1),
+                      synth.experts(rng, Q8_0, E, H, F).reshape(E, -1))
     cores = len(os.sched_getaffinity(0))
     os.environ.setdefault("OMP_NUM_THREADS", str(cores))
     n = 0
@@ -194,7 +258,16 @@ def main():
         extra, g = measure(torch, st, 8, a.steps, a.warmup, not a.no_graph)
         del g
         log(f"[bench] T=8: {json.dumps(extra)}")
-    cpu = None if a.no_cpu else cpu_baseline(st, a.tokens, a.cpu_seconds)
+    pre = None
+    if not a.no_prefill:
+        pre = prefill_leg(torch, L, a.prefill_layers, 512, max(5, a.steps // 5), 2)
+        log(f"[bench] prefill: {json.dumps(pre)}")
+        pre["roofline"] = {"bound": "hbm", "note": "512-token Q4_K prefill: 114 flop/B is below the int8 and fp16 MFMA ridge",
+                           "achieved_tflops": pre["layer_tflops"], "int8_peak_tops": INT8_PEAK_TOPS,
+                           "frac_int8_peak": pre["layer_tflops"] / INT8_PEAK_TOPS,
+                           "achieved_gbs": pre["layer_hbm_gbs"], "hbm_peak_gbs": HBM_PEAK_GBS,
+                           "frac_hbm": pre["layer_hbm_gbs"] / HBM_PEAK_GBS}
+    cpu = None if a.no_cpu else cpu_baseline(a.tokens, a.cpu_seconds)
     gu_avg_s = main_res["stage_avg_us"]["gate_up"] * 1e-6
     achieved = main_res["gate_up_bytes"] / gu_avg_s / 1e9
     line = {
@@ -222,6 +295,7 @@ def main():
         "t8": None if extra is None else {"tok_s": extra["tok_s"], "ms_per_step": extra["ms_per_step"],
                                           "stack_gbs": extra["layer_gbs"], "stage_avg_us": extra["stage_avg_us"],
                                           "distinct_experts_per_layer": extra["distinct_experts_per_layer"]},
+        "prefill": pre,
         "cpu_baseline": cpu,
     }
     print(json.dumps(line), flush=True)

@@ -127,7 +127,10 @@ int lstk_moe_route(lstk_pool *pool, int layer, const float *d_hnorm, int n_token
  * s = d_slots[t][j], summed left to right in j. x_t is quantized to the activation type ggml pairs with
  * the weight type (Q8_0 for Q8_0, Q8_K for Q4_K), and so is the SwiGLU output before down.
  * d_slots holds slot numbers from lstk_pool_acquire (streaming) or expert ids (resident).
- * d_out may alias d_resid. */
+ * d_out may alias d_resid.
+ * With Q4_K gate, up and down and at least 64 tokens (LSTK_GROUPED_MIN_TOKENS in the environment
+ * overrides the threshold) the call takes the grouped path: a stable permutation of the pairs by
+ * expert, then expert products on the matrix cores over 64-pair chunks. */
 int lstk_moe_ffn(lstk_pool *pool, int layer, const float *d_hnorm, const int32_t *d_slots, const float *d_weights,
                  const float *d_resid, float *d_out, int n_tokens, lstk_stream_t stream);
 
@@ -138,6 +141,16 @@ int lstk_moe_ffn(lstk_pool *pool, int layer, const float *d_hnorm, const int32_t
 int lstk_moe_block(lstk_pool *pool, int layer, const float *d_hnorm, const void *d_gate_inp, int gate_type,
                    const float *d_resid, float *d_out, int32_t *d_ids, float *d_weights, int n_tokens,
                    lstk_stream_t stream);
+
+/* The token-to-expert grouping of ggml's CPU mul_mat_id (the three calls at src/qwen3.cpp:201-204) on
+ * the device: the n_tokens * n_expert_used pairs (t, j), pair index t * n_expert_used + j, are sorted by
+ * bin d_bins[t][j] in [0, n_bins), bins ascending and each bin's pairs in token-major order (a stable
+ * counting sort). Writes d_counts [n_bins], d_offsets [n_bins + 1] (exclusive scan of the counts) and
+ * d_perm [n_tokens * n_expert_used] (sorted position -> pair index). n_bins <= 1024. A bin out of range
+ * is clamped on the device and reported by lstk_pool_check. The grouped (prefill) path of
+ * lstk_moe_ffn / lstk_moe_block runs the same kernel. */
+int lstk_moe_permute(lstk_pool *pool, const int32_t *d_bins, int n_tokens, int n_bins, int32_t *d_counts,
+                     int32_t *d_offsets, int32_t *d_perm, lstk_stream_t stream);
 
 /* Waits for `stream` and reports LSTK_E_BADID if a kernel has seen an id out of range since the
  * last check (the id is clamped on the device so no access leaves the pool). */

@@ -64,6 +64,7 @@ SIGNATURES = {
     "lstk_moe_route": (_I, [_P, _I, _P, _I, _P, _I, _P, _P, _P]),
     "lstk_moe_ffn": (_I, [_P, _I, _P, _P, _P, _P, _P, _I, _P]),
     "lstk_moe_block": (_I, [_P, _I, _P, _P, _I, _P, _P, _P, _P, _I, _P]),
+    "lstk_moe_permute": (_I, [_P, _P, _I, _I, _P, _P, _P, _P]),
     "lstk_pool_check": (_I, [_P, _P]),
     "lstk_pool_set_timing": (_I, [_P, _I]),
     "lstk_pool_timing": (_I, [_P, ctypes.POINTER(ctypes.c_double), ctypes.POINTER(ctypes.c_int64)]),
@@ -236,6 +237,12 @@ class ExpertStore:
         T = hnorm.shape[0] if n_tokens is None else n_tokens
         _check(lib().lstk_moe_block(self._h, layer, _ptr(hnorm), _ptr(gate_inp), gate_type, _ptr(resid), _ptr(out),
                                     _ptr(ids), _ptr(weights), T, _stream(stream)))
+
+    def permute(self, bins, n_bins, counts, offsets, perm, n_tokens=None, stream=None):
+        """Stable grouping of the (token, slot) pairs by bin, as ggml's CPU mul_mat_id walks them."""
+        T = bins.shape[0] if n_tokens is None else n_tokens
+        _check(lib().lstk_moe_permute(self._h, _ptr(bins), T, n_bins, _ptr(counts), _ptr(offsets), _ptr(perm),
+                                      _stream(stream)))
 
     def check(self, stream=None):
         _check(lib().lstk_pool_check(self._h, _stream(stream)))

@@ -12,7 +12,7 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 ROOT = os.path.dirname(HERE)
 CSRC = os.path.join(HERE, "csrc")
 LIB = os.path.join(HERE, "liblstk_moe.so")
-SOURCES = ["kernels.hip", "pool.cpp", "repack.cpp"]
+SOURCES = ["kernels.hip", "grouped.hip", "pool.cpp", "repack.cpp"]
 ARCH = os.environ.get("LSTK_OFFLOAD_ARCH", "gfx950")
 
 

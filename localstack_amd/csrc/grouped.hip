@@ -1,0 +1,453 @@
+// grouped.hip - gfx950 kernels of the grouped (prefill) path, for calls that route many tokens to
+// each expert. ggml's CPU mul_mat_id groups the (token, slot) pairs by expert and runs each expert's
+// matrix over its rows (src/qwen3.cpp:201-204); here that is:
+//   permute    one work-group: per-bin counts, exclusive offsets, the stable token-major pair order
+//              and the work list of 64-pair chunks (full chunks first, then the partial ones).
+//   gate_up    per (chunk, 64-row block): Q4_K gate and up rows x Q8_K token rows on
+//              v_mfma_i32_32x32x32_i8, fused SwiGLU (src/qwen3.cpp:201-203).
+//   act_quant  the SwiGLU rows to Q8_K, the activation type ggml pairs with Q4_K down weights.
+//   down       per (chunk, 128-row block): Q4_K down rows x Q8_K SwiGLU rows, times the router
+//              weight (src/qwen3.cpp:204-205). The existing combine kernel sums the k rows.
+//
+// Integer semantics of ggml's vec_dot_q4_K_q8_K on the matrix cores. Per super-block of 256 values
+// ggml computes d_x (d_w isum - dmin_w imin) with isum = sum_j sc_j sum_i q_ji x_ji (q in [0, 15],
+// sc_j and m_j 6-bit) and imin = sum_j m_j sum_i x_ji. sc_j q does not fit int8, so sc_j is split as
+// 8 sh_j + sl_j (both <= 7) and three int8 weight planes go through the MFMA with the same int8
+// activations: sh_j q, sl_j q (both <= 105) and m_j. Then isum = 8 accH + accL and imin = accM,
+// exactly as in ggml's integer arithmetic; only the f32 accumulation over super-blocks is ordered
+// differently.
+#include "device.h"
+#include "formats.h"
+#include "kernels.h"
+
+#include <algorithm>
+
+namespace lstk {
+namespace {
+
+typedef int i32x4 __attribute__((ext_vector_type(4)));
+typedef int i32x16 __attribute__((ext_vector_type(16)));
+typedef unsigned short u16x2 __attribute__((ext_vector_type(2)));
+
+constexpr int kGThreads = 256;        // 4 wavefronts per grouped work-group
+constexpr int kRowBytes = 256 + 16;   // LDS bytes of one staged activation row per super-block
+constexpr int kStageBytes = kGroupedChunk * kRowBytes;
+constexpr int kPermThreads = 1024;
+constexpr int kPermSeg = kPermThreads / kWave; // one pair segment per wavefront
+constexpr int kPermMaxPairs = 8192;
+
+__device__ __forceinline__ i32x16 mfma_i8(i32x4 a, i32x4 b, i32x16 c) {
+    return __builtin_amdgcn_mfma_i32_32x32x32_i8(a, b, c, 0, 0, 0);
+}
+
+// Byte-wise product of four values <= 15 with s <= 7 (s2 = s | s << 16): the products stay below
+// 128, so two 16-bit multiplies carry nothing across bytes.
+__device__ __forceinline__ int mul_bytes(unsigned v, unsigned s2) {
+    return __builtin_bit_cast(int, __builtin_bit_cast(u16x2, v) * __builtin_bit_cast(u16x2, s2));
+}
+
+__device__ __forceinline__ uint4 ld16(const uint8_t *p) { return *reinterpret_cast<const uint4 *>(p); }
+
+// ------------------------------------------------------------------------------------------------
+// permutation
+// ------------------------------------------------------------------------------------------------
+
+__device__ __forceinline__ void lds_fence() { asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory"); }
+
+// Inclusive prefix sum over the wavefront.
+__device__ __forceinline__ int wave_incl_scan(int v) {
+    const int lane = threadIdx.x % kWave;
+#pragma unroll
+    for (int o = 1; o < kWave; o <<= 1) {
+        const int y = __shfl_up(v, o, kWave);
+        if (lane >= o) v += y;
+    }
+    return v;
+}
+
+// The pairs are cut into kPermSeg contiguous segments, one per wavefront. Pass 1 counts each
+// segment's pairs per bin (16-bit counts, two bins per LDS word); per bin, the counts become an
+// exclusive prefix over segments, and the totals an exclusive prefix over bins (the offsets).
+// Pass 2: each wavefront walks its segment 64 pairs at a time; a pair's position is
+// offsets[b] + (pairs of b in earlier segments and earlier chunks) + (lanes of the chunk before it
+// with the same bin). That is the stable order by pair index t * k + j within each bin.
+__global__ __launch_bounds__(kPermThreads) void permute_kernel(PermuteParams P) {
+    __shared__ unsigned seg[kPermSeg][kGroupedMaxBins / 2];
+    __shared__ int16_t bl[kPermMaxPairs];
+    __shared__ int cnt[kGroupedMaxBins];
+    __shared__ int wsum[3][kPermSeg];
+    __shared__ __align__(16) int cb[kPermSeg][kWave];
+    const int tid = threadIdx.x, lane = tid % kWave, w = tid / kWave;
+    const int np = P.np, nb = P.n_bins;
+    for (int i = tid; i < kPermSeg * (kGroupedMaxBins / 2); i += kPermThreads) (&seg[0][0])[i] = 0u;
+    __syncthreads();
+    const int L = ((np + kPermSeg - 1) / kPermSeg + kWave - 1) / kWave * kWave;
+    const int s0 = min(np, w * L), s1 = min(np, s0 + L);
+    for (int p = s0 + lane; p < s1; p += kWave) {
+        int b = P.bins[p];
+        if (b < 0 || b >= nb) {
+            atomicOr(P.err, 1);
+            b = min(max(b, 0), nb - 1);
+        }
+        bl[p] = (int16_t) b;
+        atomicAdd(&seg[w][b >> 1], 1u << (16 * (b & 1)));
+    }
+    __syncthreads();
+    for (int wi = tid; wi < (nb + 1) / 2; wi += kPermThreads) {
+        unsigned lo = 0, hi = 0;
+        for (int s = 0; s < kPermSeg; s++) {
+            const unsigned v = seg[s][wi];
+            seg[s][wi] = lo | (hi << 16);
+            lo += v & 0xffffu;
+            hi += v >> 16;
+        }
+        cnt[2 * wi] = (int) lo;
+        if (2 * wi + 1 < nb) cnt[2 * wi + 1] = (int) hi;
+    }
+    __syncthreads();
+    // offsets and the work list: one bin per thread (n_bins <= 1024)
+    const int c = tid < nb ? cnt[tid] : 0;
+    const int full = c / P.chunk, part = (c % P.chunk) ? 1 : 0;
+    const int v0 = wave_incl_scan(c), v1 = wave_incl_scan(full), v2 = wave_incl_scan(part);
+    if (lane == kWave - 1) {
+        wsum[0][w] = v0;
+        wsum[1][w] = v1;
+        wsum[2][w] = v2;
+    }
+    __syncthreads();
+    int b0 = 0, b1 = 0, b2 = 0, tot0 = 0, tot1 = 0, tot2 = 0;
+    for (int s = 0; s < kPermSeg; s++) {
+        if (s < w) {
+            b0 += wsum[0][s];
+            b1 += wsum[1][s];
+            b2 += wsum[2][s];
+        }
+        tot0 += wsum[0][s];
+        tot1 += wsum[1][s];
+        tot2 += wsum[2][s];
+    }
+    const int off = b0 + v0 - c;
+    if (tid < nb) {
+        P.counts[tid] = c;
+        P.offsets[tid] = off;
+        if (P.items) {
+            const int fb = b1 + v1 - full, pb = tot1 + b2 + v2 - part;
+            for (int i = 0; i < full; i++) P.items[fb + i] = make_int4(tid, off + i * P.chunk, P.chunk, 0);
+            if (part) P.items[pb] = make_int4(tid, off + full * P.chunk, c - full * P.chunk, 0);
+        }
+        cnt[tid] = off;
+    }
+    if (tid == 0) {
+        P.offsets[nb] = tot0;
+        if (P.n_items) *P.n_items = tot1 + tot2;
+    }
+    __syncthreads();
+    for (int base = s0; base < s1; base += kWave) {
+        const int p = base + lane;
+        const bool on = p < s1;
+        const int b = on ? (int) bl[p] : -1;
+        cb[w][lane] = b;
+        lds_fence();
+        int before = 0, after = 0;
+#pragma unroll 4
+        for (int q = 0; q < kWave; q += 4) {
+            const int4 v = *reinterpret_cast<const int4 *>(&cb[w][q]);
+            before += (v.x == b && q < lane) + (v.y == b && q + 1 < lane) + (v.z == b && q + 2 < lane) +
+                      (v.w == b && q + 3 < lane);
+            after += (v.x == b && q > lane) + (v.y == b && q + 1 > lane) + (v.z == b && q + 2 > lane) +
+                     (v.w == b && q + 3 > lane);
+        }
+        int pos = 0;
+        if (on) {
+            const unsigned word = seg[w][b >> 1];
+            pos = cnt[b] + (int) ((b & 1) ? (word >> 16) : (word & 0xffffu)) + before;
+        }
+        lds_fence();
+        if (on) {
+            P.perm[pos] = p;
+            if (after == 0) atomicAdd(&seg[w][b >> 1], (unsigned) (before + 1) << (16 * (b & 1)));
+        }
+        lds_fence();
+    }
+}
+
+// ------------------------------------------------------------------------------------------------
+// grouped Q4_K x Q8_K products on the matrix cores
+// ------------------------------------------------------------------------------------------------
+
+// LDS of a grouped work-group.
+struct GLds {
+    unsigned char *xs; // [2][kGroupedChunk][kRowBytes] staged activation rows (double buffer)
+    float *dx;         // [2][kGroupedChunk] Q8_K scale of each staged row
+    int *pair;         // [kGroupedChunk] pair index of each chunk position
+    int *src;          // [kGroupedChunk] activation row of each chunk position
+};
+constexpr size_t kGLdsBytes = 2 * (size_t) kStageBytes + 2 * kGroupedChunk * 4 + 2 * kGroupedChunk * 4;
+
+__device__ __forceinline__ GLds g_lds(unsigned char *base) {
+    GLds g;
+    g.xs = base;
+    g.dx = reinterpret_cast<float *>(base + 2 * (size_t) kStageBytes);
+    g.pair = reinterpret_cast<int *>(g.dx + 2 * kGroupedChunk);
+    g.src = g.pair + kGroupedChunk;
+    return g;
+}
+
+// One super-block's activation rows of the chunk: 64 rows x 256 bytes, 16 bytes per thread-piece.
+struct Stage {
+    uint4 v[kGroupedChunk * 256 / 16 / kGThreads];
+    float dx;
+};
+
+__device__ __forceinline__ void stage_load(const GroupedParams &P, const GLds &g, int n, int sb, Stage &st) {
+    const int tid = threadIdx.x;
+#pragma unroll
+    for (int u = 0; u < (int) (sizeof(st.v) / sizeof(st.v[0])); u++) {
+        const int piece = tid + u * kGThreads;
+        const int r = min(piece >> 4, n - 1), part = piece & 15;
+        st.v[u] = ld16(reinterpret_cast<const uint8_t *>(P.xqs) + (size_t) g.src[r] * P.K + sb * 256 + part * 16);
+    }
+    if (tid < kGroupedChunk) st.dx = P.xd[(size_t) g.src[min(tid, n - 1)] * (P.K / 32) + sb * 8];
+}
+
+__device__ __forceinline__ void stage_store(const GLds &g, int buf, const Stage &st) {
+    const int tid = threadIdx.x;
+#pragma unroll
+    for (int u = 0; u < (int) (sizeof(st.v) / sizeof(st.v[0])); u++) {
+        const int piece = tid + u * kGThreads;
+        *reinterpret_cast<uint4 *>(g.xs + (size_t) buf * kStageBytes + (piece >> 4) * kRowBytes + (piece & 15) * 16) =
+            st.v[u];
+    }
+    if (tid < kGroupedChunk) g.dx[buf * kGroupedChunk + tid] = st.dx;
+}
+
+// The Q4_K chunks one lane needs of one super-block: the {d, dmin, scales} chunk and, for lane half
+// h = lane / 32, qs bytes [32 c + 16 h, 32 c + 16 h + 16) of each 64-value chunk c (pool chunk
+// 1 + 2 c + h). Low nibbles are values 64 c + 16 h + [0, 16) of sub-block 2 c, high nibbles values
+// 64 c + 32 + 16 h + [0, 16) of sub-block 2 c + 1: exactly the K slice the MFMA takes from this lane.
+struct WRow {
+    uint4 hdr, q[4];
+};
+
+__device__ __forceinline__ void wrow_load(const uint8_t *w, int rows, int row, int sb, WRow &r) {
+    const int h = (threadIdx.x % kWave) / 32;
+    r.hdr = ld16(w + chunk_offset(kChunksQ4_K, rows, sb, 0, row));
+#pragma unroll
+    for (int c = 0; c < 4; c++) r.q[c] = ld16(w + chunk_offset(kChunksQ4_K, rows, sb, 1 + 2 * c + h, row));
+}
+
+// Multiplies one super-block: the wavefront's 32 weight rows (lane % 32) with the staged rows of
+// buffer `buf` (M-tile mt = rows 32 mt .. 32 mt + 31 of the chunk), adding
+// d_x (d_w isum - dmin_w imin) to acc[mt][r] for staged row 32 mt + 8 (r / 4) + 4 (lane / 32) + r % 4.
+__device__ __forceinline__ void q4k_superblock(const GLds &g, int buf, int n, const WRow &wr, float (&acc)[2][16]) {
+    const int lane = threadIdx.x % kWave, h = lane / 32, r32 = lane % 32;
+    const float dw = h2f(wr.hdr.x), dmin = h2f(wr.hdr.x >> 16);
+    const unsigned s0 = wr.hdr.y, s1 = wr.hdr.z, s2 = wr.hdr.w;
+    const bool two = n > 32;
+    i32x16 aH[2], aL[2], aM[2];
+    const unsigned char *xs = g.xs + (size_t) buf * kStageBytes + (size_t) r32 * kRowBytes + 16 * h;
+#pragma unroll
+    for (int c = 0; c < 4; c++) {
+#pragma unroll
+        for (int nib = 0; nib < 2; nib++) {
+            int sc, m;
+            if (c == 0 && nib == 0) scale_min_k4<0>(s0, s1, s2, sc, m);
+            else if (c == 0) scale_min_k4<1>(s0, s1, s2, sc, m);
+            else if (c == 1 && nib == 0) scale_min_k4<2>(s0, s1, s2, sc, m);
+            else if (c == 1) scale_min_k4<3>(s0, s1, s2, sc, m);
+            else if (c == 2 && nib == 0) scale_min_k4<4>(s0, s1, s2, sc, m);
+            else if (c == 2) scale_min_k4<5>(s0, s1, s2, sc, m);
+            else if (nib == 0) scale_min_k4<6>(s0, s1, s2, sc, m);
+            else scale_min_k4<7>(s0, s1, s2, sc, m);
+            const unsigned sh = (unsigned) (sc >> 3) * 0x10001u, sl = (unsigned) (sc & 7) * 0x10001u;
+            const int mp = m * 0x01010101;
+            const uint4 q = wr.q[c];
+            const unsigned k4 = 0x0f0f0f0fu;
+            const unsigned n0 = nib ? (q.x >> 4) & k4 : q.x & k4, n1 = nib ? (q.y >> 4) & k4 : q.y & k4;
+            const unsigned n2 = nib ? (q.z >> 4) & k4 : q.z & k4, n3 = nib ? (q.w >> 4) & k4 : q.w & k4;
+            const i32x4 bh = {mul_bytes(n0, sh), mul_bytes(n1, sh), mul_bytes(n2, sh), mul_bytes(n3, sh)};
+            const i32x4 bl = {mul_bytes(n0, sl), mul_bytes(n1, sl), mul_bytes(n2, sl), mul_bytes(n3, sl)};
+            const i32x4 bm = {mp, mp, mp, mp};
+            const int off = 64 * c + 32 * nib;
+#pragma unroll
+            for (int mt = 0; mt < 2; mt++) {
+                if (mt == 1 && !two) continue;
+                const i32x4 a = *reinterpret_cast<const i32x4 *>(xs + (size_t) mt * 32 * kRowBytes + off);
+                if (c == 0 && nib == 0) {
+                    const i32x16 z = {};
+                    aH[mt] = mfma_i8(a, bh, z);
+                    aL[mt] = mfma_i8(a, bl, z);
+                    aM[mt] = mfma_i8(a, bm, z);
+                } else {
+                    aH[mt] = mfma_i8(a, bh, aH[mt]);
+                    aL[mt] = mfma_i8(a, bl, aL[mt]);
+                    aM[mt] = mfma_i8(a, bm, aM[mt]);
+                }
+            }
+        }
+    }
+    const float *dxs = g.dx + buf * kGroupedChunk;
+#pragma unroll
+    for (int mt = 0; mt < 2; mt++) {
+        if (mt == 1 && !two) continue;
+#pragma unroll
+        for (int a4 = 0; a4 < 4; a4++) {
+            const float4 d4 = *reinterpret_cast<const float4 *>(dxs + mt * 32 + 8 * a4 + 4 * h);
+            const float dv[4] = {d4.x, d4.y, d4.z, d4.w};
+#pragma unroll
+            for (int b = 0; b < 4; b++) {
+                const int r = 4 * a4 + b;
+                const int isum = 8 * aH[mt][r] + aL[mt][r];
+                acc[mt][r] += (dw * dv[b]) * (float) isum;
+                acc[mt][r] -= (dmin * dv[b]) * (float) aM[mt][r];
+            }
+        }
+    }
+}
+
+// The whole K of the wavefront's 32 rows (row0 + lane % 32 of matrix w) against the chunk's n <= 64
+// activation rows; called uniformly by the 4 wavefronts, which stage the rows together.
+__device__ __forceinline__ void q4k_rows(const GroupedParams &P, const GLds &g, int n, const uint8_t *w, int row0,
+                                         float (&acc)[2][16]) {
+    const int nsb = P.K / 256;
+    const int row = row0 + threadIdx.x % 32;
+#pragma unroll
+    for (int mt = 0; mt < 2; mt++)
+#pragma unroll
+        for (int r = 0; r < 16; r++) acc[mt][r] = 0.0f;
+    WRow cur, nxt;
+    Stage st;
+    wrow_load(w, P.rows, row, 0, cur);
+    stage_load(P, g, n, 0, st);
+    stage_store(g, 0, st);
+    __syncthreads();
+    for (int sb = 0; sb < nsb; sb++) {
+        const int buf = sb & 1;
+        if (sb + 1 < nsb) {
+            wrow_load(w, P.rows, row, sb + 1, nxt);
+            stage_load(P, g, n, sb + 1, st);
+        }
+        q4k_superblock(g, buf, n, cur, acc);
+        if (sb + 1 < nsb) {
+            stage_store(g, buf ^ 1, st);
+            cur = nxt;
+        }
+        __syncthreads();
+    }
+}
+
+// Reads the work item of this work-group; false when it has none.
+__device__ __forceinline__ bool g_item(const GroupedParams &P, int n_rb, const GLds &g, int4 &it) {
+    const int item = blockIdx.x / n_rb;
+    if (item >= *P.n_items) return false;
+    it = P.items[item];
+    const int tid = threadIdx.x;
+    if (tid < kGroupedChunk) {
+        const int p = P.perm[it.y + min(tid, it.z - 1)];
+        g.pair[tid] = p;
+        g.src[tid] = p / P.row_div;
+    }
+    __syncthreads();
+    return true;
+}
+
+// gate_up: wavefront w computes rows rb * 64 + 32 (w / 2) .. + 31 of gate (w even) or up (w odd);
+// the up wavefronts hand their sums to the gate wavefronts through LDS for the SwiGLU.
+__global__ __launch_bounds__(kGThreads) void gate_up_grouped_kernel(GroupedParams P) {
+    extern __shared__ __align__(16) unsigned char smem[];
+    const GLds g = g_lds(smem);
+    const int n_rb = P.rows / 64;
+    int4 it;
+    if (!g_item(P, n_rb, g, it)) return;
+    const int rb = blockIdx.x % n_rb, e = it.x, n = it.z;
+    const int wave = threadIdx.x / kWave, lane = threadIdx.x % kWave;
+    const int m = wave & 1, row0 = rb * 64 + 32 * (wave >> 1);
+    const uint8_t *w = m ? P.w1 + (size_t) e * P.stride1 : P.w0 + (size_t) e * P.stride0;
+    float acc[2][16];
+    q4k_rows(P, g, n, w, row0, acc);
+    float *ex = reinterpret_cast<float *>(g.xs); // [2 row halves][2 M-tiles][16][64]
+    float *mine = ex + (size_t) (wave >> 1) * 2 * 16 * kWave;
+    if (m == 1) {
+#pragma unroll
+        for (int mt = 0; mt < 2; mt++)
+#pragma unroll
+            for (int r = 0; r < 16; r++) mine[(mt * 16 + r) * kWave + lane] = acc[mt][r];
+    }
+    __syncthreads();
+    if (m == 0) {
+        const int h = lane / 32;
+#pragma unroll
+        for (int mt = 0; mt < 2; mt++) {
+#pragma unroll
+            for (int r = 0; r < 16; r++) {
+                const int pos = mt * 32 + 8 * (r / 4) + 4 * h + (r % 4);
+                if (pos < n) {
+                    const float gs = acc[mt][r], us = mine[(mt * 16 + r) * kWave + lane];
+                    P.out[(size_t) g.pair[pos] * P.rows + row0 + lane % 32] = (gs / (1.0f + expf(-gs))) * us;
+                }
+            }
+        }
+    }
+}
+
+// down: wavefront w computes rows rb * 128 + 32 w .. + 31, times the pair's router weight.
+__global__ __launch_bounds__(kGThreads) void down_grouped_kernel(GroupedParams P) {
+    extern __shared__ __align__(16) unsigned char smem[];
+    const GLds g = g_lds(smem);
+    const int n_rb = P.rows / 128;
+    int4 it;
+    if (!g_item(P, n_rb, g, it)) return;
+    const int rb = blockIdx.x % n_rb, e = it.x, n = it.z;
+    const int wave = threadIdx.x / kWave, lane = threadIdx.x % kWave, h = lane / 32;
+    const int row0 = rb * 128 + 32 * wave;
+    float acc[2][16];
+    q4k_rows(P, g, n, P.w0 + (size_t) e * P.stride0, row0, acc);
+#pragma unroll
+    for (int mt = 0; mt < 2; mt++) {
+#pragma unroll
+        for (int r = 0; r < 16; r++) {
+            const int pos = mt * 32 + 8 * (r / 4) + 4 * h + (r % 4);
+            if (pos < n) {
+                const int p = g.pair[pos];
+                P.out[(size_t) p * P.rows + row0 + lane % 32] = acc[mt][r] * P.weights[p];
+            }
+        }
+    }
+}
+
+__global__ __launch_bounds__(128) void act_quant_kernel(const float *act, int f, int8_t *qs, float *d, int32_t *bs) {
+    const size_t p = blockIdx.x;
+    quantize_row<kTypeQ4_K>(act + p * f, f, qs + p * f, d + p * (f / 32), bs + p * (f / 32));
+}
+
+}  // namespace
+
+bool grouped_supported(int tu, int tg, int td, int h, int f, int n_bins) {
+    return tu == kTypeQ4_K && tg == kTypeQ4_K && td == kTypeQ4_K && h % 256 == 0 && f % 256 == 0 && f % 64 == 0 &&
+           n_bins >= 1 && n_bins <= kGroupedMaxBins;
+}
+
+int grouped_max_items(int np, int n_bins) { return (np + kGroupedChunk - 1) / kGroupedChunk + std::min(n_bins, np); }
+
+hipError_t launch_permute(const PermuteParams &P, hipStream_t st, const LaunchTiming *tm) {
+    if (P.np <= 0) return hipSuccess;
+    if (P.np > kPermMaxPairs || P.n_bins < 1 || P.n_bins > kGroupedMaxBins) return hipErrorInvalidValue;
+    return launch(permute_kernel, dim3(1), dim3(kPermThreads), 0, st, tm, P);
+}
+
+hipError_t launch_gate_up_grouped(const GroupedParams &P, int max_items, hipStream_t st, const LaunchTiming *tm) {
+    if (max_items <= 0) return hipSuccess;
+    return launch(gate_up_grouped_kernel, dim3(max_items * (P.rows / 64)), dim3(kGThreads), kGLdsBytes, st, tm, P);
+}
+
+hipError_t launch_down_grouped(const GroupedParams &P, int max_items, hipStream_t st, const LaunchTiming *tm) {
+    if (max_items <= 0) return hipSuccess;
+    return launch(down_grouped_kernel, dim3(max_items * (P.rows / 128)), dim3(kGThreads), kGLdsBytes, st, tm, P);
+}
+
+hipError_t launch_act_quant(const float *act, int f, int np, const ActBuf &aq, hipStream_t st, const LaunchTiming *tm) {
+    if (np <= 0) return hipSuccess;
+    return launch(act_quant_kernel, dim3(np), dim3(128), 0, st, tm, act, f, aq.qs, aq.d, aq.bs);
+}
+
+}  // namespace lstk

@@ -87,6 +87,38 @@ struct CombineParams {
     int T, k, h;
 };
 
+// Grouping of the (token, slot) pairs by bin in the order of ggml's CPU mul_mat_id (bins ascending,
+// pairs of a bin in token-major order), and the chunk work list of the grouped expert kernels.
+struct PermuteParams {
+    const int32_t *bins; // [np] bin of pair t * k + j (expert id or pool slot)
+    int np, n_bins;
+    int chunk;        // pairs per work item
+    int32_t *counts;  // [n_bins]
+    int32_t *offsets; // [n_bins + 1] exclusive scan of counts
+    int32_t *perm;    // [np] sorted position -> pair index
+    int4 *items;      // [max_items] {bin, first position, pairs, 0}: full chunks first; may be null
+    int32_t *n_items; // may be null
+    int32_t *err;
+};
+
+// One grouped expert product over the work list: Q4_K weight rows x Q8_K activation rows on MFMA.
+// gate_up: w0 = gate, w1 = up, activation row of a pair = its token (pair / k), out = SwiGLU rows
+// [np][rows]. down: w0 = down, activation row = the pair, out = weighted rows [np][rows].
+struct GroupedParams {
+    const int4 *items;
+    const int32_t *n_items;
+    const int32_t *perm;
+    int k;
+    const uint8_t *w0, *w1;
+    size_t stride0, stride1; // bytes per slot
+    int rows, K;             // weight matrix rows x K (= cols)
+    const int8_t *xqs;       // activation rows [*][K] int8
+    const float *xd;         // [*][K / 32], the Q8_K scale of each super-block repeated 8 times
+    int row_div;             // activation row = pair / row_div
+    const float *weights;    // down: router weight of each pair
+    float *out;
+};
+
 // Checks the shapes the kernels assume; returns an empty string when they hold.
 const char *check_shapes(int h, int f, int E, int k, int n_bins, int n_batch);
 // Largest n_tokens for which gate_up computes the top-k itself.
@@ -96,5 +128,18 @@ hipError_t launch_topk(const TopkParams &p, hipStream_t s, const LaunchTiming *t
 hipError_t launch_gate_up(const GateUpParams &p, hipStream_t s, const LaunchTiming *t);
 hipError_t launch_down(const DownParams &p, hipStream_t s, const LaunchTiming *t);
 hipError_t launch_combine(const CombineParams &p, hipStream_t s, const LaunchTiming *t);
+
+// grouped (prefill) path, grouped.hip
+constexpr int kGroupedChunk = 64;        // pairs per work item
+constexpr int kGroupedMaxBins = 1024;    // bins the permutation kernel handles
+// True when the grouped MFMA kernels handle this layer: Q4_K gate, up and down, f % 64 == 0,
+// n_bins <= kGroupedMaxBins.
+bool grouped_supported(int tu, int tg, int td, int h, int f, int n_bins);
+// Upper bound on the work items of np pairs over n_bins bins.
+int grouped_max_items(int np, int n_bins);
+hipError_t launch_permute(const PermuteParams &p, hipStream_t s, const LaunchTiming *t);
+hipError_t launch_gate_up_grouped(const GroupedParams &p, int max_items, hipStream_t s, const LaunchTiming *t);
+hipError_t launch_act_quant(const float *act, int f, int np, const ActBuf &aq, hipStream_t s, const LaunchTiming *t);
+hipError_t launch_down_grouped(const GroupedParams &p, int max_items, hipStream_t s, const LaunchTiming *t);
 
 }  // namespace lstk

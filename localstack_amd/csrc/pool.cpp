@@ -18,6 +18,7 @@
 #include <array>
 #include <chrono>
 #include <cstdio>
+#include <cstdlib>
 #include <cstring>
 #include <map>
 #include <string>
@@ -127,6 +128,11 @@ struct lstk_pool {
     float *logits = nullptr, *act = nullptr, *Y = nullptr;
     int32_t *err = nullptr;
     int n_bins_max = 0;
+    // grouped (prefill) path: permutation, work list, Q8_K SwiGLU rows
+    int32_t *counts = nullptr, *offsets = nullptr, *perm = nullptr, *n_items = nullptr;
+    int4 *items = nullptr;
+    lstk::ActBuf aq{};
+    int grouped_min_tokens = 0;
     // timing
     bool timing = false;
     std::vector<TimedLaunch> launched[kStages];
@@ -152,7 +158,11 @@ int alloc_scratch(lstk_pool *P) {
     const size_t o_logits = take(T * E * 4);
     const size_t o_act = take(T * k * f * 4), o_Y = take(T * k * h * 4);
     const size_t o_err = take(64);
-    (void) nb;
+    const size_t np = T * k;
+    const size_t max_items = (size_t) lstk::grouped_max_items((int) np, (int) nb);
+    const size_t o_counts = take(nb * 4), o_offsets = take((nb + 1) * 4), o_perm = take(np * 4), o_nitems = take(64);
+    const size_t o_items = take(max_items * 16);
+    const size_t o_aqs = take(np * f), o_ad = take(np * (f / 32) * 4), o_abs = take(np * (f / 32) * 4);
     hipError_t e = hipMalloc(&P->scratch, off);
     if (e != hipSuccess) return hip_fail(e, "hipMalloc(scratch)");
     e = hipMemset(P->scratch, 0, off);
@@ -165,6 +175,14 @@ int alloc_scratch(lstk_pool *P) {
     P->act = reinterpret_cast<float *>(b + o_act);
     P->Y = reinterpret_cast<float *>(b + o_Y);
     P->err = reinterpret_cast<int32_t *>(b + o_err);
+    P->counts = reinterpret_cast<int32_t *>(b + o_counts);
+    P->offsets = reinterpret_cast<int32_t *>(b + o_offsets);
+    P->perm = reinterpret_cast<int32_t *>(b + o_perm);
+    P->n_items = reinterpret_cast<int32_t *>(b + o_nitems);
+    P->items = reinterpret_cast<int4 *>(b + o_items);
+    P->aq.qs = reinterpret_cast<int8_t *>(b + o_aqs);
+    P->aq.d = reinterpret_cast<float *>(b + o_ad);
+    P->aq.bs = reinterpret_cast<int32_t *>(b + o_abs);
     return LSTK_OK;
 }
 
@@ -533,6 +551,67 @@ int check_call(lstk_pool *P, int layer, int T) {
     return LSTK_OK;
 }
 
+// The grouped MFMA path serves calls with many tokens per expert (prefill): Q4_K gate, up and down,
+// at least grouped_min_tokens tokens (LSTK_GROUPED_MIN_TOKENS overrides the default of 64).
+bool use_grouped(lstk_pool *P, const Shard &s, int T) {
+    if (P->grouped_min_tokens == 0) {
+        const char *env = std::getenv("LSTK_GROUPED_MIN_TOKENS");
+        P->grouped_min_tokens = env ? std::max(1, std::atoi(env)) : 64;
+    }
+    return T >= P->grouped_min_tokens &&
+           lstk::grouped_supported(s.tu, s.tg, s.td, P->dims.n_embd, P->dims.n_ff_exp, (int) s.n_slots);
+}
+
+// permute -> gate_up (MFMA, SwiGLU) -> Q8_K of the SwiGLU rows -> down (MFMA, router weight) ->
+// combine + residual. bins: expert ids (resident) or slots (streaming), [T][k].
+int run_grouped(lstk_pool *P, const Shard &s, const int32_t *bins, const float *d_weights, const float *d_resid,
+                float *d_out, int T, hipStream_t st) {
+    const lstk_moe_dims &d = P->dims;
+    const int k = d.n_expert_used, np = T * k, h = d.n_embd, f = d.n_ff_exp;
+    const int max_items = lstk::grouped_max_items(np, (int) s.n_slots);
+    lstk::PermuteParams pp{bins, np, (int) s.n_slots, lstk::kGroupedChunk, P->counts, P->offsets, P->perm,
+                           P->items, P->n_items, P->err};
+    hipError_t e = timed(P, 0, [&](const lstk::LaunchTiming *tm) { return lstk::launch_permute(pp, st, tm); });
+    if (e != hipSuccess) return hip_fail(e, "permute launch");
+    lstk::GroupedParams gu{};
+    gu.items = P->items;
+    gu.n_items = P->n_items;
+    gu.perm = P->perm;
+    gu.k = k;
+    gu.w0 = s.d_gate;
+    gu.w1 = s.d_up;
+    gu.stride0 = s.gate_bytes;
+    gu.stride1 = s.up_bytes;
+    gu.rows = f;
+    gu.K = h;
+    gu.xqs = P->xq.qs;
+    gu.xd = P->xq.d;
+    gu.row_div = k;
+    gu.out = P->act;
+    e = timed(P, 1, [&](const lstk::LaunchTiming *tm) { return lstk::launch_gate_up_grouped(gu, max_items, st, tm); });
+    if (e != hipSuccess) return hip_fail(e, "gate_up launch");
+    e = timed(P, 2, [&](const lstk::LaunchTiming *tm) { return lstk::launch_act_quant(P->act, f, np, P->aq, st, tm); });
+    if (e != hipSuccess) return hip_fail(e, "act quant launch");
+    lstk::GroupedParams dn = gu;
+    dn.w0 = s.d_down;
+    dn.w1 = nullptr;
+    dn.stride0 = s.down_bytes;
+    dn.stride1 = 0;
+    dn.rows = h;
+    dn.K = f;
+    dn.xqs = P->aq.qs;
+    dn.xd = P->aq.d;
+    dn.row_div = 1;
+    dn.weights = d_weights;
+    dn.out = P->Y;
+    e = timed(P, 2, [&](const lstk::LaunchTiming *tm) { return lstk::launch_down_grouped(dn, max_items, st, tm); });
+    if (e != hipSuccess) return hip_fail(e, "down launch");
+    lstk::CombineParams cp{P->Y, d_resid, d_out, T, k, h};
+    e = timed(P, 3, [&](const lstk::LaunchTiming *tm) { return lstk::launch_combine(cp, st, tm); });
+    if (e != hipSuccess) return hip_fail(e, "combine launch");
+    return LSTK_OK;
+}
+
 // Router (optional) + experts + combine of one layer. mode 0: ffn with caller slots / weights;
 // mode 1: resident block, routing from gate_inp, ids / weights written to d_ids / d_weights.
 int run_block(lstk_pool *P, int layer, int mode, const float *d_hnorm, const void *d_gate_inp, int gate_type,
@@ -560,6 +639,8 @@ int run_block(lstk_pool *P, int layer, int mode, const float *d_hnorm, const voi
         e = timed(P, 0, [&](const lstk::LaunchTiming *tm) { return lstk::launch_topk(tp, st, tm); });
         if (e != hipSuccess) return hip_fail(e, "topk launch");
     }
+    if (use_grouped(P, s, T))
+        return run_grouped(P, s, mode == 1 ? d_ids : d_slots, d_weights, d_resid, d_out, T, st);
     lstk::GroupParams gp{};
     gp.T = T;
     gp.k = k;
@@ -738,6 +819,21 @@ int lstk_moe_block(lstk_pool *pool, int layer, const float *d_hnorm, const void 
     if (!d_ids || !d_weights) return fail(LSTK_E_INVALID, "ids and weights must be non-null");
     return run_block(pool, layer, 1, d_hnorm, d_gate_inp, gate_type, nullptr, d_ids, d_weights, d_resid, d_out, n_tokens,
                      static_cast<hipStream_t>(stream));
+}
+
+int lstk_moe_permute(lstk_pool *pool, const int32_t *d_bins, int n_tokens, int n_bins, int32_t *d_counts,
+                     int32_t *d_offsets, int32_t *d_perm, lstk_stream_t stream) {
+    int rc;
+    if ((rc = check_call(pool, 0, n_tokens)) != LSTK_OK) return rc;
+    if (n_bins < 1 || n_bins > lstk::kGroupedMaxBins)
+        return fail(LSTK_E_INVALID, "n_bins must be in [1, " + std::to_string(lstk::kGroupedMaxBins) + "]");
+    if (n_tokens == 0) return LSTK_OK;
+    if (!d_bins || !d_counts || !d_offsets || !d_perm) return fail(LSTK_E_INVALID, "null argument");
+    lstk::PermuteParams pp{d_bins, n_tokens * pool->dims.n_expert_used, n_bins, lstk::kGroupedChunk, d_counts, d_offsets,
+                           d_perm, nullptr, nullptr, pool->err};
+    const hipError_t e =
+        timed(pool, 0, [&](const lstk::LaunchTiming *tm) { return lstk::launch_permute(pp, static_cast<hipStream_t>(stream), tm); });
+    return e == hipSuccess ? LSTK_OK : hip_fail(e, "permute launch");
 }
 
 int lstk_pool_check(lstk_pool *pool, lstk_stream_t stream) {

@@ -80,6 +80,8 @@ def test_dry_pool_refuses_compute(lstk):
         p.ffn(0, 16, 16, 16, 16, 16, n_tokens=1, stream=0)
     with pytest.raises(lstk.LstkError, match="dry pool"):
         p.block(0, 16, 16, 1, 16, 16, 16, 16, n_tokens=1, stream=0)
+    with pytest.raises(lstk.LstkError, match="dry pool"):
+        p.permute(16, 8, 16, 16, 16, n_tokens=1, stream=0)
 
 
 def test_missing_library_fails_loudly(tmp_path, monkeypatch):
