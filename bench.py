@@ -55,6 +55,10 @@ def parse():
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-prefill", action="store_true")
     ap.add_argument("--prefill-layers", type=int, default=8)
+    ap.add_argument("--no-decode", action="store_true", help="skip the decode legs (profiling the prefill leg alone)")
+    ap.add_argument("--calibrate-copy-mib", type=int, default=0,
+                    help="first run one device-to-device copy of this many MiB (the reference kernel that scales "
+                         "rocprofv3's FETCH_SIZE / WRITE_SIZE counters to bytes)")
     return ap.parse_args()
 
 
@@ -249,6 +253,18 @@ def main():
     import torch
     import localstack_amd as L
     L.lib()
+    if a.calibrate_copy_mib:
+        n = a.calibrate_copy_mib << 18
+        src = torch.ones(n, dtype=torch.float32, device="cuda:0")
+        dst = torch.empty_like(src)
+        dst.copy_(src)
+        torch.cuda.synchronize()
+        log(f"[bench] calibration copy: {a.calibrate_copy_mib} MiB read, {a.calibrate_copy_mib} MiB written")
+        del src, dst
+    if a.no_decode:
+        pre = prefill_leg(torch, L, a.prefill_layers, 512, max(5, a.steps // 5), 2)
+        print(json.dumps({"prefill": pre}), flush=True)
+        return
     st = Stack(torch, L, a.layers, t_max=max(8, a.tokens))
     main_res, g = measure(torch, st, a.tokens, a.steps, a.warmup, not a.no_graph)
     del g

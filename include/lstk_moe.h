@@ -135,7 +135,9 @@ int lstk_moe_ffn(lstk_pool *pool, int layer, const float *d_hnorm, const int32_t
                  const float *d_resid, float *d_out, int n_tokens, lstk_stream_t stream);
 
 /* The whole MoE block of a resident layer in one call (router + experts + residual) with no host
- * round trip: up to 16 tokens the gate/up kernel runs the top-k itself from the router logits.
+ * round trip: for a single token the gate/up kernel runs the top-k itself from the router logits.
+ * With LSTK_FUSED_DECODE=1 in the environment at pool creation, single-token calls of this and of
+ * lstk_moe_ffn run as one fused launch instead (same results bit for bit).
  * d_ids / d_weights receive the routing (for traces, src/engine.cpp:301-316); they may not be NULL.
  * Valid for resident pools only. */
 int lstk_moe_block(lstk_pool *pool, int layer, const float *d_hnorm, const void *d_gate_inp, int gate_type,

@@ -12,7 +12,7 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 ROOT = os.path.dirname(HERE)
 CSRC = os.path.join(HERE, "csrc")
 LIB = os.path.join(HERE, "liblstk_moe.so")
-SOURCES = ["kernels.hip", "grouped.hip", "pool.cpp", "repack.cpp"]
+SOURCES = ["kernels.hip", "grouped.hip", "fused.hip", "pool.cpp", "repack.cpp"]
 ARCH = os.environ.get("LSTK_OFFLOAD_ARCH", "gfx950")
 
 
@@ -29,6 +29,9 @@ def build(verbose=False):
     cmd = [hipcc(), "-x", "hip", f"--offload-arch={ARCH}", "-O3", "-std=c++20", "-fPIC", "-shared",
            # packed-FP32 instructions off for all device code
            "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+           # every multiply and add rounded on its own, as written: the fused and multi-kernel paths
+           # then agree bit for bit whatever the compiler would otherwise contract in each context
+           "-ffp-contract=off",
            "-Wall", "-Wno-unused-function", "-I", os.path.join(ROOT, "include"),
            "-o", tmp] + [os.path.join(CSRC, s) for s in SOURCES] + ["-lpthread"]
     if verbose:

@@ -119,6 +119,38 @@ struct GroupedParams {
     float *out;
 };
 
+// The whole MoE block of one token in one launch (fused.hip). Work-groups [0, nB) each compute one
+// gate/up unit (pair j = w / ub, row block w % ub); the first nA of them first compute the router
+// logits. Work-groups [nB, nB + nC) each compute rd rows of down + weight + combine + residual.
+// Stages hand over through device-coherent stores and per-work-group flags holding the launch number.
+struct FusedParams {
+    const float *hnorm;
+    const void *gate_inp;
+    int route;                // 1: router in the kernel; 0: ids_in / weights_in
+    const int32_t *ids_in;    // [k] slots
+    const float *weights_in;  // [k]
+    int32_t *ids_out;         // route: written by work-group 0
+    float *weights_out;
+    int h, f, E, k, n_bins;
+    const uint8_t *w_gate, *w_up, *w_down;
+    size_t s_gate, s_up, s_down;
+    const float *resid;
+    float *out;
+    float *logits; // [E]
+    float *act;    // [k][f]
+    int *cnt;      // [nB + nC] launches seen by each work-group
+    int *flag_a;   // [nA]
+    int *flag_b;   // [nB]
+    int32_t *err;
+    int nA, nB, nC, ub, rd;
+    int spin_max;
+};
+
+struct FusedLayout {
+    int nA = 0, nB = 0, nC = 0, ub = 0, rd = 0;
+    bool ok = false;
+};
+
 // Checks the shapes the kernels assume; returns an empty string when they hold.
 const char *check_shapes(int h, int f, int E, int k, int n_bins, int n_batch);
 // Largest n_tokens for which gate_up computes the top-k itself.
@@ -141,5 +173,12 @@ hipError_t launch_permute(const PermuteParams &p, hipStream_t s, const LaunchTim
 hipError_t launch_gate_up_grouped(const GroupedParams &p, int max_items, hipStream_t s, const LaunchTiming *t);
 hipError_t launch_act_quant(const float *act, int f, int np, const ActBuf &aq, hipStream_t s, const LaunchTiming *t);
 hipError_t launch_down_grouped(const GroupedParams &p, int max_items, hipStream_t s, const LaunchTiming *t);
+
+// fused single-token path, fused.hip
+FusedLayout fused_layout(int h, int f, int E, int k);
+// True when every work-group of the fused launch for these types fits on the device at once (the
+// stages wait on each other, so they must all be resident).
+bool fused_fits(const FusedLayout &L, int gate_type, int tg, int td, int h, int f, int k);
+hipError_t launch_fused(const FusedParams &p, int gate_type, int tg, int td, hipStream_t s, const LaunchTiming *t);
 
 }  // namespace lstk

@@ -30,15 +30,11 @@
 namespace lstk {
 namespace {
 
-constexpr int kBlock = 256;
 constexpr int kRouteEPW = 2;      // experts per wavefront in the router tile
 constexpr int kRouteEG = 8;       // experts per router work-group (4 wavefronts x 2)
 constexpr int kRouteMaxNG = 16;   // n_embd <= 4096: 16 groups of 256 per lane
-constexpr int kMaxEPL = 4;        // n_expert <= 256: 4 logits per lane in the top-k
 constexpr int kDnRows = 64;       // rows per down work-group
 constexpr int kTC = 8;            // tokens staged per pass
-constexpr int kMaxG = 8;          // K-groups per work-group
-constexpr int kMaxK = 64;         // n_expert_used <= 64 (one lane per selected expert)
 constexpr int kMaxBins = 4096;
 constexpr int kMaxPairs = 8192;   // n_batch * n_expert_used
 typedef int xvec __attribute__((ext_vector_type(4))); // 16 bytes of int8 activations
@@ -125,226 +121,6 @@ __device__ __forceinline__ void route_tile(const RouteParams &P, int b, float *x
             if (lane == 0 && e < P.E) P.logits[(size_t) (t0 + t) * P.E + e] = sum;
         }
     }
-}
-
-// ------------------------------------------------------------------------------------------------
-// softmax / top-k / renormalisation (router(), src/qwen3.cpp:179-189)
-// ------------------------------------------------------------------------------------------------
-
-// Barrier among the wavefronts cooperating on one token: the whole block, or one wavefront (whose
-// lanes already run in lock step; only its LDS traffic has to land).
-__device__ __forceinline__ void group_barrier(int nsplit) {
-    if (nsplit > 1) __syncthreads();
-    else asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-}
-
-// Order key of a logit: monotone in the value (-0 and +0 equal), ties broken towards the lower
-// expert id, unique per expert.
-__device__ __forceinline__ unsigned long long order_key(float v, int e) {
-    unsigned u = __float_as_uint(v);
-    if (v == 0.0f) u = 0u;
-    u = (u & 0x80000000u) ? ~u : (u | 0x80000000u);
-    return ((unsigned long long) u << 8) | (unsigned) (255 - e);
-}
-
-// One token's softmax / top-k / renormalisation, everything in parallel. The rank of an expert is
-// the number of experts with a larger logit, or an equal logit and a lower id, so the selection is
-// largest first with ties to the lower expert id, as the oracle's sequential argmax. Ranks are
-// counted with f32 compares against the row broadcast from LDS, split over `nsplit` wavefronts
-// (partial counts summed in LDS); exact ties are rare and take a second, 64-bit-key pass.
-// p = expf(l - max) * (float)(1 / sum) with the sum in double; the k selected p are summed in rank
-// order in double, clamped to >= 2^-14 and divided out. The expert of rank j is written to ids[j],
-// its weight to weights[j].
-// Called by the `nsplit` wavefronts [w0, w0 + nsplit) of the block with part = wave - w0.
-// s_l: >= E floats, s_rank: >= nsplit * 64 * EPL ints, s_p: >= k floats, all LDS shared by the group.
-template <int EPL>
-__device__ __forceinline__ bool rank_token(const float *__restrict__ l_row, int E, int k, int part, int nsplit, float *s_l,
-                                           int *s_rank, float (&l)[EPL], bool (&valid)[EPL], int (&rank)[EPL]) {
-    const int lane = threadIdx.x % kWave;
-#pragma unroll
-    for (int i = 0; i < EPL; i++) {
-        const int e = lane + kWave * i;
-        valid[i] = e < E;
-        l[i] = l_row[min(e, E - 1)]; // unconditional: all loads in flight together
-    }
-#pragma unroll
-    for (int i = 0; i < EPL; i++)
-        if (!valid[i]) l[i] = -INFINITY;
-    if (part == 0) {
-        // the row, padded with -inf to 4 * 64 entries so the rank loop needs no remainder
-#pragma unroll
-        for (int i = 0; i < kMaxEPL; i++) s_l[lane + kWave * i] = i < EPL ? l[i] : -INFINITY;
-    }
-    group_barrier(nsplit);
-    // partial ranks over this wavefront's share of the row, 32 values per batch of LDS reads
-    const int per = (((E + nsplit - 1) / nsplit) + 31) & ~31;
-    const int a0 = part * per, a1 = min(((E + 31) & ~31), a0 + per);
-    int r[EPL];
-#pragma unroll
-    for (int i = 0; i < EPL; i++) r[i] = 0;
-    for (int e2 = a0; e2 < a1; e2 += 32) {
-        float4 v[8];
-#pragma unroll
-        for (int u = 0; u < 8; u++) v[u] = *reinterpret_cast<const float4 *>(s_l + e2 + 4 * u);
-#pragma unroll
-        for (int u = 0; u < 8; u++) {
-#pragma unroll
-            for (int i = 0; i < EPL; i++)
-                r[i] += (v[u].x > l[i]) + (v[u].y > l[i]) + (v[u].z > l[i]) + (v[u].w > l[i]);
-        }
-    }
-#pragma unroll
-    for (int i = 0; i < EPL; i++) s_rank[(part * EPL + i) * kWave + lane] = r[i];
-    group_barrier(nsplit);
-    if (part != 0) return false;
-#pragma unroll
-    for (int i = 0; i < EPL; i++) {
-        rank[i] = 0;
-        for (int q = 0; q < nsplit; q++) rank[i] += s_rank[(q * EPL + i) * kWave + lane];
-    }
-    // exact ties: an expert with an equal logit and a lower id ranks first
-    bool tie = false;
-#pragma unroll
-    for (int i = 0; i < EPL; i++) tie |= valid[i] && rank[i] < k;
-    {
-        unsigned long long seen = 0ull; // bit r set once some selected expert has rank r
-        // ranks are distinct exactly when there is no tie among the experts that reach rank < k
-        unsigned long long mine = 0ull;
-#pragma unroll
-        for (int i = 0; i < EPL; i++)
-            if (valid[i] && rank[i] < k) mine |= 1ull << rank[i];
-        int cnt = 0;
-#pragma unroll
-        for (int i = 0; i < EPL; i++) cnt += __popcll(__ballot(valid[i] && rank[i] < k));
-        // OR of every lane's bits via DPP and readlane
-        unsigned lo = (unsigned) mine, hi = (unsigned) (mine >> 32);
-        lo |= __builtin_amdgcn_update_dpp(0, (int) lo, 0xB1, 0xF, 0xF, false);
-        hi |= __builtin_amdgcn_update_dpp(0, (int) hi, 0xB1, 0xF, 0xF, false);
-        lo |= __builtin_amdgcn_update_dpp(0, (int) lo, 0x4E, 0xF, 0xF, false);
-        hi |= __builtin_amdgcn_update_dpp(0, (int) hi, 0x4E, 0xF, 0xF, false);
-        lo |= __builtin_amdgcn_update_dpp(0, (int) lo, 0x141, 0xF, 0xF, false);
-        hi |= __builtin_amdgcn_update_dpp(0, (int) hi, 0x141, 0xF, 0xF, false);
-        lo |= __builtin_amdgcn_update_dpp(0, (int) lo, 0x140, 0xF, 0xF, false);
-        hi |= __builtin_amdgcn_update_dpp(0, (int) hi, 0x140, 0xF, 0xF, false);
-        lo = (unsigned) __builtin_amdgcn_readlane((int) lo, 0) | (unsigned) __builtin_amdgcn_readlane((int) lo, 16) |
-             (unsigned) __builtin_amdgcn_readlane((int) lo, 32) | (unsigned) __builtin_amdgcn_readlane((int) lo, 48);
-        hi = (unsigned) __builtin_amdgcn_readlane((int) hi, 0) | (unsigned) __builtin_amdgcn_readlane((int) hi, 16) |
-             (unsigned) __builtin_amdgcn_readlane((int) hi, 32) | (unsigned) __builtin_amdgcn_readlane((int) hi, 48);
-        seen = ((unsigned long long) hi << 32) | lo;
-        const unsigned long long want = k >= 64 ? ~0ull : ((1ull << k) - 1ull);
-        tie = !(cnt == k && seen == want);
-    }
-    if (tie) {
-        // rare: recount with the id tie-break over the whole row
-#pragma unroll
-        for (int i = 0; i < EPL; i++) rank[i] = 0;
-        for (int e2 = 0; e2 < E; e2 += 4) {
-            const float4 v = *reinterpret_cast<const float4 *>(s_l + e2);
-            const float vv[4] = {v.x, v.y, v.z, v.w};
-#pragma unroll
-            for (int u = 0; u < 4; u++) {
-#pragma unroll
-                for (int i = 0; i < EPL; i++) {
-                    const int e = lane + kWave * i;
-                    rank[i] += (vv[u] > l[i]) || (vv[u] == l[i] && e2 + u < e);
-                }
-            }
-        }
-    }
-    return true;
-}
-
-// Softmax, renormalisation and output of one token whose ranks rank_token found (part 0 only).
-template <int EPL>
-__device__ __forceinline__ void weights_token(int k, const float (&l)[EPL], const bool (&valid)[EPL], const int (&rank)[EPL],
-                                              float *s_p, int16_t *ids16, int32_t *ids32, float *weights, int32_t *ids32_b,
-                                              float *weights_b) {
-    const int lane = threadIdx.x % kWave;
-    // softmax over the row
-    float m = -INFINITY;
-#pragma unroll
-    for (int i = 0; i < EPL; i++) m = fmaxf(m, l[i]);
-    m = wave_max(m);
-    float p[EPL];
-    double s = 0.0;
-#pragma unroll
-    for (int i = 0; i < EPL; i++) {
-        p[i] = valid[i] ? expf(l[i] - m) : 0.0f;
-        s += (double) p[i];
-    }
-    const float inv = (float) (1.0 / wave_sum_d(s));
-#pragma unroll
-    for (int i = 0; i < EPL; i++) {
-        p[i] = p[i] * inv;
-        if (valid[i] && rank[i] < k) s_p[rank[i]] = p[i];
-    }
-    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-    double ss = 0.0;
-    for (int j = 0; j < k; j++) ss += (double) s_p[j];
-    const float sf = fmaxf((float) ss, 6.103515625e-5f);
-#pragma unroll
-    for (int i = 0; i < EPL; i++) {
-        if (valid[i] && rank[i] < k) {
-            const int e = lane + kWave * i;
-            const float w = __fdiv_rn(p[i], sf);
-            if (ids16) ids16[rank[i]] = (int16_t) e;
-            if (ids32) ids32[rank[i]] = e;
-            if (weights) weights[rank[i]] = w;
-            if (ids32_b) ids32_b[rank[i]] = e;
-            if (weights_b) weights_b[rank[i]] = w;
-        }
-    }
-}
-
-
-template <int EPL>
-__device__ __forceinline__ void topk_token(const float *__restrict__ l_row, int E, int k, int part, int nsplit, float *s_l,
-                                           int *s_rank, float *s_p, int16_t *ids16, int32_t *ids32, float *weights,
-                                           int32_t *ids32_b, float *weights_b) {
-    float l[EPL];
-    bool valid[EPL];
-    int rank[EPL];
-    if (rank_token<EPL>(l_row, E, k, part, nsplit, s_l, s_rank, l, valid, rank))
-        weights_token<EPL>(k, l, valid, rank, s_p, ids16, ids32, weights, ids32_b, weights_b);
-}
-
-// Top-k of T tokens by the block's wavefronts: one wavefront per token, or all wavefronts on one
-// token when there are fewer tokens than wavefronts. The block must call this uniformly.
-__device__ __forceinline__ void topk_block(const float *__restrict__ logits, int T, int E, int k, unsigned char *lds, int16_t *ids16,
-                           int32_t *ids32, float *weights, int32_t *ids32_b, float *weights_b) {
-    const int wave = threadIdx.x / kWave, nw = blockDim.x / kWave;
-    const int nsplit = T < nw ? nw : 1;
-    const int epl = (E + kWave - 1) / kWave;
-    // one row per wavefront (or one shared row when they split a token); the rank partials of all
-    // wavefronts: nw * kMaxEPL * 64 ints in either mode
-    float *s_l = reinterpret_cast<float *>(lds);                             // [nw][256]
-    int *s_rank = reinterpret_cast<int *>(lds + (size_t) nw * 256 * 4);       // [nw * kMaxEPL * 64]
-    float *s_p = reinterpret_cast<float *>(s_rank + (size_t) nw * kMaxEPL * kWave); // [nw][kMaxK]
-    for (int t0 = 0; t0 < T; t0 += (nsplit > 1 ? 1 : nw)) {
-        const int t = nsplit > 1 ? t0 : t0 + wave;
-        const int part = nsplit > 1 ? wave : 0;
-        const int slot = nsplit > 1 ? 0 : wave; // LDS set of this token's group
-        if (t < T) {
-            const size_t o = (size_t) t * k;
-            float *sl = s_l + slot * 256;
-            int *sr = s_rank + (size_t) slot * kMaxEPL * kWave;
-            float *sp = s_p + slot * kMaxK;
-            const float *lr = logits + (size_t) t * E;
-            int16_t *a = ids16 ? ids16 + o : nullptr;
-            int32_t *b = ids32 ? ids32 + o : nullptr;
-            float *c = weights ? weights + o : nullptr;
-            int32_t *d = ids32_b ? ids32_b + o : nullptr;
-            float *f = weights_b ? weights_b + o : nullptr;
-            if (epl == 1) topk_token<1>(lr, E, k, part, nsplit, sl, sr, sp, a, b, c, d, f);
-            else if (epl == 2) topk_token<2>(lr, E, k, part, nsplit, sl, sr, sp, a, b, c, d, f);
-            else topk_token<4>(lr, E, k, part, nsplit, sl, sr, sp, a, b, c, d, f);
-        }
-        if (nsplit > 1) __syncthreads();
-    }
-}
-
-__device__ __host__ inline size_t topk_lds_bytes(int nw) {
-    return (size_t) nw * 256 * 4 + (size_t) nw * kMaxEPL * kWave * 4 + (size_t) nw * kMaxK * 4;
 }
 
 template <int GT, int NG>
@@ -530,102 +306,6 @@ __device__ __forceinline__ bool group_pairs(const GroupParams &P, GroupLds g) {
     }
     __syncthreads();
     return g.misc[0] >= 0;
-}
-
-// ------------------------------------------------------------------------------------------------
-// super-block dot products (ggml_vec_dot_q8_0_q8_0 / ggml_vec_dot_q4_K_q8_K)
-// ------------------------------------------------------------------------------------------------
-
-template <int I>
-__device__ __forceinline__ unsigned dword_of(const uint4 &v) {
-    return I == 0 ? v.x : I == 1 ? v.y : I == 2 ? v.z : v.w;
-}
-
-// Q8_0: 8 blocks of 32; per block an exact int32 sum, then acc += sumi * (d_w * d_x).
-__device__ __forceinline__ float dot_sb_q8_0(const uint4 (&w)[kChunksQ8_0], const int8_t *x, const float *xd,
-                                             float acc) {
-#pragma unroll
-    for (int blk = 0; blk < 8; blk++) {
-        const uint4 q0 = w[1 + 2 * blk], q1 = w[2 + 2 * blk];
-        const int4 x0 = *reinterpret_cast<const int4 *>(x + 32 * blk);
-        const int4 x1 = *reinterpret_cast<const int4 *>(x + 32 * blk + 16);
-        int s = 0;
-        s = __builtin_amdgcn_sdot4((int) q0.x, x0.x, s, false);
-        s = __builtin_amdgcn_sdot4((int) q0.y, x0.y, s, false);
-        s = __builtin_amdgcn_sdot4((int) q0.z, x0.z, s, false);
-        s = __builtin_amdgcn_sdot4((int) q0.w, x0.w, s, false);
-        s = __builtin_amdgcn_sdot4((int) q1.x, x1.x, s, false);
-        s = __builtin_amdgcn_sdot4((int) q1.y, x1.y, s, false);
-        s = __builtin_amdgcn_sdot4((int) q1.z, x1.z, s, false);
-        s = __builtin_amdgcn_sdot4((int) q1.w, x1.w, s, false);
-        const unsigned dw2 = blk < 2 ? w[0].x : blk < 4 ? w[0].y : blk < 6 ? w[0].z : w[0].w;
-        const float dw = h2f((blk & 1) ? (dw2 >> 16) : dw2);
-        acc += (float) s * (dw * xd[blk]);
-    }
-    return acc;
-}
-
-
-// Q4_K x Q8_K: isum = sum_j sc_j * dot_j, imin = sum_j m_j * bsum_j;
-// acc += (d_w d_x) isum, then acc -= (dmin_w d_x) imin.
-template <int C>
-__device__ __forceinline__ void q4_chunk(const uint4 &qa, const uint4 &qb, const int8_t *x, int &lo, int &hi) {
-    const int4 xl0 = *reinterpret_cast<const int4 *>(x);
-    const int4 xl1 = *reinterpret_cast<const int4 *>(x + 16);
-    const int4 xh0 = *reinterpret_cast<const int4 *>(x + 32);
-    const int4 xh1 = *reinterpret_cast<const int4 *>(x + 48);
-    const unsigned m4 = 0x0f0f0f0fu;
-    lo = __builtin_amdgcn_sdot4((int) (qa.x & m4), xl0.x, 0, false);
-    lo = __builtin_amdgcn_sdot4((int) (qa.y & m4), xl0.y, lo, false);
-    lo = __builtin_amdgcn_sdot4((int) (qa.z & m4), xl0.z, lo, false);
-    lo = __builtin_amdgcn_sdot4((int) (qa.w & m4), xl0.w, lo, false);
-    lo = __builtin_amdgcn_sdot4((int) (qb.x & m4), xl1.x, lo, false);
-    lo = __builtin_amdgcn_sdot4((int) (qb.y & m4), xl1.y, lo, false);
-    lo = __builtin_amdgcn_sdot4((int) (qb.z & m4), xl1.z, lo, false);
-    lo = __builtin_amdgcn_sdot4((int) (qb.w & m4), xl1.w, lo, false);
-    hi = __builtin_amdgcn_sdot4((int) ((qa.x >> 4) & m4), xh0.x, 0, false);
-    hi = __builtin_amdgcn_sdot4((int) ((qa.y >> 4) & m4), xh0.y, hi, false);
-    hi = __builtin_amdgcn_sdot4((int) ((qa.z >> 4) & m4), xh0.z, hi, false);
-    hi = __builtin_amdgcn_sdot4((int) ((qa.w >> 4) & m4), xh0.w, hi, false);
-    hi = __builtin_amdgcn_sdot4((int) ((qb.x >> 4) & m4), xh1.x, hi, false);
-    hi = __builtin_amdgcn_sdot4((int) ((qb.y >> 4) & m4), xh1.y, hi, false);
-    hi = __builtin_amdgcn_sdot4((int) ((qb.z >> 4) & m4), xh1.z, hi, false);
-    hi = __builtin_amdgcn_sdot4((int) ((qb.w >> 4) & m4), xh1.w, hi, false);
-}
-
-__device__ __forceinline__ float dot_sb_q4_K(const uint4 (&w)[kChunksQ4_K], const int8_t *x, const float *xd,
-                                             const int *xb, float acc) {
-    const float dw = h2f(w[0].x), dmin = h2f(w[0].x >> 16);
-    const unsigned s0 = w[0].y, s1 = w[0].z, s2 = w[0].w;
-    int isum = 0, imin = 0;
-    int lo, hi, sc, m;
-    q4_chunk<0>(w[1], w[2], x, lo, hi);
-    scale_min_k4<0>(s0, s1, s2, sc, m); isum += sc * lo; imin += m * xb[0];
-    scale_min_k4<1>(s0, s1, s2, sc, m); isum += sc * hi; imin += m * xb[1];
-    q4_chunk<1>(w[3], w[4], x + 64, lo, hi);
-    scale_min_k4<2>(s0, s1, s2, sc, m); isum += sc * lo; imin += m * xb[2];
-    scale_min_k4<3>(s0, s1, s2, sc, m); isum += sc * hi; imin += m * xb[3];
-    q4_chunk<2>(w[5], w[6], x + 128, lo, hi);
-    scale_min_k4<4>(s0, s1, s2, sc, m); isum += sc * lo; imin += m * xb[4];
-    scale_min_k4<5>(s0, s1, s2, sc, m); isum += sc * hi; imin += m * xb[5];
-    q4_chunk<3>(w[7], w[8], x + 192, lo, hi);
-    scale_min_k4<6>(s0, s1, s2, sc, m); isum += sc * lo; imin += m * xb[6];
-    scale_min_k4<7>(s0, s1, s2, sc, m); isum += sc * hi; imin += m * xb[7];
-    const float dx = xd[0];
-    acc += (dw * dx) * (float) isum;
-    acc -= (dmin * dx) * (float) imin;
-    return acc;
-}
-
-template <int WT>
-__device__ __forceinline__ float dot_sb(const uint4 (&w)[chunks_of(WT)], const int8_t *x, const float *xd,
-                                        const int *xb, float acc) {
-    if constexpr (WT == kTypeQ8_0) {
-        (void) xb;
-        return dot_sb_q8_0(w, x, xd, acc);
-    } else {
-        return dot_sb_q4_K(w, x, xd, xb, acc);
-    }
 }
 
 // ------------------------------------------------------------------------------------------------
@@ -851,21 +531,6 @@ __global__ __launch_bounds__(kBlock) void combine_kernel(CombineParams P) {
 // host side
 // ------------------------------------------------------------------------------------------------
 
-// Super-blocks per thread S and K-groups G for nsb super-blocks: the smallest S <= 2 dividing nsb
-// with nsb / S <= 8 (S = 3 would need more than 256 VGPRs and spill).
-bool pick_split(int nsb, int *S, int *G) {
-    for (int s = 1; s <= 2; s++) {
-        if (nsb % s == 0 && nsb / s <= kMaxG) {
-            *S = s;
-            *G = nsb / s;
-            return true;
-        }
-    }
-    return false;
-}
-
-// gate_up additionally needs 128 % G == 0 (rows per work-group = 128 / G).
-bool pick_split_gate_up(int nsb, int *S, int *G) { return pick_split(nsb, S, G) && 128 % *G == 0; }
 
 int route_tile_tokens(int h) { return std::max(1, std::min(8, 32768 / (h * 4))); }
 

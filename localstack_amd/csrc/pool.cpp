@@ -133,6 +133,11 @@ struct lstk_pool {
     int4 *items = nullptr;
     lstk::ActBuf aq{};
     int grouped_min_tokens = 0;
+    // fused single-token path: launch counters and stage flags (zero at creation)
+    lstk::FusedLayout fl{};
+    bool fused_enabled = false;
+    int *f_cnt = nullptr, *f_flag_a = nullptr, *f_flag_b = nullptr;
+    std::map<std::array<int, 4>, bool> fused_fit; // (gate type, tg, td, 0) -> all work-groups resident
     // timing
     bool timing = false;
     std::vector<TimedLaunch> launched[kStages];
@@ -163,6 +168,10 @@ int alloc_scratch(lstk_pool *P) {
     const size_t o_counts = take(nb * 4), o_offsets = take((nb + 1) * 4), o_perm = take(np * 4), o_nitems = take(64);
     const size_t o_items = take(max_items * 16);
     const size_t o_aqs = take(np * f), o_ad = take(np * (f / 32) * 4), o_abs = take(np * (f / 32) * 4);
+    P->fl = lstk::fused_layout((int) h, (int) f, (int) E, (int) k);
+    const size_t n_fused = P->fl.ok ? (size_t) (P->fl.nB + P->fl.nC) : 1;
+    const size_t o_fcnt = take(n_fused * 4), o_fa = take((size_t) std::max(P->fl.nA, 1) * 4),
+                 o_fb = take((size_t) std::max(P->fl.nB, 1) * 4);
     hipError_t e = hipMalloc(&P->scratch, off);
     if (e != hipSuccess) return hip_fail(e, "hipMalloc(scratch)");
     e = hipMemset(P->scratch, 0, off);
@@ -183,6 +192,13 @@ int alloc_scratch(lstk_pool *P) {
     P->aq.qs = reinterpret_cast<int8_t *>(b + o_aqs);
     P->aq.d = reinterpret_cast<float *>(b + o_ad);
     P->aq.bs = reinterpret_cast<int32_t *>(b + o_abs);
+    P->f_cnt = reinterpret_cast<int *>(b + o_fcnt);
+    P->f_flag_a = reinterpret_cast<int *>(b + o_fa);
+    P->f_flag_b = reinterpret_cast<int *>(b + o_fb);
+    {
+        const char *env = std::getenv("LSTK_FUSED_DECODE");
+        P->fused_enabled = env && env[0] == '1';
+    }
     return LSTK_OK;
 }
 
@@ -612,6 +628,65 @@ int run_grouped(lstk_pool *P, const Shard &s, const int32_t *bins, const float *
     return LSTK_OK;
 }
 
+// The fused single-token path (one launch per block) is opt-in: LSTK_FUSED_DECODE=1 at pool creation.
+// On MI355X its in-kernel hand-overs (device-coherent polls and reads, about 2 us each) cost more
+// than the kernel boundaries they replace (about 1.6 us in a replayed graph), so the multi-kernel
+// path is the default. It runs when every work-group of its grid fits on the device at once
+// (checked once per type combination).
+bool use_fused(lstk_pool *P, const Shard &s, int gate_type) {
+    if (!P->fused_enabled || !P->fl.ok || s.tu != s.tg) return false;
+    const std::array<int, 4> key{gate_type, s.tg, s.td, 0};
+    auto it = P->fused_fit.find(key);
+    if (it == P->fused_fit.end())
+        it = P->fused_fit
+                 .emplace(key, lstk::fused_fits(P->fl, gate_type, s.tg, s.td, P->dims.n_embd, P->dims.n_ff_exp,
+                                                P->dims.n_expert_used))
+                 .first;
+    return it->second;
+}
+
+int run_fused(lstk_pool *P, const Shard &s, int mode, const float *d_hnorm, const void *d_gate_inp, int gate_type,
+              const int32_t *d_slots, int32_t *d_ids, float *d_weights, const float *d_resid, float *d_out, hipStream_t st) {
+    const lstk_moe_dims &d = P->dims;
+    lstk::FusedParams fp{};
+    fp.hnorm = d_hnorm;
+    fp.gate_inp = d_gate_inp;
+    fp.route = mode == 1;
+    fp.ids_in = d_slots;
+    fp.weights_in = d_weights;
+    fp.ids_out = d_ids;
+    fp.weights_out = d_weights;
+    fp.h = d.n_embd;
+    fp.f = d.n_ff_exp;
+    fp.E = d.n_expert;
+    fp.k = d.n_expert_used;
+    fp.n_bins = (int) s.n_slots;
+    fp.w_gate = s.d_gate;
+    fp.w_up = s.d_up;
+    fp.w_down = s.d_down;
+    fp.s_gate = s.gate_bytes;
+    fp.s_up = s.up_bytes;
+    fp.s_down = s.down_bytes;
+    fp.resid = d_resid;
+    fp.out = d_out;
+    fp.logits = P->logits;
+    fp.act = P->act;
+    fp.cnt = P->f_cnt;
+    fp.flag_a = P->f_flag_a;
+    fp.flag_b = P->f_flag_b;
+    fp.err = P->err;
+    fp.nA = P->fl.nA;
+    fp.nB = P->fl.nB;
+    fp.nC = P->fl.nC;
+    fp.ub = P->fl.ub;
+    fp.rd = P->fl.rd;
+    fp.spin_max = 200000;
+    const hipError_t e = timed(P, 1, [&](const lstk::LaunchTiming *tm) {
+        return lstk::launch_fused(fp, mode == 1 ? gate_type : lstk::kTypeF16, s.tg, s.td, st, tm);
+    });
+    return e == hipSuccess ? LSTK_OK : hip_fail(e, "fused launch");
+}
+
 // Router (optional) + experts + combine of one layer. mode 0: ffn with caller slots / weights;
 // mode 1: resident block, routing from gate_inp, ids / weights written to d_ids / d_weights.
 int run_block(lstk_pool *P, int layer, int mode, const float *d_hnorm, const void *d_gate_inp, int gate_type,
@@ -620,6 +695,8 @@ int run_block(lstk_pool *P, int layer, int mode, const float *d_hnorm, const voi
     const lstk_moe_dims &d = P->dims;
     const Shard &s = P->shards[P->layer_shard[layer]];
     const int k = d.n_expert_used;
+    if (T == 1 && use_fused(P, s, mode == 1 ? gate_type : lstk::kTypeF16))
+        return run_fused(P, s, mode, d_hnorm, d_gate_inp, gate_type, d_slots, d_ids, d_weights, d_resid, d_out, st);
     lstk::RouteParams rp{};
     rp.hnorm = d_hnorm;
     rp.T = T;
@@ -849,6 +926,7 @@ int lstk_pool_check(lstk_pool *pool, lstk_stream_t stream) {
         std::string msg = "a kernel saw";
         if (flag & 1) msg += " an expert/slot id out of range (clamped)";
         if (flag & 2) msg += std::string(flag & 1 ? " and" : "") + " an expert repeated within one token";
+        if (flag & 4) msg += std::string(flag & 3 ? " and" : "") + " a fused stage that timed out waiting for another work-group";
         return fail(LSTK_E_BADID, msg);
     }
     return LSTK_OK;
