@@ -7,6 +7,7 @@ import os
 import shutil
 import subprocess
 import sys
+import tempfile
 
 HERE = os.path.dirname(os.path.abspath(__file__))
 ROOT = os.path.dirname(HERE)
@@ -23,17 +24,19 @@ def hipcc():
     raise RuntimeError("hipcc not found")
 
 
-def build(verbose=False):
-    """Compiles every source for gfx950 and links the shared library; always rebuilds."""
-    tmp = LIB + ".tmp"
-    cmd = [hipcc(), "-x", "hip", f"--offload-arch={ARCH}", "-O3", "-std=c++20", "-fPIC", "-shared",
-           # packed-FP32 instructions off for all device code
-           "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
-           # every multiply and add rounded on its own, as written: the fused and multi-kernel paths
-           # then agree bit for bit whatever the compiler would otherwise contract in each context
-           "-ffp-contract=off",
-           "-Wall", "-Wno-unused-function", "-I", os.path.join(ROOT, "include"),
-           "-o", tmp] + [os.path.join(CSRC, s) for s in SOURCES] + ["-lpthread"]
+# Per-source extra flags. The grouped MFMA kernels keep their accumulators in VGPRs (the VALU
+# epilogue then reads them without v_accvgpr_read moves).
+EXTRA = {"grouped.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"]}
+COMMON = ["-O3", "-std=c++20", "-fPIC",
+          # packed-FP32 instructions off for all device code
+          "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+          # every multiply and add rounded on its own, as written: the fused and multi-kernel paths
+          # then agree bit for bit whatever the compiler would otherwise contract in each context
+          "-ffp-contract=off",
+          "-Wall", "-Wno-unused-function"]
+
+
+def _run(cmd, verbose):
     if verbose:
         print(" ".join(cmd), flush=True)
     r = subprocess.run(cmd, capture_output=True, text=True)
@@ -41,10 +44,30 @@ def build(verbose=False):
                     if "packed-fp32-ops' is not a recognized feature" not in l)
     if r.returncode != 0:
         sys.stderr.write(out + "\n")
-        raise RuntimeError("hipcc failed")
+        raise RuntimeError("hipcc failed: " + " ".join(cmd))
     if out.strip() and verbose:
         print(out)
-    os.replace(tmp, LIB)
+
+
+def build(verbose=False):
+    """Compiles every source for gfx950 (in parallel) and links the shared library; always rebuilds."""
+    from concurrent.futures import ThreadPoolExecutor
+    tmpdir = tempfile.mkdtemp(prefix="lstk_build_")
+    try:
+        objs = []
+        cmds = []
+        for s in SOURCES:
+            o = os.path.join(tmpdir, s + ".o")
+            objs.append(o)
+            cmds.append([hipcc(), "-x", "hip", f"--offload-arch={ARCH}"] + COMMON + EXTRA.get(s, []) +
+                        ["-I", os.path.join(ROOT, "include"), "-c", os.path.join(CSRC, s), "-o", o])
+        with ThreadPoolExecutor(max_workers=min(len(cmds), 8)) as ex:
+            list(ex.map(lambda c: _run(c, verbose), cmds))
+        tmp = LIB + ".tmp"
+        _run([hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", tmp] + objs + ["-lpthread"], verbose)
+        os.replace(tmp, LIB)
+    finally:
+        shutil.rmtree(tmpdir, ignore_errors=True)
     return LIB
 
 

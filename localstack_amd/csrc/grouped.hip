@@ -30,8 +30,6 @@ typedef int i32x16 __attribute__((ext_vector_type(16)));
 typedef unsigned short u16x2 __attribute__((ext_vector_type(2)));
 
 constexpr int kGThreads = 256;        // 4 wavefronts per grouped work-group
-constexpr int kRowBytes = 256 + 16;   // LDS bytes of one staged activation row per super-block
-constexpr int kStageBytes = kGroupedChunk * kRowBytes;
 constexpr int kPermThreads = 1024;
 constexpr int kPermSeg = kPermThreads / kWave; // one pair segment per wavefront
 constexpr int kPermMaxPairs = 8192;
@@ -45,8 +43,6 @@ __device__ __forceinline__ i32x16 mfma_i8(i32x4 a, i32x4 b, i32x16 c) {
 __device__ __forceinline__ int mul_bytes(unsigned v, unsigned s2) {
     return __builtin_bit_cast(int, __builtin_bit_cast(u16x2, v) * __builtin_bit_cast(u16x2, s2));
 }
-
-__device__ __forceinline__ uint4 ld16(const uint8_t *p) { return *reinterpret_cast<const uint4 *>(p); }
 
 // ------------------------------------------------------------------------------------------------
 // permutation
@@ -70,27 +66,38 @@ __device__ __forceinline__ int wave_incl_scan(int v) {
 // exclusive prefix over segments, and the totals an exclusive prefix over bins (the offsets).
 // Pass 2: each wavefront walks its segment 64 pairs at a time; a pair's position is
 // offsets[b] + (pairs of b in earlier segments and earlier chunks) + (lanes of the chunk before it
-// with the same bin). That is the stable order by pair index t * k + j within each bin.
+// with the same bin, found by matching ballots of the bin's bits). That is the stable order by pair
+// index t * k + j within each bin.
 __global__ __launch_bounds__(kPermThreads) void permute_kernel(PermuteParams P) {
     __shared__ unsigned seg[kPermSeg][kGroupedMaxBins / 2];
     __shared__ int16_t bl[kPermMaxPairs];
     __shared__ int cnt[kGroupedMaxBins];
     __shared__ int wsum[3][kPermSeg];
-    __shared__ __align__(16) int cb[kPermSeg][kWave];
     const int tid = threadIdx.x, lane = tid % kWave, w = tid / kWave;
     const int np = P.np, nb = P.n_bins;
     for (int i = tid; i < kPermSeg * (kGroupedMaxBins / 2); i += kPermThreads) (&seg[0][0])[i] = 0u;
     __syncthreads();
     const int L = ((np + kPermSeg - 1) / kPermSeg + kWave - 1) / kWave * kWave;
     const int s0 = min(np, w * L), s1 = min(np, s0 + L);
-    for (int p = s0 + lane; p < s1; p += kWave) {
-        int b = P.bins[p];
-        if (b < 0 || b >= nb) {
-            atomicOr(P.err, 1);
-            b = min(max(b, 0), nb - 1);
+    // the segment's bins, all loads in flight together (a segment holds at most 8 * 64 pairs)
+    int bv[kPermMaxPairs / kPermSeg / kWave];
+#pragma unroll
+    for (int u = 0; u < kPermMaxPairs / kPermSeg / kWave; u++) {
+        const int p = s0 + lane + u * kWave;
+        bv[u] = p < s1 ? P.bins[p] : 0;
+    }
+#pragma unroll
+    for (int u = 0; u < kPermMaxPairs / kPermSeg / kWave; u++) {
+        const int p = s0 + lane + u * kWave;
+        if (p < s1) {
+            int b = bv[u];
+            if (b < 0 || b >= nb) {
+                atomicOr(P.err, 1);
+                b = min(max(b, 0), nb - 1);
+            }
+            bl[p] = (int16_t) b;
+            atomicAdd(&seg[w][b >> 1], 1u << (16 * (b & 1)));
         }
-        bl[p] = (int16_t) b;
-        atomicAdd(&seg[w][b >> 1], 1u << (16 * (b & 1)));
     }
     __syncthreads();
     for (int wi = tid; wi < (nb + 1) / 2; wi += kPermThreads) {
@@ -145,18 +152,17 @@ __global__ __launch_bounds__(kPermThreads) void permute_kernel(PermuteParams P) 
     for (int base = s0; base < s1; base += kWave) {
         const int p = base + lane;
         const bool on = p < s1;
-        const int b = on ? (int) bl[p] : -1;
-        cb[w][lane] = b;
-        lds_fence();
-        int before = 0, after = 0;
-#pragma unroll 4
-        for (int q = 0; q < kWave; q += 4) {
-            const int4 v = *reinterpret_cast<const int4 *>(&cb[w][q]);
-            before += (v.x == b && q < lane) + (v.y == b && q + 1 < lane) + (v.z == b && q + 2 < lane) +
-                      (v.w == b && q + 3 < lane);
-            after += (v.x == b && q > lane) + (v.y == b && q + 1 > lane) + (v.z == b && q + 2 > lane) +
-                     (v.w == b && q + 3 > lane);
+        const int b = on ? (int) bl[p] : kGroupedMaxBins; // a key no real bin has (bit 10)
+        // lanes with the same bin: the AND over the key's 11 bits of the matching ballots
+        unsigned long long mask = ~0ull;
+#pragma unroll
+        for (int bit = 0; bit < 11; bit++) {
+            const bool set = (b >> bit) & 1;
+            const unsigned long long bb = __ballot(set);
+            mask &= set ? bb : ~bb;
         }
+        const unsigned long long lt = (1ull << lane) - 1ull;
+        const int before = __popcll(mask & lt), after = __popcll(mask & ~lt) - 1;
         int pos = 0;
         if (on) {
             const unsigned word = seg[w][b >> 1];
@@ -175,77 +181,111 @@ __global__ __launch_bounds__(kPermThreads) void permute_kernel(PermuteParams P) 
 // grouped Q4_K x Q8_K products on the matrix cores
 // ------------------------------------------------------------------------------------------------
 
-// LDS of a grouped work-group.
+// The operands of one super-block of a work-group (a stage of an LDS ring of kNS stages):
+//   A   [kGroupedChunk rows][16 pieces of 16 B]: the staged activation rows, piece p of row t at slot
+//       16 t + (p ^ (t & 15)), so 16 consecutive rows reading one piece hit 16 different bank groups;
+//   DX  [kGroupedChunk] f32: the rows' Q8_K scales;
+//   W   [4 wavefronts][9 chunks][32 rows][16 B]: each wavefront's Q4_K rows.
+// Everything arrives by global_load_lds (lane i of an instruction lands at ldsptr + size * i), so the
+// staging holds no registers. Per stage, wavefront 0 issues kLoads0 loads and the others kLoads1.
+#ifndef LSTK_GROUPED_STAGES
+#define LSTK_GROUPED_STAGES 2
+#endif
+constexpr int kNS = LSTK_GROUPED_STAGES;
+constexpr int kMT = kGroupedChunk / 32;              // 32-row M-tiles per wavefront
+constexpr int kAInstr = kGroupedChunk * 16 / kWave / 4; // activation loads per wavefront
+constexpr int kABytes = kGroupedChunk * 256;
+constexpr int kDXBytes = kGroupedChunk * 4;
+constexpr int kWWaveBytes = 9 * 32 * 16;
+constexpr int kStageBytes = kABytes + kDXBytes + 4 * kWWaveBytes;
+constexpr int kLoads1 = kAInstr + 5, kLoads0 = kLoads1 + 1;
+constexpr size_t kGLdsBytes = (size_t) kNS * kStageBytes + 2 * kGroupedChunk * 4;
+
+typedef __attribute__((address_space(3))) void lds_void;
+
+__device__ __forceinline__ void dma16(const void *g, unsigned char *l) {
+    __builtin_amdgcn_global_load_lds(g, (lds_void *) l, 16, 0, 0);
+}
+__device__ __forceinline__ void dma4(const void *g, unsigned char *l) {
+    __builtin_amdgcn_global_load_lds(g, (lds_void *) l, 4, 0, 0);
+}
+template <int N>
+__device__ __forceinline__ void wait_vm() {
+    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
+}
+
 struct GLds {
-    unsigned char *xs; // [2][kGroupedChunk][kRowBytes] staged activation rows (double buffer)
-    float *dx;         // [2][kGroupedChunk] Q8_K scale of each staged row
-    int *pair;         // [kGroupedChunk] pair index of each chunk position
-    int *src;          // [kGroupedChunk] activation row of each chunk position
+    unsigned char *ring; // [kNS][kStageBytes]
+    int *pair;           // [kGroupedChunk] pair index of each chunk position
+    int *src;            // [kGroupedChunk] activation row of each chunk position
 };
-constexpr size_t kGLdsBytes = 2 * (size_t) kStageBytes + 2 * kGroupedChunk * 4 + 2 * kGroupedChunk * 4;
 
 __device__ __forceinline__ GLds g_lds(unsigned char *base) {
     GLds g;
-    g.xs = base;
-    g.dx = reinterpret_cast<float *>(base + 2 * (size_t) kStageBytes);
-    g.pair = reinterpret_cast<int *>(g.dx + 2 * kGroupedChunk);
+    g.ring = base;
+    g.pair = reinterpret_cast<int *>(base + (size_t) kNS * kStageBytes);
     g.src = g.pair + kGroupedChunk;
     return g;
 }
 
-// One super-block's activation rows of the chunk: 64 rows x 256 bytes, 16 bytes per thread-piece.
-struct Stage {
-    uint4 v[kGroupedChunk * 256 / 16 / kGThreads];
-    float dx;
+// Per-lane byte offsets of a work item's loads (fixed over the super-blocks, so the loop only moves
+// the wave-uniform bases): kAInstr activation pieces, the row scale, 5 weight chunk pairs.
+struct DmaOffs {
+    unsigned a[kAInstr], dx, w[5];
 };
 
-__device__ __forceinline__ void stage_load(const GroupedParams &P, const GLds &g, int n, int sb, Stage &st) {
-    const int tid = threadIdx.x;
+__device__ __forceinline__ DmaOffs dma_offsets(const GroupedParams &P, const GLds &g, int n, int row0) {
+    const int wave = threadIdx.x / kWave, lane = threadIdx.x % kWave;
+    DmaOffs o;
 #pragma unroll
-    for (int u = 0; u < (int) (sizeof(st.v) / sizeof(st.v[0])); u++) {
-        const int piece = tid + u * kGThreads;
-        const int r = min(piece >> 4, n - 1), part = piece & 15;
-        st.v[u] = ld16(reinterpret_cast<const uint8_t *>(P.xqs) + (size_t) g.src[r] * P.K + sb * 256 + part * 16);
+    for (int i = 0; i < kAInstr; i++) {
+        const int s = (wave * kAInstr + i) * kWave + lane;
+        const int t = s >> 4, part = (s & 15) ^ (t & 15);
+        o.a[i] = (unsigned) g.src[min(t, n - 1)] * (unsigned) P.K + part * 16;
     }
-    if (tid < kGroupedChunk) st.dx = P.xd[(size_t) g.src[min(tid, n - 1)] * (P.K / 32) + sb * 8];
-}
-
-__device__ __forceinline__ void stage_store(const GLds &g, int buf, const Stage &st) {
-    const int tid = threadIdx.x;
+    o.dx = (unsigned) g.src[min(lane, n - 1)] * (unsigned) (P.K / 32) * 4;
 #pragma unroll
-    for (int u = 0; u < (int) (sizeof(st.v) / sizeof(st.v[0])); u++) {
-        const int piece = tid + u * kGThreads;
-        *reinterpret_cast<uint4 *>(g.xs + (size_t) buf * kStageBytes + (piece >> 4) * kRowBytes + (piece & 15) * 16) =
-            st.v[u];
+    for (int i = 0; i < 5; i++) {
+        const int c = min(2 * i + (lane >> 5), 8);
+        o.w[i] = (unsigned) chunk_offset(kChunksQ4_K, P.rows, 0, c, row0 + (lane & 31));
     }
-    if (tid < kGroupedChunk) g.dx[buf * kGroupedChunk + tid] = st.dx;
+    return o;
 }
 
-// The Q4_K chunks one lane needs of one super-block: the {d, dmin, scales} chunk and, for lane half
-// h = lane / 32, qs bytes [32 c + 16 h, 32 c + 16 h + 16) of each 64-value chunk c (pool chunk
-// 1 + 2 c + h). Low nibbles are values 64 c + 16 h + [0, 16) of sub-block 2 c, high nibbles values
-// 64 c + 32 + 16 h + [0, 16) of sub-block 2 c + 1: exactly the K slice the MFMA takes from this lane.
-struct WRow {
-    uint4 hdr, q[4];
-};
-
-__device__ __forceinline__ void wrow_load(const uint8_t *w, int rows, int row, int sb, WRow &r) {
-    const int h = (threadIdx.x % kWave) / 32;
-    r.hdr = ld16(w + chunk_offset(kChunksQ4_K, rows, sb, 0, row));
+// Issues the loads of super-block sb (activation rows of the chunk, the wavefront's 32 weight rows
+// of matrix w) into ring stage `slot`.
+__device__ __forceinline__ void issue_stage(const GroupedParams &P, const GLds &g, const DmaOffs &o, const uint8_t *w,
+                                            int sb, int slot) {
+    const int wave = threadIdx.x / kWave, lane = threadIdx.x % kWave;
+    unsigned char *st = g.ring + (size_t) slot * kStageBytes;
+    const uint8_t *xa = reinterpret_cast<const uint8_t *>(P.xqs) + sb * 256;
 #pragma unroll
-    for (int c = 0; c < 4; c++) r.q[c] = ld16(w + chunk_offset(kChunksQ4_K, rows, sb, 1 + 2 * c + h, row));
+    for (int i = 0; i < kAInstr; i++) dma16(xa + o.a[i], st + (wave * kAInstr + i) * 1024);
+    if (wave == 0 && lane < kGroupedChunk) dma4(reinterpret_cast<const uint8_t *>(P.xd) + sb * 32 + o.dx, st + kABytes);
+    const uint8_t *wb = w + (size_t) sb * kChunksQ4_K * P.rows * 16;
+    unsigned char *wl = st + kABytes + kDXBytes + wave * kWWaveBytes;
+#pragma unroll
+    for (int i = 0; i < 4; i++) dma16(wb + o.w[i], wl + i * 1024);
+    if (lane < 32) dma16(wb + o.w[4], wl + 4 * 1024);
 }
 
-// Multiplies one super-block: the wavefront's 32 weight rows (lane % 32) with the staged rows of
-// buffer `buf` (M-tile mt = rows 32 mt .. 32 mt + 31 of the chunk), adding
-// d_x (d_w isum - dmin_w imin) to acc[mt][r] for staged row 32 mt + 8 (r / 4) + 4 (lane / 32) + r % 4.
-__device__ __forceinline__ void q4k_superblock(const GLds &g, int buf, int n, const WRow &wr, float (&acc)[2][16]) {
-    const int lane = threadIdx.x % kWave, h = lane / 32, r32 = lane % 32;
-    const float dw = h2f(wr.hdr.x), dmin = h2f(wr.hdr.x >> 16);
-    const unsigned s0 = wr.hdr.y, s1 = wr.hdr.z, s2 = wr.hdr.w;
-    const bool two = n > 32;
-    i32x16 aH[2], aL[2], aM[2];
-    const unsigned char *xs = g.xs + (size_t) buf * kStageBytes + (size_t) r32 * kRowBytes + 16 * h;
+// Multiplies one staged super-block: the wavefront's 32 weight rows (lane % 32) with the chunk's
+// rows (M-tile mt = rows 32 mt .. 32 mt + 31), adding d_x (d_w isum - dmin_w imin) to acc[mt][r] for
+// chunk row 32 mt + 8 (r / 4) + 4 (lane / 32) + r % 4.
+//
+// Lane half h = lane / 32 takes qs bytes [32 c + 16 h, + 16) of each 64-value chunk c of its row:
+// low nibbles are values 64 c + 16 h + [0, 16) of sub-block 2 c, high nibbles values
+// 64 c + 32 + 16 h + [0, 16) of sub-block 2 c + 1, exactly the K slice the MFMA takes from the lane.
+__device__ __forceinline__ void q4k_superblock(const unsigned char *st, int n, float (&acc)[kMT][16]) {
+    const int wave = threadIdx.x / kWave, lane = threadIdx.x % kWave, h = lane / 32, r32 = lane % 32;
+    const unsigned char *wl = st + kABytes + kDXBytes + wave * kWWaveBytes;
+    const uint4 hdr = *reinterpret_cast<const uint4 *>(wl + r32 * 16);
+    uint4 qv[4];
+#pragma unroll
+    for (int c = 0; c < 4; c++) qv[c] = *reinterpret_cast<const uint4 *>(wl + (1 + 2 * c + h) * 512 + r32 * 16);
+    const float dw = h2f(hdr.x), dmin = h2f(hdr.x >> 16);
+    const unsigned s0 = hdr.y, s1 = hdr.z, s2 = hdr.w;
+    i32x16 aH[kMT], aL[kMT], aM[kMT];
 #pragma unroll
     for (int c = 0; c < 4; c++) {
 #pragma unroll
@@ -260,19 +300,20 @@ __device__ __forceinline__ void q4k_superblock(const GLds &g, int buf, int n, co
             else if (nib == 0) scale_min_k4<6>(s0, s1, s2, sc, m);
             else scale_min_k4<7>(s0, s1, s2, sc, m);
             const unsigned sh = (unsigned) (sc >> 3) * 0x10001u, sl = (unsigned) (sc & 7) * 0x10001u;
-            const int mp = m * 0x01010101;
-            const uint4 q = wr.q[c];
+            const int mp = (int) __builtin_amdgcn_perm(0u, (unsigned) m, 0u); // m in all 4 bytes
+            const uint4 q = qv[c];
             const unsigned k4 = 0x0f0f0f0fu;
             const unsigned n0 = nib ? (q.x >> 4) & k4 : q.x & k4, n1 = nib ? (q.y >> 4) & k4 : q.y & k4;
             const unsigned n2 = nib ? (q.z >> 4) & k4 : q.z & k4, n3 = nib ? (q.w >> 4) & k4 : q.w & k4;
             const i32x4 bh = {mul_bytes(n0, sh), mul_bytes(n1, sh), mul_bytes(n2, sh), mul_bytes(n3, sh)};
             const i32x4 bl = {mul_bytes(n0, sl), mul_bytes(n1, sl), mul_bytes(n2, sl), mul_bytes(n3, sl)};
             const i32x4 bm = {mp, mp, mp, mp};
-            const int off = 64 * c + 32 * nib;
+            const int part = 4 * c + 2 * nib + h;
 #pragma unroll
-            for (int mt = 0; mt < 2; mt++) {
-                if (mt == 1 && !two) continue;
-                const i32x4 a = *reinterpret_cast<const i32x4 *>(xs + (size_t) mt * 32 * kRowBytes + off);
+            for (int mt = 0; mt < kMT; mt++) {
+                if (mt > 0 && n <= 32 * mt) continue;
+                const int t = mt * 32 + r32;
+                const i32x4 a = *reinterpret_cast<const i32x4 *>(st + (t * 16 + (part ^ (t & 15))) * 16);
                 if (c == 0 && nib == 0) {
                     const i32x16 z = {};
                     aH[mt] = mfma_i8(a, bh, z);
@@ -286,10 +327,10 @@ __device__ __forceinline__ void q4k_superblock(const GLds &g, int buf, int n, co
             }
         }
     }
-    const float *dxs = g.dx + buf * kGroupedChunk;
+    const float *dxs = reinterpret_cast<const float *>(st + kABytes);
 #pragma unroll
-    for (int mt = 0; mt < 2; mt++) {
-        if (mt == 1 && !two) continue;
+    for (int mt = 0; mt < kMT; mt++) {
+        if (mt > 0 && n <= 32 * mt) continue;
 #pragma unroll
         for (int a4 = 0; a4 < 4; a4++) {
             const float4 d4 = *reinterpret_cast<const float4 *>(dxs + mt * 32 + 8 * a4 + 4 * h);
@@ -297,41 +338,36 @@ __device__ __forceinline__ void q4k_superblock(const GLds &g, int buf, int n, co
 #pragma unroll
             for (int b = 0; b < 4; b++) {
                 const int r = 4 * a4 + b;
-                const int isum = 8 * aH[mt][r] + aL[mt][r];
-                acc[mt][r] += (dw * dv[b]) * (float) isum;
-                acc[mt][r] -= (dmin * dv[b]) * (float) aM[mt][r];
+                const float isum = (float) (8 * aH[mt][r] + aL[mt][r]);
+                acc[mt][r] = fmaf(dv[b], fmaf(dw, isum, -(dmin * (float) aM[mt][r])), acc[mt][r]);
             }
         }
     }
 }
 
-// The whole K of the wavefront's 32 rows (row0 + lane % 32 of matrix w) against the chunk's n <= 64
-// activation rows; called uniformly by the 4 wavefronts, which stage the rows together.
+// The whole K of the wavefront's 32 rows (row0 + lane % 32 of matrix w) against the chunk's n
+// activation rows; called uniformly by the 4 wavefronts. Stage sb + kNS - 1 is in flight while
+// stage sb is multiplied.
 __device__ __forceinline__ void q4k_rows(const GroupedParams &P, const GLds &g, int n, const uint8_t *w, int row0,
-                                         float (&acc)[2][16]) {
+                                         float (&acc)[kMT][16]) {
     const int nsb = P.K / 256;
-    const int row = row0 + threadIdx.x % 32;
+    const bool w0 = threadIdx.x < kWave;
 #pragma unroll
-    for (int mt = 0; mt < 2; mt++)
+    for (int mt = 0; mt < kMT; mt++)
 #pragma unroll
         for (int r = 0; r < 16; r++) acc[mt][r] = 0.0f;
-    WRow cur, nxt;
-    Stage st;
-    wrow_load(w, P.rows, row, 0, cur);
-    stage_load(P, g, n, 0, st);
-    stage_store(g, 0, st);
-    __syncthreads();
+    const DmaOffs o = dma_offsets(P, g, n, row0);
+    for (int s = 0; s < kNS - 1 && s < nsb; s++) issue_stage(P, g, o, w, s, s);
     for (int sb = 0; sb < nsb; sb++) {
-        const int buf = sb & 1;
-        if (sb + 1 < nsb) {
-            wrow_load(w, P.rows, row, sb + 1, nxt);
-            stage_load(P, g, n, sb + 1, st);
+        if (sb + kNS - 1 < nsb) {
+            issue_stage(P, g, o, w, sb + kNS - 1, (sb + kNS - 1) % kNS);
+            if (w0) wait_vm<kLoads0 * (kNS - 1)>();
+            else wait_vm<kLoads1 * (kNS - 1)>();
+        } else {
+            wait_vm<0>();
         }
-        q4k_superblock(g, buf, n, cur, acc);
-        if (sb + 1 < nsb) {
-            stage_store(g, buf ^ 1, st);
-            cur = nxt;
-        }
+        __syncthreads();
+        q4k_superblock(g.ring + (size_t) (sb % kNS) * kStageBytes, n, acc);
         __syncthreads();
     }
 }
@@ -363,13 +399,13 @@ __global__ __launch_bounds__(kGThreads) void gate_up_grouped_kernel(GroupedParam
     const int wave = threadIdx.x / kWave, lane = threadIdx.x % kWave;
     const int m = wave & 1, row0 = rb * 64 + 32 * (wave >> 1);
     const uint8_t *w = m ? P.w1 + (size_t) e * P.stride1 : P.w0 + (size_t) e * P.stride0;
-    float acc[2][16];
+    float acc[kMT][16];
     q4k_rows(P, g, n, w, row0, acc);
-    float *ex = reinterpret_cast<float *>(g.xs); // [2 row halves][2 M-tiles][16][64]
-    float *mine = ex + (size_t) (wave >> 1) * 2 * 16 * kWave;
+    float *ex = reinterpret_cast<float *>(g.ring); // [2 row halves][kMT M-tiles][16][64]
+    float *mine = ex + (size_t) (wave >> 1) * kMT * 16 * kWave;
     if (m == 1) {
 #pragma unroll
-        for (int mt = 0; mt < 2; mt++)
+        for (int mt = 0; mt < kMT; mt++)
 #pragma unroll
             for (int r = 0; r < 16; r++) mine[(mt * 16 + r) * kWave + lane] = acc[mt][r];
     }
@@ -377,7 +413,7 @@ __global__ __launch_bounds__(kGThreads) void gate_up_grouped_kernel(GroupedParam
     if (m == 0) {
         const int h = lane / 32;
 #pragma unroll
-        for (int mt = 0; mt < 2; mt++) {
+        for (int mt = 0; mt < kMT; mt++) {
 #pragma unroll
             for (int r = 0; r < 16; r++) {
                 const int pos = mt * 32 + 8 * (r / 4) + 4 * h + (r % 4);
@@ -400,10 +436,10 @@ __global__ __launch_bounds__(kGThreads) void down_grouped_kernel(GroupedParams P
     const int rb = blockIdx.x % n_rb, e = it.x, n = it.z;
     const int wave = threadIdx.x / kWave, lane = threadIdx.x % kWave, h = lane / 32;
     const int row0 = rb * 128 + 32 * wave;
-    float acc[2][16];
+    float acc[kMT][16];
     q4k_rows(P, g, n, P.w0 + (size_t) e * P.stride0, row0, acc);
 #pragma unroll
-    for (int mt = 0; mt < 2; mt++) {
+    for (int mt = 0; mt < kMT; mt++) {
 #pragma unroll
         for (int r = 0; r < 16; r++) {
             const int pos = mt * 32 + 8 * (r / 4) + 4 * h + (r % 4);
@@ -435,13 +471,28 @@ hipError_t launch_permute(const PermuteParams &P, hipStream_t st, const LaunchTi
     return launch(permute_kernel, dim3(1), dim3(kPermThreads), 0, st, tm, P);
 }
 
+// The grouped kernels take more than 64 KiB of dynamic LDS (gfx950 has 160 KiB per CU).
+hipError_t allow_lds() {
+    static hipError_t e = [] {
+        hipError_t r = hipFuncSetAttribute(reinterpret_cast<const void *>(&gate_up_grouped_kernel),
+                                           hipFuncAttributeMaxDynamicSharedMemorySize, (int) kGLdsBytes);
+        if (r == hipSuccess)
+            r = hipFuncSetAttribute(reinterpret_cast<const void *>(&down_grouped_kernel),
+                                    hipFuncAttributeMaxDynamicSharedMemorySize, (int) kGLdsBytes);
+        return r;
+    }();
+    return e;
+}
+
 hipError_t launch_gate_up_grouped(const GroupedParams &P, int max_items, hipStream_t st, const LaunchTiming *tm) {
     if (max_items <= 0) return hipSuccess;
+    if (const hipError_t e = allow_lds(); e != hipSuccess) return e;
     return launch(gate_up_grouped_kernel, dim3(max_items * (P.rows / 64)), dim3(kGThreads), kGLdsBytes, st, tm, P);
 }
 
 hipError_t launch_down_grouped(const GroupedParams &P, int max_items, hipStream_t st, const LaunchTiming *tm) {
     if (max_items <= 0) return hipSuccess;
+    if (const hipError_t e = allow_lds(); e != hipSuccess) return e;
     return launch(down_grouped_kernel, dim3(max_items * (P.rows / 128)), dim3(kGThreads), kGLdsBytes, st, tm, P);
 }
 

@@ -162,7 +162,10 @@ hipError_t launch_down(const DownParams &p, hipStream_t s, const LaunchTiming *t
 hipError_t launch_combine(const CombineParams &p, hipStream_t s, const LaunchTiming *t);
 
 // grouped (prefill) path, grouped.hip
-constexpr int kGroupedChunk = 64;        // pairs per work item
+#ifndef LSTK_GROUPED_CHUNK
+#define LSTK_GROUPED_CHUNK 32
+#endif
+constexpr int kGroupedChunk = LSTK_GROUPED_CHUNK; // pairs per work item (32 or 64)
 constexpr int kGroupedMaxBins = 1024;    // bins the permutation kernel handles
 // True when the grouped MFMA kernels handle this layer: Q4_K gate, up and down, f % 64 == 0,
 // n_bins <= kGroupedMaxBins.
