@@ -52,12 +52,11 @@ constexpr int kDecodeRouteT = 1;  // gate_up runs the top-k itself for a single 
 // ggml's CPU mul_mat converts src1 to the F16 vec_dot_type (src/qwen3.cpp:178).
 // The wavefront's two weight rows are loaded before the activations are staged.
 template <int GT, int NG>
-__device__ __forceinline__ void route_tile(const RouteParams &P, int b, float *xs, int tt) {
+__device__ __forceinline__ void route_tile(const RouteParams &P, int b, float *xs, int tt, int ns) {
     const int n_eg = (P.E + kRouteEG - 1) / kRouteEG;
     const int tile = b / n_eg, eg = b - tile * n_eg;
-    const int t0 = tile * tt;
-    const int nt = min(tt, P.T - t0);
     constexpr int h = NG * 256;
+    constexpr int kPre = 32768 / 16 / kBlock; // float4 of one stage per thread (tt * h * 4 <= 32 KiB)
     const int wave = threadIdx.x / kWave, lane = threadIdx.x % kWave;
     float w[kRouteEPW][NG][4];
     // every load unconditional and unrolled, so all of them are in flight before the first use
@@ -84,51 +83,75 @@ __device__ __forceinline__ void route_tile(const RouteParams &P, int b, float *x
             }
         }
     }
-    const float4 *src = reinterpret_cast<const float4 *>(P.hnorm + (size_t) t0 * h);
-    float4 *dst = reinterpret_cast<float4 *>(xs);
-    for (int i = threadIdx.x; i < nt * h / 4; i += blockDim.x) {
-        float4 v = src[i];
-        if (GT == kTypeF16) {
-            v.x = round_f16(v.x);
-            v.y = round_f16(v.y);
-            v.z = round_f16(v.z);
-            v.w = round_f16(v.w);
+    // the work-group's ns stages of tt tokens: stage s + 1 is loaded into registers while the
+    // tokens of stage s are multiplied from LDS
+    const int tbase = tile * tt * ns;
+    float4 pre[kPre];
+    auto load = [&](int s) {
+        const int t0 = tbase + s * tt, nt = max(0, min(tt, P.T - t0));
+        const float4 *src = reinterpret_cast<const float4 *>(P.hnorm + (size_t) t0 * h);
+#pragma unroll
+        for (int u = 0; u < kPre; u++) {
+            const int i = threadIdx.x + u * kBlock;
+            if (i < nt * h / 4) pre[u] = src[i];
         }
-        dst[i] = v;
-    }
-    __syncthreads();
-    for (int t = 0; t < nt; t++) {
-        float acc[kRouteEPW];
+    };
+    load(0);
+    for (int s = 0; s < ns; s++) {
+        const int t0 = tbase + s * tt;
+        const int nt = min(tt, P.T - t0);
+        if (nt <= 0) break;
+        __syncthreads();
+        float4 *dst = reinterpret_cast<float4 *>(xs);
 #pragma unroll
-        for (int ee = 0; ee < kRouteEPW; ee++) acc[ee] = 0.0f;
-#pragma unroll
-        for (int g = 0; g < NG; g++) {
-            {
-                const float4 x = *reinterpret_cast<const float4 *>(xs + (size_t) t * h + 256 * g + 4 * lane);
-#pragma unroll
-                for (int ee = 0; ee < kRouteEPW; ee++) {
-                    acc[ee] = fmaf(x.x, w[ee][g][0], acc[ee]);
-                    acc[ee] = fmaf(x.y, w[ee][g][1], acc[ee]);
-                    acc[ee] = fmaf(x.z, w[ee][g][2], acc[ee]);
-                    acc[ee] = fmaf(x.w, w[ee][g][3], acc[ee]);
+        for (int u = 0; u < kPre; u++) {
+            const int i = threadIdx.x + u * kBlock;
+            if (i < nt * h / 4) {
+                float4 v = pre[u];
+                if (GT == kTypeF16) {
+                    v.x = round_f16(v.x);
+                    v.y = round_f16(v.y);
+                    v.z = round_f16(v.z);
+                    v.w = round_f16(v.w);
                 }
+                dst[i] = v;
             }
         }
+        __syncthreads();
+        if (s + 1 < ns) load(s + 1);
+        for (int t = 0; t < nt; t++) {
+            float acc[kRouteEPW];
 #pragma unroll
-        for (int ee = 0; ee < kRouteEPW; ee++) {
-            const int e = eg * kRouteEG + wave * kRouteEPW + ee;
-            const float sum = wave_sum_tree(acc[ee]);
-            if (lane == 0 && e < P.E) P.logits[(size_t) (t0 + t) * P.E + e] = sum;
+            for (int ee = 0; ee < kRouteEPW; ee++) acc[ee] = 0.0f;
+#pragma unroll
+            for (int g = 0; g < NG; g++) {
+                {
+                    const float4 x = *reinterpret_cast<const float4 *>(xs + (size_t) t * h + 256 * g + 4 * lane);
+#pragma unroll
+                    for (int ee = 0; ee < kRouteEPW; ee++) {
+                        acc[ee] = fmaf(x.x, w[ee][g][0], acc[ee]);
+                        acc[ee] = fmaf(x.y, w[ee][g][1], acc[ee]);
+                        acc[ee] = fmaf(x.z, w[ee][g][2], acc[ee]);
+                        acc[ee] = fmaf(x.w, w[ee][g][3], acc[ee]);
+                    }
+                }
+            }
+#pragma unroll
+            for (int ee = 0; ee < kRouteEPW; ee++) {
+                const int e = eg * kRouteEG + wave * kRouteEPW + ee;
+                const float sum = wave_sum_tree(acc[ee]);
+                if (lane == 0 && e < P.E) P.logits[(size_t) (t0 + t) * P.E + e] = sum;
+            }
         }
     }
 }
 
 template <int GT, int NG>
-__global__ __launch_bounds__(kBlock) void route_kernel(RouteParams P, int n_route_wg, int n_quant_wg, int route_tt) {
+__global__ __launch_bounds__(kBlock) void route_kernel(RouteParams P, int n_route_wg, int n_quant_wg, int route_tt, int route_ns) {
     extern __shared__ __align__(16) float lds[];
     const int b = blockIdx.x;
     if (b < n_route_wg) {
-        route_tile<GT, NG>(P, b, lds, route_tt);
+        route_tile<GT, NG>(P, b, lds, route_tt, route_ns);
     } else if (P.qtype != 0) {
         const int h = P.h;
         for (int t = b - n_route_wg; t < P.T; t += n_quant_wg) {
@@ -538,15 +561,17 @@ size_t align16(size_t x) { return (x + 15) / 16 * 16; }
 
 template <int GT, int NG>
 hipError_t launch_route_t(const RouteParams &P, hipStream_t st, const LaunchTiming *tm) {
-    int n_route = 0, tt = 1;
+    int n_route = 0, tt = 1, ns = 1;
     if (P.do_route) {
         tt = route_tile_tokens(P.h);
-        n_route = ((P.T + tt - 1) / tt) * ((P.E + kRouteEG - 1) / kRouteEG);
+        // many tokens: each work-group keeps its router rows in registers over 4 stages of tokens
+        ns = P.T > 8 * tt ? 4 : 1;
+        n_route = ((P.T + tt * ns - 1) / (tt * ns)) * ((P.E + kRouteEG - 1) / kRouteEG);
     }
     const int n_quant = P.qtype ? std::min(P.T, 256) : 0;
     const int grid = std::max(1, n_route + n_quant);
     const size_t lds = P.do_route ? (size_t) tt * P.h * 4 : 16;
-    return launch(route_kernel<GT, NG>, dim3(grid), dim3(kBlock), lds, st, tm, P, n_route, n_quant, tt);
+    return launch(route_kernel<GT, NG>, dim3(grid), dim3(kBlock), lds, st, tm, P, n_route, n_quant, tt, ns);
 }
 
 template <int GT>
