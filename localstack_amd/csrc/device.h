@@ -196,6 +196,56 @@ __device__ __forceinline__ void quantize_row(const float *__restrict__ x, int n,
     }
 }
 
+// quantize_row for n <= NP * 8 * blockDim.x with every load issued before the first pass is
+// quantized (one memory round trip instead of one per pass).
+// Split form: quantize_row_load issues the loads into v, quantize_row_store quantizes v.
+// Every load is unconditional (addresses clamped into [0, n), n >= 8), so no branch separates them
+// from the caller's next loads.
+template <int NP>
+__device__ __forceinline__ void quantize_row_load(const float *__restrict__ x, int n, float (&v)[NP][8]) {
+#pragma unroll
+    for (int p = 0; p < NP; p++) {
+        const int i0 = (p * blockDim.x + threadIdx.x) * 8;
+        const int ia = min(i0, n - 8);
+        const float4 a = *reinterpret_cast<const float4 *>(x + ia);
+        const float4 b = *reinterpret_cast<const float4 *>(x + ia + 4);
+        const bool in = i0 < n;
+        v[p][0] = in ? a.x : 0.0f; v[p][1] = in ? a.y : 0.0f; v[p][2] = in ? a.z : 0.0f; v[p][3] = in ? a.w : 0.0f;
+        v[p][4] = in ? b.x : 0.0f; v[p][5] = in ? b.y : 0.0f; v[p][6] = in ? b.z : 0.0f; v[p][7] = in ? b.w : 0.0f;
+    }
+}
+template <int QT, int NP>
+__device__ __forceinline__ void quantize_row_store(const float (&v)[NP][8], int n, int8_t *qs, float *d, int32_t *bs) {
+#pragma unroll
+    for (int p = 0; p < NP; p++) {
+        const int i0 = (p * blockDim.x + threadIdx.x) * 8;
+        if (p * (int) blockDim.x * 8 < n) quantize8<QT>(v[p], i0, i0 < n, qs, d, bs);
+    }
+}
+
+template <int QT, int NP>
+__device__ __forceinline__ void quantize_row_pre(const float *__restrict__ x, int n, int8_t *qs, float *d, int32_t *bs) {
+    float v[NP][8];
+#pragma unroll
+    for (int p = 0; p < NP; p++) {
+        const int i0 = (p * blockDim.x + threadIdx.x) * 8;
+        if (i0 < n) {
+            const float4 a = *reinterpret_cast<const float4 *>(x + i0);
+            const float4 b = *reinterpret_cast<const float4 *>(x + i0 + 4);
+            v[p][0] = a.x; v[p][1] = a.y; v[p][2] = a.z; v[p][3] = a.w;
+            v[p][4] = b.x; v[p][5] = b.y; v[p][6] = b.z; v[p][7] = b.w;
+        } else {
+#pragma unroll
+            for (int j = 0; j < 8; j++) v[p][j] = 0.0f;
+        }
+    }
+#pragma unroll
+    for (int p = 0; p < NP; p++) {
+        const int i0 = (p * blockDim.x + threadIdx.x) * 8;
+        if (p * (int) blockDim.x * 8 < n) quantize8<QT>(v[p], i0, i0 < n, qs, d, bs);
+    }
+}
+
 // quantize_row of values another work-group stored in this launch (device-coherent loads), for
 // n <= NP * 8 * blockDim.x: every load is issued before the first pass is quantized.
 template <int QT, int NP>

@@ -80,6 +80,22 @@ struct DownParams {
     float *Y; // [T*k][h] weighted expert outputs by pair index
 };
 
+// down + router weight + k-way combine + residual of one token (n_tokens = 1) in one launch:
+// work-group b computes rows [b rd, (b + 1) rd) of all k pairs and sums them in slot order.
+struct DownCombineParams {
+    const int32_t *ids;   // [k] expert ids or pool slots
+    const float *weights; // [k]
+    int k, n_bins;
+    const uint8_t *w_down;
+    size_t stride_down;
+    int type;
+    int h, f;
+    const float *act; // [k][f] SwiGLU rows
+    const float *resid;
+    float *out;
+    int32_t *err;
+};
+
 struct CombineParams {
     const float *Y;
     const float *resid;
@@ -160,6 +176,9 @@ hipError_t launch_topk(const TopkParams &p, hipStream_t s, const LaunchTiming *t
 hipError_t launch_gate_up(const GateUpParams &p, hipStream_t s, const LaunchTiming *t);
 hipError_t launch_down(const DownParams &p, hipStream_t s, const LaunchTiming *t);
 hipError_t launch_combine(const CombineParams &p, hipStream_t s, const LaunchTiming *t);
+// True when launch_down_combine handles this shape (k * f <= 16384 SwiGLU values in LDS).
+bool down_combine_supported(int h, int f, int k);
+hipError_t launch_down_combine(const DownCombineParams &p, hipStream_t s, const LaunchTiming *t);
 
 // grouped (prefill) path, grouped.hip
 #ifndef LSTK_GROUPED_CHUNK

@@ -350,8 +350,8 @@ __global__ __launch_bounds__(kBlock) void gate_up_kernel(GateUpParams P) {
     const int f = P.f, h = P.h, k = P.gp.k;
     const int row = blockIdx.x * RW + r;
     GroupLds gl = group_lds(smem, P.gp.T, k, P.gp.n_bins, ROUTE);
-    unsigned char *work = smem + group_lds_bytes(P.gp.T, k, P.gp.n_bins, ROUTE);
-    work = reinterpret_cast<unsigned char *>((reinterpret_cast<uintptr_t>(work) + 15) & ~uintptr_t(15));
+    // offset from the LDS base (no integer round trip, so the accesses stay ds_read / ds_write)
+    unsigned char *work = smem + ((group_lds_bytes(P.gp.T, k, P.gp.n_bins, ROUTE) + 15) & ~size_t(15));
     if (!group_pairs<ROUTE>(P.gp, gl)) return;
     const int e = gl.misc[0], cnt = gl.misc[1];
     const uint8_t *base = m ? P.w_up + (size_t) e * P.stride_up : P.w_gate + (size_t) e * P.stride_gate;
@@ -467,8 +467,7 @@ __global__ __launch_bounds__(kDnRows * kMaxG) void down_kernel(DownParams P) {
     const int h = P.h, f = P.f;
     const int row = blockIdx.x * kDnRows + r;
     GroupLds gl = group_lds(smem, P.gp.T, P.gp.k, P.gp.n_bins, 0);
-    unsigned char *work = smem + group_lds_bytes(P.gp.T, P.gp.k, P.gp.n_bins, 0);
-    work = reinterpret_cast<unsigned char *>((reinterpret_cast<uintptr_t>(work) + 15) & ~uintptr_t(15));
+    unsigned char *work = smem + ((group_lds_bytes(P.gp.T, P.gp.k, P.gp.n_bins, 0) + 15) & ~size_t(15));
     if (!group_pairs<false>(P.gp, gl)) return;
     const int e = gl.misc[0], cnt = gl.misc[1];
     const uint8_t *base = P.w_down + (size_t) e * P.stride_down;
@@ -514,6 +513,68 @@ __global__ __launch_bounds__(kDnRows * kMaxG) void down_kernel(DownParams P) {
         __syncthreads();
     }
     (void) row;
+}
+
+// ------------------------------------------------------------------------------------------------
+// down + router weight + combine + residual of a single token
+// ------------------------------------------------------------------------------------------------
+
+constexpr int kDcMaxAct = 16384; // k * f SwiGLU values quantized in a work-group's LDS
+
+// Thread (q, rr) with q = j * nsbf + sb holds super-block sb of row blockIdx.x * rd + rr of pair j's
+// down matrix. The pair's slot and the token's k SwiGLU rows are loaded first (one round trip), the
+// weight loads are issued as soon as the slot is known, and the SwiGLU rows are quantized into LDS
+// while the weights stream in. Each thread's partial dot lands in LDS,
+// and threads rr < rd sum, per pair j in ascending order, the partials over sb ascending (the
+// order of down_kernel), multiply by the router weight and add the pairs left to right in j, then
+// the residual (the order of combine_kernel), so the result equals down + combine bit for bit.
+template <int WT, int NP>
+__global__ __launch_bounds__(kBlock) void down_combine_kernel(DownCombineParams P, int rd) {
+    constexpr int C = chunks_of(WT);
+    constexpr int QT = WT == kTypeQ4_K ? kTypeQ4_K : kTypeQ8_0;
+    extern __shared__ __align__(16) unsigned char smem[];
+    const int tid = threadIdx.x, k = P.k, f = P.f, nsbf = f / 256, nact = k * f;
+    const int rr = tid % rd, q = tid / rd, sb = q % nsbf, j = q / nsbf;
+    const bool on = j < k;
+    const int row = blockIdx.x * rd + rr;
+    int8_t *qs = reinterpret_cast<int8_t *>(smem);
+    float *qd = reinterpret_cast<float *>(smem + nact);
+    int *qb = reinterpret_cast<int *>(qd + nact / 32);
+    float *part = reinterpret_cast<float *>(qb + nact / 32);
+    float *s_w = part + (size_t) k * nsbf * rd;
+    // unconditional loads (indexes clamped), so the weight loads follow without a branch
+    int b = P.ids[min(j, k - 1)];
+    const float wj = P.weights[min(tid, k - 1)];
+    float v[NP][8];
+    quantize_row_load<NP>(P.act, nact, v);
+    if (b < 0 || b >= P.n_bins) {
+        if (on && blockIdx.x == 0 && rr == 0 && sb == 0) atomicOr(P.err, 1);
+        b = min(max(b, 0), P.n_bins - 1);
+    }
+    const uint8_t *base = P.w_down + (size_t) b * P.stride_down;
+    uint4 w[C];
+#pragma unroll
+    for (int c = 0; c < C; c++) w[c] = *reinterpret_cast<const uint4 *>(base + chunk_offset(C, P.h, on ? sb : 0, c, row));
+    quantize_row_store<QT, NP>(v, nact, qs, qd, qb);
+    if (tid < k) s_w[tid] = wj;
+    __syncthreads();
+    if (on) {
+        const int o = j * f + sb * 256;
+        part[(j * rd + rr) * nsbf + sb] = dot_sb<WT>(w, qs + o, qd + o / 32, qb + o / 32, 0.0f);
+    }
+    __syncthreads();
+    if (tid < rd) {
+        float acc = 0.0f;
+        for (int jj = 0; jj < k; jj++) {
+            const float *pp = part + (jj * rd + tid) * nsbf;
+            float ds = pp[0];
+            for (int s2 = 1; s2 < nsbf; s2++) ds += pp[s2];
+            const float y = ds * s_w[jj];
+            acc = jj == 0 ? y : acc + y;
+        }
+        const int orow = blockIdx.x * rd + tid;
+        P.out[orow] = acc + P.resid[orow];
+    }
 }
 
 // ------------------------------------------------------------------------------------------------
@@ -604,7 +665,41 @@ hipError_t launch_down_t(const DownParams &P, int G, hipStream_t st, const Launc
     return launch(down_kernel<WT, S>, dim3(P.h / kDnRows, P.max_active), dim3(kDnRows * G), lds, st, tm, P);
 }
 
+// Rows per down_combine work-group: the largest power of two with k * nsbf * rd <= 256 threads.
+int down_combine_rows(int f, int k) {
+    const int per = k * (f / 256);
+    int rd = 1;
+    while (rd * 2 * per <= kBlock) rd *= 2;
+    return rd;
+}
+
+template <int WT>
+hipError_t launch_down_combine_t(const DownCombineParams &P, hipStream_t st, const LaunchTiming *tm) {
+    const int rd = down_combine_rows(P.f, P.k), nsbf = P.f / 256, nact = P.k * P.f;
+    const int threads = (P.k * nsbf * rd + kWave - 1) / kWave * kWave;
+    const size_t lds = (size_t) nact + (size_t) nact / 32 * 8 + (size_t) P.k * nsbf * rd * 4 + (size_t) P.k * 4;
+    const int np = (nact + threads * 8 - 1) / (threads * 8);
+    const dim3 grid(P.h / rd), block(threads);
+    if (np <= 1) return launch(down_combine_kernel<WT, 1>, grid, block, lds, st, tm, P, rd);
+    if (np <= 2) return launch(down_combine_kernel<WT, 2>, grid, block, lds, st, tm, P, rd);
+    if (np <= 4) return launch(down_combine_kernel<WT, 4>, grid, block, lds, st, tm, P, rd);
+    return launch(down_combine_kernel<WT, 8>, grid, block, lds, st, tm, P, rd);
+}
+
 }  // namespace
+
+bool down_combine_supported(int h, int f, int k) {
+    if (k < 1 || k > kMaxK || f % 256 != 0 || h % 256 != 0 || (long) k * f > kDcMaxAct) return false;
+    if (k * (f / 256) > kBlock) return false;
+    const int rd = down_combine_rows(f, k);
+    const int threads = (k * (f / 256) * rd + kWave - 1) / kWave * kWave;
+    return h % rd == 0 && (long) k * f <= 8L * threads * 8;
+}
+
+hipError_t launch_down_combine(const DownCombineParams &P, hipStream_t st, const LaunchTiming *tm) {
+    if (!down_combine_supported(P.h, P.f, P.k)) return hipErrorInvalidValue;
+    return P.type == kTypeQ8_0 ? launch_down_combine_t<kTypeQ8_0>(P, st, tm) : launch_down_combine_t<kTypeQ4_K>(P, st, tm);
+}
 
 int decode_route_max_tokens() { return kDecodeRouteT; }
 

@@ -744,6 +744,25 @@ int run_block(lstk_pool *P, int layer, int mode, const float *d_hnorm, const voi
     gu.act = P->act;
     e = timed(P, 1, [&](const lstk::LaunchTiming *tm) { return lstk::launch_gate_up(gu, st, tm); });
     if (e != hipSuccess) return hip_fail(e, "gate_up launch");
+    if (T == 1 && lstk::down_combine_supported(d.n_embd, d.n_ff_exp, k)) {
+        // one token: down, router weights, combine and residual in one launch
+        lstk::DownCombineParams dc{};
+        dc.ids = gp.ids;
+        dc.weights = d_weights;
+        dc.k = k;
+        dc.n_bins = (int) s.n_slots;
+        dc.w_down = s.d_down;
+        dc.stride_down = s.down_bytes;
+        dc.type = s.td;
+        dc.h = d.n_embd;
+        dc.f = d.n_ff_exp;
+        dc.act = P->act;
+        dc.resid = d_resid;
+        dc.out = d_out;
+        dc.err = P->err;
+        e = timed(P, 2, [&](const lstk::LaunchTiming *tm) { return lstk::launch_down_combine(dc, st, tm); });
+        return e == hipSuccess ? LSTK_OK : hip_fail(e, "down_combine launch");
+    }
     lstk::DownParams dn{};
     dn.gp = gp;
     dn.gp.route = 0;
