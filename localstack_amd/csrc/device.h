@@ -407,6 +407,57 @@ __device__ __forceinline__ bool rank_token(const float *__restrict__ l_row, int 
     return true;
 }
 
+// Order key of a logit for the selection rounds: monotone in the value, -0 and +0 equal, every real
+// logit > 0 (0 marks an expert that is out of range or already selected).
+__device__ __forceinline__ unsigned select_key(float v) {
+    unsigned u = __float_as_uint(v);
+    if (v == 0.0f) u = 0u;
+    return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+}
+
+__device__ __forceinline__ unsigned wave_max_u32(unsigned v) {
+    v = max(v, (unsigned) __builtin_amdgcn_update_dpp(0, (int) v, 0xB1, 0xF, 0xF, false));
+    v = max(v, (unsigned) __builtin_amdgcn_update_dpp(0, (int) v, 0x4E, 0xF, 0xF, false));
+    v = max(v, (unsigned) __builtin_amdgcn_update_dpp(0, (int) v, 0x141, 0xF, 0xF, false));
+    v = max(v, (unsigned) __builtin_amdgcn_update_dpp(0, (int) v, 0x140, 0xF, 0xF, false));
+    return max(max((unsigned) __builtin_amdgcn_readlane((int) v, 0), (unsigned) __builtin_amdgcn_readlane((int) v, 16)),
+               max((unsigned) __builtin_amdgcn_readlane((int) v, 32), (unsigned) __builtin_amdgcn_readlane((int) v, 48)));
+}
+
+// Top-k of one token's row by one wavefront, no LDS and no barrier: k rounds, each taking the
+// largest remaining key and, among equal keys, the lowest expert id (expert lane + 64 i, searched
+// i = 0 first, lowest lane first), so the selection is largest first with ties to the lower id, the
+// order rank_token computes. rank[i] = the round that took expert lane + 64 i, INT_MAX if none.
+template <int EPL>
+__device__ __forceinline__ void select_topk(const float (&l)[EPL], const bool (&valid)[EPL], int k, int (&rank)[EPL]) {
+    const int lane = threadIdx.x % kWave;
+    unsigned key[EPL];
+#pragma unroll
+    for (int i = 0; i < EPL; i++) {
+        key[i] = valid[i] ? select_key(l[i]) : 0u;
+        rank[i] = INT_MAX;
+    }
+    for (int r = 0; r < k; r++) {
+        unsigned m = key[0];
+#pragma unroll
+        for (int i = 1; i < EPL; i++) m = max(m, key[i]);
+        m = wave_max_u32(m);
+        int sel = -1;
+#pragma unroll
+        for (int i = 0; i < EPL; i++) {
+            const unsigned long long b = __ballot(key[i] == m && m != 0u);
+            if (sel < 0 && b) sel = kWave * i + __ffsll((long long) b) - 1;
+        }
+#pragma unroll
+        for (int i = 0; i < EPL; i++) {
+            if (lane + kWave * i == sel) {
+                rank[i] = r;
+                key[i] = 0u;
+            }
+        }
+    }
+}
+
 // Softmax, renormalisation and output of one token whose ranks rank_token found (part 0 only).
 template <int EPL>
 __device__ __forceinline__ void weights_token(int k, const float (&l)[EPL], const bool (&valid)[EPL], const int (&rank)[EPL],

@@ -180,7 +180,7 @@ __global__ __launch_bounds__(kBlock) void topk_kernel(TopkParams P) {
 
 // LDS layout of the grouping step, in front of each expert kernel's own LDS.
 struct GroupLds {
-    unsigned char *scratch; // top-k scratch (route mode), topk_lds_bytes(4)
+    unsigned char *scratch; // top-k scratch (route mode), kTopkLds bytes
     int16_t *ids;   // [T*k] bins
     float *w;       // [T*k] router weights (route mode only)
     unsigned *bm;   // [n_bins / 32] bins in use
@@ -188,8 +188,10 @@ struct GroupLds {
     int *misc;      // [0] = expert or -1, [1] = number of pairs
 };
 
-constexpr size_t kTopkLds = (size_t) (kBlock / kWave) * 256 * 4 + (size_t) (kBlock / kWave) * kMaxEPL * kWave * 4 +
-                            (size_t) (kBlock / kWave) * kMaxK * 4;
+// route mode: the selected probabilities of weights_token, then the experts' 64-bit keys, the
+// partial rank counts and the logits of route_one
+constexpr size_t kTopkLds = (size_t) kMaxK * 4 + (size_t) kMaxEPL * kWave * 8 + (size_t) kBlock * 4 +
+                            (size_t) kMaxEPL * kWave * 4;
 
 // The top-k scratch and the weights exist only when the work-group routes (route = 1).
 __device__ __host__ inline size_t group_lds_bytes(int T, int k, int n_bins, int route) {
@@ -217,23 +219,57 @@ __device__ __forceinline__ GroupLds group_lds(unsigned char *base, int T, int k,
     return g;
 }
 
-// Single-token routing inside an expert work-group (route mode): exact ranks of the token's row
-// by all wavefronts, the block's expert = the y-th selected expert by ascending id, its pair index
-// = t * k + rank = rank. Returns false when y >= k.
+// Single-token routing inside an expert work-group (route mode). Every expert e < E gets a unique
+// 64-bit key (select_key(logit) << 8 | 255 - e: larger logit first, ties to the lower id) in LDS;
+// the work-group's threads count, in parallel, how many keys exceed each expert's key (expert
+// t % Ep against a 1 / (256 / Ep) share of the row, Ep = E rounded up to 64), so rank = that count
+// is the position in the descending selection order of rank_token / the oracle. Wavefront 0 then
+// takes the block's expert = the y-th expert of rank < k by ascending id, and its pair index
+// j = t * k + rank = rank. Work-group (0, 0) also runs the softmax and stores ids / weights.
+// Returns false when y >= k.
 template <int EPL>
 __device__ __forceinline__ bool route_one(const GroupParams &P, GroupLds g) {
-    const int lane = threadIdx.x % kWave, wave = threadIdx.x / kWave, nw = blockDim.x / kWave;
-    float *s_l = reinterpret_cast<float *>(g.scratch);
-    int *s_rank = reinterpret_cast<int *>(g.scratch + (size_t) nw * 256 * 4);
-    float *s_p = reinterpret_cast<float *>(s_rank + (size_t) nw * kMaxEPL * kWave);
-    float l[EPL];
-    bool valid[EPL];
-    int rank[EPL];
-    if (rank_token<EPL>(P.logits, P.E, P.k, wave, nw, s_l, s_rank, l, valid, rank)) {
+    const int tid = threadIdx.x, lane = tid % kWave, wave = tid / kWave;
+    const int E = P.E, Ep = EPL * kWave, nsplit = kBlock / Ep, span = Ep / nsplit;
+    unsigned long long *s_key = reinterpret_cast<unsigned long long *>(g.scratch + kMaxK * 4); // [Ep]
+    int *s_cnt = reinterpret_cast<int *>(s_key + Ep);                                          // [nsplit][Ep]
+    float *s_l = reinterpret_cast<float *>(s_cnt + kBlock);                                    // [Ep]
+    float *s_p = reinterpret_cast<float *>(g.scratch);
+    const int e = tid % Ep, part = tid / Ep;
+    const float le = P.logits[min(e, E - 1)];
+    if (part == 0) {
+        s_key[e] = e < E ? ((unsigned long long) select_key(le) << 8) | (unsigned) (255 - e) : 0ull;
+        s_l[e] = le;
+    }
+    __syncthreads();
+    {
+        const unsigned long long mine = s_key[e];
+        const unsigned long long *row = s_key + part * span;
+        int c = 0;
+        for (int i = 0; i < span; i += 2) {
+            const ulonglong2 v = *reinterpret_cast<const ulonglong2 *>(row + i);
+            c += (v.x > mine) + (v.y > mine);
+        }
+        s_cnt[part * Ep + e] = c;
+    }
+    __syncthreads();
+    if (wave == 0) {
+        float l[EPL];
+        bool valid[EPL];
+        int rank[EPL];
+#pragma unroll
+        for (int i = 0; i < EPL; i++) {
+            const int ee = lane + kWave * i;
+            valid[i] = ee < E;
+            l[i] = valid[i] ? s_l[ee] : -INFINITY;
+            int r = 0;
+            for (int q = 0; q < nsplit; q++) r += s_cnt[q * Ep + ee];
+            rank[i] = valid[i] ? r : INT_MAX;
+        }
         if (blockIdx.x == 0 && blockIdx.y == 0)
             weights_token<EPL>(P.k, l, valid, rank, s_p, nullptr, nullptr, nullptr, P.ids_out, P.weights_out);
         const int y = blockIdx.y;
-        int e = -1, j = 0, cum = 0;
+        int ex = -1, j = 0, cum = 0;
 #pragma unroll
         for (int i = 0; i < EPL; i++) {
             unsigned long long mk = __ballot(valid[i] && rank[i] < P.k);
@@ -241,14 +277,14 @@ __device__ __forceinline__ bool route_one(const GroupParams &P, GroupLds g) {
             if (y >= cum && y < cum + c) {
                 for (int r = y - cum; r > 0; r--) mk &= mk - 1ull;
                 const int src = __ffsll((long long) mk) - 1;
-                e = src + kWave * i;
+                ex = src + kWave * i;
                 j = __builtin_amdgcn_readlane(rank[i], src);
             }
             cum += c;
         }
         if (lane == 0) {
-            g.misc[0] = e;
-            g.misc[1] = e >= 0 ? 1 : 0;
+            g.misc[0] = ex;
+            g.misc[1] = ex >= 0 ? 1 : 0;
             g.list[0] = j;
         }
     }
