@@ -56,6 +56,12 @@ def parse():
     ap.add_argument("--no-prefill", action="store_true")
     ap.add_argument("--prefill-layers", type=int, default=8)
     ap.add_argument("--no-decode", action="store_true", help="skip the decode legs (profiling the prefill leg alone)")
+    ap.add_argument("--stack235", action="store_true",
+                    help="also run the Qwen3-235B-A22B-shaped 94-layer Q4_K stack: resident (~128 GB of HBM) and "
+                         "with the pool capped at --pool-gib GiB (misses streamed from the pinned host tier)")
+    ap.add_argument("--stack235-layers", type=int, default=94)
+    ap.add_argument("--pool-gib", type=int, default=32)
+    ap.add_argument("--stream-tokens", type=int, default=8)
     ap.add_argument("--calibrate-copy-mib", type=int, default=0,
                     help="first run one device-to-device copy of this many MiB (the reference kernel that scales "
                          "rocprofv3's FETCH_SIZE / WRITE_SIZE counters to bytes)")
@@ -213,6 +219,101 @@ def prefill_leg(torch, L, n_layer, T, steps, warmup):
                 gate_up_tflops=flops_gu / gu_s / 1e12)
 
 
+def stack235_leg(torch, L, n_layer, pool_gib, steps, warmup, stream_tokens):
+    """The Qwen3-235B-A22B-shaped MoE stack (94 layers, h 4096, f 1536, 128 experts top-8, Q4_K,
+    Zipf(1.1)-biased F16 router), batch-1 decode, two runs:
+      resident   every expert of every layer in HBM (~128 GB): one captured HIP graph of the 94 MoE
+                 blocks per token (router, top-8, gate/up + SwiGLU, down, combine, residual);
+      streaming  the pool capped at pool_gib GiB (ExpertStore::init's slot split); per layer, in the
+                 order of Engine::run_segment (src/engine.cpp:343-399): router on the device, ids to
+                 the host, acquire (hits pin, misses evict the LRU head and are copied from the pinned
+                 host tier on the pool's side stream), experts on the slots, release_all.
+    One layer's expert bytes are generated and passed for every layer (the host tier then holds one
+    copy); every layer has its own HBM slots, router weights and hnorm rows."""
+    from localstack_amd import synth
+    H5, F5 = 4096, 1536
+    rng = np.random.default_rng(235)
+    t0 = time.time()
+    up, gate, down = (synth.experts(rng, Q4_K, E, F5, H5), synth.experts(rng, Q4_K, E, F5, H5),
+                      synth.experts(rng, Q4_K, E, H5, F5))
+    log(f"[bench] 235B stack: generated one layer of Q4_K experts ({3 * up.nbytes / 1e9:.2f} GB) in {time.time() - t0:.1f}s")
+    dev = torch.device("cuda:0")
+    d = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to(dev)
+    routers = [d(synth.zipf_router_f16(rng, E, H5)) for _ in range(n_layer)]
+    mat = 3538944  # bytes of one Q4_K expert matrix at this shape
+    layers = [((Q4_K,) * 3, up, gate, down)] * n_layer
+    res = {"n_layer": n_layer, "n_embd": H5, "n_ff_exp": F5}
+    # (i) resident
+    t0 = time.time()
+    store = L.ExpertStore(n_layer, H5, F5, E, K, 1, layers)
+    log(f"[bench] 235B stack: resident pool {store.total_bytes() / 1e9:.1f} GB in HBM, built in {time.time() - t0:.1f}s")
+    xs = [d(synth.activations(rng, 1, H5, bias_unit=True)) for _ in range(n_layer)]
+    resid = [d(synth.activations(rng, 1, H5)) for _ in range(n_layer)]
+    out = [torch.zeros((1, H5), dtype=torch.float32, device=dev) for _ in range(n_layer)]
+    ids = [torch.zeros((1, K), dtype=torch.int32, device=dev) for _ in range(n_layer)]
+    w = [torch.zeros((1, K), dtype=torch.float32, device=dev) for _ in range(n_layer)]
+
+    def step():
+        for l in range(n_layer):
+            store.block(l, xs[l], routers[l], 1, resid[l], out[l], ids[l], w[l])
+
+    step()
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        step()
+    ms = time_steps(torch, graph.replay, steps, warmup)
+    store.check()
+    per_tok = n_layer * (K * 3 * mat + E * H5 * 2 + H5 * 8)
+    res["resident"] = {"tok_s": 1000.0 / ms, "ms_per_token": ms, "bytes_per_token": per_tok,
+                       "gbs": per_tok / (ms * 1e-3) / 1e9, "frac_hbm": per_tok / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS,
+                       "hbm_gb": store.total_bytes() / 1e9}
+    del graph
+    store.close()
+    torch.cuda.synchronize()
+    torch.cuda.empty_cache()
+    # (ii) streaming, pool capped at pool_gib GiB
+    t0 = time.time()
+    store = L.ExpertStore(n_layer, H5, F5, E, K, 1, layers, pool_bytes=pool_gib << 30, min_slots=2 * K + 2,
+                          streaming=True)
+    log(f"[bench] 235B stack: streaming pool {store.total_bytes() / 2**30:.1f} GiB, {store.total_slots()} slots, "
+        f"built in {time.time() - t0:.1f}s")
+    # every token routes new hnorm rows (2 warm-up tokens + the timed ones)
+    n_tok = 2 + stream_tokens
+    xs_tok = [[d(synth.activations(rng, 1, H5, bias_unit=True)) for _ in range(n_layer)] for _ in range(n_tok)]
+    ids_h = torch.zeros((n_layer, K), dtype=torch.int32).pin_memory()
+    slots_h = torch.zeros((n_layer, K), dtype=torch.int32).pin_memory()
+    slots_d = torch.zeros((n_layer, K), dtype=torch.int32, device=dev)
+
+    def token(xt):
+        for l in range(n_layer):
+            store.route(l, xt[l], routers[l], 1, ids[l], w[l])
+            ids_h[l].copy_(ids[l][0])  # synchronous: the host needs the routing (as the reference does)
+            slots_h[l] = torch.from_numpy(store.acquire(l, ids_h[l].numpy()))
+            slots_d[l].copy_(slots_h[l], non_blocking=True)
+            store.ffn(l, xt[l], slots_d[l:l + 1], w[l], resid[l], out[l])
+            store.release_all()
+
+    for i in range(2):
+        token(xs_tok[i])
+    torch.cuda.synchronize()
+    s0 = store.stats()
+    t0 = time.time()
+    for i in range(stream_tokens):
+        token(xs_tok[2 + i])
+    torch.cuda.synchronize()
+    el = time.time() - t0
+    s1 = store.stats()
+    hits, misses = s1["hits"] - s0["hits"], s1["misses"] - s0["misses"]
+    rd = s1["bytes_read"] - s0["bytes_read"]
+    res["streaming"] = {"pool_gib": pool_gib, "slots": store.total_slots(), "tokens": stream_tokens,
+                        "tok_s": stream_tokens / el, "ms_per_token": el * 1e3 / stream_tokens,
+                        "hit_rate": hits / max(1, hits + misses), "misses_per_token": misses / stream_tokens,
+                        "host_to_hbm_gbs": rd / el / 1e9, "bytes_read_per_token": rd / stream_tokens}
+    store.close()
+    return res
+
+
 def cpu_baseline(T, seconds):
     """Times the oracle on this host over whole layer passes of the same workload."""
     import oracle
@@ -262,8 +363,13 @@ def main():
         log(f"[bench] calibration copy: {a.calibrate_copy_mib} MiB read, {a.calibrate_copy_mib} MiB written")
         del src, dst
     if a.no_decode:
-        pre = prefill_leg(torch, L, a.prefill_layers, 512, max(5, a.steps // 5), 2)
-        print(json.dumps({"prefill": pre}), flush=True)
+        out = {}
+        if not a.no_prefill:
+            out["prefill"] = prefill_leg(torch, L, a.prefill_layers, 512, max(5, a.steps // 5), 2)
+        if a.stack235:
+            out["stack235"] = stack235_leg(torch, L, a.stack235_layers, a.pool_gib, max(5, a.steps // 2), 2,
+                                           a.stream_tokens)
+        print(json.dumps(out), flush=True)
         return
     st = Stack(torch, L, a.layers, t_max=max(8, a.tokens))
     main_res, g = measure(torch, st, a.tokens, a.steps, a.warmup, not a.no_graph)
@@ -283,6 +389,10 @@ def main():
                            "frac_int8_peak": pre["layer_tflops"] / INT8_PEAK_TOPS,
                            "achieved_gbs": pre["layer_hbm_gbs"], "hbm_peak_gbs": HBM_PEAK_GBS,
                            "frac_hbm": pre["layer_hbm_gbs"] / HBM_PEAK_GBS}
+    s235 = None
+    if a.stack235:
+        s235 = stack235_leg(torch, L, a.stack235_layers, a.pool_gib, max(5, a.steps // 2), 2, a.stream_tokens)
+        log(f"[bench] 235B stack: {json.dumps(s235)}")
     cpu = None if a.no_cpu else cpu_baseline(a.tokens, a.cpu_seconds)
     gu_avg_s = main_res["stage_avg_us"]["gate_up"] * 1e-6
     achieved = main_res["gate_up_bytes"] / gu_avg_s / 1e9
@@ -312,6 +422,7 @@ def main():
                                           "stack_gbs": extra["layer_gbs"], "stage_avg_us": extra["stage_avg_us"],
                                           "distinct_experts_per_layer": extra["distinct_experts_per_layer"]},
         "prefill": pre,
+        "stack235": s235,
         "cpu_baseline": cpu,
     }
     print(json.dumps(line), flush=True)

@@ -91,7 +91,8 @@ int lstk_abi_version(void);
  * (up, gate, down) type triple, each group gets pool_bytes * n_layers_in_group / n_layer, shards hold
  * at most 1024 slots and at least min_slots; the full expert table is copied once into pinned host
  * memory (the host tier, standing in for the GGUF file) and misses are served from it with
- * hipMemcpyAsync on the pool's side stream.
+ * hipMemcpyAsync on the pool's side stream. Layers that pass the same three host pointers (and
+ * types) share one host-tier copy.
  * The layers' host pointers are only read during this call. */
 int lstk_pool_create(const lstk_moe_dims *dims, const lstk_expert_layer *layers, size_t pool_bytes,
                      uint32_t min_slots, uint32_t flags, lstk_pool **out);

@@ -581,8 +581,26 @@ __global__ __launch_bounds__(kBlock) void down_combine_kernel(DownCombineParams 
     // unconditional loads (indexes clamped), so the weight loads follow without a branch
     int b = P.ids[min(j, k - 1)];
     const float wj = P.weights[min(tid, k - 1)];
-    float v[NP][8];
-    quantize_row_load<NP>(P.act, nact, v);
+    // Q8_0 activations: NP whole 32-value blocks per thread (one amax and one pair of divisions per
+    // block); Q8_K: NP passes of 8 values per thread (32 threads per 256-value block)
+    constexpr int NV = QT == kTypeQ8_0 ? 32 : 8;
+    float v[NP][NV];
+    if constexpr (QT == kTypeQ8_0) {
+#pragma unroll
+        for (int u = 0; u < NP; u++) {
+            const int blk = min(tid + u * (int) blockDim.x, nact / 32 - 1);
+#pragma unroll
+            for (int q4 = 0; q4 < 8; q4++) {
+                const float4 a = *reinterpret_cast<const float4 *>(P.act + (size_t) blk * 32 + 4 * q4);
+                v[u][4 * q4] = a.x;
+                v[u][4 * q4 + 1] = a.y;
+                v[u][4 * q4 + 2] = a.z;
+                v[u][4 * q4 + 3] = a.w;
+            }
+        }
+    } else {
+        quantize_row_load<NP>(P.act, nact, v);
+    }
     if (b < 0 || b >= P.n_bins) {
         if (on && blockIdx.x == 0 && rr == 0 && sb == 0) atomicOr(P.err, 1);
         b = min(max(b, 0), P.n_bins - 1);
@@ -591,7 +609,33 @@ __global__ __launch_bounds__(kBlock) void down_combine_kernel(DownCombineParams 
     uint4 w[C];
 #pragma unroll
     for (int c = 0; c < C; c++) w[c] = *reinterpret_cast<const uint4 *>(base + chunk_offset(C, P.h, on ? sb : 0, c, row));
-    quantize_row_store<QT, NP>(v, nact, qs, qd, qb);
+    if constexpr (QT == kTypeQ8_0) {
+        // quantize_row_q8_0 (x86 path): d = amax / 127 stored as fp16, q = rne(x * 127 / amax)
+#pragma unroll
+        for (int u = 0; u < NP; u++) {
+            const int blk = tid + u * (int) blockDim.x;
+            if (blk < nact / 32) {
+                float amax = 0.0f;
+#pragma unroll
+                for (int i = 0; i < 32; i++) amax = fmaxf(amax, fabsf(v[u][i]));
+                const float id = amax != 0.0f ? __fdiv_rn(127.0f, amax) : 0.0f;
+                unsigned pk[8];
+#pragma unroll
+                for (int w4 = 0; w4 < 8; w4++) {
+                    unsigned word = 0;
+#pragma unroll
+                    for (int bb = 0; bb < 4; bb++) word |= ((unsigned) (int) rintf(v[u][4 * w4 + bb] * id) & 0xffu) << (8 * bb);
+                    pk[w4] = word;
+                }
+                uint4 *dst = reinterpret_cast<uint4 *>(qs + (size_t) blk * 32);
+                dst[0] = make_uint4(pk[0], pk[1], pk[2], pk[3]);
+                dst[1] = make_uint4(pk[4], pk[5], pk[6], pk[7]);
+                qd[blk] = round_f16(__fdiv_rn(amax, 127.0f));
+            }
+        }
+    } else {
+        quantize_row_store<QT, NP>(v, nact, qs, qd, qb);
+    }
     if (tid < k) s_w[tid] = wj;
     __syncthreads();
     if (on) {
@@ -714,7 +758,9 @@ hipError_t launch_down_combine_t(const DownCombineParams &P, hipStream_t st, con
     const int rd = down_combine_rows(P.f, P.k), nsbf = P.f / 256, nact = P.k * P.f;
     const int threads = (P.k * nsbf * rd + kWave - 1) / kWave * kWave;
     const size_t lds = (size_t) nact + (size_t) nact / 32 * 8 + (size_t) P.k * nsbf * rd * 4 + (size_t) P.k * 4;
-    const int np = (nact + threads * 8 - 1) / (threads * 8);
+    // Q8_0: whole 32-value blocks per thread; Q8_K: passes of 8 values per thread
+    const int per = WT == kTypeQ4_K ? threads * 8 : threads * 32;
+    const int np = (nact + per - 1) / per;
     const dim3 grid(P.h / rd), block(threads);
     if (np <= 1) return launch(down_combine_kernel<WT, 1>, grid, block, lds, st, tm, P, rd);
     if (np <= 2) return launch(down_combine_kernel<WT, 2>, grid, block, lds, st, tm, P, rd);
@@ -729,7 +775,7 @@ bool down_combine_supported(int h, int f, int k) {
     if (k * (f / 256) > kBlock) return false;
     const int rd = down_combine_rows(f, k);
     const int threads = (k * (f / 256) * rd + kWave - 1) / kWave * kWave;
-    return h % rd == 0 && (long) k * f <= 8L * threads * 8;
+    return h % rd == 0 && (long) k * f <= 8L * threads * 8; // at most 8 passes (or blocks) per thread
 }
 
 hipError_t launch_down_combine(const DownCombineParams &P, hipStream_t st, const LaunchTiming *tm) {

@@ -368,9 +368,23 @@ int create(const lstk_moe_dims *dims, const lstk_expert_layer *layers, size_t po
     }
     const int h = d.n_embd, f = d.n_ff_exp, E = d.n_expert;
     if (P->streaming) {
-        // pinned host tier with every layer's experts in pool layout (the stand-in for the GGUF file)
+        // pinned host tier with every layer's experts in pool layout (the stand-in for the GGUF file);
+        // layers that pass the same host matrices (and so the same types) share one copy
+        std::vector<int> first_of(d.n_layer);
         size_t total = 0;
-        for (int l = 0; l < d.n_layer; l++) total += (size_t) E * P->shards[P->layer_shard[l]].slab;
+        for (int l = 0; l < d.n_layer; l++) {
+            first_of[l] = l;
+            for (int q = 0; q < l; q++) {
+                if (first_of[q] == q && layers[q].host_up == layers[l].host_up &&
+                    layers[q].host_gate == layers[l].host_gate && layers[q].host_down == layers[l].host_down &&
+                    layers[q].type_up == layers[l].type_up && layers[q].type_gate == layers[l].type_gate &&
+                    layers[q].type_down == layers[l].type_down) {
+                    first_of[l] = q;
+                    break;
+                }
+            }
+            if (first_of[l] == l) total += (size_t) E * P->shards[P->layer_shard[l]].slab;
+        }
         if ((e = hipHostMalloc((void **) &P->tier, total, hipHostMallocDefault)) != hipSuccess) {
             destroy(P);
             return fail(LSTK_E_NOMEM, std::string("cannot allocate the pinned host tier: ") + hipGetErrorString(e));
@@ -378,6 +392,10 @@ int create(const lstk_moe_dims *dims, const lstk_expert_layer *layers, size_t po
         size_t off = 0;
         P->tier_of.resize(d.n_layer);
         for (int l = 0; l < d.n_layer; l++) {
+            if (first_of[l] != l) {
+                P->tier_of[l] = P->tier_of[first_of[l]];
+                continue;
+            }
             const Shard &s = P->shards[P->layer_shard[l]];
             uint8_t *u = P->tier + off, *g = u + (size_t) E * s.up_bytes, *dn = g + (size_t) E * s.gate_bytes;
             P->tier_of[l] = {u, g, dn};

@@ -38,6 +38,8 @@ def model(name):
         "30b_q4": dict(h=2048, f=768, E=128, k=8, types=(Q4_K,) * 3, n_layer=1, n_batch=512),
         # mixed classes: Q4_K gate/up, Q8_0 down
         "mixed": dict(h=256, f=768, E=16, k=4, types=(Q4_K, Q4_K, Q8_0), n_layer=1, n_batch=64),
+        # Qwen3-235B-A22B MoE layer shape (h 4096, f 1536, top-8, Q4_K) over 16 experts
+        "235b_q4": dict(h=4096, f=1536, E=16, k=8, types=(Q4_K,) * 3, n_layer=1, n_batch=64),
     }[name]
     rng = np.random.default_rng(sum(map(ord, name)))
     layers = [layer_bytes(rng, cfg["types"], cfg["E"], cfg["h"], cfg["f"]) for _ in range(cfg["n_layer"])]
@@ -98,7 +100,8 @@ def test_route_f32_weights_and_zipf(orc, lstk, dev):
 
 
 @pytest.mark.parametrize("name,T", [("tiny", 1), ("tiny", 16), ("30b_q8", 1), ("30b_q8", 8), ("30b_q8", 32),
-                                    ("30b_q4", 1), ("30b_q4", 8), ("30b_q4", 64), ("mixed", 5)])
+                                    ("30b_q4", 1), ("30b_q4", 8), ("30b_q4", 64), ("mixed", 5), ("235b_q4", 1),
+                                    ("235b_q4", 8), ("235b_q4", 64)])
 def test_ffn_matches_oracle(orc, lstk, dev, name, T):
     import torch
     cfg, layers, routers, store = model(name)
@@ -117,7 +120,7 @@ def test_ffn_matches_oracle(orc, lstk, dev, name, T):
     assert err <= FFN_TOL
 
 
-@pytest.mark.parametrize("name,T", [("tiny", 16), ("30b_q8", 1), ("30b_q8", 8), ("30b_q4", 16)])
+@pytest.mark.parametrize("name,T", [("tiny", 16), ("30b_q8", 1), ("30b_q8", 8), ("30b_q4", 16), ("235b_q4", 1)])
 def test_block_matches_oracle(orc, lstk, dev, name, T):
     import torch
     cfg, layers, routers, store = model(name)
@@ -199,6 +202,35 @@ def test_streaming_pool_is_bit_identical_to_resident(orc, lstk, dev):
             assert np.array_equal(got[l], ref[l]), (name, l)
         print(f"[stream {name}] {st.stats()}", flush=True)
     assert chunked.stats()["misses"] > 0 and chunked.layer_slots(0) == 2 * k + 2
+
+
+def test_streaming_layers_sharing_host_matrices(orc, lstk, dev):
+    # layers passed the same host matrices share one host-tier copy; every layer still owns its own
+    # slots, and the result equals the resident pool's bit for bit
+    import torch
+    import localstack_amd as L
+    cfg, layers, routers, res_store = model("tiny")
+    T, k, h, E = 8, cfg["k"], cfg["h"], cfg["E"]
+    lb = (cfg["types"],) + layers[0]
+    shared = L.ExpertStore(3, h, cfg["f"], E, k, T, [lb] * 3, pool_bytes=1, min_slots=E, streaming=True)
+    resident = L.ExpertStore(3, h, cfg["f"], E, k, T, [lb] * 3)
+    rng = np.random.default_rng(410)
+    for step in range(3):
+        for l in range(3):
+            x = synth.activations(rng, T, h)
+            resid = synth.activations(rng, T, h)
+            rids, rw, _, _ = orc.router(x, routers[0], 1, k)
+            outs = []
+            for st, streaming in ((shared, True), (resident, False)):
+                slots = st.acquire(l, rids) if streaming else rids
+                o = torch.zeros((T, h), dtype=torch.float32, device=dev)
+                st.ffn(l, to_dev(x, dev), to_dev(slots, dev), to_dev(rw, dev), to_dev(resid, dev), o)
+                if streaming:
+                    st.release_all()
+                st.check()
+                outs.append(o.cpu().numpy())
+            assert np.array_equal(outs[0], outs[1]), (step, l)
+    assert shared.stats()["misses"] > 0
 
 
 def test_bad_ids_are_reported_not_faulted(orc, lstk, dev):
