@@ -557,6 +557,72 @@ __global__ __launch_bounds__(kDnRows * kMaxG) void down_kernel(DownParams P) {
 
 constexpr int kDcMaxAct = 16384; // k * f SwiGLU values quantized in a work-group's LDS
 
+// Q8_K quantization (quantize_row_q8_K_ref) of one 256-value block by `lanes` consecutive lanes of a
+// wavefront, lane r holding values [r VPT, (r + 1) VPT) of the block in v: the first largest |x| of
+// the block (ties to the lower index) by a shuffle reduction over the lanes, iscale = -127 / max,
+// q = min(127, rne(iscale x)), d = 1 / iscale. Writes the block's qs (at qs), its scale into each of
+// the 8 per-32 slots d8[0..8) and the per-32 sums of q into bs8[0..8).
+template <int VPT>
+__device__ __forceinline__ void q8k_block_lanes(const float (&v)[VPT], int lanes, int r, int8_t *qs, float *d8,
+                                                int *bs8) {
+    float amax = 0.0f, mx = 0.0f;
+    int idx = INT_MAX;
+#pragma unroll
+    for (int i = 0; i < VPT; i++) {
+        const float ax = fabsf(v[i]);
+        if (ax > amax) {
+            amax = ax;
+            mx = v[i];
+            idx = r * VPT + i;
+        }
+    }
+    for (int o = 1; o < lanes; o <<= 1) {
+        const float oa = __shfl_xor(amax, o), om = __shfl_xor(mx, o);
+        const int oi = __shfl_xor(idx, o);
+        if (oa > amax || (oa == amax && oi < idx)) {
+            amax = oa;
+            mx = om;
+            idx = oi;
+        }
+    }
+    int q[VPT];
+    float dd = 0.0f;
+    if (amax == 0.0f) {
+#pragma unroll
+        for (int i = 0; i < VPT; i++) q[i] = 0;
+    } else {
+        const float iscale = __fdiv_rn(-127.0f, mx);
+#pragma unroll
+        for (int i = 0; i < VPT; i++) q[i] = min(127, (int) rintf(iscale * v[i]));
+        dd = __fdiv_rn(1.0f, iscale);
+    }
+#pragma unroll
+    for (int w4 = 0; w4 < VPT / 4; w4++) {
+        const unsigned word = ((unsigned) q[4 * w4] & 0xffu) | (((unsigned) q[4 * w4 + 1] & 0xffu) << 8) |
+                              (((unsigned) q[4 * w4 + 2] & 0xffu) << 16) | (((unsigned) q[4 * w4 + 3] & 0xffu) << 24);
+        reinterpret_cast<unsigned *>(qs + r * VPT)[w4] = word;
+    }
+    if (VPT >= 32) {
+#pragma unroll
+        for (int g = 0; g < VPT / 32; g++) {
+            int sum = 0;
+#pragma unroll
+            for (int i = 0; i < 32; i++) sum += q[32 * g + i];
+            bs8[r * (VPT / 32) + g] = sum;
+            d8[r * (VPT / 32) + g] = dd;
+        }
+    } else {
+        int sum = 0;
+#pragma unroll
+        for (int i = 0; i < VPT; i++) sum += q[i];
+        for (int o = 1; o < 32 / VPT; o <<= 1) sum += __shfl_xor(sum, o);
+        if (r % (32 / VPT) == 0) {
+            bs8[r / (32 / VPT)] = sum;
+            d8[r / (32 / VPT)] = dd;
+        }
+    }
+}
+
 // Thread (q, rr) with q = j * nsbf + sb holds super-block sb of row blockIdx.x * rd + rr of pair j's
 // down matrix. The pair's slot and the token's k SwiGLU rows are loaded first (one round trip), the
 // weight loads are issued as soon as the slot is known, and the SwiGLU rows are quantized into LDS
@@ -564,15 +630,19 @@ constexpr int kDcMaxAct = 16384; // k * f SwiGLU values quantized in a work-grou
 // and threads rr < rd sum, per pair j in ascending order, the partials over sb ascending (the
 // order of down_kernel), multiply by the router weight and add the pairs left to right in j, then
 // the residual (the order of combine_kernel), so the result equals down + combine bit for bit.
-template <int WT, int NP>
-__global__ __launch_bounds__(kBlock) void down_combine_kernel(DownCombineParams P, int rd) {
+// SEG > 0 (Q8_K activations with k * nsbf * rd0 threads exactly): the rd0 threads of pair j and
+// super-block sb quantize that 256-value Q8_K block together, SEG = 256 / rd0 values each, in one
+// pass (q8k_block_lanes); otherwise every thread takes NP passes of 8 values (quantize_row).
+template <int WT, int NP, int R, int SEG>
+__global__ __launch_bounds__(kBlock) void down_combine_kernel(DownCombineParams P, int rd0) {
     constexpr int C = chunks_of(WT);
     constexpr int QT = WT == kTypeQ4_K ? kTypeQ4_K : kTypeQ8_0;
     extern __shared__ __align__(16) unsigned char smem[];
     const int tid = threadIdx.x, k = P.k, f = P.f, nsbf = f / 256, nact = k * f;
-    const int rr = tid % rd, q = tid / rd, sb = q % nsbf, j = q / nsbf;
+    // R rows per thread: local row ir * rd0 + rr of the work-group's rd = R * rd0 rows
+    const int rd = R * rd0;
+    const int rr = tid % rd0, q = tid / rd0, sb = q % nsbf, j = q / nsbf;
     const bool on = j < k;
-    const int row = blockIdx.x * rd + rr;
     int8_t *qs = reinterpret_cast<int8_t *>(smem);
     float *qd = reinterpret_cast<float *>(smem + nact);
     int *qb = reinterpret_cast<int *>(qd + nact / 32);
@@ -585,7 +655,18 @@ __global__ __launch_bounds__(kBlock) void down_combine_kernel(DownCombineParams 
     // block); Q8_K: NP passes of 8 values per thread (32 threads per 256-value block)
     constexpr int NV = QT == kTypeQ8_0 ? 32 : 8;
     float v[NP][NV];
-    if constexpr (QT == kTypeQ8_0) {
+    float vs[SEG > 0 ? SEG : 1];
+    if constexpr (SEG > 0) {
+        const float4 *src = reinterpret_cast<const float4 *>(P.act + (size_t) min(q, nact / 256 - 1) * 256 + rr * SEG);
+#pragma unroll
+        for (int i = 0; i < SEG / 4; i++) {
+            const float4 a = src[i];
+            vs[4 * i] = a.x;
+            vs[4 * i + 1] = a.y;
+            vs[4 * i + 2] = a.z;
+            vs[4 * i + 3] = a.w;
+        }
+    } else if constexpr (QT == kTypeQ8_0) {
 #pragma unroll
         for (int u = 0; u < NP; u++) {
             const int blk = min(tid + u * (int) blockDim.x, nact / 32 - 1);
@@ -606,10 +687,16 @@ __global__ __launch_bounds__(kBlock) void down_combine_kernel(DownCombineParams 
         b = min(max(b, 0), P.n_bins - 1);
     }
     const uint8_t *base = P.w_down + (size_t) b * P.stride_down;
-    uint4 w[C];
+    uint4 w[R][C];
 #pragma unroll
-    for (int c = 0; c < C; c++) w[c] = *reinterpret_cast<const uint4 *>(base + chunk_offset(C, P.h, on ? sb : 0, c, row));
-    if constexpr (QT == kTypeQ8_0) {
+    for (int ir = 0; ir < R; ir++) {
+        const int row = blockIdx.x * rd + ir * rd0 + rr;
+#pragma unroll
+        for (int c = 0; c < C; c++) w[ir][c] = *reinterpret_cast<const uint4 *>(base + chunk_offset(C, P.h, on ? sb : 0, c, row));
+    }
+    if constexpr (SEG > 0) {
+        q8k_block_lanes<SEG>(vs, rd0, rr, qs + (size_t) q * 256, qd + (size_t) q * 8, qb + (size_t) q * 8);
+    } else if constexpr (QT == kTypeQ8_0) {
         // quantize_row_q8_0 (x86 path): d = amax / 127 stored as fp16, q = rne(x * 127 / amax)
 #pragma unroll
         for (int u = 0; u < NP; u++) {
@@ -640,7 +727,9 @@ __global__ __launch_bounds__(kBlock) void down_combine_kernel(DownCombineParams 
     __syncthreads();
     if (on) {
         const int o = j * f + sb * 256;
-        part[(j * rd + rr) * nsbf + sb] = dot_sb<WT>(w, qs + o, qd + o / 32, qb + o / 32, 0.0f);
+#pragma unroll
+        for (int ir = 0; ir < R; ir++)
+            part[(j * rd + ir * rd0 + rr) * nsbf + sb] = dot_sb<WT>(w[ir], qs + o, qd + o / 32, qb + o / 32, 0.0f);
     }
     __syncthreads();
     if (tid < rd) {
@@ -745,7 +834,8 @@ hipError_t launch_down_t(const DownParams &P, int G, hipStream_t st, const Launc
     return launch(down_kernel<WT, S>, dim3(P.h / kDnRows, P.max_active), dim3(kDnRows * G), lds, st, tm, P);
 }
 
-// Rows per down_combine work-group: the largest power of two with k * nsbf * rd <= 256 threads.
+// Row stride of a down_combine work-group: the largest power of two rd0 with k * nsbf * rd0 <= 256
+// threads.
 int down_combine_rows(int f, int k) {
     const int per = k * (f / 256);
     int rd = 1;
@@ -753,19 +843,47 @@ int down_combine_rows(int f, int k) {
     return rd;
 }
 
+// Rows per thread: up to 4 (Q4_K) or 2 (Q8_0) while the grid keeps at least 256 work-groups, so a
+// wide layer does not quantize the token's SwiGLU rows in more work-groups than the device has CUs.
+int down_combine_rows_per_thread(int type, int h, int rd0) {
+    const int rmax = type == kTypeQ4_K ? 4 : 2;
+    int r = 1;
+    while (r < rmax && h % (rd0 * r * 2) == 0 && h / (rd0 * r * 2) >= 256) r *= 2;
+    return r;
+}
+
+template <int WT, int R>
+hipError_t launch_down_combine_r(const DownCombineParams &P, int rd0, int np, size_t lds, int threads, hipStream_t st,
+                                 const LaunchTiming *tm) {
+    const dim3 grid(P.h / (rd0 * R)), block(threads);
+    if (WT == kTypeQ4_K && threads == P.k * (P.f / 256) * rd0) {
+        // one Q8_K block per (pair, super-block), quantized by that combination's rd0 threads
+        switch (rd0) {
+            case 4: return launch(down_combine_kernel<WT, 1, R, 64>, grid, block, lds, st, tm, P, rd0);
+            case 8: return launch(down_combine_kernel<WT, 1, R, 32>, grid, block, lds, st, tm, P, rd0);
+            case 16: return launch(down_combine_kernel<WT, 1, R, 16>, grid, block, lds, st, tm, P, rd0);
+            case 32: return launch(down_combine_kernel<WT, 1, R, 8>, grid, block, lds, st, tm, P, rd0);
+            default: break;
+        }
+    }
+    if (np <= 1) return launch(down_combine_kernel<WT, 1, R, 0>, grid, block, lds, st, tm, P, rd0);
+    if (np <= 2) return launch(down_combine_kernel<WT, 2, R, 0>, grid, block, lds, st, tm, P, rd0);
+    if (np <= 4) return launch(down_combine_kernel<WT, 4, R, 0>, grid, block, lds, st, tm, P, rd0);
+    return launch(down_combine_kernel<WT, 8, R, 0>, grid, block, lds, st, tm, P, rd0);
+}
+
 template <int WT>
 hipError_t launch_down_combine_t(const DownCombineParams &P, hipStream_t st, const LaunchTiming *tm) {
-    const int rd = down_combine_rows(P.f, P.k), nsbf = P.f / 256, nact = P.k * P.f;
-    const int threads = (P.k * nsbf * rd + kWave - 1) / kWave * kWave;
-    const size_t lds = (size_t) nact + (size_t) nact / 32 * 8 + (size_t) P.k * nsbf * rd * 4 + (size_t) P.k * 4;
+    const int rd0 = down_combine_rows(P.f, P.k), nsbf = P.f / 256, nact = P.k * P.f;
+    const int R = down_combine_rows_per_thread(WT, P.h, rd0);
+    const int threads = (P.k * nsbf * rd0 + kWave - 1) / kWave * kWave;
+    const size_t lds = (size_t) nact + (size_t) nact / 32 * 8 + (size_t) P.k * nsbf * rd0 * R * 4 + (size_t) P.k * 4;
     // Q8_0: whole 32-value blocks per thread; Q8_K: passes of 8 values per thread
     const int per = WT == kTypeQ4_K ? threads * 8 : threads * 32;
     const int np = (nact + per - 1) / per;
-    const dim3 grid(P.h / rd), block(threads);
-    if (np <= 1) return launch(down_combine_kernel<WT, 1>, grid, block, lds, st, tm, P, rd);
-    if (np <= 2) return launch(down_combine_kernel<WT, 2>, grid, block, lds, st, tm, P, rd);
-    if (np <= 4) return launch(down_combine_kernel<WT, 4>, grid, block, lds, st, tm, P, rd);
-    return launch(down_combine_kernel<WT, 8>, grid, block, lds, st, tm, P, rd);
+    if (R == 4) return launch_down_combine_r<WT, 4>(P, rd0, np, lds, threads, st, tm);
+    if (R == 2) return launch_down_combine_r<WT, 2>(P, rd0, np, lds, threads, st, tm);
+    return launch_down_combine_r<WT, 1>(P, rd0, np, lds, threads, st, tm);
 }
 
 }  // namespace

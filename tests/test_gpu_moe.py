@@ -268,7 +268,7 @@ def test_stage_timing_counts_launches(orc, lstk, dev):
     assert n == [3 + 2, 4, 4, 1] and all(m > 0 for m in ms)
 
 
-@pytest.mark.parametrize("name", ["tiny", "30b_q8", "30b_q4", "mixed"])
+@pytest.mark.parametrize("name", ["tiny", "30b_q8", "30b_q4", "mixed", "235b_q4"])
 def test_single_token_equals_batched_row(orc, lstk, dev, name):
     """A single token (gate_up ranking its experts, down + combine in one launch) gives the bits of
     the same token inside a batch (separate top-k, down and combine launches)."""
