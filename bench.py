@@ -345,6 +345,21 @@ def cpu_baseline(T, seconds):
                        f"{per_layer * 1e3:.2f} ms per layer")
 
 
+def measured_traffic(key):
+    """HBM bytes per launch of a kernel from the committed rocprofv3 PMC summary (FETCH_SIZE and
+    WRITE_SIZE passes scaled by a plain copy of known size; the commands are in the file), or None."""
+    path = os.path.join(ROOT, "profiles", "moe_decode_30b_q8_0_traffic.txt")
+    try:
+        with open(path) as fh:
+            for line in fh:
+                parts = line.split()
+                if len(parts) == 3 and parts[0] == "traffic_bytes_per_launch" and parts[1] == key:
+                    return float(parts[2])
+    except OSError:
+        pass
+    return None
+
+
 def main():
     a = parse()
     if a.gpus != 1:
@@ -413,7 +428,9 @@ def main():
                                f"F16 router", "n_layer": a.layers, "tokens": a.tokens, "n_embd": H, "n_ff_exp": F,
                    "n_expert": E, "top_k": K, "expert_type": "Q8_0", "hip_graph": main_res["graph"]},
         "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": achieved / HBM_PEAK_GBS, "traffic": None, "kernel": "gate_up",
+                     "frac": achieved / HBM_PEAK_GBS,
+                     "traffic": measured_traffic("gate_up_T1") if (a.tokens == 1 and a.layers == N_LAYER) else None,
+                     "kernel": "gate_up",
                      "kernel_avg_us": main_res["stage_avg_us"]["gate_up"],
                      "bytes_per_launch": main_res["gate_up_bytes"]},
         "stack_gbs": main_res["layer_gbs"],
