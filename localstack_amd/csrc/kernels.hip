@@ -39,6 +39,9 @@ constexpr int kMaxBins = 4096;
 constexpr int kMaxPairs = 8192;   // n_batch * n_expert_used
 typedef int xvec __attribute__((ext_vector_type(4))); // 16 bytes of int8 activations
 constexpr int kDecodeRouteT = 1;  // gate_up runs the top-k itself for a single token
+// Threads of a gate_up work-group: single-token (routing) launches use 512 (32 rows per matrix at
+// h = 2048; fewer, larger work-groups stream the 8 experts' rows faster on MI355X), batches 256.
+constexpr int kGuRouteBlock = 512;
 
 
 // ------------------------------------------------------------------------------------------------
@@ -190,7 +193,7 @@ struct GroupLds {
 
 // route mode: the selected probabilities of weights_token, then the experts' 64-bit keys, the
 // partial rank counts and the logits of route_one
-constexpr size_t kTopkLds = (size_t) kMaxK * 4 + (size_t) kMaxEPL * kWave * 8 + (size_t) kBlock * 4 +
+constexpr size_t kTopkLds = (size_t) kMaxK * 4 + (size_t) kMaxEPL * kWave * 8 + (size_t) kGuRouteBlock * 4 +
                             (size_t) kMaxEPL * kWave * 4;
 
 // The top-k scratch and the weights exist only when the work-group routes (route = 1).
@@ -230,10 +233,10 @@ __device__ __forceinline__ GroupLds group_lds(unsigned char *base, int T, int k,
 template <int EPL>
 __device__ __forceinline__ bool route_one(const GroupParams &P, GroupLds g) {
     const int tid = threadIdx.x, lane = tid % kWave, wave = tid / kWave;
-    const int E = P.E, Ep = EPL * kWave, nsplit = kBlock / Ep, span = Ep / nsplit;
+    const int E = P.E, Ep = EPL * kWave, nsplit = (int) blockDim.x / Ep, span = Ep / nsplit;
     unsigned long long *s_key = reinterpret_cast<unsigned long long *>(g.scratch + kMaxK * 4); // [Ep]
     int *s_cnt = reinterpret_cast<int *>(s_key + Ep);                                          // [nsplit][Ep]
-    float *s_l = reinterpret_cast<float *>(s_cnt + kBlock);                                    // [Ep]
+    float *s_l = reinterpret_cast<float *>(s_cnt + kGuRouteBlock);                             // [Ep]
     float *s_p = reinterpret_cast<float *>(g.scratch);
     const int e = tid % Ep, part = tid / Ep;
     const float le = P.logits[min(e, E - 1)];
@@ -371,16 +374,16 @@ __device__ __forceinline__ bool group_pairs(const GroupParams &P, GroupLds g) {
 // gate + up + SwiGLU
 // ------------------------------------------------------------------------------------------------
 
-// Work-group (row block, y): rows = 128 / G per matrix, thread (g, m, r) holds super-blocks
+// Work-group (row block, y) of NT threads: rows RW = NT / (2 G) per matrix, thread (g, m, r) holds super-blocks
 // g, g + G, ... of row r of gate (m = 0) or up (m = 1) in registers, loaded before anything else.
 // The y-th active expert's tokens are staged 8 at a time in LDS; partial dots are reduced over g in
 // ascending order, then act[pair] = silu(gate) * up.
-template <int WT, int S, bool ROUTE>
-__global__ __launch_bounds__(kBlock) void gate_up_kernel(GateUpParams P) {
+template <int WT, int S, bool ROUTE, int NT>
+__global__ __launch_bounds__(NT) void gate_up_kernel(GateUpParams P) {
     constexpr int C = chunks_of(WT);
     extern __shared__ __align__(16) unsigned char smem[];
     const int G = P.h / 256 / S;
-    const int RW = 128 / G;
+    const int RW = NT / (2 * G);
     const int tid = threadIdx.x;
     const int r = tid % RW, m = (tid / RW) & 1, g = tid / (2 * RW);
     const int f = P.f, h = P.h, k = P.gp.k;
@@ -816,14 +819,29 @@ hipError_t launch_route_g(const RouteParams &P, hipStream_t st, const LaunchTimi
     }
 }
 
+// Dynamic LDS of a gate_up launch: grouping, kTC staged tokens and the partial sums of RW rows.
+size_t gate_up_lds(int T, int k, int n_bins, int route, int h, int G, int RW) {
+    return align16(group_lds_bytes(T, k, n_bins, route)) + 16 + (size_t) kTC * h + (size_t) 2 * kTC * (h / 32) * 4 +
+           (size_t) kTC * G * 2 * RW * 4;
+}
+
 template <int WT, int S>
 hipError_t launch_gate_up_t(const GateUpParams &P, int G, hipStream_t st, const LaunchTiming *tm) {
-    const int h32 = P.h / 32, RW = 128 / G;
-    const size_t lds = align16(group_lds_bytes(P.gp.T, P.gp.k, P.gp.n_bins, P.gp.route)) + 16 + (size_t) kTC * P.h +
-                       (size_t) 2 * kTC * h32 * 4 + (size_t) kTC * G * 2 * RW * 4;
-    if (P.gp.route)
-        return launch(gate_up_kernel<WT, S, true>, dim3(P.f / RW, P.max_active), dim3(2 * RW * G), lds, st, tm, P);
-    return launch(gate_up_kernel<WT, S, false>, dim3(P.f / RW, P.max_active), dim3(2 * RW * G), lds, st, tm, P);
+    if (P.gp.route) {
+        const int RW = kGuRouteBlock / (2 * G);
+        const size_t lds = gate_up_lds(P.gp.T, P.gp.k, P.gp.n_bins, 1, P.h, G, RW);
+        return launch(gate_up_kernel<WT, S, true, kGuRouteBlock>, dim3(P.f / RW, P.max_active), dim3(kGuRouteBlock), lds,
+                      st, tm, P);
+    }
+    if (P.gp.T == 1) { // one token with caller-given slots: the single-token shape as well
+        const int RW = kGuRouteBlock / (2 * G);
+        const size_t lds = gate_up_lds(1, P.gp.k, P.gp.n_bins, 0, P.h, G, RW);
+        return launch(gate_up_kernel<WT, S, false, kGuRouteBlock>, dim3(P.f / RW, P.max_active), dim3(kGuRouteBlock),
+                      lds, st, tm, P);
+    }
+    const int RW = kBlock / (2 * G);
+    const size_t lds = gate_up_lds(P.gp.T, P.gp.k, P.gp.n_bins, 0, P.h, G, RW);
+    return launch(gate_up_kernel<WT, S, false, kBlock>, dim3(P.f / RW, P.max_active), dim3(kBlock), lds, st, tm, P);
 }
 
 template <int WT, int S>
@@ -920,11 +938,11 @@ const char *check_shapes(int h, int f, int E, int k, int n_bins, int n_batch) {
     if (!pick_split_gate_up(h / 256, &S, &G)) return "n_embd / 256 must split into 1, 2, 4 or 8 groups of <= 2 super-blocks";
     if (!pick_split(f / 256, &S, &G)) return "n_ff_exp / 256 has no split into <= 8 groups of <= 2 super-blocks";
     pick_split_gate_up(h / 256, &S, &G);
-    if (f % (128 / G) != 0) return "n_ff_exp must be a multiple of the gate/up row block";
+    if (f % (kGuRouteBlock / (2 * G)) != 0 || f % (kBlock / (2 * G)) != 0)
+        return "n_ff_exp must be a multiple of the gate/up row block";
     // LDS: grouping + staging must fit in 64 KiB
-    const size_t work = 16 + (size_t) kTC * h + (size_t) 2 * kTC * (h / 32) * 4 + (size_t) kTC * G * 2 * (128 / G) * 4;
-    const size_t gu_route = align16(group_lds_bytes(std::min(n_batch, kDecodeRouteT), k, n_bins, 1)) + work;
-    const size_t gu = align16(group_lds_bytes(n_batch, k, n_bins, 0)) + work;
+    const size_t gu_route = gate_up_lds(std::min(n_batch, kDecodeRouteT), k, n_bins, 1, h, G, kGuRouteBlock / (2 * G));
+    const size_t gu = gate_up_lds(n_batch, k, n_bins, 0, h, G, kBlock / (2 * G));
     if (gu > 65536 || gu_route > 65536) return "n_batch * n_expert_used too large for the gate/up work-group's LDS";
     return "";
 }
