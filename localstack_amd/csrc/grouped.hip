@@ -199,7 +199,7 @@ constexpr int kDXBytes = kGroupedChunk * 4;
 constexpr int kWWaveBytes = 9 * 32 * 16;
 constexpr int kStageBytes = kABytes + kDXBytes + 4 * kWWaveBytes;
 constexpr int kLoads1 = kAInstr + 5, kLoads0 = kLoads1 + 1;
-constexpr size_t kGLdsBytes = (size_t) kNS * kStageBytes + 3 * kGroupedChunk * 4;
+constexpr size_t kGLdsBytes = (size_t) kNS * kStageBytes + 2 * kGroupedChunk * 4;
 
 typedef __attribute__((address_space(3))) void lds_void;
 
@@ -218,7 +218,6 @@ struct GLds {
     unsigned char *ring; // [kNS][kStageBytes]
     int *pair;           // [kGroupedChunk] pair index of each chunk position
     int *src;            // [kGroupedChunk] activation row of each chunk position
-    float *wt;           // [kGroupedChunk] router weight of each chunk position (down)
 };
 
 __device__ __forceinline__ GLds g_lds(unsigned char *base) {
@@ -226,7 +225,6 @@ __device__ __forceinline__ GLds g_lds(unsigned char *base) {
     g.ring = base;
     g.pair = reinterpret_cast<int *>(base + (size_t) kNS * kStageBytes);
     g.src = g.pair + kGroupedChunk;
-    g.wt = reinterpret_cast<float *>(g.src + kGroupedChunk);
     return g;
 }
 
@@ -384,8 +382,6 @@ __device__ __forceinline__ bool g_item(const GroupedParams &P, int n_rb, const G
         const int p = P.perm[it.y + min(tid, it.z - 1)];
         g.pair[tid] = p;
         g.src[tid] = p / P.row_div;
-        // down: the pair's router weight, needed by the epilogue, fetched with the item
-        if (P.weights) g.wt[tid] = P.weights[p];
     }
     __syncthreads();
     return true;
@@ -449,7 +445,7 @@ __global__ __launch_bounds__(kGThreads) void down_grouped_kernel(GroupedParams P
             const int pos = mt * 32 + 8 * (r / 4) + 4 * h + (r % 4);
             if (pos < n) {
                 const int p = g.pair[pos];
-                P.out[(size_t) p * P.rows + row0 + lane % 32] = acc[mt][r] * g.wt[pos];
+                P.out[(size_t) p * P.rows + row0 + lane % 32] = acc[mt][r] * P.weights[p];
             }
         }
     }
