@@ -8,6 +8,9 @@ ctypes view of that ABI that mirrors the reference's interface for the path:
   ExpertStore.route    router()    src/qwen3.cpp:175-192
   ExpertStore.ffn      moe_apply() src/qwen3.cpp:197-214 plus the residual add (:250 / :287)
   ExpertStore.block    the resident MoE block of qwen3_build_graph (src/qwen3.cpp:239-250)
+  Qwen3Model           the forward pass around it (include/lstk_qwen3.h): Engine::decode
+                       (src/engine.cpp:250-278) over qwen3_build_graph (src/qwen3.cpp:223-259)
+                       with the KvCache block table (src/kv_cache.cpp:59-150)
 
 Device buffers are torch tensors on a ROCm device (or raw integer device pointers); torch is used
 only to own device memory and streams. There is no CPU fallback: every compute call runs the HIP
@@ -47,7 +50,23 @@ class PoolStats(ctypes.Structure):
                 ("acquires", ctypes.c_uint64), ("wait_ms", ctypes.c_double)]
 
 
-# name -> (restype, argtypes); every function declared in include/lstk_moe.h
+class Qwen3HParams(ctypes.Structure):
+    _fields_ = [(n, ctypes.c_int32) for n in ("n_layer", "n_embd", "n_head", "n_head_kv", "head_dim", "n_vocab",
+                                              "n_expert", "n_expert_used", "n_ff_exp", "n_ctx_train")] + \
+               [("rms_eps", ctypes.c_float), ("rope_freq_base", ctypes.c_float)]
+
+
+class Qwen3Layer(ctypes.Structure):
+    _fields_ = [(n, ctypes.c_void_p) for n in ("attn_norm", "wq", "wk", "wv", "wo", "q_norm", "k_norm", "ffn_norm",
+                                               "gate_inp")] + [("gate_inp_type", ctypes.c_int32)]
+
+
+class Qwen3Weights(ctypes.Structure):
+    _fields_ = [("tok_embd", ctypes.c_void_p), ("output_norm", ctypes.c_void_p), ("output", ctypes.c_void_p),
+                ("layers", ctypes.c_void_p)]
+
+
+# name -> (restype, argtypes); every function declared in include/lstk_moe.h and include/lstk_qwen3.h
 _P, _I, _SZ = ctypes.c_void_p, ctypes.c_int, ctypes.c_size_t
 SIGNATURES = {
     "lstk_last_error": (ctypes.c_char_p, []),
@@ -72,6 +91,15 @@ SIGNATURES = {
     "lstk_repack_matrix": (_I, [_I, _I, _I, _P, _P]),
     "lstk_unpack_matrix": (_I, [_I, _I, _I, _P, _P]),
     "lstk_pool_debug_fail_copies": (_I, [_P, _I]),
+    "lstk_model_create": (_I, [ctypes.POINTER(Qwen3HParams), ctypes.POINTER(Qwen3Weights), _P, ctypes.c_uint32,
+                               ctypes.c_uint32, ctypes.POINTER(_P)]),
+    "lstk_model_destroy": (None, [_P]),
+    "lstk_model_decode": (_I, [_P, ctypes.c_int32, _P, _I, _P, _P, _P]),
+    "lstk_model_remove_seq": (_I, [_P, ctypes.c_int32]),
+    "lstk_model_truncate_seq": (_I, [_P, ctypes.c_int32, ctypes.c_int32]),
+    "lstk_model_seq_len": (ctypes.c_int32, [_P, ctypes.c_int32]),
+    "lstk_model_set_timing": (_I, [_P, _I]),
+    "lstk_model_timing": (_I, [_P, ctypes.POINTER(ctypes.c_double), ctypes.POINTER(ctypes.c_int64)]),
 }
 
 _lib = None
@@ -255,4 +283,86 @@ class ExpertStore:
         ms = (ctypes.c_double * 4)()
         n = (ctypes.c_int64 * 4)()
         _check(lib().lstk_pool_timing(self._h, ms, n))
+        return list(ms), list(n)
+
+
+class Qwen3Model:
+    """The Qwen3-MoE forward pass on the device (include/lstk_qwen3.h), mirroring Engine::decode.
+
+    hp: dict of the lstk_qwen3_hparams fields. weights: dict with numpy arrays tok_embd (fp16
+    [n_vocab][n_embd]), output_norm (f32), optional output (fp16), and layers, a list of dicts with
+    attn_norm, wq, wk, wv, wo, q_norm, k_norm (or None), ffn_norm and gate_inp (fp16 [n_expert][n_embd]).
+    The dense tensors are uploaded to `device` here (torch owns that memory); the experts live in
+    `store`, an ExpertStore of matching dims created by the caller (resident or streaming).
+    """
+
+    def __init__(self, hp, weights, store, kv_size, n_batch, device="cuda"):
+        import torch
+        self.hp = dict(hp)
+        self.store = store
+        self.device = torch.device(device)
+        self._keep = []
+
+        def up(a, dtype):
+            if a is None:
+                return None
+            t = torch.from_numpy(np.ascontiguousarray(a).view(dtype)).to(self.device)
+            self._keep.append(t)
+            return t.data_ptr()
+
+        f16, f32 = np.uint16, np.float32
+        self._hp = Qwen3HParams(*(int(self.hp[n]) for n in ("n_layer", "n_embd", "n_head", "n_head_kv", "head_dim",
+                                                             "n_vocab", "n_expert", "n_expert_used", "n_ff_exp")),
+                                int(self.hp.get("n_ctx_train", 0)), float(self.hp["rms_eps"]),
+                                float(self.hp["rope_freq_base"]))
+        n_layer = self.hp["n_layer"]
+        self._layers = (Qwen3Layer * n_layer)()
+        for l, L in enumerate(weights["layers"]):
+            self._layers[l] = Qwen3Layer(up(L["attn_norm"], f32), up(L["wq"], f16), up(L["wk"], f16), up(L["wv"], f16),
+                                         up(L["wo"], f16), up(L.get("q_norm"), f32), up(L.get("k_norm"), f32),
+                                         up(L["ffn_norm"], f32), up(L["gate_inp"], f16), TYPE_F16)
+        self._w = Qwen3Weights(up(weights["tok_embd"], f16), up(weights["output_norm"], f32),
+                               up(weights.get("output"), f16), ctypes.cast(self._layers, ctypes.c_void_p))
+        h = ctypes.c_void_p()
+        _check(lib().lstk_model_create(ctypes.byref(self._hp), ctypes.byref(self._w), store._h, int(kv_size),
+                                       int(n_batch), ctypes.byref(h)))
+        self._h = h
+        self.logits = torch.empty(self.hp["n_vocab"], dtype=torch.float32, device=self.device)
+
+    def close(self):
+        if getattr(self, "_h", None):
+            lib().lstk_model_destroy(self._h)
+            self._h = None
+
+    def __del__(self):
+        self.close()
+
+    def decode(self, seq, tokens, trace=None, logits=None, stream=None):
+        """Appends tokens to sequence seq; returns the device logits [n_vocab] of the last token.
+
+        trace: optional device int32 tensor [n_layer, n_step_tokens, n_expert_used] for the router ids
+        of the last step (-1 for rows the last layer skips)."""
+        tok = np.ascontiguousarray(tokens, dtype=np.int32).ravel()
+        out = self.logits if logits is None else logits
+        _check(lib().lstk_model_decode(self._h, int(seq), tok.ctypes.data, tok.size, _ptr(out), _ptr(trace),
+                                       _stream(stream)))
+        return out
+
+    def remove_seq(self, seq):
+        _check(lib().lstk_model_remove_seq(self._h, int(seq)))
+
+    def truncate_seq(self, seq, keep):
+        _check(lib().lstk_model_truncate_seq(self._h, int(seq), int(keep)))
+
+    def seq_len(self, seq):
+        return lib().lstk_model_seq_len(self._h, int(seq))
+
+    def set_timing(self, on):
+        _check(lib().lstk_model_set_timing(self._h, 1 if on else 0))
+
+    def timing(self):
+        """(ms, launches) per stage: norms, Q/K/V + RoPE, attention, o-proj, output head."""
+        ms = (ctypes.c_double * 5)()
+        n = (ctypes.c_int64 * 5)()
+        _check(lib().lstk_model_timing(self._h, ms, n))
         return list(ms), list(n)

@@ -1,7 +1,9 @@
 """Builds localstack_amd/liblstk_moe.so (gfx950) with hipcc, in place.
 
-The library is the product: the HIP kernels (csrc/kernels.hip), the HBM expert pool and the C ABI
-(csrc/pool.cpp, include/lstk_moe.h) and the host repacker (csrc/repack.cpp).
+The library is the product: the MoE kernels (csrc/kernels.hip, grouped.hip, fused.hip), the HBM
+expert pool and the MoE C ABI (csrc/pool.cpp, include/lstk_moe.h), the host repacker
+(csrc/repack.cpp), and the forward pass around the MoE block (csrc/forward.hip, csrc/model.cpp,
+include/lstk_qwen3.h).
 """
 import os
 import shutil
@@ -13,7 +15,7 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 ROOT = os.path.dirname(HERE)
 CSRC = os.path.join(HERE, "csrc")
 LIB = os.path.join(HERE, "liblstk_moe.so")
-SOURCES = ["kernels.hip", "grouped.hip", "fused.hip", "pool.cpp", "repack.cpp"]
+SOURCES = ["kernels.hip", "grouped.hip", "fused.hip", "forward.hip", "pool.cpp", "repack.cpp", "model.cpp"]
 ARCH = os.environ.get("LSTK_OFFLOAD_ARCH", "gfx950")
 
 

@@ -1,0 +1,508 @@
+// model.cpp - the Qwen3-MoE forward pass around the MoE block (include/lstk_qwen3.h).
+//
+// lstk_model plays the part of the reference's Engine + qwen3_build_graph + KvCache
+// (src/engine.cpp:193-341, src/qwen3.cpp:128-259, src/kv_cache.cpp:59-150) for one GPU and one
+// stream. Instead of building a ggml graph per step it launches a fixed kernel sequence:
+//   layer 0:  embedding gather + attn_norm             (rmsnorm_kernel)
+//   each layer l:
+//     Q, K, V projections in one launch                 (gemv_kernel, 3 segments)
+//     QK-norm + NEOX RoPE + K/V store into the cache    (rope_kernel)
+//     attention over the step's n_kv cells              (attn_kernel [+ attn_combine_kernel])
+//     o-proj + residual                                 (gemv_kernel with add)
+//     ffn_norm on the rows the FFN needs                (rmsnorm_kernel)
+//     MoE block: lstk_moe_block (resident pool) or route -> acquire -> lstk_moe_ffn (streaming pool)
+//     the last layer runs its FFN on the output row only (src/qwen3.cpp:233-237)
+//   output_norm + head on the last row                  (rmsnorm_kernel, gemv_kernel)
+// The KV cache keeps the reference's block table (32-cell blocks handed out per sequence, cell_seq /
+// cell_pos per cell) on the host; the device holds the cells' fp16 K and V in layouts chosen for
+// coalesced reads (forward.h) and a copy of cell_seq / cell_pos that the step's RoPE launch updates.
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cmath>
+#include <cstring>
+#include <map>
+#include <string>
+#include <vector>
+
+#include "../../include/lstk_qwen3.h"
+#include "forward.h"
+#include "internal.h"
+
+namespace {
+
+using lstk::set_error;
+
+constexpr int kStages = 5;
+constexpr uint32_t kCellBlock = 32; // KvCache::block_size (src/kv_cache.h:27)
+
+int hip_fail(hipError_t e, const char *what) { return set_error(LSTK_E_DEVICE, std::string(what) + ": " + hipGetErrorString(e)); }
+
+// KvCache's host bookkeeping (src/kv_cache.cpp:59-150): blocks of 32 cells handed out per sequence
+// from a free list that returns block 0 first, cell = blocks[pos / 32] * 32 + pos % 32.
+struct KvBook {
+    uint32_t size = 0;
+    std::vector<int32_t> cell_seq, cell_pos;
+    std::vector<uint32_t> free_blocks;
+    std::map<int32_t, std::vector<uint32_t>> seq_blocks;
+    std::map<int32_t, int32_t> seq_len;
+    uint32_t used_hwm = 0;
+
+    void init(uint32_t n) {
+        size = n;
+        cell_seq.assign(n, -1);
+        cell_pos.assign(n, -1);
+        free_blocks.clear();
+        for (uint32_t b = n / kCellBlock; b > 0; b--) free_blocks.push_back(b - 1);
+        seq_blocks.clear();
+        seq_len.clear();
+        used_hwm = 0;
+    }
+    bool alloc(int32_t seq, int n, std::vector<int32_t> &cells, std::vector<int32_t> &positions) {
+        std::vector<uint32_t> &blocks = seq_blocks[seq];
+        int32_t &len = seq_len[seq];
+        const uint32_t have = (uint32_t) blocks.size() * kCellBlock;
+        const uint32_t need = (uint32_t) len + (uint32_t) n;
+        const uint32_t extra = need > have ? (need - have + kCellBlock - 1) / kCellBlock : 0;
+        if (extra > free_blocks.size()) {
+            if (blocks.empty() && len == 0) {
+                seq_blocks.erase(seq);
+                seq_len.erase(seq);
+            }
+            return false;
+        }
+        for (uint32_t i = 0; i < extra; i++) {
+            blocks.push_back(free_blocks.back());
+            free_blocks.pop_back();
+        }
+        cells.resize(n);
+        positions.resize(n);
+        for (int i = 0; i < n; i++) {
+            const uint32_t cell = blocks[(uint32_t) len / kCellBlock] * kCellBlock + (uint32_t) len % kCellBlock;
+            cell_seq[cell] = seq;
+            cell_pos[cell] = len;
+            cells[i] = (int32_t) cell;
+            positions[i] = len;
+            used_hwm = std::max(used_hwm, cell + 1);
+            len++;
+        }
+        return true;
+    }
+    void rescan() {
+        used_hwm = 0;
+        for (uint32_t c = 0; c < size; c++)
+            if (cell_seq[c] >= 0) used_hwm = c + 1;
+    }
+    void remove_seq(int32_t seq) {
+        auto it = seq_blocks.find(seq);
+        if (it == seq_blocks.end()) return;
+        for (uint32_t b : it->second) {
+            for (uint32_t c = b * kCellBlock; c < (b + 1) * kCellBlock; c++) {
+                cell_seq[c] = -1;
+                cell_pos[c] = -1;
+            }
+            free_blocks.push_back(b);
+        }
+        seq_blocks.erase(it);
+        seq_len.erase(seq);
+        rescan();
+    }
+    void truncate_seq(int32_t seq, int32_t keep) {
+        auto it = seq_blocks.find(seq);
+        if (it == seq_blocks.end()) return;
+        if (keep <= 0) {
+            remove_seq(seq);
+            return;
+        }
+        std::vector<uint32_t> &blocks = it->second;
+        int32_t &len = seq_len[seq];
+        if (keep >= len) return;
+        for (int32_t p = keep; p < len; p++) {
+            const uint32_t cell = blocks[(uint32_t) p / kCellBlock] * kCellBlock + (uint32_t) p % kCellBlock;
+            cell_seq[cell] = -1;
+            cell_pos[cell] = -1;
+        }
+        const uint32_t keep_blocks = ((uint32_t) keep + kCellBlock - 1) / kCellBlock;
+        while (blocks.size() > keep_blocks) {
+            free_blocks.push_back(blocks.back());
+            blocks.pop_back();
+        }
+        len = keep;
+        rescan();
+    }
+    // Engine::n_kv_for (src/engine.cpp:193-196) over the high-water mark after this step's cells
+    // were assigned: the attended cells, a multiple of 256 (at least 256) capped at the cache size.
+    int n_kv() const {
+        const uint32_t padded = (used_hwm + 255) / 256 * 256;
+        return (int) std::min<uint32_t>(size, std::max<uint32_t>(256, padded));
+    }
+};
+
+struct TimedLaunch {
+    hipEvent_t start = nullptr, end = nullptr;
+};
+
+}  // namespace
+
+struct lstk_model {
+    lstk_qwen3_hparams hp{};
+    std::vector<lstk_qwen3_layer> layers;
+    const uint16_t *tok_embd = nullptr, *output = nullptr;
+    const float *output_norm = nullptr;
+    lstk_pool *pool = nullptr;
+    bool streaming = false;
+    int n_batch = 0;
+    float theta_scale = 0.0f;
+    KvBook kv;
+    // device
+    void *mem = nullptr;
+    uint16_t *kcache = nullptr, *vcache = nullptr;
+    size_t layer_elems = 0; // fp16 values of one layer's K (or V) cache
+    int32_t *cell_seq = nullptr, *cell_pos = nullptr;
+    float *x = nullptr, *hn = nullptr, *q = nullptr, *k = nullptr, *v = nullptr, *qr = nullptr, *attn = nullptr,
+          *part = nullptr, *weights = nullptr;
+    int32_t *ids = nullptr, *slots = nullptr, *in = nullptr; // in = tokens | cells | positions
+    // pinned host staging
+    int32_t *h_in = nullptr, *h_ids = nullptr, *h_slots = nullptr;
+    hipEvent_t in_free = nullptr;
+    // timing
+    bool timing = false;
+    std::vector<TimedLaunch> launched[kStages];
+};
+
+namespace {
+
+template <typename F>
+hipError_t timed(lstk_model *M, int stage, F &&launch) {
+    if (!M->timing) return launch(nullptr);
+    TimedLaunch t{};
+    hipError_t e;
+    if ((e = hipEventCreate(&t.start)) != hipSuccess) return e;
+    if ((e = hipEventCreate(&t.end)) != hipSuccess) return e;
+    lstk::LaunchTiming tm;
+    tm.start = t.start;
+    tm.stop = t.end;
+    const hipError_t le = launch(&tm);
+    M->launched[stage].push_back(t);
+    return le;
+}
+
+void destroy(lstk_model *M) {
+    if (!M) return;
+    if (M->mem) (void) hipFree(M->mem);
+    if (M->h_in) (void) hipHostFree(M->h_in);
+    if (M->in_free) (void) hipEventDestroy(M->in_free);
+    for (auto &v : M->launched)
+        for (TimedLaunch &t : v) {
+            (void) hipEventDestroy(t.start);
+            (void) hipEventDestroy(t.end);
+        }
+    delete M;
+}
+
+int create(const lstk_qwen3_hparams *hpp, const lstk_qwen3_weights *w, lstk_pool *pool, uint32_t kv_size, uint32_t n_batch,
+           lstk_model **out) {
+    if (!out) return set_error(LSTK_E_INVALID, "out must be non-null");
+    *out = nullptr;
+    if (!hpp || !w || !pool || !w->layers) return set_error(LSTK_E_INVALID, "null argument");
+    const lstk_qwen3_hparams &hp = *hpp;
+    if (hp.n_layer < 1 || hp.n_embd < 1 || hp.n_head < 1 || hp.n_head_kv < 1 || hp.head_dim < 1 || hp.n_vocab < 1)
+        return set_error(LSTK_E_INVALID, "hyperparameters must be positive");
+    if (hp.n_head % hp.n_head_kv) return set_error(LSTK_E_INVALID, "n_head must be a multiple of n_head_kv");
+    if (!lstk::attn_supported(hp.head_dim)) return set_error(LSTK_E_INVALID, "head_dim must be a power of two in [16, 256]");
+    if (!lstk::gemv_supported(hp.n_embd) || !lstk::gemv_supported(hp.n_head * hp.head_dim))
+        return set_error(LSTK_E_INVALID, "n_embd and n_head * head_dim must be multiples of 8 and at most 32768");
+    if (!(hp.rms_eps >= 0.0f) || !(hp.rope_freq_base > 0.0f)) return set_error(LSTK_E_INVALID, "bad rms_eps or rope_freq_base");
+    if (kv_size == 0 || kv_size % kCellBlock) return set_error(LSTK_E_INVALID, "kv_size must be a positive multiple of 32");
+    if (n_batch == 0) return set_error(LSTK_E_INVALID, "n_batch must be >= 1");
+    if (lstk::pool_dry(pool)) return set_error(LSTK_E_INVALID, "the pool was created without device memory");
+    const lstk_moe_dims &d = lstk::pool_dims(pool);
+    if (d.n_layer != hp.n_layer || d.n_embd != hp.n_embd || d.n_ff_exp != hp.n_ff_exp || d.n_expert != hp.n_expert ||
+        d.n_expert_used != hp.n_expert_used)
+        return set_error(LSTK_E_INVALID, "the pool's dims do not match the hyperparameters");
+    if ((uint32_t) d.n_batch < n_batch) return set_error(LSTK_E_INVALID, "n_batch exceeds the pool's n_batch");
+    if (!w->tok_embd || !w->output_norm) return set_error(LSTK_E_INVALID, "tok_embd and output_norm must be non-null");
+    for (int l = 0; l < hp.n_layer; l++) {
+        const lstk_qwen3_layer &L = w->layers[l];
+        if (!L.attn_norm || !L.wq || !L.wk || !L.wv || !L.wo || !L.ffn_norm || !L.gate_inp)
+            return set_error(LSTK_E_INVALID, "layer " + std::to_string(l) + ": a required tensor is null");
+        if (L.gate_inp_type != LSTK_TYPE_F16 && L.gate_inp_type != LSTK_TYPE_F32)
+            return set_error(LSTK_E_INVALID, "layer " + std::to_string(l) + ": gate_inp must be F16 or F32");
+    }
+
+    lstk_model *M = new lstk_model();
+    M->hp = hp;
+    M->layers.assign(w->layers, w->layers + hp.n_layer);
+    M->tok_embd = w->tok_embd;
+    M->output = w->output ? w->output : w->tok_embd;
+    M->output_norm = w->output_norm;
+    M->pool = pool;
+    M->streaming = lstk::pool_streaming(pool);
+    M->n_batch = (int) n_batch;
+    M->theta_scale = powf(hp.rope_freq_base, -2.0f / (float) hp.head_dim);
+    M->kv.init(kv_size);
+
+    const size_t nb = n_batch, h = (size_t) hp.n_embd, hq = (size_t) hp.n_head * hp.head_dim,
+                 hk = (size_t) hp.n_head_kv * hp.head_dim, k = (size_t) hp.n_expert_used;
+    M->layer_elems = (size_t) kv_size * hk;
+    // part rows: only steps with fewer than 1024 (token, head) pairs split the cells, into < 2048 rows
+    const size_t part_rows = 2048;
+    struct Piece {
+        void **dst;
+        size_t bytes;
+    };
+    std::vector<Piece> pieces = {
+        {(void **) &M->kcache, 2 * M->layer_elems * hp.n_layer * sizeof(uint16_t)},
+        {(void **) &M->x, nb * h * 4},
+        {(void **) &M->hn, nb * h * 4},
+        {(void **) &M->q, nb * hq * 4},
+        {(void **) &M->qr, nb * hq * 4},
+        {(void **) &M->attn, nb * hq * 4},
+        {(void **) &M->k, nb * hk * 4},
+        {(void **) &M->v, nb * hk * 4},
+        {(void **) &M->part, part_rows * (hp.head_dim + 2) * 4},
+        {(void **) &M->weights, nb * k * 4},
+        {(void **) &M->ids, nb * k * 4},
+        {(void **) &M->slots, nb * k * 4},
+        {(void **) &M->in, 3 * nb * 4},
+        {(void **) &M->cell_seq, (size_t) kv_size * 4},
+        {(void **) &M->cell_pos, (size_t) kv_size * 4},
+    };
+    size_t total = 0;
+    for (const Piece &p : pieces) total += (p.bytes + 255) / 256 * 256;
+    hipError_t e = hipMalloc(&M->mem, total);
+    if (e != hipSuccess) {
+        destroy(M);
+        return set_error(LSTK_E_NOMEM, "hipMalloc of " + std::to_string(total) + " bytes failed");
+    }
+    size_t off = 0;
+    for (const Piece &p : pieces) {
+        *p.dst = static_cast<uint8_t *>(M->mem) + off;
+        off += (p.bytes + 255) / 256 * 256;
+    }
+    M->vcache = M->kcache + M->layer_elems * hp.n_layer;
+    // zero K/V (a masked cell is never read, but keep the cache free of stale NaNs as the reference
+    // does, src/kv_cache.cpp:31) and mark every cell empty
+    if ((e = hipMemset(M->kcache, 0, 2 * M->layer_elems * hp.n_layer * sizeof(uint16_t))) != hipSuccess ||
+        (e = hipMemset(M->cell_seq, 0xff, (size_t) kv_size * 4)) != hipSuccess ||
+        (e = hipMemset(M->cell_pos, 0xff, (size_t) kv_size * 4)) != hipSuccess) {
+        destroy(M);
+        return hip_fail(e, "hipMemset");
+    }
+    if ((e = hipHostMalloc((void **) &M->h_in, (3 * nb + 2 * nb * k) * 4, hipHostMallocDefault)) != hipSuccess) {
+        destroy(M);
+        return set_error(LSTK_E_NOMEM, "hipHostMalloc of the step staging failed");
+    }
+    M->h_ids = M->h_in + 3 * nb;
+    M->h_slots = M->h_ids + nb * k;
+    if ((e = hipEventCreateWithFlags(&M->in_free, hipEventDisableTiming)) != hipSuccess ||
+        (e = hipEventRecord(M->in_free, nullptr)) != hipSuccess) {
+        destroy(M);
+        return hip_fail(e, "hipEventCreate");
+    }
+    *out = M;
+    return LSTK_OK;
+}
+
+// Copies the host bookkeeping of the cells to the device (after removals; rare, synchronous).
+int sync_cells(lstk_model *M) {
+    hipError_t e;
+    if ((e = hipDeviceSynchronize()) != hipSuccess ||
+        (e = hipMemcpy(M->cell_seq, M->kv.cell_seq.data(), M->kv.size * 4, hipMemcpyHostToDevice)) != hipSuccess ||
+        (e = hipMemcpy(M->cell_pos, M->kv.cell_pos.data(), M->kv.size * 4, hipMemcpyHostToDevice)) != hipSuccess)
+        return hip_fail(e, "cell table upload");
+    return LSTK_OK;
+}
+
+// The MoE block of layer l on `rows` rows of hn, added into the residual rows xr in place.
+int moe(lstk_model *M, int l, int rows, float *xr, int32_t *ids, hipStream_t st) {
+    const lstk_qwen3_layer &L = M->layers[l];
+    if (!M->streaming)
+        return lstk_moe_block(M->pool, l, M->hn, L.gate_inp, L.gate_inp_type, xr, xr, ids, M->weights, rows, st);
+    // Engine::run_segment (src/engine.cpp:343-392): the host sees the router's choice, acquires the
+    // experts (misses are copied on the pool's side stream) and the experts run on their slots.
+    const int k = M->hp.n_expert_used;
+    int rc = lstk_moe_route(M->pool, l, M->hn, rows, L.gate_inp, L.gate_inp_type, ids, M->weights, st);
+    if (rc != LSTK_OK) return rc;
+    hipError_t e;
+    if ((e = hipMemcpyAsync(M->h_ids, ids, (size_t) rows * k * 4, hipMemcpyDeviceToHost, st)) != hipSuccess ||
+        (e = hipStreamSynchronize(st)) != hipSuccess)
+        return hip_fail(e, "router ids download");
+    if ((rc = lstk_pool_acquire(M->pool, l, M->h_ids, rows * k, M->h_slots, st)) != LSTK_OK) {
+        (void) lstk_pool_release_all(M->pool, st);
+        return rc;
+    }
+    if ((e = hipMemcpyAsync(M->slots, M->h_slots, (size_t) rows * k * 4, hipMemcpyHostToDevice, st)) != hipSuccess)
+        return hip_fail(e, "slot upload");
+    rc = lstk_moe_ffn(M->pool, l, M->hn, M->slots, M->weights, xr, xr, rows, st);
+    const int rrc = lstk_pool_release_all(M->pool, st);
+    return rc != LSTK_OK ? rc : rrc;
+}
+
+int step(lstk_model *M, int32_t seq, const int32_t *tokens, int T, float *d_logits, int32_t *d_trace, hipStream_t st) {
+    const lstk_qwen3_hparams &hp = M->hp;
+    std::vector<int32_t> cells, pos;
+    if (!M->kv.alloc(seq, T, cells, pos)) return set_error(LSTK_E_EXHAUSTED, "KV cache is full");
+    const int n_cells = M->kv.n_kv();
+    const int nb = M->n_batch, h = hp.n_embd, hd = hp.head_dim, k = hp.n_expert_used;
+    const int hq = hp.n_head * hd, hk = hp.n_head_kv * hd;
+    hipError_t e;
+    // the staging buffer is reused once the previous step's upload has left it
+    if ((e = hipEventSynchronize(M->in_free)) != hipSuccess) return hip_fail(e, "hipEventSynchronize");
+    std::memcpy(M->h_in, tokens, (size_t) T * 4);
+    std::memcpy(M->h_in + nb, cells.data(), (size_t) T * 4);
+    std::memcpy(M->h_in + 2 * nb, pos.data(), (size_t) T * 4);
+    if ((e = hipMemcpyAsync(M->in, M->h_in, (size_t) 3 * nb * 4, hipMemcpyHostToDevice, st)) != hipSuccess ||
+        (e = hipEventRecord(M->in_free, st)) != hipSuccess)
+        return hip_fail(e, "step input upload");
+    const int32_t *d_tok = M->in, *d_cells = M->in + nb, *d_pos = M->in + 2 * nb;
+
+    int n_chunk = 1;
+    const int chunk = lstk::attn_chunk_cells(T, hp.n_head, n_cells, &n_chunk);
+    for (int l = 0; l < hp.n_layer; l++) {
+        const lstk_qwen3_layer &L = M->layers[l];
+        lstk::NormParams np{M->x, l == 0 ? M->tok_embd : nullptr, d_tok, M->x, L.attn_norm, M->hn, T, h, hp.rms_eps};
+        if ((e = timed(M, 0, [&](const lstk::LaunchTiming *tm) { return lstk::launch_rmsnorm(np, st, tm); })) != hipSuccess)
+            return hip_fail(e, "attn_norm launch");
+        lstk::GemvParams gp{};
+        gp.seg[0] = {L.wq, M->q, nullptr, hq, hq};
+        gp.seg[1] = {L.wk, M->k, nullptr, hk, hk};
+        gp.seg[2] = {L.wv, M->v, nullptr, hk, hk};
+        gp.nseg = 3;
+        gp.rows_total = hq + 2 * hk;
+        gp.cols = h;
+        gp.x = M->hn;
+        gp.T = T;
+        if ((e = timed(M, 1, [&](const lstk::LaunchTiming *tm) { return lstk::launch_gemv(gp, st, tm); })) != hipSuccess)
+            return hip_fail(e, "qkv launch");
+        uint16_t *kc = M->kcache + M->layer_elems * l, *vc = M->vcache + M->layer_elems * l;
+        lstk::RopeParams rp{M->q, M->k, M->v, L.q_norm, L.k_norm, hp.rms_eps, d_pos, d_cells, seq, M->cell_seq, M->cell_pos,
+                            T, hp.n_head, hp.n_head_kv, hd, (int) M->kv.size, M->theta_scale, M->qr, kc, vc};
+        if ((e = timed(M, 1, [&](const lstk::LaunchTiming *tm) { return lstk::launch_rope(rp, st, tm); })) != hipSuccess)
+            return hip_fail(e, "rope launch");
+        lstk::AttnParams ap{M->qr, kc, vc, M->cell_seq, M->cell_pos, d_pos, seq, T, hp.n_head, hp.n_head_kv, hd,
+                            (int) M->kv.size, n_cells, chunk, n_chunk, 1.0f / sqrtf((float) hd), M->part, M->attn};
+        if ((e = timed(M, 2, [&](const lstk::LaunchTiming *tm) { return lstk::launch_attn(ap, st, tm); })) != hipSuccess ||
+            (e = timed(M, 2, [&](const lstk::LaunchTiming *tm) { return lstk::launch_attn_combine(ap, st, tm); })) != hipSuccess)
+            return hip_fail(e, "attention launch");
+        lstk::GemvParams op{};
+        op.seg[0] = {L.wo, M->x, M->x, h, h};
+        op.nseg = 1;
+        op.rows_total = h;
+        op.cols = hq;
+        op.x = M->attn;
+        op.T = T;
+        if ((e = timed(M, 3, [&](const lstk::LaunchTiming *tm) { return lstk::launch_gemv(op, st, tm); })) != hipSuccess)
+            return hip_fail(e, "o-proj launch");
+        // after the last attention only the output row goes on (src/qwen3.cpp:233-237)
+        const bool last = l == hp.n_layer - 1;
+        const int rows = last ? 1 : T;
+        float *xr = M->x + (size_t) (T - rows) * h;
+        lstk::NormParams fp{xr, nullptr, nullptr, nullptr, L.ffn_norm, M->hn, rows, h, hp.rms_eps};
+        if ((e = timed(M, 0, [&](const lstk::LaunchTiming *tm) { return lstk::launch_rmsnorm(fp, st, tm); })) != hipSuccess)
+            return hip_fail(e, "ffn_norm launch");
+        int32_t *ids = d_trace ? d_trace + ((size_t) l * T + (T - rows)) * k : M->ids;
+        if (last && d_trace && T > 1) {
+            lstk::FillParams fl{d_trace + (size_t) l * T * k, (T - 1) * k, -1};
+            if ((e = lstk::launch_fill(fl, st, nullptr)) != hipSuccess) return hip_fail(e, "trace fill launch");
+        }
+        const int rc = moe(M, l, rows, xr, ids, st);
+        if (rc != LSTK_OK) return rc;
+    }
+    lstk::NormParams onp{M->x + (size_t) (T - 1) * h, nullptr, nullptr, nullptr, M->output_norm, M->hn, 1, h, hp.rms_eps};
+    if ((e = timed(M, 0, [&](const lstk::LaunchTiming *tm) { return lstk::launch_rmsnorm(onp, st, tm); })) != hipSuccess)
+        return hip_fail(e, "output_norm launch");
+    lstk::GemvParams hpp{};
+    hpp.seg[0] = {M->output, d_logits, nullptr, hp.n_vocab, hp.n_vocab};
+    hpp.nseg = 1;
+    hpp.rows_total = hp.n_vocab;
+    hpp.cols = h;
+    hpp.x = M->hn;
+    hpp.T = 1;
+    if ((e = timed(M, 4, [&](const lstk::LaunchTiming *tm) { return lstk::launch_gemv(hpp, st, tm); })) != hipSuccess)
+        return hip_fail(e, "output head launch");
+    return LSTK_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int lstk_model_create(const lstk_qwen3_hparams *hp, const lstk_qwen3_weights *w, lstk_pool *pool, uint32_t kv_size,
+                      uint32_t n_batch, lstk_model **out) {
+    try {
+        return create(hp, w, pool, kv_size, n_batch, out);
+    } catch (const std::exception &ex) {
+        return set_error(LSTK_E_NOMEM, std::string("lstk_model_create: ") + ex.what());
+    }
+}
+
+void lstk_model_destroy(lstk_model *model) { destroy(model); }
+
+int lstk_model_decode(lstk_model *model, int32_t seq, const int32_t *tokens, int n_tokens, float *d_logits,
+                      int32_t *d_trace, lstk_stream_t stream) {
+    if (!model) return set_error(LSTK_E_INVALID, "null model");
+    if (n_tokens < 1 || !tokens || !d_logits) return set_error(LSTK_E_INVALID, "need at least one token and a logits buffer");
+    if (seq < 0) return set_error(LSTK_E_INVALID, "seq must be >= 0");
+    for (int i = 0; i < n_tokens; i++)
+        if (tokens[i] < 0 || tokens[i] >= model->hp.n_vocab)
+            return set_error(LSTK_E_INVALID, "token id " + std::to_string(tokens[i]) + " out of range");
+    hipStream_t st = static_cast<hipStream_t>(stream);
+    try {
+        for (int done = 0; done < n_tokens;) {
+            const int n = std::min(model->n_batch, n_tokens - done);
+            const int rc = step(model, seq, tokens + done, n, d_logits, d_trace, st);
+            if (rc != LSTK_OK) return rc;
+            done += n;
+        }
+    } catch (const std::exception &ex) {
+        return set_error(LSTK_E_NOMEM, std::string("lstk_model_decode: ") + ex.what());
+    }
+    return LSTK_OK;
+}
+
+int lstk_model_remove_seq(lstk_model *model, int32_t seq) {
+    if (!model) return set_error(LSTK_E_INVALID, "null model");
+    model->kv.remove_seq(seq);
+    return sync_cells(model);
+}
+
+int lstk_model_truncate_seq(lstk_model *model, int32_t seq, int32_t keep) {
+    if (!model) return set_error(LSTK_E_INVALID, "null model");
+    model->kv.truncate_seq(seq, keep);
+    return sync_cells(model);
+}
+
+int32_t lstk_model_seq_len(const lstk_model *model, int32_t seq) {
+    if (!model) return 0;
+    auto it = model->kv.seq_len.find(seq);
+    return it == model->kv.seq_len.end() ? 0 : it->second;
+}
+
+int lstk_model_set_timing(lstk_model *model, int enable) {
+    if (!model) return set_error(LSTK_E_INVALID, "null model");
+    model->timing = enable != 0;
+    return LSTK_OK;
+}
+
+int lstk_model_timing(lstk_model *model, double ms[5], int64_t launches[5]) {
+    if (!model || !ms || !launches) return set_error(LSTK_E_INVALID, "null argument");
+    for (int s = 0; s < kStages; s++) {
+        ms[s] = 0.0;
+        launches[s] = 0;
+        for (TimedLaunch &t : model->launched[s]) {
+            hipError_t e = hipEventSynchronize(t.end);
+            if (e != hipSuccess) return hip_fail(e, "hipEventSynchronize");
+            float v = 0.0f;
+            if ((e = hipEventElapsedTime(&v, t.start, t.end)) != hipSuccess) return hip_fail(e, "hipEventElapsedTime");
+            ms[s] += v;
+            launches[s]++;
+            (void) hipEventDestroy(t.start);
+            (void) hipEventDestroy(t.end);
+        }
+        model->launched[s].clear();
+    }
+    return LSTK_OK;
+}
+
+}  // extern "C"

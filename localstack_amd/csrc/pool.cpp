@@ -28,6 +28,7 @@
 
 #include "../../include/lstk_moe.h"
 #include "formats.h"
+#include "internal.h"
 #include "kernels.h"
 
 namespace lstk {
@@ -815,6 +816,13 @@ int check_act(const float *p, const char *name) {
 }
 
 }  // namespace
+
+namespace lstk {
+int set_error(int code, const std::string &msg) { return fail(code, msg); }
+const lstk_moe_dims &pool_dims(const lstk_pool *pool) { return pool->dims; }
+bool pool_streaming(const lstk_pool *pool) { return pool->streaming; }
+bool pool_dry(const lstk_pool *pool) { return pool->dry; }
+}  // namespace lstk
 
 extern "C" {
 

@@ -8,7 +8,10 @@ benchmark and test shapes, using numpy's PCG64 so that every machine draws ident
   - q4_k_random: Q4_K blocks with uniform 4-bit values and 6-bit scales/mins, d ~ U(0.5, 1.5) * d0
     and dmin = 7.5 d, so dequantized weights are roughly zero-mean with |w| ~ 1e-2;
   - router weights F16 N(0, 0.02), optionally with a Zipf(s) per-expert logit bias carried by a
-    constant activation column (zipf_router_f16).
+    constant activation column (zipf_router_f16);
+  - qwen3_weights: a whole Qwen3-MoE model in the tensor set make_tiny_moe.py writes
+    (tools/make_tiny_moe.py:122-136): F16 embedding (tied output head) and attention, f32 norms of
+    1.0 (as that writer sets them), F16 router, quantized experts.
 """
 import numpy as np
 
@@ -49,14 +52,35 @@ def q4_k_random(rng, rows, cols, d0=1e-4):
     return out.reshape(-1)
 
 
-def experts(rng, wtype, n_expert, rows, cols, std=0.02):
-    """Stacked expert tensor [n_expert][rows][cols] as GGUF bytes of wtype (8 = Q8_0, 12 = Q4_K)."""
+def q4_k_centered(rng, rows, cols, std=0.02):
+    """Q4_K blocks whose dequantized values are zero-mean with standard deviation about std, as a
+    trained model's are: sub-block scales sc in [4, 8], mins m = round(7.5 sc), dmin = d, so that
+    w = d (sc q - m) with q uniform in 0..15 (std 4.61) centres each sub-block on zero."""
+    nb = rows * (cols // 256)
+    sc = rng.integers(4, 9, (nb, 8)).astype(np.uint8)
+    m = np.rint(7.5 * sc.astype(np.float64)).astype(np.uint8)
+    d = (rng.uniform(0.8, 1.2, nb) * std / (4.61 * 6.0)).astype(np.float16)
+    out = np.empty((nb, Q4_K_BLOCK), np.uint8)
+    out[:, 0:2] = d.view(np.uint8).reshape(nb, 2)
+    out[:, 2:4] = d.view(np.uint8).reshape(nb, 2)
+    # get_scale_min_k4 packing: bytes 0-3 / 4-7 hold sc / m of sub-blocks 0-3 (6 bits) plus the top two
+    # bits of sub-blocks 4-7; bytes 8-11 hold the low nibbles of sc / m of sub-blocks 4-7
+    out[:, 4:8] = sc[:, :4] | ((sc[:, 4:] >> 4) << 6)
+    out[:, 8:12] = m[:, :4] | ((m[:, 4:] >> 4) << 6)
+    out[:, 12:16] = (sc[:, 4:] & 0xF) | ((m[:, 4:] & 0xF) << 4)
+    out[:, 16:] = rng.integers(0, 256, (nb, 128), dtype=np.uint8)
+    return out.reshape(-1)
+
+
+def experts(rng, wtype, n_expert, rows, cols, std=0.02, centered=False):
+    """Stacked expert tensor [n_expert][rows][cols] as GGUF bytes of wtype (8 = Q8_0, 12 = Q4_K).
+    Q4_K is q4_k_random unless centered (q4_k_centered with the given std)."""
     parts = []
     for _ in range(n_expert):
         if wtype == 8:
             parts.append(q8_0_from_normal(rng, rows, cols, std))
         elif wtype == 12:
-            parts.append(q4_k_random(rng, rows, cols))
+            parts.append(q4_k_centered(rng, rows, cols, std) if centered else q4_k_random(rng, rows, cols))
         else:
             raise ValueError(f"unsupported expert type {wtype}")
     return np.concatenate(parts)
@@ -89,3 +113,26 @@ def activations(rng, n_tokens, n_embd, bias_unit=False):
     if bias_unit:
         x[:, 0] = 1.0
     return x
+
+
+def qwen3_weights(rng, hp, wtype=8, std=0.02):
+    """Seeded Qwen3-MoE weights for hp (dict with n_layer, n_embd, n_head, n_head_kv, head_dim, n_vocab,
+    n_expert, n_ff_exp). Dense weights N(0, std) as fp16 [rows][cols]; norms 1.0; experts GGUF bytes of
+    wtype (Q4_K centred), stacked [n_expert] per matrix (up, gate: n_ff_exp x n_embd; down: n_embd x
+    n_ff_exp)."""
+    h, hd, E, f = hp["n_embd"], hp["head_dim"], hp["n_expert"], hp["n_ff_exp"]
+    hq, hk = hp["n_head"] * hd, hp["n_head_kv"] * hd
+
+    def f16(rows, cols):
+        return (rng.standard_normal((rows, cols), dtype=np.float32) * np.float32(std)).astype(np.float16)
+
+    ones = lambda n: np.ones(n, np.float32)
+    w = {"tok_embd": f16(hp["n_vocab"], h), "output_norm": ones(h), "output": None, "layers": []}
+    for _ in range(hp["n_layer"]):
+        w["layers"].append({
+            "attn_norm": ones(h), "wq": f16(hq, h), "wk": f16(hk, h), "wv": f16(hk, h), "wo": f16(h, hq),
+            "q_norm": ones(hd), "k_norm": ones(hd), "ffn_norm": ones(h), "gate_inp": f16(E, h),
+            "types": (wtype, wtype, wtype),
+            "up": experts(rng, wtype, E, f, h, std, True), "gate": experts(rng, wtype, E, f, h, std, True),
+            "down": experts(rng, wtype, E, h, f, std, True)})
+    return w

@@ -65,6 +65,16 @@ def lib():
             "or_pool_shard_slots": (i32, [P, i32]),
             "or_pool_slot_owner": (i32, [P, i32, i32, P, P]),
             "or_pool_lru": (i32, [P, i32, P, i32]),
+            "or_dot_f16": (f32, [P, P, i32]),
+            "or_matmul_f16": (None, [P, i32, i32, P, i32, P]),
+            "or_rms_norm": (None, [P, i32, P, f32, P]),
+            "or_rope_neox": (None, [P, i32, i32, f32, P]),
+            "or_attn_row": (None, [P, P, P, i32, i32, i32, f32, P]),
+            "or_qwen3_create": (P, [P, P, P, P, P, i32]),
+            "or_qwen3_destroy": (None, [P]),
+            "or_qwen3_decode": (i32, [P, P, i32, P, P]),
+            "or_qwen3_len": (i32, [P]),
+            "or_qwen3_truncate": (None, [P, i32]),
         }
         for name, (res, args) in sig.items():
             fn = getattr(L, name)
@@ -257,3 +267,110 @@ class Pool:
         out = np.zeros(cap, np.int32)
         n = lib().or_pool_lru(self._h, shard, _p(out), cap)
         return out[:n].tolist()
+
+
+# ---- forward pass around the MoE block ------------------------------------------------------
+
+def dot_f16(w, x):
+    w = _c(w, np.float16)
+    x = _c(x, np.float16)
+    return lib().or_dot_f16(_p(w), _p(x), w.size)
+
+
+def matmul_f16(W, x):
+    W = _c(W, np.float16)
+    x = _c(np.atleast_2d(x), np.float32)
+    y = np.zeros((x.shape[0], W.shape[0]), np.float32)
+    lib().or_matmul_f16(_p(W), W.shape[0], W.shape[1], _p(x), x.shape[0], _p(y))
+    return y
+
+
+def rms_norm(x, w, eps):
+    x = _c(x, np.float32)
+    y = np.zeros_like(x)
+    wv = None if w is None else _c(w, np.float32)
+    lib().or_rms_norm(_p(x), x.size, None if wv is None else _p(wv), eps, _p(y))
+    return y
+
+
+def rope_neox(x, pos, theta_scale):
+    x = _c(x, np.float32)
+    y = np.zeros_like(x)
+    lib().or_rope_neox(_p(x), x.size, int(pos), float(theta_scale), _p(y))
+    return y
+
+
+def attn_row(q, K, V, scale):
+    q = _c(q, np.float32)
+    K = _c(K, np.float16)
+    V = _c(V, np.float16)
+    out = np.zeros_like(q)
+    lib().or_attn_row(_p(q), _p(K), _p(V), K.shape[0], q.size, K.shape[1], float(scale), _p(out))
+    return out
+
+
+class _HP(ctypes.Structure):
+    _fields_ = [(n, ctypes.c_int32) for n in ("n_layer", "n_embd", "n_head", "n_head_kv", "head_dim", "n_vocab",
+                                              "n_expert", "n_expert_used", "n_ff_exp")] + \
+               [("rms_eps", ctypes.c_float), ("rope_freq_base", ctypes.c_float)]
+
+
+class _Layer(ctypes.Structure):
+    _fields_ = [(n, ctypes.c_void_p) for n in ("attn_norm", "wq", "wk", "wv", "wo", "q_norm", "k_norm", "ffn_norm",
+                                               "gate_inp")] + \
+               [(n, ctypes.c_int32) for n in ("type_up", "type_gate", "type_down")] + \
+               [(n, ctypes.c_void_p) for n in ("up", "gate", "down")]
+
+
+class Qwen3:
+    """The forward pass of one sequence (src/qwen3.cpp:223-259) on the CPU. hp / weights as for
+    localstack_amd.Qwen3Model (weights['layers'][l] also holds types, up, gate, down)."""
+
+    def __init__(self, hp, weights, max_ctx):
+        self.hp = dict(hp)
+        self._keep = []
+
+        def ptr(a, dtype):
+            if a is None:
+                return None
+            a = np.ascontiguousarray(a).view(dtype) if dtype is not None else np.ascontiguousarray(a)
+            self._keep.append(a)
+            return a.ctypes.data
+
+        f16, f32 = np.uint16, np.float32
+        names = ("n_layer", "n_embd", "n_head", "n_head_kv", "head_dim", "n_vocab", "n_expert", "n_expert_used",
+                 "n_ff_exp")
+        self._hp = _HP(*(int(self.hp[n]) for n in names), float(self.hp["rms_eps"]), float(self.hp["rope_freq_base"]))
+        n_layer = self.hp["n_layer"]
+        self._layers = (_Layer * n_layer)()
+        for l, L in enumerate(weights["layers"]):
+            t = L["types"]
+            self._layers[l] = _Layer(ptr(L["attn_norm"], f32), ptr(L["wq"], f16), ptr(L["wk"], f16), ptr(L["wv"], f16),
+                                     ptr(L["wo"], f16), ptr(L.get("q_norm"), f32), ptr(L.get("k_norm"), f32),
+                                     ptr(L["ffn_norm"], f32), ptr(L["gate_inp"], f16), t[0], t[1], t[2],
+                                     ptr(L["up"], None), ptr(L["gate"], None), ptr(L["down"], None))
+        self._h = lib().or_qwen3_create(ctypes.byref(self._hp), self._layers, ptr(weights["tok_embd"], f16),
+                                        ptr(weights["output_norm"], f32), ptr(weights.get("output"), f16), int(max_ctx))
+        if not self._h:
+            raise ValueError("unsupported shape")
+
+    def __del__(self):
+        if getattr(self, "_h", None):
+            lib().or_qwen3_destroy(self._h)
+            self._h = None
+
+    def decode(self, tokens, want_trace=False):
+        """One step over `tokens`; returns the last token's logits (and the router trace [n_layer][T][k])."""
+        tok = _c(np.ravel(tokens), np.int32)
+        logits = np.zeros(self.hp["n_vocab"], np.float32)
+        trace = np.zeros((self.hp["n_layer"], tok.size, self.hp["n_expert_used"]), np.int32) if want_trace else None
+        rc = lib().or_qwen3_decode(self._h, _p(tok), tok.size, _p(logits), _p(trace) if want_trace else None)
+        if rc != 0:
+            raise RuntimeError("context full")
+        return (logits, trace) if want_trace else logits
+
+    def __len__(self):
+        return lib().or_qwen3_len(self._h)
+
+    def truncate(self, keep):
+        lib().or_qwen3_truncate(self._h, int(keep))

@@ -8,6 +8,8 @@
  *   router()      src/qwen3.cpp:175-192
  *   moe_apply()   src/qwen3.cpp:197-214, residual add :250 / :287
  *   ExpertStore   src/expert_store.cpp:106-295 (slot bookkeeping only, no I/O)
+ *   the forward pass around the MoE block (src/qwen3.cpp:112-171, :223-259): RMSNorm, F16 mat-muls,
+ *   NEOX RoPE, fp16 KV cache, attention, output head, for one sequence
  * ggml itself (llama.cpp submodule pinned at 23b0202a189c44a54625aadcb37a946dd1d6278d,
  * docs/llama_cpp_commit.txt:1) is not present, so its kernels are restated from its published
  * algorithm: Q8_0/Q4_K/Q8_K block formats, quantize_row_q8_0 (x86 AVX path: id = 127/amax,
@@ -19,6 +21,9 @@
  *   - ggml's SIMD reduction order inside each dot product (the oracle uses the fixed orders
  *     documented per function; router logits use the 64-lane order the GPU kernel uses);
  *   - ggml's SIMD expf / silu approximations (the oracle calls libm expf);
+ *   - whether ggml's CPU flash attention accumulates V in f32 or f16 for an F16 cache (the oracle
+ *     accumulates in f32, as the graph requests with GGML_PREC_F32, src/qwen3.cpp:167), and the x86
+ *     contraction of RoPE's x0*cos - x1*sin into fused multiply-adds;
  *   - std::sort's order among exactly equal probabilities (the oracle breaks ties to the lower id).
  * Every other function is pinned by the tests listed in tests/test_oracle_*.py.
  */
@@ -108,6 +113,38 @@ int or_pool_shard_slots(const or_pool *p, int shard);
 int or_pool_slot_owner(const or_pool *p, int shard, int slot, int32_t *layer, int32_t *expert);
 /* LRU order of a shard, head (evicted next) first; returns the count written. */
 int or_pool_lru(const or_pool *p, int shard, int32_t *out, int cap);
+
+/* ---- Qwen3-MoE forward pass around the MoE block (src/qwen3.cpp:112-171, :223-259) ----
+ * One sequence whose cells are its positions (what the reference's KvCache hands a lone sequence in an
+ * empty cache: blocks 0, 1, 2, ... in order). Dense weights F16 [rows][cols], norms f32, router F16,
+ * experts in GGUF layout stacked [n_expert] per matrix. */
+typedef struct or_qwen3_hparams {
+    int32_t n_layer, n_embd, n_head, n_head_kv, head_dim, n_vocab, n_expert, n_expert_used, n_ff_exp;
+    float rms_eps, rope_freq_base;
+} or_qwen3_hparams;
+typedef struct or_qwen3_layer {
+    const float *attn_norm;
+    const uint16_t *wq, *wk, *wv, *wo;
+    const float *q_norm, *k_norm; /* may be NULL */
+    const float *ffn_norm;
+    const uint16_t *gate_inp;
+    int32_t type_up, type_gate, type_down;
+    const void *up, *gate, *down;
+} or_qwen3_layer;
+typedef struct or_qwen3 or_qwen3;
+
+float or_dot_f16(const uint16_t *w, const uint16_t *x, int n);                                /* ggml_vec_dot_f16 */
+void or_matmul_f16(const uint16_t *W, int rows, int cols, const float *x, int T, float *y);     /* y [T][rows] */
+void or_rms_norm(const float *x, int n, const float *w, float eps, float *y);                  /* rms_norm (+ mul) */
+void or_rope_neox(const float *x, int hd, int pos, float theta_scale, float *y);               /* one head */
+void or_attn_row(const float *q, const uint16_t *K, const uint16_t *V, int n, int hd, int ld, float scale,
+                 float *out);                                                                  /* one query row */
+or_qwen3 *or_qwen3_create(const or_qwen3_hparams *hp, const or_qwen3_layer *layers, const uint16_t *tok_embd,
+                          const float *output_norm, const uint16_t *output, int max_ctx);
+void or_qwen3_destroy(or_qwen3 *m);
+int or_qwen3_decode(or_qwen3 *m, const int32_t *tokens, int T, float *logits, int32_t *trace);
+int or_qwen3_len(const or_qwen3 *m);
+void or_qwen3_truncate(or_qwen3 *m, int keep);
 
 #ifdef __cplusplus
 }

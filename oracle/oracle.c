@@ -660,3 +660,224 @@ int or_pool_lru(const or_pool *P, int shard, int32_t *out, int cap) {
     for (int32_t s = p->lru_head; s >= 0 && n < cap; s = p->next[s]) out[n++] = s;
     return n;
 }
+
+/* ------------------------------------------------------------------------------------------ */
+/* Qwen3-MoE forward pass around the MoE block (src/qwen3.cpp:112-171, :223-259)              */
+/* ------------------------------------------------------------------------------------------ */
+
+/* ggml_vec_dot_f16, x86 F16C/AVX path: both operands fp16 (the caller rounds the f32 activations to
+ * fp16, ggml's vec_dot_type for F16 weights); 4 accumulators of 8 lanes over steps of 32 values,
+ * reduced x0+x2, x1+x3, then x0+x1, then the two 128-bit halves, then two horizontal adds; the tail
+ * (n % 32 values) is summed in double. The fp16 products are exact in f32. */
+float or_dot_f16(const uint16_t *w, const uint16_t *x, int n) {
+    float acc[4][8];
+    memset(acc, 0, sizeof(acc));
+    const int np = n & ~31;
+    for (int i = 0; i < np; i += 32)
+        for (int a = 0; a < 4; a++)
+            for (int l = 0; l < 8; l++) acc[a][l] = acc[a][l] + h2f(w[i + 8 * a + l]) * h2f(x[i + 8 * a + l]);
+    for (int l = 0; l < 8; l++) {
+        acc[0][l] = acc[0][l] + acc[2][l];
+        acc[1][l] = acc[1][l] + acc[3][l];
+    }
+    for (int l = 0; l < 8; l++) acc[0][l] = acc[0][l] + acc[1][l];
+    float t[4];
+    for (int l = 0; l < 4; l++) t[l] = acc[0][l] + acc[0][l + 4];
+    const float h0 = t[0] + t[1], h1 = t[2] + t[3];
+    double sum = (double) (h0 + h1);
+    for (int i = np; i < n; i++) sum += (double) (h2f(w[i]) * h2f(x[i]));
+    return (float) sum;
+}
+
+/* ggml_mul_mat(W, x) for an F16 W of `rows` rows x `cols` and f32 x [T][cols]: y [T][rows]. */
+void or_matmul_f16(const uint16_t *W, int rows, int cols, const float *x, int T, float *y) {
+    uint16_t *xh = (uint16_t *) malloc(sizeof(uint16_t) * (size_t) T * cols);
+    for (size_t i = 0; i < (size_t) T * cols; i++) xh[i] = or_fp32_to_fp16(x[i]);
+#pragma omp parallel for collapse(2) schedule(static)
+    for (int t = 0; t < T; t++)
+        for (int r = 0; r < rows; r++)
+            y[(size_t) t * rows + r] = or_dot_f16(W + (size_t) r * cols, xh + (size_t) t * cols, cols);
+    free(xh);
+}
+
+/* ggml_rms_norm (sum of x*x in double, mean rounded to float, scale = 1/sqrtf(mean + eps), y = x * scale)
+ * followed by ggml_mul with the weight (src/qwen3.cpp:112-114). w may be NULL (no weight). */
+void or_rms_norm(const float *x, int n, const float *w, float eps, float *y) {
+    double sum = 0.0;
+    for (int i = 0; i < n; i++) sum += (double) (x[i] * x[i]);
+    const float mean = (float) (sum / n);
+    const float scale = 1.0f / sqrtf(mean + eps);
+    for (int i = 0; i < n; i++) y[i] = w ? (x[i] * scale) * w[i] : x[i] * scale;
+}
+
+/* ggml_rope_ext, NEOX mode, freq_scale 1, ext_factor 0, attn_factor 1 (src/qwen3.cpp:143-146): pair i
+ * = (x[i], x[i + hd/2]) is rotated by theta_i, theta_0 = pos and theta_{i+1} = theta_i * theta_scale
+ * (theta_scale = freq_base^(-2/hd), computed by the caller with powf). */
+void or_rope_neox(const float *x, int hd, int pos, float theta_scale, float *y) {
+    float theta = (float) pos;
+    const int half = hd / 2;
+    for (int i = 0; i < half; i++) {
+        const float c = cosf(theta), s = sinf(theta);
+        const float x0 = x[i], x1 = x[i + half];
+        y[i] = x0 * c - x1 * s;
+        y[i + half] = x0 * s + x1 * c;
+        theta *= theta_scale;
+    }
+}
+
+/* ggml_flash_attn_ext for one query row (src/qwen3.cpp:165-167): q rounded to fp16, s_j = dot_f16(K_j, q) *
+ * scale over the n visible cells in cell order, online softmax (running max M, sum S, rescale by
+ * expf(M_old - M)), V accumulated in f32 (GGML_PREC_F32), out = acc / S. K, V: n rows of hd fp16 at
+ * row stride `ld` values. */
+void or_attn_row(const float *q, const uint16_t *K, const uint16_t *V, int n, int hd, int ld, float scale, float *out) {
+    uint16_t qh[512];
+    float *acc = (float *) calloc((size_t) hd, sizeof(float));
+    for (int d = 0; d < hd; d++) qh[d] = or_fp32_to_fp16(q[d]);
+    float M = -INFINITY, S = 0.0f;
+    for (int j = 0; j < n; j++) {
+        const float s = or_dot_f16(K + (size_t) j * ld, qh, hd) * scale;
+        float ms = 1.0f, vs = 1.0f;
+        const float Mold = M;
+        if (s > M) {
+            M = s;
+            ms = expf(Mold - M);
+            for (int d = 0; d < hd; d++) acc[d] *= ms;
+        } else {
+            vs = expf(s - M);
+        }
+        const uint16_t *v = V + (size_t) j * ld;
+        for (int d = 0; d < hd; d++) acc[d] = acc[d] + h2f(v[d]) * vs;
+        S = S * ms + vs;
+    }
+    for (int d = 0; d < hd; d++) out[d] = acc[d] / S;
+    free(acc);
+}
+
+struct or_qwen3 {
+    or_qwen3_hparams hp;
+    or_qwen3_layer *layers;
+    const uint16_t *tok_embd, *output;
+    const float *output_norm;
+    int max_ctx, len;
+    float theta_scale;
+    uint16_t *K, *V; /* [n_layer][max_ctx][n_head_kv * head_dim] */
+};
+
+or_qwen3 *or_qwen3_create(const or_qwen3_hparams *hp, const or_qwen3_layer *layers, const uint16_t *tok_embd,
+                          const float *output_norm, const uint16_t *output, int max_ctx) {
+    if (hp->head_dim > 512 || hp->n_head % hp->n_head_kv) return NULL;
+    or_qwen3 *m = (or_qwen3 *) calloc(1, sizeof(or_qwen3));
+    m->hp = *hp;
+    m->layers = (or_qwen3_layer *) malloc(sizeof(or_qwen3_layer) * (size_t) hp->n_layer);
+    memcpy(m->layers, layers, sizeof(or_qwen3_layer) * (size_t) hp->n_layer);
+    m->tok_embd = tok_embd;
+    m->output = output ? output : tok_embd;
+    m->output_norm = output_norm;
+    m->max_ctx = max_ctx;
+    m->theta_scale = powf(hp->rope_freq_base, -2.0f / (float) hp->head_dim);
+    const size_t kv = (size_t) hp->n_layer * max_ctx * hp->n_head_kv * hp->head_dim;
+    m->K = (uint16_t *) calloc(kv, sizeof(uint16_t));
+    m->V = (uint16_t *) calloc(kv, sizeof(uint16_t));
+    return m;
+}
+
+void or_qwen3_destroy(or_qwen3 *m) {
+    if (!m) return;
+    free(m->layers);
+    free(m->K);
+    free(m->V);
+    free(m);
+}
+
+int or_qwen3_len(const or_qwen3 *m) { return m->len; }
+
+void or_qwen3_truncate(or_qwen3 *m, int keep) {
+    if (keep < m->len) m->len = keep < 0 ? 0 : keep;
+}
+
+/* One Engine step of one sequence (qwen3_build_graph, src/qwen3.cpp:223-259): T tokens at positions
+ * len .. len+T-1, each attending to every earlier position and itself; the last layer runs its FFN on
+ * the last row only; logits [n_vocab] of the last token. trace (optional) [n_layer][T][k] receives the
+ * router ids, -1 for the rows the last layer skips. Returns 0, or -1 when the context is full. */
+int or_qwen3_decode(or_qwen3 *m, const int32_t *tokens, int T, float *logits, int32_t *trace) {
+    const or_qwen3_hparams *hp = &m->hp;
+    if (T < 1 || m->len + T > m->max_ctx) return -1;
+    const int h = hp->n_embd, hd = hp->head_dim, nh = hp->n_head, nkv = hp->n_head_kv, k = hp->n_expert_used;
+    const int hq = nh * hd, hk = nkv * hd, E = hp->n_expert, f = hp->n_ff_exp;
+    const float kq_scale = 1.0f / sqrtf((float) hd);
+    float *x = (float *) malloc(sizeof(float) * (size_t) T * h);
+    float *hn = (float *) malloc(sizeof(float) * (size_t) T * h);
+    float *q = (float *) malloc(sizeof(float) * (size_t) T * hq);
+    float *kk = (float *) malloc(sizeof(float) * (size_t) T * hk);
+    float *vv = (float *) malloc(sizeof(float) * (size_t) T * hk);
+    float *att = (float *) malloc(sizeof(float) * (size_t) T * hq);
+    float *o = (float *) malloc(sizeof(float) * (size_t) T * h);
+    float *tmp = (float *) malloc(sizeof(float) * (size_t) (hd > h ? hd : h));
+    float *wts = (float *) malloc(sizeof(float) * (size_t) T * k);
+    int32_t *ids = (int32_t *) malloc(sizeof(int32_t) * (size_t) T * k);
+    for (int t = 0; t < T; t++)
+        for (int i = 0; i < h; i++) x[(size_t) t * h + i] = h2f(m->tok_embd[(size_t) tokens[t] * h + i]);
+    for (int l = 0; l < hp->n_layer; l++) {
+        const or_qwen3_layer *L = &m->layers[l];
+        for (int t = 0; t < T; t++) or_rms_norm(x + (size_t) t * h, h, L->attn_norm, hp->rms_eps, hn + (size_t) t * h);
+        or_matmul_f16(L->wq, hq, h, hn, T, q);
+        or_matmul_f16(L->wk, hk, h, hn, T, kk);
+        or_matmul_f16(L->wv, hk, h, hn, T, vv);
+        uint16_t *Kl = m->K + (size_t) l * m->max_ctx * hk, *Vl = m->V + (size_t) l * m->max_ctx * hk;
+        for (int t = 0; t < T; t++) {
+            const int pos = m->len + t;
+            for (int j = 0; j < nh; j++) {
+                float *qh = q + (size_t) t * hq + (size_t) j * hd;
+                if (L->q_norm) or_rms_norm(qh, hd, L->q_norm, hp->rms_eps, qh);
+                or_rope_neox(qh, hd, pos, m->theta_scale, tmp);
+                memcpy(qh, tmp, sizeof(float) * (size_t) hd);
+            }
+            for (int j = 0; j < nkv; j++) {
+                float *kh = kk + (size_t) t * hk + (size_t) j * hd;
+                if (L->k_norm) or_rms_norm(kh, hd, L->k_norm, hp->rms_eps, kh);
+                or_rope_neox(kh, hd, pos, m->theta_scale, tmp);
+                for (int d = 0; d < hd; d++) {
+                    Kl[(size_t) pos * hk + (size_t) j * hd + d] = or_fp32_to_fp16(tmp[d]);
+                    Vl[(size_t) pos * hk + (size_t) j * hd + d] = or_fp32_to_fp16(vv[(size_t) t * hk + (size_t) j * hd + d]);
+                }
+            }
+        }
+#pragma omp parallel for collapse(2) schedule(static)
+        for (int t = 0; t < T; t++)
+            for (int j = 0; j < nh; j++) {
+                const int g = j / (nh / nkv);
+                or_attn_row(q + (size_t) t * hq + (size_t) j * hd, Kl + (size_t) g * hd, Vl + (size_t) g * hd, m->len + t + 1, hd,
+                            hk, kq_scale, att + (size_t) t * hq + (size_t) j * hd);
+            }
+        or_matmul_f16(L->wo, h, hq, att, T, o);
+        for (size_t i = 0; i < (size_t) T * h; i++) x[i] = o[i] + x[i];
+        const int last = l == hp->n_layer - 1;
+        const int rows = last ? 1 : T;
+        float *xr = x + (size_t) (T - rows) * h;
+        for (int t = 0; t < rows; t++) or_rms_norm(xr + (size_t) t * h, h, L->ffn_norm, hp->rms_eps, hn + (size_t) t * h);
+        or_router(hn, rows, h, L->gate_inp, 1, E, k, ids, wts, NULL, NULL);
+        const size_t su = or_row_bytes(L->type_up, h) * f, sg = or_row_bytes(L->type_gate, h) * f,
+                     sd = or_row_bytes(L->type_down, f) * h;
+        or_moe_ffn(hn, rows, h, f, k, ids, wts, xr, L->up, L->gate, L->down, su, sg, sd, L->type_up, L->type_gate,
+                   L->type_down, xr, NULL, 8);
+        if (trace) {
+            int32_t *tr = trace + (size_t) l * T * k;
+            for (int i = 0; i < (T - rows) * k; i++) tr[i] = -1;
+            memcpy(tr + (size_t) (T - rows) * k, ids, sizeof(int32_t) * (size_t) rows * k);
+        }
+    }
+    or_rms_norm(x + (size_t) (T - 1) * h, h, m->output_norm, hp->rms_eps, tmp);
+    or_matmul_f16(m->output, hp->n_vocab, h, tmp, 1, logits);
+    m->len += T;
+    free(x);
+    free(hn);
+    free(q);
+    free(kk);
+    free(vv);
+    free(att);
+    free(o);
+    free(tmp);
+    free(wts);
+    free(ids);
+    return 0;
+}

@@ -1,4 +1,4 @@
-"""The C ABI library: it loads, exports every symbol include/lstk_moe.h declares, validates its
+"""The C ABI library: it loads, exports every symbol include/*.h declares, validates its
 inputs, and its host repacker round-trips GGUF bytes (no GPU: no compute call is made)."""
 import ctypes
 import os
@@ -13,9 +13,13 @@ ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 
 
 def declared_functions():
-    src = open(os.path.join(ROOT, "include", "lstk_moe.h")).read()
-    src = re.sub(r"/\*.*?\*/", "", src, flags=re.S)
-    return sorted(set(re.findall(r"\b(lstk_[a-z_0-9]+)\s*\(", src)))
+    names = set()
+    for hdr in sorted(os.listdir(os.path.join(ROOT, "include"))):
+        if hdr.endswith(".h"):
+            src = open(os.path.join(ROOT, "include", hdr)).read()
+            src = re.sub(r"/\*.*?\*/", "", src, flags=re.S)
+            names |= set(re.findall(r"\b(lstk_[a-z_0-9]+)\s*\(", src))
+    return sorted(names)
 
 
 def test_exports_every_declared_symbol(lstk):
