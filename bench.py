@@ -21,6 +21,10 @@ prefill: the same layer with Q4_K experts as a 512-token prefill with a Zipf(1.1
 roofline (algorithmic flops per second against the int8 MFMA peak, and expert bytes per second
 against HBM).
 
+model30b (--model30b): the whole 30B-A3B-shaped model - attention, MoE blocks and the 151936-token
+output head - decoding one sequence at a 4096-token KV context, T = 1, 8 and 32 tokens per step, each
+step a replay of the captured forward pass.
+
 cpu_baseline: the oracle (a C restatement of ggml's CPU algorithm: Q8_0 activations, int8 block
 dots, OpenMP) runs the same layer on the host cores for a bounded sample of layer passes, each with
 new hnorm rows (so new experts).
@@ -62,6 +66,11 @@ def parse():
     ap.add_argument("--stack235-layers", type=int, default=94)
     ap.add_argument("--pool-gib", type=int, default=32)
     ap.add_argument("--stream-tokens", type=int, default=8)
+    ap.add_argument("--model30b", action="store_true",
+                    help="also decode the whole 30B-A3B-shaped model (attention + MoE + head) at a long KV context")
+    ap.add_argument("--model30b-layers", type=int, default=N_LAYER)
+    ap.add_argument("--context", type=int, default=4096)
+    ap.add_argument("--model30b-tokens", type=str, default="1,8,32", help="tokens per decode step, comma-separated")
     ap.add_argument("--calibrate-copy-mib", type=int, default=0,
                     help="first run one device-to-device copy of this many MiB (the reference kernel that scales "
                          "rocprofv3's FETCH_SIZE / WRITE_SIZE counters to bytes)")
@@ -314,6 +323,99 @@ def stack235_leg(torch, L, n_layer, pool_gib, steps, warmup, stream_tokens):
     return res
 
 
+def model30b_leg(torch, L, n_layer, ctx, steps, warmup, t_list=(1, 8, 32)):
+    """The whole Qwen3-30B-A3B-shaped model: 48 layers, h 2048, 32 query / 4 KV heads of 128, vocab
+    151936 (head tied to the F16 embedding), 128 experts top-8 with f 768 as Q4_K (centred), F16
+    attention and router, all resident in HBM. Decode of one sequence at a ctx-token KV context
+    (synthetic: lstk_model_fill_context writes seeded K/V for ctx positions) with T in t_list tokens per
+    step. One step = lstk_model_prepare (host KV bookkeeping and input upload) + the replay of a captured
+    lstk_model_forward (every layer's attention and MoE block, the final norm and the output head).
+    One layer's tensors are generated and uploaded into every layer's own HBM copies.
+    Algorithmic HBM bytes per T=1 token: 48 x (attention weights + the K/V of ctx cells + router + 8
+    experts) + the 151936 x 2048 head."""
+    from localstack_amd import synth
+    hp = dict(n_layer=n_layer, n_embd=H, n_head=32, n_head_kv=4, head_dim=128, n_vocab=151936, n_expert=E,
+              n_expert_used=K, n_ff_exp=F, n_ctx_train=40960, rms_eps=1e-6, rope_freq_base=1e6)
+    rng = np.random.default_rng(30)
+    t0 = time.time()
+    L0 = synth.qwen3_weights(rng, dict(hp, n_layer=1, n_vocab=8), wtype=Q4_K)["layers"][0]
+    tok = (rng.standard_normal((hp["n_vocab"], H), dtype=np.float32) * np.float32(0.02)).astype(np.float16)
+    w = {"tok_embd": tok, "output_norm": np.ones(H, np.float32), "output": None, "layers": [L0] * n_layer}
+    t_max = max(t_list)
+    store = L.ExpertStore(n_layer, H, F, E, K, t_max, [(L0["types"], L0["up"], L0["gate"], L0["down"])] * n_layer)
+    kv = (ctx + t_max * (steps + warmup + 3) + 255) // 256 * 256
+    dev = torch.device("cuda:0")
+    model = L.Qwen3Model(hp, w, store, kv, t_max, device=dev)
+    del tok
+    log(f"[bench] 30B model: {n_layer} layers built in {time.time() - t0:.1f}s, experts {store.total_bytes() / 1e9:.1f} GB, "
+        f"KV cache {kv} cells")
+    hq, hk = 32 * 128, 4 * 128
+    attn_w = (hq * H * 2 + hk * H * 2 * 2)  # q, o, k, v (bytes, fp16)
+    kv_b = ctx * hk * 2 * 2
+    moe_b = E * H * 2 + K * 3 * (F * (H // 256) * 144)
+    head_b = hp["n_vocab"] * H * 2
+    per_tok = n_layer * (attn_w + kv_b + moe_b) + head_b
+    res = {"n_layer": n_layer, "context": ctx, "bytes_per_token_T1": per_tok,
+           "bytes_split_T1": {"attention_weights": n_layer * attn_w, "kv": n_layer * kv_b, "moe": n_layer * moe_b,
+                              "head": head_b}}
+    stream = torch.cuda.Stream()
+    logits = torch.zeros(hp["n_vocab"], dtype=torch.float32, device=dev)
+    for T in t_list:
+        seq = T
+        model.fill_context(seq, ctx, seed=T)
+        # the attended cells of the last step: a forward over at least the prepared count is exact (cells
+        # past a sequence's end are masked), so one capture serves the whole run
+        n_cells = (ctx + T * (steps + warmup + 3) + 255) // 256 * 256
+        toks = rng.integers(0, hp["n_vocab"], (steps + warmup + 4, T)).astype(np.int32)
+        # per-stage device time from two eager steps
+        model.set_timing(True)
+        store.set_timing(True)
+        for i in range(2):
+            model.decode(seq, toks[i], logits=logits)
+        torch.cuda.synchronize()
+        mms, mn = model.timing()
+        pms, pn = store.timing()
+        model.set_timing(False)
+        store.set_timing(False)
+        with torch.cuda.stream(stream):
+            model.prepare(seq, toks[2], stream=stream)
+            graph = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(graph, stream=stream):
+                model.forward(seq, T, n_cells, logits=logits, stream=stream)
+            graph.replay()
+            for i in range(warmup):
+                model.prepare(seq, toks[3 + i], stream=stream)
+                graph.replay()
+            stream.synchronize()
+            s_ev, e_ev = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            s_ev.record(stream)
+            for i in range(steps):
+                model.prepare(seq, toks[3 + warmup + i], stream=stream)
+                graph.replay()
+            e_ev.record(stream)
+            stream.synchronize()
+        ms = s_ev.elapsed_time(e_ev) / steps
+        assert torch.isfinite(logits).all()
+        stage = {"norms": mms[0] / 2, "qkv_rope": mms[1] / 2, "attention": mms[2] / 2, "o_proj": mms[3] / 2,
+                 "head": mms[4] / 2, "moe_router": pms[0] / 2, "moe_gate_up": pms[1] / 2, "moe_down": pms[2] / 2,
+                 "moe_combine": pms[3] / 2}
+        moe_ms = sum(pms) / 2
+        r = {"tok_s": T * 1000.0 / ms, "ms_per_step": ms, "steps": steps,
+             "eager_stage_ms_per_step": stage, "moe_ms_per_step": moe_ms,
+             "launches_per_step": (sum(mn) + sum(pn)) // 2, "seq_len_end": model.seq_len(seq)}
+        if T == 1:
+            r["gbs"] = per_tok / (ms * 1e-3) / 1e9
+            r["frac_hbm"] = r["gbs"] / HBM_PEAK_GBS
+            r["moe_gbs_eager"] = n_layer * moe_b / (moe_ms * 1e-3) / 1e9
+        res[f"T{T}"] = r
+        log(f"[bench] 30B model T={T}: {json.dumps(r)}")
+        del graph
+        model.remove_seq(seq)
+    model.close()
+    store.close()
+    return res
+
+
 def cpu_baseline(T, seconds):
     """Times the oracle on this host over whole layer passes of the same workload."""
     import oracle
@@ -384,6 +486,9 @@ def main():
         if a.stack235:
             out["stack235"] = stack235_leg(torch, L, a.stack235_layers, a.pool_gib, max(5, a.steps // 2), 2,
                                            a.stream_tokens)
+        if a.model30b:
+            out["model30b"] = model30b_leg(torch, L, a.model30b_layers, a.context, max(5, a.steps // 5), 2,
+                                            tuple(int(t) for t in a.model30b_tokens.split(",")))
         print(json.dumps(out), flush=True)
         return
     st = Stack(torch, L, a.layers, t_max=max(8, a.tokens))
@@ -408,6 +513,10 @@ def main():
     if a.stack235:
         s235 = stack235_leg(torch, L, a.stack235_layers, a.pool_gib, max(5, a.steps // 2), 2, a.stream_tokens)
         log(f"[bench] 235B stack: {json.dumps(s235)}")
+    m30 = None
+    if a.model30b:
+        m30 = model30b_leg(torch, L, a.model30b_layers, a.context, max(5, a.steps // 5), 2,
+                                            tuple(int(t) for t in a.model30b_tokens.split(",")))
     cpu = None if a.no_cpu else cpu_baseline(a.tokens, a.cpu_seconds)
     gu_avg_s = main_res["stage_avg_us"]["gate_up"] * 1e-6
     achieved = main_res["gate_up_bytes"] / gu_avg_s / 1e9
@@ -440,6 +549,7 @@ def main():
                                           "distinct_experts_per_layer": extra["distinct_experts_per_layer"]},
         "prefill": pre,
         "stack235": s235,
+        "model30b": m30,
         "cpu_baseline": cpu,
     }
     print(json.dumps(line), flush=True)

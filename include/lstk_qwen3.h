@@ -71,8 +71,8 @@ typedef struct lstk_qwen3_weights {
 
 /* Creates the forward pass over `pool` (whose dims must match hp) with a KV cache of kv_size cells
  * (a multiple of 256, like the reference's n_ctx) and steps of at most n_batch tokens
- * (EngineParams::n_batch, at most the pool's n_batch). head_dim must be a power of two in [16, 256];
- * n_embd and n_head * head_dim multiples of 8 and at most 32768. The KV cache (fp16,
+ * (EngineParams::n_batch, at most the pool's n_batch). head_dim must be 64, 128 or 256;
+ * n_embd and n_head * head_dim multiples of 8 and at most 8192. The KV cache (fp16,
  * 2 * n_layer * kv_size * n_head_kv * head_dim * 2 bytes) and the step scratch are allocated here, on
  * the current device. The pool is not owned and must outlive the model. */
 int lstk_model_create(const lstk_qwen3_hparams *hp, const lstk_qwen3_weights *w, lstk_pool *pool, uint32_t kv_size,
@@ -89,10 +89,29 @@ void lstk_model_destroy(lstk_model *model);
 int lstk_model_decode(lstk_model *model, int32_t seq, const int32_t *tokens, int n_tokens, float *d_logits,
                       int32_t *d_trace, lstk_stream_t stream);
 
+/* lstk_model_decode in two halves, for callers that replay a step as a HIP graph.
+ * prepare: Engine::make_step_inputs (src/engine.cpp:200-243) - reserves the KV cells of n_tokens
+ *   (<= n_batch) host tokens of `seq`, queues their upload to the model's input buffer on `stream` and
+ *   returns the number of attended cells in *n_cells.
+ * forward: the step's kernels over those inputs, writing the last token's logits (and the trace, as
+ *   lstk_model_decode). With a resident pool it makes no host synchronisation and no allocation, so it
+ *   may be captured; a captured forward replays correctly after each prepare of the same seq,
+ *   n_tokens and n_cells (n_cells changes only when the sequence crosses a multiple of 256 cells).
+ *   With a streaming pool it synchronises the stream once per layer (the router's ids go to the host). */
+int lstk_model_prepare(lstk_model *model, int32_t seq, const int32_t *tokens, int n_tokens, int32_t *n_cells,
+                       lstk_stream_t stream);
+int lstk_model_forward(lstk_model *model, int32_t seq, int n_tokens, int32_t n_cells, float *d_logits,
+                       int32_t *d_trace, lstk_stream_t stream);
+
 /* KvCache::remove_seq / truncate_seq / length (src/kv_cache.cpp:97-150, src/engine.h:75-80). */
 int lstk_model_remove_seq(lstk_model *model, int32_t seq);
 int lstk_model_truncate_seq(lstk_model *model, int32_t seq, int32_t keep);
 int32_t lstk_model_seq_len(const lstk_model *model, int32_t seq);
+
+/* Appends n_cells positions to sequence `seq` without running tokens: their K and V cells hold seeded
+ * pseudo-random fp16 values in [-1, 1). A synthetic context of a given length, for measuring decode
+ * at that KV length without a prefill; it has no counterpart in the reference. */
+int lstk_model_fill_context(lstk_model *model, int32_t seq, int n_cells, uint64_t seed, lstk_stream_t stream);
 
 /* Per-stage device time of the forward pass's own kernels, recorded like lstk_pool_timing:
  * stage 0 = norms + embedding, 1 = Q/K/V + QK-norm + RoPE + KV store, 2 = attention,

@@ -95,6 +95,9 @@ SIGNATURES = {
                                ctypes.c_uint32, ctypes.POINTER(_P)]),
     "lstk_model_destroy": (None, [_P]),
     "lstk_model_decode": (_I, [_P, ctypes.c_int32, _P, _I, _P, _P, _P]),
+    "lstk_model_prepare": (_I, [_P, ctypes.c_int32, _P, _I, ctypes.POINTER(ctypes.c_int32), _P]),
+    "lstk_model_forward": (_I, [_P, ctypes.c_int32, _I, ctypes.c_int32, _P, _P, _P]),
+    "lstk_model_fill_context": (_I, [_P, ctypes.c_int32, _I, ctypes.c_uint64, _P]),
     "lstk_model_remove_seq": (_I, [_P, ctypes.c_int32]),
     "lstk_model_truncate_seq": (_I, [_P, ctypes.c_int32, ctypes.c_int32]),
     "lstk_model_seq_len": (ctypes.c_int32, [_P, ctypes.c_int32]),
@@ -347,6 +350,24 @@ class Qwen3Model:
         _check(lib().lstk_model_decode(self._h, int(seq), tok.ctypes.data, tok.size, _ptr(out), _ptr(trace),
                                        _stream(stream)))
         return out
+
+    def prepare(self, seq, tokens, stream=None):
+        """First half of a step: KV cells and input upload; returns the attended cell count."""
+        tok = np.ascontiguousarray(tokens, dtype=np.int32).ravel()
+        n = ctypes.c_int32()
+        _check(lib().lstk_model_prepare(self._h, int(seq), tok.ctypes.data, tok.size, ctypes.byref(n), _stream(stream)))
+        return n.value
+
+    def forward(self, seq, n_tokens, n_cells, trace=None, logits=None, stream=None):
+        """Second half of a step: the kernels (capturable in a HIP graph with a resident pool)."""
+        out = self.logits if logits is None else logits
+        _check(lib().lstk_model_forward(self._h, int(seq), int(n_tokens), int(n_cells), _ptr(out), _ptr(trace),
+                                        _stream(stream)))
+        return out
+
+    def fill_context(self, seq, n_cells, seed=0, stream=None):
+        """Appends n_cells synthetic positions (seeded random K/V, no tokens run) to sequence seq."""
+        _check(lib().lstk_model_fill_context(self._h, int(seq), int(n_cells), int(seed), _stream(stream)))
 
     def remove_seq(self, seq):
         _check(lib().lstk_model_remove_seq(self._h, int(seq)))

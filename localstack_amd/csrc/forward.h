@@ -34,7 +34,9 @@ struct GemvSeg {
 };
 
 // Up to three matrices with the same input (Q, K and V) in one launch; rows of the segments are
-// numbered one after the other.
+// numbered one after the other. For a single token (T == 1) the input row may be normalised on the way
+// in: with norm_w set, x is replaced by rms_norm(x) * norm_w (the reference's attn_norm before Q/K/V),
+// and with emb set, x is first gathered from the F16 embedding row tokens[0] and written to x_out.
 struct GemvParams {
     GemvSeg seg[3];
     int nseg;
@@ -42,11 +44,18 @@ struct GemvParams {
     int cols;
     const float *x; // [T][cols]
     int T;
+    const float *norm_w;
+    float eps;
+    const uint16_t *emb;
+    const int32_t *tokens;
+    float *x_out;
 };
 
 // Per-head RMSNorm (optional), NEOX RoPE and the KV-cache store of one step.
-// K cache layout [n_head_kv][head_dim / 8][kv_size][8] fp16 (a wavefront reading 64 consecutive cells of
-// one 8-value group issues one 1 KiB load); V cache layout [n_head_kv][kv_size][head_dim] fp16.
+// The cache layouts are the operand fragments of the attention's matrix-core products (16 x 16 x 16
+// fp16): K [n_head_kv][head_dim / 4][kv_size][4] (4 consecutive dims of a cell, 16 cells side by side)
+// and V [n_head_kv][kv_size / 4][head_dim][4] (4 consecutive cells of a dim, 16 dims side by side), so
+// every fragment a lane needs is one 8-byte load and 16 lanes read 128 contiguous bytes.
 struct RopeParams {
     const float *q, *k, *v; // [T][n_head * hd], [T][n_head_kv * hd] x 2
     const float *q_norm, *k_norm;
@@ -60,17 +69,19 @@ struct RopeParams {
     uint16_t *kc, *vc; // this layer's caches
 };
 
-// Causal attention of one step over cells [0, n_cells) of one layer's cache. Work-group (c, h, t) covers
-// cells [c * chunk, (c + 1) * chunk) for query head h of token t; with n_chunk == 1 it writes `out`
-// directly, otherwise partial (max, sum, unnormalised output) rows into `part` for the combine.
+// Causal attention of one step over cells [0, n_cells) of one layer's cache. The query rows of a KV head
+// are its n_head / n_kv query heads times the T tokens (row r = token r / grp, head r % grp); work-group
+// (rb, c, g) covers rows [rb * rb_rows, (rb + 1) * rb_rows) of KV head g against cells
+// [c * chunk, (c + 1) * chunk), reading each K/V fragment once for all of them. With n_chunk == 1 it
+// writes `out` directly, otherwise partial (max, sum, unnormalised output) rows into `part`.
 struct AttnParams {
     const float *q; // [T][n_head][hd]
     const uint16_t *kc, *vc;
     const int32_t *cell_seq, *cell_pos, *pos;
     int32_t seq;
-    int T, n_head, n_kv, hd, kv_size, n_cells, chunk, n_chunk;
+    int T, n_head, n_kv, hd, kv_size, n_cells, chunk, n_chunk, n_rowblk, rb_rows;
     float scale;
-    float *part; // [T][n_head][n_chunk][hd + 2]
+    float *part; // [T][n_head][n_chunk][hd + 4]: max, sum, 2 unused, unnormalised output
     float *out;  // [T][n_head * hd]
 };
 
@@ -81,9 +92,27 @@ struct FillParams {
     int32_t v;
 };
 
+// Synthetic context: for the T cells of `cells` (positions `pos`), every layer's K and V get
+// pseudo-random fp16 values in [-1, 1) derived from (seed, layer, position, head, dim); the cells are
+// marked as belonging to `seq`.
+struct FillKvParams {
+    const int32_t *cells, *pos;
+    int32_t seq;
+    int32_t *cell_seq, *cell_pos;
+    int T, n_layer, n_kv, hd, kv_size;
+    size_t layer_elems;
+    uint16_t *kcache, *vcache;
+    uint64_t seed;
+};
+
 bool gemv_supported(int cols);
+bool rmsnorm_supported(int n);
 bool attn_supported(int hd);
-int attn_chunk_cells(int T, int n_head, int n_cells, int *n_chunk);
+// Plans the attention launch of a step: fills chunk, n_chunk, n_rowblk and rb_rows of P from T, n_head,
+// n_kv and n_cells. The partial rows (T * n_head * n_chunk when n_chunk > 1) stay below
+// attn_part_rows(n_batch, n_head).
+void attn_plan(AttnParams &P);
+size_t attn_part_rows(int n_batch, int n_head);
 
 hipError_t launch_rmsnorm(const NormParams &P, hipStream_t st, const LaunchTiming *tm);
 hipError_t launch_gemv(const GemvParams &P, hipStream_t st, const LaunchTiming *tm);
@@ -91,5 +120,6 @@ hipError_t launch_rope(const RopeParams &P, hipStream_t st, const LaunchTiming *
 hipError_t launch_attn(const AttnParams &P, hipStream_t st, const LaunchTiming *tm);
 hipError_t launch_attn_combine(const AttnParams &P, hipStream_t st, const LaunchTiming *tm);
 hipError_t launch_fill(const FillParams &P, hipStream_t st, const LaunchTiming *tm);
+hipError_t launch_fill_kv(const FillKvParams &P, hipStream_t st, const LaunchTiming *tm);
 
 }  // namespace lstk

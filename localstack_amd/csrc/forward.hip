@@ -21,7 +21,6 @@ constexpr int kGvWaves = 4;     // wavefronts per GEMV work-group
 constexpr int kGvRows = 4;      // rows per wavefront
 constexpr int kGvMaxLds = 64 * 1024;
 constexpr int kAtBlock = 256;   // attention: one cell per thread per pass
-constexpr int kAtMaxHd = 256;
 
 __device__ __forceinline__ uint16_t f2h(float f) { return __half_as_ushort(__float2half_rn(f)); }
 __device__ __forceinline__ uint32_t pack2(float a, float b) { return (uint32_t) f2h(a) | ((uint32_t) f2h(b) << 16); }
@@ -38,27 +37,38 @@ __device__ __forceinline__ float dot8(const uint4 &a, const uint4 &b, float c) {
 // RMSNorm (ggml_rms_norm + ggml_mul), optionally gathering the row from the embedding table first
 // ------------------------------------------------------------------------------------------------
 
+// NPT values per thread, all loaded before any is used (one memory round trip per row).
+template <int NPT>
 __global__ __launch_bounds__(kNormBlock) void rmsnorm_kernel(NormParams P) {
     __shared__ double s_part[kNormBlock / kWave];
     const int r = blockIdx.x, tid = threadIdx.x;
     const size_t off = (size_t) r * P.n;
     const uint16_t *e = P.emb ? P.emb + (size_t) P.tokens[r] * P.n : nullptr;
     const float *x = P.x + off;
-    double s = 0.0;
-    for (int i = tid; i < P.n; i += kNormBlock) {
-        const float v = e ? h2f(e[i]) : x[i];
-        if (e) P.x_out[off + i] = v;
-        s += (double) (v * v);
+    float v[NPT], w[NPT];
+#pragma unroll
+    for (int k = 0; k < NPT; k++) {
+        const int i = tid + k * kNormBlock;
+        const bool on = i < P.n;
+        v[k] = !on ? 0.0f : e ? h2f(e[i]) : x[i];
+        w[k] = on ? P.w[i] : 0.0f;
     }
+    double s = 0.0;
+#pragma unroll
+    for (int k = 0; k < NPT; k++) s += (double) (v[k] * v[k]);
     s = wave_sum_d(s);
     if ((tid & (kWave - 1)) == 0) s_part[tid / kWave] = s;
     __syncthreads();
     const double tot = (s_part[0] + s_part[1]) + (s_part[2] + s_part[3]);
     const float mean = (float) (tot / (double) P.n);
     const float scale = 1.0f / sqrtf(mean + P.eps);
-    for (int i = tid; i < P.n; i += kNormBlock) {
-        const float v = e ? h2f(e[i]) : x[i];
-        P.y[off + i] = (v * scale) * P.w[i];
+#pragma unroll
+    for (int k = 0; k < NPT; k++) {
+        const int i = tid + k * kNormBlock;
+        if (i < P.n) {
+            if (e) P.x_out[off + i] = v[k];
+            P.y[off + i] = (v[k] * scale) * w[k];
+        }
     }
 }
 
@@ -138,11 +148,125 @@ __global__ __launch_bounds__(kGvWaves *kWave) void gemv_kernel(GemvParams P) {
 }
 
 // ------------------------------------------------------------------------------------------------
+// single-token F16 GEMV: every weight chunk of the wavefront's RW rows is requested before anything
+// waits (NJ = ceil(cols / 512) 16-byte chunks per lane per row), the activation row comes straight
+// from memory into registers (no LDS, no barrier), optionally gathered from the embedding and
+// RMS-normalised on the way (one wavefront-wide double sum per wavefront).
+// ------------------------------------------------------------------------------------------------
+
+template <int NJ, int RW>
+__global__ __launch_bounds__(kGvWaves *kWave) void gemv1_kernel(GemvParams P) {
+    const int tid = threadIdx.x, lane = tid & (kWave - 1), wv = tid / kWave;
+    const int cols = P.cols, nc = cols / 8;
+    const int row0 = (blockIdx.x * kGvWaves + wv) * RW;
+    const uint4 *wr[RW];
+    float *yr[RW];
+    const float *ar[RW];
+    bool on[RW];
+#pragma unroll
+    for (int rr = 0; rr < RW; rr++) {
+        const int r = row0 + rr;
+        on[rr] = r < P.rows_total;
+        int loc = on[rr] ? r : 0, s = 0;
+        while (s + 1 < P.nseg && loc >= P.seg[s].rows) {
+            loc -= P.seg[s].rows;
+            s++;
+        }
+        wr[rr] = reinterpret_cast<const uint4 *>(P.seg[s].w + (size_t) loc * cols);
+        yr[rr] = P.seg[s].y + loc;
+        ar[rr] = P.seg[s].add ? P.seg[s].add + loc : nullptr;
+    }
+    uint4 w[RW][NJ];
+#pragma unroll
+    for (int j = 0; j < NJ; j++) {
+        const int c = lane + kWave * j;
+#pragma unroll
+        for (int rr = 0; rr < RW; rr++) w[rr][j] = c < nc ? wr[rr][c] : make_uint4(0, 0, 0, 0);
+    }
+    float xv[NJ][8];
+    const uint16_t *e = P.emb ? P.emb + (size_t) P.tokens[0] * cols : nullptr;
+#pragma unroll
+    for (int j = 0; j < NJ; j++) {
+        const int c = lane + kWave * j;
+        if (c < nc) {
+            if (e) {
+                const uint4 hv = reinterpret_cast<const uint4 *>(e)[c];
+                const uint32_t hw[4] = {hv.x, hv.y, hv.z, hv.w};
+#pragma unroll
+                for (int q = 0; q < 4; q++) {
+                    xv[j][2 * q] = h2f(hw[q]);
+                    xv[j][2 * q + 1] = h2f(hw[q] >> 16);
+                }
+            } else {
+                const float4 a = reinterpret_cast<const float4 *>(P.x)[2 * c];
+                const float4 b = reinterpret_cast<const float4 *>(P.x)[2 * c + 1];
+                xv[j][0] = a.x, xv[j][1] = a.y, xv[j][2] = a.z, xv[j][3] = a.w;
+                xv[j][4] = b.x, xv[j][5] = b.y, xv[j][6] = b.z, xv[j][7] = b.w;
+            }
+        } else {
+#pragma unroll
+            for (int q = 0; q < 8; q++) xv[j][q] = 0.0f;
+        }
+    }
+    if (e && blockIdx.x == 0 && wv == 0) {
+#pragma unroll
+        for (int j = 0; j < NJ; j++) {
+            const int c = lane + kWave * j;
+            if (c < nc) {
+                reinterpret_cast<float4 *>(P.x_out)[2 * c] = make_float4(xv[j][0], xv[j][1], xv[j][2], xv[j][3]);
+                reinterpret_cast<float4 *>(P.x_out)[2 * c + 1] = make_float4(xv[j][4], xv[j][5], xv[j][6], xv[j][7]);
+            }
+        }
+    }
+    if (P.norm_w) {
+        float nw[NJ][8];
+#pragma unroll
+        for (int j = 0; j < NJ; j++) {
+            const int c = lane + kWave * j;
+            const float4 a = c < nc ? reinterpret_cast<const float4 *>(P.norm_w)[2 * c] : make_float4(0, 0, 0, 0);
+            const float4 b = c < nc ? reinterpret_cast<const float4 *>(P.norm_w)[2 * c + 1] : make_float4(0, 0, 0, 0);
+            nw[j][0] = a.x, nw[j][1] = a.y, nw[j][2] = a.z, nw[j][3] = a.w;
+            nw[j][4] = b.x, nw[j][5] = b.y, nw[j][6] = b.z, nw[j][7] = b.w;
+        }
+        double s = 0.0;
+#pragma unroll
+        for (int j = 0; j < NJ; j++)
+#pragma unroll
+            for (int q = 0; q < 8; q++) s += (double) (xv[j][q] * xv[j][q]);
+        s = wave_sum_d(s);
+        const float mean = (float) (s / (double) cols);
+        const float scale = 1.0f / sqrtf(mean + P.eps);
+#pragma unroll
+        for (int j = 0; j < NJ; j++)
+#pragma unroll
+            for (int q = 0; q < 8; q++) xv[j][q] = (xv[j][q] * scale) * nw[j][q];
+    }
+    float acc[RW];
+#pragma unroll
+    for (int rr = 0; rr < RW; rr++) acc[rr] = 0.0f;
+#pragma unroll
+    for (int j = 0; j < NJ; j++) {
+        const uint4 xh = make_uint4(pack2(xv[j][0], xv[j][1]), pack2(xv[j][2], xv[j][3]), pack2(xv[j][4], xv[j][5]),
+                                    pack2(xv[j][6], xv[j][7]));
+#pragma unroll
+        for (int rr = 0; rr < RW; rr++) acc[rr] = dot8(w[rr][j], xh, acc[rr]);
+    }
+#pragma unroll
+    for (int rr = 0; rr < RW; rr++) {
+        const float sum = wave_sum_tree(acc[rr]);
+        if (lane == 0 && on[rr]) yr[rr][0] = ar[rr] ? sum + ar[rr][0] : sum;
+    }
+}
+
+// ------------------------------------------------------------------------------------------------
 // QK-norm + NEOX RoPE + KV store: one wavefront per (token, head) of Q, K and V
 // ------------------------------------------------------------------------------------------------
 
 __device__ __forceinline__ size_t k_index(int head, int d, int cell, int hd, int kv_size) {
-    return (((size_t) head * (hd / 8) + d / 8) * kv_size + cell) * 8 + (d & 7);
+    return (((size_t) head * (hd / 4) + d / 4) * kv_size + cell) * 4 + (d & 3);
+}
+__device__ __forceinline__ size_t v_index(int head, int d, int cell, int hd, int kv_size) {
+    return (((size_t) head * (kv_size / 4) + cell / 4) * hd + d) * 4 + (cell & 3);
 }
 
 __global__ __launch_bounds__(kWave) void rope_kernel(RopeParams P) {
@@ -156,8 +280,7 @@ __global__ __launch_bounds__(kWave) void rope_kernel(RopeParams P) {
     if (j >= P.n_head + P.n_kv) {
         const int head = j - P.n_head - P.n_kv;
         const float *src = P.v + ((size_t) t * P.n_kv + head) * hd;
-        uint16_t *dst = P.vc + ((size_t) head * P.kv_size + cell) * hd;
-        for (int d = lane; d < hd; d += kWave) dst[d] = f2h(src[d]);
+        for (int d = lane; d < hd; d += kWave) P.vc[v_index(head, d, cell, hd, P.kv_size)] = f2h(src[d]);
         return;
     }
     const bool is_q = j < P.n_head;
@@ -199,118 +322,266 @@ __global__ __launch_bounds__(kWave) void rope_kernel(RopeParams P) {
 }
 
 // ------------------------------------------------------------------------------------------------
-// attention: work-group (chunk, head, token); 256 cells per pass (one per thread for the scores),
-// online softmax across passes, P.V with (hd / 8) threads per cell and 256 / (hd / 8) cells at once
+// attention on the matrix cores. Work-group (rb, c, g): up to 64 query rows (the query heads of KV head
+// g times the step's tokens) against its chunk of cells, 64 cells per pass:
+//   S = Q K^T   wavefront w owns cells [16 w, 16 w + 16) of the pass: HD / 16 products per 16-row tile,
+//               K fragments loaded straight from the cache (one 8-byte load per lane per product);
+//   softmax     4 threads per row over the pass's 64 cells, online across passes (running max, sum and a
+//               rescale factor per row in LDS);
+//   O += P V    wavefront w owns output dims [16 HD/64 w, ...): P is split into fp16 hi + lo parts
+//               (p = hi + lo to 2^-22), both multiplied by the V fragments, so the product keeps the
+//               f32 precision of the probabilities; V fragments are requested at the start of the pass.
+// Q and K enter as fp16 (Q rounded, as ggml rounds Q to F16 for F16 K), all accumulation is f32.
 // ------------------------------------------------------------------------------------------------
 
+typedef _Float16 half4v __attribute__((ext_vector_type(4)));
+typedef float f32x4v __attribute__((ext_vector_type(4)));
+constexpr int kFaCells = 64;
+
+__device__ __forceinline__ f32x4v mfma16(half4v a, half4v b, f32x4v c) {
+    return __builtin_amdgcn_mfma_f32_16x16x16f16(a, b, c, 0, 0, 0);
+}
+__device__ __forceinline__ half4v ld_half4(const uint16_t *p) {
+    return __builtin_bit_cast(half4v, *reinterpret_cast<const uint2 *>(p));
+}
+
+template <int HD, int NRT>
 __global__ __launch_bounds__(kAtBlock) void attn_kernel(AttnParams P) {
-    __shared__ uint4 s_q4[kAtMaxHd / 8];
-    __shared__ float s_p[kAtBlock];
-    __shared__ float s_red[2 * (kAtBlock / kWave)];
-    __shared__ float s_acc[kAtBlock * 8];
-    uint32_t *s_q = reinterpret_cast<uint32_t *>(s_q4);
-    const int c = blockIdx.x, h = blockIdx.y, t = blockIdx.z, tid = threadIdx.x;
-    const int lane = tid & (kWave - 1), wv = tid / kWave;
-    const int hd = P.hd, n8 = hd / 8, G = kAtBlock / n8;
-    const int kvh = h / (P.n_head / P.n_kv);
-    const float *q = P.q + ((size_t) t * P.n_head + h) * hd;
-    for (int i = tid; i < hd / 2; i += kAtBlock) s_q[i] = pack2(q[2 * i], q[2 * i + 1]);
+    constexpr int NK = HD / 16, DT = NK / 4, RB = 16 * NRT, PS = kFaCells + 8; // P row stride (halves)
+    __shared__ float s_S[RB][kFaCells];
+    __shared__ uint16_t s_Ph[RB][PS], s_Pl[RB][PS];
+    __shared__ float s_M[RB], s_L[RB], s_f[RB];
+    __shared__ int s_pos[RB];
+    const int tid = threadIdx.x, w = tid / kWave, l = tid & (kWave - 1), lr = l & 15, lq = l >> 4;
+    const int grp = P.n_head / P.n_kv;
+    const int g = blockIdx.x % P.n_kv, rest = blockIdx.x / P.n_kv;
+    const int c = rest % P.n_chunk, rb = rest / P.n_chunk;
+    const int row0 = rb * P.rb_rows, rows = P.T * grp;
+    if (tid < RB) {
+        const int r = row0 + tid;
+        s_pos[tid] = r < rows ? P.pos[r / grp] : -1;
+        s_M[tid] = -INFINITY;
+        s_L[tid] = 0.0f;
+    }
+    // Q fragments (A operand): row rt*16 + lr, dims ks*16 + 4 lq .. +3
+    half4v qa[NRT][NK];
+#pragma unroll
+    for (int rt = 0; rt < NRT; rt++) {
+        const int r = row0 + rt * 16 + lr;
+        const bool on = r < rows;
+        const float *q = P.q + ((size_t) (on ? r / grp : 0) * P.n_head + g * grp + (on ? r % grp : 0)) * HD;
+#pragma unroll
+        for (int ks = 0; ks < NK; ks++) {
+            const float4 v = on ? *reinterpret_cast<const float4 *>(q + ks * 16 + 4 * lq) : make_float4(0, 0, 0, 0);
+            qa[rt][ks] = half4v{(_Float16) v.x, (_Float16) v.y, (_Float16) v.z, (_Float16) v.w};
+        }
+    }
+    f32x4v O[NRT][DT];
+#pragma unroll
+    for (int rt = 0; rt < NRT; rt++)
+#pragma unroll
+        for (int dt = 0; dt < DT; dt++) O[rt][dt] = f32x4v{0, 0, 0, 0};
     __syncthreads();
 
-    const int my_pos = P.pos[t];
-    const int begin = c * P.chunk, end = min(begin + P.chunk, P.n_cells);
-    const int d8 = tid % n8, g = tid / n8;
-    const uint16_t *kbase = P.kc + (size_t) kvh * n8 * P.kv_size * 8;
-    const uint16_t *vbase = P.vc + (size_t) kvh * P.kv_size * hd;
-    float m_run = -INFINITY, l_run = 0.0f;
-    float acc[8];
+    const uint16_t *kb = P.kc + (size_t) g * (HD / 4) * P.kv_size * 4;
+    const int begin = c * P.chunk, end = min(begin + P.chunk, P.n_cells), last4 = P.kv_size - 4;
+    for (int c0 = begin; c0 < end; c0 += kFaCells) {
+        // V fragments of this pass (B operand of O += P V): cells kc*16 + 4 lq .. +3, dim (w*DT + dt)*16 + lr
+        half4v vf[4][DT];
 #pragma unroll
-    for (int e = 0; e < 8; e++) acc[e] = 0.0f;
-
-    for (int base = begin; base < end; base += kAtBlock) {
-        const int j = base + tid;
-        float s = -INFINITY;
-        if (j < end && P.cell_seq[j] == P.seq && P.cell_pos[j] <= my_pos) {
-            float d = 0.0f;
-            for (int cc = 0; cc < n8; cc++) {
-                const uint4 kv = *reinterpret_cast<const uint4 *>(kbase + ((size_t) cc * P.kv_size + j) * 8);
-                d = dot8(kv, s_q4[cc], d);
-            }
-            s = d * P.scale;
+        for (int kc = 0; kc < 4; kc++) {
+            const int cg = min(c0 + kc * 16 + 4 * lq, last4);
+#pragma unroll
+            for (int dt = 0; dt < DT; dt++) vf[kc][dt] = ld_half4(P.vc + v_index(g, (w * DT + dt) * 16 + lr, cg, HD, P.kv_size));
         }
-        const float wm = wave_max(s);
-        if (lane == 0) s_red[wv] = wm;
-        __syncthreads();
-        const float m = fmaxf(fmaxf(s_red[0], s_red[1]), fmaxf(s_red[2], s_red[3]));
-        __syncthreads();
-        const float m_new = fmaxf(m_run, m);
-        if (m_new == -INFINITY) continue; // nothing visible yet (uniform across the work-group)
-        const float p = s == -INFINITY ? 0.0f : expf(s - m_new);
-        s_p[tid] = p;
-        const float ws = wave_sum_tree(p);
-        if (lane == 0) s_red[4 + wv] = ws;
-        __syncthreads();
-        const float psum = (s_red[4] + s_red[5]) + (s_red[6] + s_red[7]);
-        const float f = expf(m_run - m_new);
-        l_run = l_run * f + psum;
+        // S = Q K^T for this wavefront's 16 cells
+        const int cell = c0 + 16 * w + lr;
+        const int cc = min(cell, P.kv_size - 1);
+        half4v kf[NK];
 #pragma unroll
-        for (int e = 0; e < 8; e++) acc[e] *= f;
-        m_run = m_new;
-        for (int jj = g; jj < kAtBlock; jj += G) {
-            const float pj = s_p[jj];
-            if (pj != 0.0f) {
-                const uint4 vv = *reinterpret_cast<const uint4 *>(vbase + (size_t) (base + jj) * hd + d8 * 8);
-                acc[0] += pj * h2f(vv.x);
-                acc[1] += pj * h2f(vv.x >> 16);
-                acc[2] += pj * h2f(vv.y);
-                acc[3] += pj * h2f(vv.y >> 16);
-                acc[4] += pj * h2f(vv.z);
-                acc[5] += pj * h2f(vv.z >> 16);
-                acc[6] += pj * h2f(vv.w);
-                acc[7] += pj * h2f(vv.w >> 16);
+        for (int ks = 0; ks < NK; ks++) kf[ks] = ld_half4(kb + ((size_t) (ks * 4 + lq) * P.kv_size + cc) * 4);
+        const bool live = cell < end && P.cell_seq[cc] == P.seq;
+        const int cpos = P.cell_pos[cc];
+#pragma unroll
+        for (int rt = 0; rt < NRT; rt++) {
+            f32x4v sacc = f32x4v{0, 0, 0, 0};
+#pragma unroll
+            for (int ks = 0; ks < NK; ks++) sacc = mfma16(qa[rt][ks], kf[ks], sacc);
+#pragma unroll
+            for (int v = 0; v < 4; v++) {
+                const int r = rt * 16 + 4 * lq + v;
+                const bool vis = live && s_pos[r] >= 0 && cpos <= s_pos[r];
+                s_S[r][16 * w + lr] = vis ? sacc[v] * P.scale : -INFINITY;
+            }
+        }
+        __syncthreads();
+        // online softmax: 4 threads per row, 16 cells each
+        {
+            const int r = tid >> 2, part = tid & 3;
+            if (r < RB) {
+                float sv[16];
+                float m = -INFINITY;
+#pragma unroll
+                for (int i = 0; i < 16; i++) {
+                    sv[i] = s_S[r][part * 16 + i];
+                    m = fmaxf(m, sv[i]);
+                }
+                m = fmaxf(m, __shfl_xor(m, 1));
+                m = fmaxf(m, __shfl_xor(m, 2));
+                const float m_old = s_M[r], m_new = fmaxf(m_old, m);
+                float sum = 0.0f;
+#pragma unroll
+                for (int i = 0; i < 16; i++) {
+                    const float p = sv[i] == -INFINITY ? 0.0f : expf(sv[i] - m_new);
+                    const _Float16 hi = (_Float16) p;
+                    const _Float16 lo = (_Float16) (p - (float) hi);
+                    s_Ph[r][part * 16 + i] = __builtin_bit_cast(uint16_t, hi);
+                    s_Pl[r][part * 16 + i] = __builtin_bit_cast(uint16_t, lo);
+                    sum += p;
+                }
+                sum += __shfl_xor(sum, 1);
+                sum += __shfl_xor(sum, 2);
+                if (part == 0) {
+                    const float f = m_old == -INFINITY ? 0.0f : expf(m_old - m_new);
+                    s_f[r] = f;
+                    s_L[r] = s_L[r] * f + sum;
+                    s_M[r] = m_new;
+                }
+            }
+        }
+        __syncthreads();
+        // O = O * f + P V
+#pragma unroll
+        for (int rt = 0; rt < NRT; rt++) {
+#pragma unroll
+            for (int v = 0; v < 4; v++) {
+                const float f = s_f[rt * 16 + 4 * lq + v];
+#pragma unroll
+                for (int dt = 0; dt < DT; dt++) O[rt][dt][v] *= f;
+            }
+#pragma unroll
+            for (int kc = 0; kc < 4; kc++) {
+                const half4v ph = ld_half4(&s_Ph[rt * 16 + lr][kc * 16 + 4 * lq]);
+                const half4v pl = ld_half4(&s_Pl[rt * 16 + lr][kc * 16 + 4 * lq]);
+#pragma unroll
+                for (int dt = 0; dt < DT; dt++) {
+                    O[rt][dt] = mfma16(ph, vf[kc][dt], O[rt][dt]);
+                    O[rt][dt] = mfma16(pl, vf[kc][dt], O[rt][dt]);
+                }
             }
         }
         __syncthreads();
     }
+    // rows of this lane: rt*16 + 4 lq + v, dims (w*DT + dt)*16 + lr
 #pragma unroll
-    for (int e = 0; e < 8; e++) s_acc[g * hd + d8 * 8 + e] = acc[e];
-    __syncthreads();
-    if (tid < hd) {
-        float o = 0.0f;
-        for (int gg = 0; gg < G; gg++) o += s_acc[gg * hd + tid];
-        if (P.n_chunk == 1) {
-            P.out[((size_t) t * P.n_head + h) * hd + tid] = o / l_run;
-        } else {
-            float *pp = P.part + (((size_t) t * P.n_head + h) * P.n_chunk + c) * (hd + 2);
-            pp[2 + tid] = o;
-            if (tid == 0) {
-                pp[0] = m_run;
-                pp[1] = l_run;
+    for (int rt = 0; rt < NRT; rt++) {
+#pragma unroll
+        for (int v = 0; v < 4; v++) {
+            const int rl = rt * 16 + 4 * lq + v, r = row0 + rl;
+            if (r >= rows) continue;
+            const int t = r / grp, h = g * grp + r % grp;
+            if (P.n_chunk == 1) {
+                const float inv_l = s_L[rl];
+#pragma unroll
+                for (int dt = 0; dt < DT; dt++) P.out[((size_t) t * P.n_head + h) * HD + (w * DT + dt) * 16 + lr] = O[rt][dt][v] / inv_l;
+            } else {
+                float *pp = P.part + (((size_t) t * P.n_head + h) * P.n_chunk + c) * (HD + 4);
+#pragma unroll
+                for (int dt = 0; dt < DT; dt++) pp[4 + (w * DT + dt) * 16 + lr] = O[rt][dt][v];
+                if (w == 0 && lr == 0) {
+                    pp[0] = s_M[rl];
+                    pp[1] = s_L[rl];
+                }
             }
         }
     }
 }
 
-__global__ __launch_bounds__(kAtMaxHd) void attn_combine_kernel(AttnParams P) {
-    const int h = blockIdx.x, t = blockIdx.y, d = threadIdx.x;
-    const int hd = P.hd;
-    const float *pp = P.part + ((size_t) t * P.n_head + h) * P.n_chunk * (hd + 2);
-    float M = -INFINITY;
-    for (int c = 0; c < P.n_chunk; c++) M = fmaxf(M, pp[(size_t) c * (hd + 2)]);
-    float L = 0.0f, o = 0.0f;
-    for (int c = 0; c < P.n_chunk; c++) {
-        const float *q = pp + (size_t) c * (hd + 2);
-        if (q[0] == -INFINITY) continue;
-        const float f = expf(q[0] - M);
-        L += q[1] * f;
-        o += q[2 + d] * f;
+// Merges the chunks' partial rows of one (query head, token): out = sum_c o_c e^(m_c - M) / sum_c l_c e^(m_c - M).
+// Every thread takes chunks for the max and the factors; then hd / 4 threads per chunk read float4
+// slices of the partial outputs, 256 / (hd / 4) chunks at a time, four batches in flight.
+__global__ __launch_bounds__(kBlock) void attn_combine_kernel(AttnParams P) {
+    extern __shared__ float s_f[]; // [n_chunk] factors, then [kBlock / (hd / 4)][hd] sums
+    __shared__ float s_red[kBlock / kWave];
+    const int h = blockIdx.x, t = blockIdx.y, tid = threadIdx.x, lane = tid & (kWave - 1), wv = tid / kWave;
+    const int hd = P.hd, n = P.n_chunk, stride = hd + 4;
+    const float *pp = P.part + ((size_t) t * P.n_head + h) * n * stride;
+    float m = -INFINITY;
+    for (int c = tid; c < n; c += kBlock) m = fmaxf(m, pp[(size_t) c * stride]);
+    m = wave_max(m);
+    if (lane == 0) s_red[wv] = m;
+    __syncthreads();
+    const float M = fmaxf(fmaxf(s_red[0], s_red[1]), fmaxf(s_red[2], s_red[3]));
+    __syncthreads();
+    float ls = 0.0f;
+    for (int c = tid; c < n; c += kBlock) {
+        const float mc = pp[(size_t) c * stride];
+        const float f = mc == -INFINITY ? 0.0f : expf(mc - M);
+        s_f[c] = f;
+        ls += pp[(size_t) c * stride + 1] * f;
     }
-    P.out[((size_t) t * P.n_head + h) * hd + d] = o / L;
+    ls = wave_sum_tree(ls);
+    if (lane == 0) s_red[wv] = ls;
+    __syncthreads();
+    const float L = (s_red[0] + s_red[1]) + (s_red[2] + s_red[3]);
+    const int nq = hd / 4, CL = kBlock / nq, dq = tid % nq, cl = tid / nq;
+    float4 acc = make_float4(0, 0, 0, 0);
+    for (int c0 = cl; c0 < n; c0 += 4 * CL) {
+        float4 v[4];
+        float f[4];
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const int c = c0 + i * CL;
+            f[i] = c < n ? s_f[c] : 0.0f;
+            v[i] = c < n ? *reinterpret_cast<const float4 *>(pp + (size_t) c * stride + 4 + 4 * dq) : make_float4(0, 0, 0, 0);
+        }
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            if (f[i] == 0.0f) continue;
+            acc.x += v[i].x * f[i];
+            acc.y += v[i].y * f[i];
+            acc.z += v[i].z * f[i];
+            acc.w += v[i].w * f[i];
+        }
+    }
+    float *s_o = s_f + ((n + 3) & ~3); // 16-byte aligned
+    reinterpret_cast<float4 *>(s_o)[cl * nq + dq] = acc;
+    __syncthreads();
+    if (tid < hd) {
+        float o = 0.0f;
+        for (int i = 0; i < CL; i++) o += s_o[i * hd + tid];
+        P.out[((size_t) t * P.n_head + h) * hd + tid] = o / L;
+    }
 }
 
 __global__ __launch_bounds__(kBlock) void fill_kernel(FillParams P) {
     const int i = blockIdx.x * kBlock + threadIdx.x;
     if (i < P.n) P.p[i] = P.v;
+}
+
+// splitmix64 finaliser: a well-mixed 64-bit hash of the cell coordinates
+__device__ __forceinline__ uint64_t mix64(uint64_t z) {
+    z = (z ^ (z >> 30)) * 0xbf58476d1ce4e5b9ull;
+    z = (z ^ (z >> 27)) * 0x94d049bb133111ebull;
+    return z ^ (z >> 31);
+}
+
+__global__ __launch_bounds__(kBlock) void fill_kv_kernel(FillKvParams P) {
+    const int t = blockIdx.x, l = blockIdx.y;
+    const int cell = P.cells[t], pos = P.pos[t], hk = P.n_kv * P.hd;
+    if (l == 0 && threadIdx.x == 0) {
+        P.cell_seq[cell] = P.seq;
+        P.cell_pos[cell] = pos;
+    }
+    uint16_t *kc = P.kcache + P.layer_elems * l, *vc = P.vcache + P.layer_elems * l;
+    for (int i = threadIdx.x; i < hk; i += kBlock) {
+        const int head = i / P.hd, d = i - head * P.hd;
+        const uint64_t z = mix64(P.seed ^ mix64(((uint64_t) l << 48) ^ ((uint64_t) pos << 20) ^ (uint64_t) i));
+        const float kv = (float) (z & 0xffffff) * (2.0f / 16777216.0f) - 1.0f;
+        const float vv = (float) ((z >> 24) & 0xffffff) * (2.0f / 16777216.0f) - 1.0f;
+        kc[k_index(head, d, cell, P.hd, P.kv_size)] = f2h(kv);
+        vc[v_index(head, d, cell, P.hd, P.kv_size)] = f2h(vv);
+    }
 }
 
 template <int TG>
@@ -320,37 +591,64 @@ size_t gemv_lds(int cols) {
 
 }  // namespace
 
-bool gemv_supported(int cols) { return cols > 0 && cols % 8 == 0 && gemv_lds<1>(cols) <= (size_t) kGvMaxLds; }
+bool gemv_supported(int cols) { return cols > 0 && cols % 8 == 0 && cols <= 8192; }
 
-// head_dim a power of two in [16, 256]: the P.V phase splits the 256 threads into 256 / (hd / 8) groups.
-bool attn_supported(int hd) { return hd >= 16 && hd <= kAtMaxHd && (hd & (hd - 1)) == 0; }
+// head_dim 64, 128 or 256: the output dims split into 16-wide tiles over the 4 wavefronts.
+bool attn_supported(int hd) { return hd == 64 || hd == 128 || hd == 256; }
 
-// Splits the attended cells into chunks (multiples of 256 cells) so that a step with few
-// (token, head) pairs still launches about 1024 work-groups; returns the chunk size.
-int attn_chunk_cells(int T, int n_head, int n_cells, int *n_chunk) {
-    const int passes = (n_cells + kAtBlock - 1) / kAtBlock;
-    const int pairs = T * n_head;
-    int want = (1024 + pairs - 1) / pairs;
+// Rows of a work-group: 16, 32 or 64 (one, two or four 16-row tiles). Chunks are whole 64-cell passes,
+// as many as bring the launch to about 512 work-groups. Then T * n_head * n_chunk <= 32768 + T * n_head.
+void attn_plan(AttnParams &P) {
+    const int rows = P.T * (P.n_head / P.n_kv);
+    P.rb_rows = rows <= 16 ? 16 : rows <= 32 ? 32 : 64;
+    P.n_rowblk = (rows + P.rb_rows - 1) / P.rb_rows;
+    const int passes = (P.n_cells + kFaCells - 1) / kFaCells;
+    int want = (512 + P.n_kv * P.n_rowblk - 1) / (P.n_kv * P.n_rowblk);
     want = want < 1 ? 1 : (want > passes ? passes : want);
-    const int per = (passes + want - 1) / want;
-    const int chunk = per * kAtBlock;
-    *n_chunk = (n_cells + chunk - 1) / chunk;
-    return chunk;
+    P.chunk = (passes + want - 1) / want * kFaCells;
+    P.n_chunk = (P.n_cells + P.chunk - 1) / P.chunk;
 }
+
+size_t attn_part_rows(int n_batch, int n_head) { return 32768 + (size_t) n_batch * n_head; }
+
+bool rmsnorm_supported(int n) { return n > 0 && n <= 32 * kNormBlock; }
 
 hipError_t launch_rmsnorm(const NormParams &P, hipStream_t st, const LaunchTiming *tm) {
     if (P.rows == 0) return hipSuccess;
-    return launch(rmsnorm_kernel, dim3(P.rows), dim3(kNormBlock), 0, st, tm, P);
+    const dim3 g(P.rows), b(kNormBlock);
+    const int npt = (P.n + kNormBlock - 1) / kNormBlock;
+    if (npt <= 1) return launch(rmsnorm_kernel<1>, g, b, 0, st, tm, P);
+    if (npt <= 2) return launch(rmsnorm_kernel<2>, g, b, 0, st, tm, P);
+    if (npt <= 4) return launch(rmsnorm_kernel<4>, g, b, 0, st, tm, P);
+    if (npt <= 8) return launch(rmsnorm_kernel<8>, g, b, 0, st, tm, P);
+    if (npt <= 16) return launch(rmsnorm_kernel<16>, g, b, 0, st, tm, P);
+    return launch(rmsnorm_kernel<32>, g, b, 0, st, tm, P);
+}
+
+template <int NJ, int RW>
+hipError_t launch_gemv1_t(const GemvParams &P, hipStream_t st, const LaunchTiming *tm) {
+    const int per_wg = kGvWaves * RW;
+    return launch(gemv1_kernel<NJ, RW>, dim3((P.rows_total + per_wg - 1) / per_wg), dim3(kGvWaves * kWave), 0, st, tm, P);
 }
 
 hipError_t launch_gemv(const GemvParams &P, hipStream_t st, const LaunchTiming *tm) {
     if (P.T == 0 || P.rows_total == 0) return hipSuccess;
+    if (P.T == 1) {
+        // 16-byte chunks per lane per row; fewer rows per wavefront for long rows keep the weight
+        // registers at 16 chunks and the grid above 256 work-groups
+        const int nj = (P.cols / 8 + kWave - 1) / kWave;
+        if (nj <= 1) return launch_gemv1_t<1, 4>(P, st, tm);
+        if (nj <= 2) return launch_gemv1_t<2, 4>(P, st, tm);
+        if (nj <= 4) return launch_gemv1_t<4, 4>(P, st, tm);
+        if (nj <= 8) return launch_gemv1_t<8, 2>(P, st, tm);
+        if (nj <= 16) return launch_gemv1_t<16, 1>(P, st, tm);
+    }
+    if (P.norm_w || P.emb) return hipErrorInvalidValue; // fused normalisation is single-token only
     const int per_wg = kGvWaves * kGvRows;
     const dim3 grid((P.rows_total + per_wg - 1) / per_wg), block(kGvWaves * kWave);
     // tokens per group: enough for the step, as many as the activations' LDS allows
-    int tg = P.T == 1 ? 1 : P.T == 2 ? 2 : P.T <= 4 ? 4 : 8;
-    while (tg > 1 && gemv_lds<1>(P.cols) * tg > (size_t) kGvMaxLds) tg /= 2;
-    if (tg == 1) return launch(gemv_kernel<1>, grid, block, gemv_lds<1>(P.cols), st, tm, P);
+    int tg = P.T == 2 ? 2 : P.T <= 4 ? 4 : 8;
+    while (tg > 2 && gemv_lds<1>(P.cols) * tg > (size_t) kGvMaxLds) tg /= 2;
     if (tg == 2) return launch(gemv_kernel<2>, grid, block, gemv_lds<2>(P.cols), st, tm, P);
     if (tg == 4) return launch(gemv_kernel<4>, grid, block, gemv_lds<4>(P.cols), st, tm, P);
     return launch(gemv_kernel<8>, grid, block, gemv_lds<8>(P.cols), st, tm, P);
@@ -361,14 +659,33 @@ hipError_t launch_rope(const RopeParams &P, hipStream_t st, const LaunchTiming *
     return launch(rope_kernel, dim3(P.T, P.n_head + 2 * P.n_kv), dim3(kWave), 0, st, tm, P);
 }
 
+template <int HD>
+hipError_t launch_attn_hd(const AttnParams &P, hipStream_t st, const LaunchTiming *tm) {
+    const dim3 grid(P.n_kv * P.n_chunk * P.n_rowblk), block(kAtBlock);
+    if (P.rb_rows == 16) return launch(attn_kernel<HD, 1>, grid, block, 0, st, tm, P);
+    if (P.rb_rows == 32) return launch(attn_kernel<HD, 2>, grid, block, 0, st, tm, P);
+    return launch(attn_kernel<HD, 4>, grid, block, 0, st, tm, P);
+}
+
 hipError_t launch_attn(const AttnParams &P, hipStream_t st, const LaunchTiming *tm) {
     if (P.T == 0) return hipSuccess;
-    return launch(attn_kernel, dim3(P.n_chunk, P.n_head, P.T), dim3(kAtBlock), 0, st, tm, P);
+    switch (P.hd) {
+    case 64: return launch_attn_hd<64>(P, st, tm);
+    case 128: return launch_attn_hd<128>(P, st, tm);
+    case 256: return launch_attn_hd<256>(P, st, tm);
+    default: return hipErrorInvalidValue;
+    }
 }
 
 hipError_t launch_attn_combine(const AttnParams &P, hipStream_t st, const LaunchTiming *tm) {
     if (P.T == 0 || P.n_chunk == 1) return hipSuccess;
-    return launch(attn_combine_kernel, dim3(P.n_head, P.T), dim3(P.hd), 0, st, tm, P);
+    const size_t lds = ((size_t) ((P.n_chunk + 3) & ~3) + (size_t) kBlock / (P.hd / 4) * P.hd) * sizeof(float);
+    return launch(attn_combine_kernel, dim3(P.n_head, P.T), dim3(kBlock), lds, st, tm, P);
+}
+
+hipError_t launch_fill_kv(const FillKvParams &P, hipStream_t st, const LaunchTiming *tm) {
+    if (P.T == 0) return hipSuccess;
+    return launch(fill_kv_kernel, dim3(P.T, P.n_layer), dim3(kBlock), 0, st, tm, P);
 }
 
 hipError_t launch_fill(const FillParams &P, hipStream_t st, const LaunchTiming *tm) {

@@ -209,9 +209,10 @@ int create(const lstk_qwen3_hparams *hpp, const lstk_qwen3_weights *w, lstk_pool
     if (hp.n_layer < 1 || hp.n_embd < 1 || hp.n_head < 1 || hp.n_head_kv < 1 || hp.head_dim < 1 || hp.n_vocab < 1)
         return set_error(LSTK_E_INVALID, "hyperparameters must be positive");
     if (hp.n_head % hp.n_head_kv) return set_error(LSTK_E_INVALID, "n_head must be a multiple of n_head_kv");
-    if (!lstk::attn_supported(hp.head_dim)) return set_error(LSTK_E_INVALID, "head_dim must be a power of two in [16, 256]");
-    if (!lstk::gemv_supported(hp.n_embd) || !lstk::gemv_supported(hp.n_head * hp.head_dim))
-        return set_error(LSTK_E_INVALID, "n_embd and n_head * head_dim must be multiples of 8 and at most 32768");
+    if (!lstk::attn_supported(hp.head_dim)) return set_error(LSTK_E_INVALID, "head_dim must be 64, 128 or 256");
+    if (!lstk::gemv_supported(hp.n_embd) || !lstk::gemv_supported(hp.n_head * hp.head_dim) ||
+        !lstk::rmsnorm_supported(hp.n_embd))
+        return set_error(LSTK_E_INVALID, "n_embd and n_head * head_dim must be multiples of 8 and at most 8192");
     if (!(hp.rms_eps >= 0.0f) || !(hp.rope_freq_base > 0.0f)) return set_error(LSTK_E_INVALID, "bad rms_eps or rope_freq_base");
     if (kv_size == 0 || kv_size % kCellBlock) return set_error(LSTK_E_INVALID, "kv_size must be a positive multiple of 32");
     if (n_batch == 0) return set_error(LSTK_E_INVALID, "n_batch must be >= 1");
@@ -245,8 +246,7 @@ int create(const lstk_qwen3_hparams *hpp, const lstk_qwen3_weights *w, lstk_pool
     const size_t nb = n_batch, h = (size_t) hp.n_embd, hq = (size_t) hp.n_head * hp.head_dim,
                  hk = (size_t) hp.n_head_kv * hp.head_dim, k = (size_t) hp.n_expert_used;
     M->layer_elems = (size_t) kv_size * hk;
-    // part rows: only steps with fewer than 1024 (token, head) pairs split the cells, into < 2048 rows
-    const size_t part_rows = 2048;
+    const size_t part_rows = lstk::attn_part_rows((int) nb, hp.n_head);
     struct Piece {
         void **dst;
         size_t bytes;
@@ -260,7 +260,7 @@ int create(const lstk_qwen3_hparams *hpp, const lstk_qwen3_weights *w, lstk_pool
         {(void **) &M->attn, nb * hq * 4},
         {(void **) &M->k, nb * hk * 4},
         {(void **) &M->v, nb * hk * 4},
-        {(void **) &M->part, part_rows * (hp.head_dim + 2) * 4},
+        {(void **) &M->part, part_rows * (hp.head_dim + 4) * 4},
         {(void **) &M->weights, nb * k * 4},
         {(void **) &M->ids, nb * k * 4},
         {(void **) &M->slots, nb * k * 4},
@@ -285,7 +285,8 @@ int create(const lstk_qwen3_hparams *hpp, const lstk_qwen3_weights *w, lstk_pool
     // does, src/kv_cache.cpp:31) and mark every cell empty
     if ((e = hipMemset(M->kcache, 0, 2 * M->layer_elems * hp.n_layer * sizeof(uint16_t))) != hipSuccess ||
         (e = hipMemset(M->cell_seq, 0xff, (size_t) kv_size * 4)) != hipSuccess ||
-        (e = hipMemset(M->cell_pos, 0xff, (size_t) kv_size * 4)) != hipSuccess) {
+        (e = hipMemset(M->cell_pos, 0xff, (size_t) kv_size * 4)) != hipSuccess ||
+        (e = hipMemset(M->in, 0, (size_t) 3 * nb * 4)) != hipSuccess) {
         destroy(M);
         return hip_fail(e, "hipMemset");
     }
@@ -339,13 +340,13 @@ int moe(lstk_model *M, int l, int rows, float *xr, int32_t *ids, hipStream_t st)
     return rc != LSTK_OK ? rc : rrc;
 }
 
-int step(lstk_model *M, int32_t seq, const int32_t *tokens, int T, float *d_logits, int32_t *d_trace, hipStream_t st) {
-    const lstk_qwen3_hparams &hp = M->hp;
+// Engine::make_step_inputs (src/engine.cpp:200-243): reserves the KV cells of T tokens of seq and queues
+// the upload of the tokens, cells and positions to the model's input buffer; *n_cells = the attended cells.
+int prepare(lstk_model *M, int32_t seq, const int32_t *tokens, int T, int *n_cells, hipStream_t st) {
     std::vector<int32_t> cells, pos;
     if (!M->kv.alloc(seq, T, cells, pos)) return set_error(LSTK_E_EXHAUSTED, "KV cache is full");
-    const int n_cells = M->kv.n_kv();
-    const int nb = M->n_batch, h = hp.n_embd, hd = hp.head_dim, k = hp.n_expert_used;
-    const int hq = hp.n_head * hd, hk = hp.n_head_kv * hd;
+    *n_cells = M->kv.n_kv();
+    const int nb = M->n_batch;
     hipError_t e;
     // the staging buffer is reused once the previous step's upload has left it
     if ((e = hipEventSynchronize(M->in_free)) != hipSuccess) return hip_fail(e, "hipEventSynchronize");
@@ -355,15 +356,20 @@ int step(lstk_model *M, int32_t seq, const int32_t *tokens, int T, float *d_logi
     if ((e = hipMemcpyAsync(M->in, M->h_in, (size_t) 3 * nb * 4, hipMemcpyHostToDevice, st)) != hipSuccess ||
         (e = hipEventRecord(M->in_free, st)) != hipSuccess)
         return hip_fail(e, "step input upload");
+    return LSTK_OK;
+}
+
+// The kernels of one step (qwen3_build_graph, src/qwen3.cpp:223-259) over the inputs prepare() uploaded.
+// With a resident pool this makes no host synchronisation, so a caller may capture it in a HIP graph.
+int forward(lstk_model *M, int32_t seq, int T, int n_cells, float *d_logits, int32_t *d_trace, hipStream_t st) {
+    const lstk_qwen3_hparams &hp = M->hp;
+    const int nb = M->n_batch, h = hp.n_embd, hd = hp.head_dim, k = hp.n_expert_used;
+    const int hq = hp.n_head * hd, hk = hp.n_head_kv * hd;
+    hipError_t e;
     const int32_t *d_tok = M->in, *d_cells = M->in + nb, *d_pos = M->in + 2 * nb;
 
-    int n_chunk = 1;
-    const int chunk = lstk::attn_chunk_cells(T, hp.n_head, n_cells, &n_chunk);
     for (int l = 0; l < hp.n_layer; l++) {
         const lstk_qwen3_layer &L = M->layers[l];
-        lstk::NormParams np{M->x, l == 0 ? M->tok_embd : nullptr, d_tok, M->x, L.attn_norm, M->hn, T, h, hp.rms_eps};
-        if ((e = timed(M, 0, [&](const lstk::LaunchTiming *tm) { return lstk::launch_rmsnorm(np, st, tm); })) != hipSuccess)
-            return hip_fail(e, "attn_norm launch");
         lstk::GemvParams gp{};
         gp.seg[0] = {L.wq, M->q, nullptr, hq, hq};
         gp.seg[1] = {L.wk, M->k, nullptr, hk, hk};
@@ -371,8 +377,23 @@ int step(lstk_model *M, int32_t seq, const int32_t *tokens, int T, float *d_logi
         gp.nseg = 3;
         gp.rows_total = hq + 2 * hk;
         gp.cols = h;
-        gp.x = M->hn;
         gp.T = T;
+        if (T == 1) {
+            // one token: attn_norm (and layer 0's embedding gather) run inside the Q/K/V launch
+            gp.x = M->x;
+            gp.norm_w = L.attn_norm;
+            gp.eps = hp.rms_eps;
+            if (l == 0) {
+                gp.emb = M->tok_embd;
+                gp.tokens = d_tok;
+                gp.x_out = M->x;
+            }
+        } else {
+            lstk::NormParams np{M->x, l == 0 ? M->tok_embd : nullptr, d_tok, M->x, L.attn_norm, M->hn, T, h, hp.rms_eps};
+            if ((e = timed(M, 0, [&](const lstk::LaunchTiming *tm) { return lstk::launch_rmsnorm(np, st, tm); })) != hipSuccess)
+                return hip_fail(e, "attn_norm launch");
+            gp.x = M->hn;
+        }
         if ((e = timed(M, 1, [&](const lstk::LaunchTiming *tm) { return lstk::launch_gemv(gp, st, tm); })) != hipSuccess)
             return hip_fail(e, "qkv launch");
         uint16_t *kc = M->kcache + M->layer_elems * l, *vc = M->vcache + M->layer_elems * l;
@@ -380,10 +401,27 @@ int step(lstk_model *M, int32_t seq, const int32_t *tokens, int T, float *d_logi
                             T, hp.n_head, hp.n_head_kv, hd, (int) M->kv.size, M->theta_scale, M->qr, kc, vc};
         if ((e = timed(M, 1, [&](const lstk::LaunchTiming *tm) { return lstk::launch_rope(rp, st, tm); })) != hipSuccess)
             return hip_fail(e, "rope launch");
-        lstk::AttnParams ap{M->qr, kc, vc, M->cell_seq, M->cell_pos, d_pos, seq, T, hp.n_head, hp.n_head_kv, hd,
-                            (int) M->kv.size, n_cells, chunk, n_chunk, 1.0f / sqrtf((float) hd), M->part, M->attn};
+        lstk::AttnParams ap{};
+        ap.q = M->qr;
+        ap.kc = kc;
+        ap.vc = vc;
+        ap.cell_seq = M->cell_seq;
+        ap.cell_pos = M->cell_pos;
+        ap.pos = d_pos;
+        ap.seq = seq;
+        ap.T = T;
+        ap.n_head = hp.n_head;
+        ap.n_kv = hp.n_head_kv;
+        ap.hd = hd;
+        ap.kv_size = (int) M->kv.size;
+        ap.n_cells = n_cells;
+        ap.scale = 1.0f / sqrtf((float) hd);
+        ap.part = M->part;
+        ap.out = M->attn;
+        lstk::attn_plan(ap);
         if ((e = timed(M, 2, [&](const lstk::LaunchTiming *tm) { return lstk::launch_attn(ap, st, tm); })) != hipSuccess ||
-            (e = timed(M, 2, [&](const lstk::LaunchTiming *tm) { return lstk::launch_attn_combine(ap, st, tm); })) != hipSuccess)
+            (ap.n_chunk > 1 &&
+             (e = timed(M, 2, [&](const lstk::LaunchTiming *tm) { return lstk::launch_attn_combine(ap, st, tm); })) != hipSuccess))
             return hip_fail(e, "attention launch");
         lstk::GemvParams op{};
         op.seg[0] = {L.wo, M->x, M->x, h, h};
@@ -424,6 +462,19 @@ int step(lstk_model *M, int32_t seq, const int32_t *tokens, int T, float *d_logi
     return LSTK_OK;
 }
 
+int step(lstk_model *M, int32_t seq, const int32_t *tokens, int T, float *d_logits, int32_t *d_trace, hipStream_t st) {
+    int n_cells = 0;
+    const int rc = prepare(M, seq, tokens, T, &n_cells, st);
+    return rc != LSTK_OK ? rc : forward(M, seq, T, n_cells, d_logits, d_trace, st);
+}
+
+int check_tokens(const lstk_model *M, const int32_t *tokens, int n) {
+    for (int i = 0; i < n; i++)
+        if (tokens[i] < 0 || tokens[i] >= M->hp.n_vocab)
+            return set_error(LSTK_E_INVALID, "token id " + std::to_string(tokens[i]) + " out of range");
+    return LSTK_OK;
+}
+
 }  // namespace
 
 extern "C" {
@@ -444,9 +495,7 @@ int lstk_model_decode(lstk_model *model, int32_t seq, const int32_t *tokens, int
     if (!model) return set_error(LSTK_E_INVALID, "null model");
     if (n_tokens < 1 || !tokens || !d_logits) return set_error(LSTK_E_INVALID, "need at least one token and a logits buffer");
     if (seq < 0) return set_error(LSTK_E_INVALID, "seq must be >= 0");
-    for (int i = 0; i < n_tokens; i++)
-        if (tokens[i] < 0 || tokens[i] >= model->hp.n_vocab)
-            return set_error(LSTK_E_INVALID, "token id " + std::to_string(tokens[i]) + " out of range");
+    if (check_tokens(model, tokens, n_tokens) != LSTK_OK) return LSTK_E_INVALID;
     hipStream_t st = static_cast<hipStream_t>(stream);
     try {
         for (int done = 0; done < n_tokens;) {
@@ -457,6 +506,60 @@ int lstk_model_decode(lstk_model *model, int32_t seq, const int32_t *tokens, int
         }
     } catch (const std::exception &ex) {
         return set_error(LSTK_E_NOMEM, std::string("lstk_model_decode: ") + ex.what());
+    }
+    return LSTK_OK;
+}
+
+int lstk_model_prepare(lstk_model *model, int32_t seq, const int32_t *tokens, int n_tokens, int32_t *n_cells,
+                       lstk_stream_t stream) {
+    if (!model || !tokens || !n_cells) return set_error(LSTK_E_INVALID, "null argument");
+    if (seq < 0 || n_tokens < 1 || n_tokens > model->n_batch)
+        return set_error(LSTK_E_INVALID, "seq must be >= 0 and n_tokens in [1, n_batch]");
+    if (check_tokens(model, tokens, n_tokens) != LSTK_OK) return LSTK_E_INVALID;
+    try {
+        int nc = 0;
+        const int rc = prepare(model, seq, tokens, n_tokens, &nc, static_cast<hipStream_t>(stream));
+        *n_cells = nc;
+        return rc;
+    } catch (const std::exception &ex) {
+        return set_error(LSTK_E_NOMEM, std::string("lstk_model_prepare: ") + ex.what());
+    }
+}
+
+int lstk_model_forward(lstk_model *model, int32_t seq, int n_tokens, int32_t n_cells, float *d_logits, int32_t *d_trace,
+                       lstk_stream_t stream) {
+    if (!model || !d_logits) return set_error(LSTK_E_INVALID, "null argument");
+    if (seq < 0 || n_tokens < 1 || n_tokens > model->n_batch || n_cells < 1 || n_cells > (int32_t) model->kv.size)
+        return set_error(LSTK_E_INVALID, "seq must be >= 0, n_tokens in [1, n_batch], n_cells in [1, kv_size]");
+    return forward(model, seq, n_tokens, n_cells, d_logits, d_trace, static_cast<hipStream_t>(stream));
+}
+
+int lstk_model_fill_context(lstk_model *model, int32_t seq, int n_cells, uint64_t seed, lstk_stream_t stream) {
+    if (!model) return set_error(LSTK_E_INVALID, "null model");
+    if (seq < 0 || n_cells < 0) return set_error(LSTK_E_INVALID, "seq and n_cells must be >= 0");
+    lstk_model *M = model;
+    hipStream_t st = static_cast<hipStream_t>(stream);
+    const int nb = M->n_batch;
+    try {
+        for (int done = 0; done < n_cells;) {
+            const int T = std::min(nb, n_cells - done);
+            std::vector<int32_t> cells, pos;
+            if (!M->kv.alloc(seq, T, cells, pos)) return set_error(LSTK_E_EXHAUSTED, "KV cache is full");
+            hipError_t e;
+            if ((e = hipEventSynchronize(M->in_free)) != hipSuccess) return hip_fail(e, "hipEventSynchronize");
+            std::memcpy(M->h_in + nb, cells.data(), (size_t) T * 4);
+            std::memcpy(M->h_in + 2 * nb, pos.data(), (size_t) T * 4);
+            if ((e = hipMemcpyAsync(M->in, M->h_in, (size_t) 3 * nb * 4, hipMemcpyHostToDevice, st)) != hipSuccess ||
+                (e = hipEventRecord(M->in_free, st)) != hipSuccess)
+                return hip_fail(e, "context upload");
+            lstk::FillKvParams fp{M->in + nb, M->in + 2 * nb, seq, M->cell_seq, M->cell_pos, T, M->hp.n_layer,
+                                  M->hp.n_head_kv, M->hp.head_dim, (int) M->kv.size, M->layer_elems, M->kcache,
+                                  M->vcache, seed};
+            if ((e = lstk::launch_fill_kv(fp, st, nullptr)) != hipSuccess) return hip_fail(e, "fill launch");
+            done += T;
+        }
+    } catch (const std::exception &ex) {
+        return set_error(LSTK_E_NOMEM, std::string("lstk_model_fill_context: ") + ex.what());
     }
     return LSTK_OK;
 }

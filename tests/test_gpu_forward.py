@@ -173,6 +173,35 @@ def test_30b_shaped_layers(lstk, dev):
         feed = np.array([np.argmax(rl)], np.int32)
 
 
+def test_graph_replay_matches_eager(lstk, dev):
+    """prepare + a captured forward replayed per step reproduces the eager decode bit for bit."""
+    import torch
+    hp, w = weights("tiny")
+    _, eager = build(lstk, dev, hp, w)
+    _, gm = build(lstk, dev, hp, w)
+    toks = prompt(21, 16, hp["n_vocab"])
+    a, _ = run(eager, 0, toks, hp, dev)
+    b, _ = run(gm, 0, toks, hp, dev)
+    np.testing.assert_array_equal(a, b)
+    feed = np.array([np.argmax(a)], np.int32)
+    stream = torch.cuda.Stream()
+    logits = torch.zeros(hp["n_vocab"], dtype=torch.float32, device=dev)
+    graph = None
+    for step in range(6):
+        ea, _ = run(eager, 0, feed, hp, dev)
+        with torch.cuda.stream(stream):
+            n = gm.prepare(0, feed, stream=stream)
+            if graph is None:
+                graph = torch.cuda.CUDAGraph()
+                with torch.cuda.graph(graph, stream=stream):
+                    gm.forward(0, 1, n, logits=logits, stream=stream)
+            graph.replay()
+        torch.cuda.synchronize()
+        np.testing.assert_array_equal(logits.cpu().numpy(), ea, err_msg=f"replay {step}")
+        feed = np.array([np.argmax(ea)], np.int32)
+    assert gm.seq_len(0) == eager.seq_len(0) == 22
+
+
 def test_errors_are_reported(lstk, dev):
     hp, w = weights("tiny")
     _, model = build(lstk, dev, hp, w, kv_size=32)
