@@ -50,6 +50,12 @@ class PoolStats(ctypes.Structure):
                 ("acquires", ctypes.c_uint64), ("wait_ms", ctypes.c_double)]
 
 
+class GgufTensor(ctypes.Structure):
+    _fields_ = [("name", ctypes.c_char_p), ("type", ctypes.c_int32), ("n_dims", ctypes.c_int32),
+                ("ne", ctypes.c_int64 * 4), ("offset", ctypes.c_uint64), ("nbytes", ctypes.c_uint64),
+                ("data", ctypes.c_void_p)]
+
+
 class Qwen3HParams(ctypes.Structure):
     _fields_ = [(n, ctypes.c_int32) for n in ("n_layer", "n_embd", "n_head", "n_head_kv", "head_dim", "n_vocab",
                                               "n_expert", "n_expert_used", "n_ff_exp", "n_ctx_train")] + \
@@ -101,6 +107,20 @@ SIGNATURES = {
     "lstk_model_remove_seq": (_I, [_P, ctypes.c_int32]),
     "lstk_model_truncate_seq": (_I, [_P, ctypes.c_int32, ctypes.c_int32]),
     "lstk_model_seq_len": (ctypes.c_int32, [_P, ctypes.c_int32]),
+    "lstk_gguf_open": (_I, [ctypes.c_char_p, ctypes.POINTER(_P)]),
+    "lstk_gguf_close": (None, [_P]),
+    "lstk_gguf_arch": (ctypes.c_char_p, [_P]),
+    "lstk_gguf_version": (_I, [_P]),
+    "lstk_gguf_alignment": (_I, [_P]),
+    "lstk_gguf_has": (_I, [_P, ctypes.c_char_p]),
+    "lstk_gguf_get_int": (ctypes.c_int64, [_P, ctypes.c_char_p, ctypes.c_int64]),
+    "lstk_gguf_get_float": (ctypes.c_double, [_P, ctypes.c_char_p, ctypes.c_double]),
+    "lstk_gguf_get_str": (ctypes.c_char_p, [_P, ctypes.c_char_p, ctypes.c_char_p]),
+    "lstk_gguf_n_tensors": (_I, [_P]),
+    "lstk_gguf_tensor_at": (_I, [_P, _I, ctypes.POINTER(GgufTensor)]),
+    "lstk_gguf_find_tensor": (_I, [_P, ctypes.c_char_p, ctypes.POINTER(GgufTensor)]),
+    "lstk_gguf_qwen3_hparams": (_I, [_P, ctypes.POINTER(Qwen3HParams)]),
+    "lstk_gguf_qwen3_experts": (_I, [_P, ctypes.POINTER(Qwen3HParams), _P]),
     "lstk_model_set_timing": (_I, [_P, _I]),
     "lstk_model_timing": (_I, [_P, ctypes.POINTER(ctypes.c_double), ctypes.POINTER(ctypes.c_int64)]),
 }
@@ -196,8 +216,8 @@ class ExpertStore:
         for l, (types, up, gate, down) in enumerate(layers):
             ptrs = []
             for a in (up, gate, down):
-                if a is None:
-                    ptrs.append(None)
+                if a is None or isinstance(a, int):
+                    ptrs.append(a)
                 else:
                     a = np.ascontiguousarray(a)
                     self._keep.append(a)
@@ -309,7 +329,10 @@ class Qwen3Model:
         def up(a, dtype):
             if a is None:
                 return None
-            t = torch.from_numpy(np.ascontiguousarray(a).view(dtype)).to(self.device)
+            a = np.ascontiguousarray(a)
+            if not a.flags.writeable:  # a view of a read-only file mapping: torch wants a writable source
+                a = a.copy()
+            t = torch.from_numpy(a.view(dtype)).to(self.device)
             self._keep.append(t)
             return t.data_ptr()
 
@@ -323,7 +346,9 @@ class Qwen3Model:
         for l, L in enumerate(weights["layers"]):
             self._layers[l] = Qwen3Layer(up(L["attn_norm"], f32), up(L["wq"], f16), up(L["wk"], f16), up(L["wv"], f16),
                                          up(L["wo"], f16), up(L.get("q_norm"), f32), up(L.get("k_norm"), f32),
-                                         up(L["ffn_norm"], f32), up(L["gate_inp"], f16), TYPE_F16)
+                                         up(L["ffn_norm"], f32),
+                                         up(L["gate_inp"], f32 if L["gate_inp"].dtype == np.float32 else f16),
+                                         TYPE_F32 if L["gate_inp"].dtype == np.float32 else TYPE_F16)
         self._w = Qwen3Weights(up(weights["tok_embd"], f16), up(weights["output_norm"], f32),
                                up(weights.get("output"), f16), ctypes.cast(self._layers, ctypes.c_void_p))
         h = ctypes.c_void_p()
@@ -387,3 +412,127 @@ class Qwen3Model:
         n = (ctypes.c_int64 * 5)()
         _check(lib().lstk_model_timing(self._h, ms, n))
         return list(ms), list(n)
+
+
+_GGML_NP = {0: np.float32, 1: np.float16}
+_GGML_NAME = {0: "F32", 1: "F16", 8: "Q8_0", 12: "Q4_K", 14: "Q6_K", 30: "BF16"}
+
+
+class GgufFile:
+    """A memory-mapped GGUF file (include/lstk_gguf.h), mirroring GgufModel (src/gguf_model.h:31-60)."""
+
+    def __init__(self, path):
+        h = ctypes.c_void_p()
+        _check(lib().lstk_gguf_open(os.fsencode(path), ctypes.byref(h)))
+        self._h = h
+        self.path = path
+
+    def close(self):
+        if getattr(self, "_h", None):
+            lib().lstk_gguf_close(self._h)
+            self._h = None
+
+    def __del__(self):
+        self.close()
+
+    @property
+    def arch(self):
+        return lib().lstk_gguf_arch(self._h).decode()
+
+    @property
+    def version(self):
+        return lib().lstk_gguf_version(self._h)
+
+    @property
+    def alignment(self):
+        return lib().lstk_gguf_alignment(self._h)
+
+    def has(self, key):
+        return bool(lib().lstk_gguf_has(self._h, key.encode()))
+
+    def get_int(self, key, default=0):
+        return lib().lstk_gguf_get_int(self._h, key.encode(), int(default))
+
+    def get_float(self, key, default=0.0):
+        return lib().lstk_gguf_get_float(self._h, key.encode(), float(default))
+
+    def get_str(self, key, default=""):
+        r = lib().lstk_gguf_get_str(self._h, key.encode(), None)
+        return default if r is None else r.decode()
+
+    def _info(self, t):
+        return {"name": t.name.decode(), "type": t.type, "ne": tuple(t.ne[:t.n_dims]), "offset": t.offset,
+                "nbytes": t.nbytes, "data": t.data}
+
+    def tensors(self):
+        out = []
+        for i in range(lib().lstk_gguf_n_tensors(self._h)):
+            t = GgufTensor()
+            _check(lib().lstk_gguf_tensor_at(self._h, i, ctypes.byref(t)))
+            out.append(self._info(t))
+        return out
+
+    def tensor_info(self, name):
+        t = GgufTensor()
+        _check(lib().lstk_gguf_find_tensor(self._h, name.encode(), ctypes.byref(t)))
+        return self._info(t)
+
+    def tensor_bytes(self, name):
+        """A read-only uint8 view of the tensor's bytes in the mapping (valid while the file is open)."""
+        info = self.tensor_info(name)
+        buf = (ctypes.c_uint8 * info["nbytes"]).from_address(info["data"])
+        a = np.ctypeslib.as_array(buf)
+        a.flags.writeable = False
+        return a
+
+    def tensor_array(self, name):
+        """F32 / F16 tensors as numpy arrays shaped [ne[n-1]]...[ne[0]] (a view of the mapping)."""
+        info = self.tensor_info(name)
+        if info["type"] not in _GGML_NP:
+            raise LstkError(E_INVALID, f"tensor {name} is {_GGML_NAME.get(info['type'], info['type'])}, not F32/F16")
+        return self.tensor_bytes(name).view(_GGML_NP[info["type"]]).reshape(tuple(reversed(info["ne"])))
+
+    def qwen3_hparams(self):
+        hp = Qwen3HParams()
+        _check(lib().lstk_gguf_qwen3_hparams(self._h, ctypes.byref(hp)))
+        return {n: getattr(hp, n) for n, _ in Qwen3HParams._fields_}
+
+    def qwen3_experts(self, hp):
+        c = Qwen3HParams(*(hp[n] for n, _ in Qwen3HParams._fields_))
+        arr = (ExpertLayer * hp["n_layer"])()
+        _check(lib().lstk_gguf_qwen3_experts(self._h, ctypes.byref(c), ctypes.cast(arr, ctypes.c_void_p)))
+        return [((L.type_up, L.type_gate, L.type_down), L.host_up, L.host_gate, L.host_down) for L in arr]
+
+
+def load_qwen3_gguf(path, n_batch=64, kv_size=4096, device="cuda", pool_bytes=0, min_slots=0, streaming=False):
+    """qwen3_load_hparams + qwen3_map_weights + the expert pool (src/qwen3.cpp:16-109,
+    src/engine.cpp:31-173) from a qwen3moe GGUF: returns (hparams, ExpertStore, Qwen3Model, GgufFile).
+    The experts go to the pool straight from the mapping; the dense tensors must be F16 (embedding,
+    attention, output) and F32 (norms), the router F16 or F32 - other types are rejected."""
+    g = GgufFile(path)
+    hp = g.qwen3_hparams()
+    experts = g.qwen3_experts(hp)
+
+    def dense(name, types=(1,), optional=False):
+        if optional and not any(t["name"] == name for t in g.tensors()):
+            return None
+        t = g.tensor_info(name)
+        if t["type"] not in types:
+            want = "/".join(_GGML_NAME[x] for x in types)
+            raise LstkError(E_INVALID, f"tensor {name} is {_GGML_NAME.get(t['type'], t['type'])}; the forward pass takes {want}")
+        return g.tensor_array(name)
+
+    w = {"tok_embd": dense("token_embd.weight"), "output_norm": dense("output_norm.weight", (0,)),
+         "output": dense("output.weight", optional=True), "layers": []}
+    for l in range(hp["n_layer"]):
+        p = f"blk.{l}."
+        w["layers"].append({
+            "attn_norm": dense(p + "attn_norm.weight", (0,)), "wq": dense(p + "attn_q.weight"),
+            "wk": dense(p + "attn_k.weight"), "wv": dense(p + "attn_v.weight"), "wo": dense(p + "attn_output.weight"),
+            "q_norm": dense(p + "attn_q_norm.weight", (0,), optional=True),
+            "k_norm": dense(p + "attn_k_norm.weight", (0,), optional=True),
+            "ffn_norm": dense(p + "ffn_norm.weight", (0,)), "gate_inp": dense(p + "ffn_gate_inp.weight", (0, 1))})
+    store = ExpertStore(hp["n_layer"], hp["n_embd"], hp["n_ff_exp"], hp["n_expert"], hp["n_expert_used"], n_batch,
+                        experts, pool_bytes=pool_bytes, min_slots=min_slots, streaming=streaming)
+    model = Qwen3Model(hp, w, store, kv_size, n_batch, device=device)
+    return hp, store, model, g

@@ -2,8 +2,8 @@
 
 The library is the product: the MoE kernels (csrc/kernels.hip, grouped.hip, fused.hip), the HBM
 expert pool and the MoE C ABI (csrc/pool.cpp, include/lstk_moe.h), the host repacker
-(csrc/repack.cpp), and the forward pass around the MoE block (csrc/forward.hip, csrc/model.cpp,
-include/lstk_qwen3.h).
+(csrc/repack.cpp), the forward pass around the MoE block (csrc/forward.hip, csrc/model.cpp,
+include/lstk_qwen3.h) and the GGUF reader (csrc/gguf.cpp, include/lstk_gguf.h).
 """
 import os
 import shutil
@@ -15,7 +15,7 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 ROOT = os.path.dirname(HERE)
 CSRC = os.path.join(HERE, "csrc")
 LIB = os.path.join(HERE, "liblstk_moe.so")
-SOURCES = ["kernels.hip", "grouped.hip", "fused.hip", "forward.hip", "pool.cpp", "repack.cpp", "model.cpp"]
+SOURCES = ["kernels.hip", "grouped.hip", "fused.hip", "forward.hip", "pool.cpp", "repack.cpp", "model.cpp", "gguf.cpp"]
 ARCH = os.environ.get("LSTK_OFFLOAD_ARCH", "gfx950")
 
 

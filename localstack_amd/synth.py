@@ -11,8 +11,13 @@ benchmark and test shapes, using numpy's PCG64 so that every machine draws ident
     constant activation column (zipf_router_f16);
   - qwen3_weights: a whole Qwen3-MoE model in the tensor set make_tiny_moe.py writes
     (tools/make_tiny_moe.py:122-136): F16 embedding (tied output head) and attention, f32 norms of
-    1.0 (as that writer sets them), F16 router, quantized experts.
+    1.0 (as that writer sets them), F16 router, quantized experts;
+  - write_gguf / write_qwen3_gguf: a GGUF v3 file of such a model, laid out as the reference's
+    writer lays it out (tools/make_tiny_moe.py:37-77: header, metadata, tensor index, 32-byte aligned
+    data), with the qwen3moe metadata keys of tools/make_tiny_moe.py:106-120.
 """
+import struct
+
 import numpy as np
 
 Q8_0_BLOCK = 34
@@ -136,3 +141,79 @@ def qwen3_weights(rng, hp, wtype=8, std=0.02):
             "up": experts(rng, wtype, E, f, h, std, True), "gate": experts(rng, wtype, E, f, h, std, True),
             "down": experts(rng, wtype, E, h, f, std, True)})
     return w
+
+
+# GGUF metadata value types
+GGUF_U8, GGUF_I8, GGUF_U16, GGUF_I16, GGUF_U32, GGUF_I32, GGUF_F32, GGUF_BOOL, GGUF_STR, GGUF_ARR, GGUF_U64, GGUF_I64, \
+    GGUF_F64 = range(13)
+_SCALAR = {GGUF_U8: "<B", GGUF_I8: "<b", GGUF_U16: "<H", GGUF_I16: "<h", GGUF_U32: "<I", GGUF_I32: "<i", GGUF_F32: "<f",
+           GGUF_BOOL: "<?", GGUF_U64: "<Q", GGUF_I64: "<q", GGUF_F64: "<d"}
+
+
+def _gguf_str(s):
+    b = s.encode()
+    return struct.pack("<Q", len(b)) + b
+
+
+def _gguf_value(t, v):
+    if t == GGUF_STR:
+        return _gguf_str(v)
+    if t == GGUF_ARR:
+        et, items = v
+        body = struct.pack("<IQ", et, len(items))
+        return body + b"".join(_gguf_str(x) if et == GGUF_STR else struct.pack(_SCALAR[et], x) for x in items)
+    return struct.pack(_SCALAR[t], v)
+
+
+def write_gguf(path, kv, tensors, align=32, version=3):
+    """kv: list of (key, type, value) (arrays: (element type, items)); tensors: list of (name, ne in ggml
+    order, ggml type, bytes). Tensor data start at multiples of `align` after the padded index."""
+    body = bytearray(b"GGUF" + struct.pack("<IQQ", version, len(tensors), len(kv)))
+    for k, t, v in kv:
+        body += _gguf_str(k) + struct.pack("<I", t) + _gguf_value(t, v)
+    offsets, off = [], 0
+    for _, _, _, data in tensors:
+        offsets.append(off)
+        off += (len(data) + align - 1) // align * align
+    for (name, ne, gtype, _), o in zip(tensors, offsets):
+        body += _gguf_str(name) + struct.pack("<I", len(ne)) + b"".join(struct.pack("<Q", d) for d in ne)
+        body += struct.pack("<IQ", gtype, o)
+    body += b"\0" * ((align - len(body) % align) % align)
+    for _, _, _, data in tensors:
+        body += bytes(data) + b"\0" * ((align - len(data) % align) % align)
+    with open(path, "wb") as f:
+        f.write(body)
+
+
+def write_qwen3_gguf(path, hp, w, extra_kv=()):
+    """The model of qwen3_weights(hp) as a qwen3moe GGUF (tied head: no output.weight)."""
+    a = "qwen3moe."
+    kv = [("general.architecture", GGUF_STR, "qwen3moe"), ("general.name", GGUF_STR, "synthetic-qwen3moe"),
+          (a + "block_count", GGUF_U32, hp["n_layer"]), (a + "context_length", GGUF_U32, hp.get("n_ctx_train", 1024)),
+          (a + "embedding_length", GGUF_U32, hp["n_embd"]),
+          (a + "feed_forward_length", GGUF_U32, hp["n_ff_exp"] * hp["n_expert_used"]),
+          (a + "attention.head_count", GGUF_U32, hp["n_head"]), (a + "attention.head_count_kv", GGUF_U32, hp["n_head_kv"]),
+          (a + "attention.key_length", GGUF_U32, hp["head_dim"]), (a + "attention.value_length", GGUF_U32, hp["head_dim"]),
+          (a + "attention.layer_norm_rms_epsilon", GGUF_F32, hp["rms_eps"]),
+          (a + "rope.freq_base", GGUF_F32, hp["rope_freq_base"]), (a + "expert_count", GGUF_U32, hp["n_expert"]),
+          (a + "expert_used_count", GGUF_U32, hp["n_expert_used"]),
+          (a + "expert_feed_forward_length", GGUF_U32, hp["n_ff_exp"])] + list(extra_kv)
+    h, E, f, hd = hp["n_embd"], hp["n_expert"], hp["n_ff_exp"], hp["head_dim"]
+    b = lambda arr: np.ascontiguousarray(arr).tobytes()
+    ts = [("token_embd.weight", [h, hp["n_vocab"]], 1, b(w["tok_embd"])), ("output_norm.weight", [h], 0, b(w["output_norm"]))]
+    if w.get("output") is not None:
+        ts.append(("output.weight", [h, hp["n_vocab"]], 1, b(w["output"])))
+    for l, L in enumerate(w["layers"]):
+        p = f"blk.{l}."
+        ts += [(p + "attn_norm.weight", [h], 0, b(L["attn_norm"])),
+               (p + "attn_q.weight", [h, hp["n_head"] * hd], 1, b(L["wq"])),
+               (p + "attn_k.weight", [h, hp["n_head_kv"] * hd], 1, b(L["wk"])),
+               (p + "attn_v.weight", [h, hp["n_head_kv"] * hd], 1, b(L["wv"])),
+               (p + "attn_output.weight", [hp["n_head"] * hd, h], 1, b(L["wo"])),
+               (p + "attn_q_norm.weight", [hd], 0, b(L["q_norm"])), (p + "attn_k_norm.weight", [hd], 0, b(L["k_norm"])),
+               (p + "ffn_norm.weight", [h], 0, b(L["ffn_norm"])),
+               (p + "ffn_gate_inp.weight", [h, E], 1 if L["gate_inp"].dtype == np.float16 else 0, b(L["gate_inp"])),
+               (p + "ffn_up_exps.weight", [h, f, E], L["types"][0], b(L["up"])),
+               (p + "ffn_gate_exps.weight", [h, f, E], L["types"][1], b(L["gate"])),
+               (p + "ffn_down_exps.weight", [f, h, E], L["types"][2], b(L["down"]))]
+    write_gguf(path, kv, ts)

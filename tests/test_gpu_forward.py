@@ -5,7 +5,8 @@ f 512, Q8_0 experts; 16-token prefill of seeded uniform ids, then 32 greedy step
 logits within LOGITS_TOL max-abs of the oracle at every step, top-1 agreement on every step (the
 99.9% bar over 33 choices), and the router's expert ids of every layer and step bit-exact.
 Invariants of the device path itself are held exactly: chunked prefill, interleaved sequences,
-truncation and a streaming pool all reproduce the plain run bit for bit.
+truncation, a streaming pool, graph replay and a model loaded from a GGUF file all reproduce the plain
+run bit for bit.
 
 Why the logits differ at all: both sides quantize activations to Q8_0 / Q8_K before the expert
 products, so an f32 rounding difference upstream can move a value across a quantization step. The
@@ -200,6 +201,31 @@ def test_graph_replay_matches_eager(lstk, dev):
         np.testing.assert_array_equal(logits.cpu().numpy(), ea, err_msg=f"replay {step}")
         feed = np.array([np.argmax(ea)], np.int32)
     assert gm.seq_len(0) == eager.seq_len(0) == 22
+
+
+def test_model_loaded_from_gguf_matches(lstk, dev, tmp_path):
+    """load_qwen3_gguf (experts straight from the file mapping into the pool) decodes exactly like the
+    model built from the same arrays, resident and streaming."""
+    hp, w = weights("tiny")
+    path = tmp_path / "tiny.gguf"
+    synth.write_qwen3_gguf(path, hp, w)
+    _, ref = build(lstk, dev, hp, w)
+    ghp, _, gm, g = lstk.load_qwen3_gguf(path, n_batch=64, kv_size=1024, device=dev)
+    for k in ("n_layer", "n_embd", "n_head", "n_head_kv", "head_dim", "n_vocab", "n_expert", "n_expert_used", "n_ff_exp"):
+        assert ghp[k] == hp[k], k
+    slab = 3 * 512 * 256 // 32 * 34
+    _, _, sm, g2 = lstk.load_qwen3_gguf(path, n_batch=64, kv_size=1024, device=dev, pool_bytes=8 * slab, min_slots=8,
+                                        streaming=True)
+    feed = prompt(31, 16, hp["n_vocab"])
+    for step in range(5):
+        a, ta = run(ref, 0, feed, hp, dev)
+        b, tb = run(gm, 0, feed, hp, dev)
+        c, tc = run(sm, 0, feed, hp, dev)
+        np.testing.assert_array_equal(a, b)
+        np.testing.assert_array_equal(a, c)
+        np.testing.assert_array_equal(ta, tb)
+        np.testing.assert_array_equal(ta, tc)
+        feed = np.array([np.argmax(a)], np.int32)
 
 
 def test_errors_are_reported(lstk, dev):
