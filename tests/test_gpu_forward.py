@@ -12,8 +12,10 @@ Why the logits differ at all: both sides quantize activations to Q8_0 / Q8_K bef
 products, so an f32 rounding difference upstream can move a value across a quantization step. The
 oracle's own logits move by up to 1.5e-3 (tiny model) and 7.8e-3 (30B-shaped layers, logit std 0.92)
 when only the summation order of its F16 dot products changes (f32 SIMD order vs double), with the
-router ids unchanged; the device path measures 4.8e-3 .. 6.8e-3 on the 30B-shaped layers. A structural
-mistake moves logits by 0.1 or more (dropping the QK-norm moves the tiny model's by 0.7).
+router ids unchanged; the device path measures 4.8e-3 .. 6.8e-3 on the 30B-shaped layers. At the
+235B attention shape (h 4096, logit std 1.3) the oracle's own logits move by up to 1.21e-2 under the
+same change of summation order, so that case is held to BIG_TOL = 2e-2 (measured 5.7e-3 .. 1.06e-2).
+A structural mistake moves logits by 0.1 or more (dropping the QK-norm moves the tiny model's by 0.7).
 """
 import numpy as np
 import pytest
@@ -24,6 +26,7 @@ from localstack_amd import synth
 pytestmark = pytest.mark.gpu
 
 LOGITS_TOL = 1e-2
+BIG_TOL = 2e-2
 
 TINY = dict(n_layer=2, n_embd=256, n_head=4, n_head_kv=2, head_dim=64, n_vocab=1024, n_expert=8, n_expert_used=2,
             n_ff_exp=512, n_ctx_train=1024, rms_eps=1e-6, rope_freq_base=10000.0)
@@ -31,12 +34,17 @@ TINY = dict(n_layer=2, n_embd=256, n_head=4, n_head_kv=2, head_dim=64, n_vocab=1
 MID = dict(n_layer=2, n_embd=2048, n_head=32, n_head_kv=4, head_dim=128, n_vocab=4096, n_expert=128, n_expert_used=8,
            n_ff_exp=768, n_ctx_train=4096, rms_eps=1e-6, rope_freq_base=1000000.0)
 
+# Qwen3-235B-A22B attention shape (64 query / 4 KV heads of 128: o-proj over 8192 columns, 16 query heads
+# per KV head) with 16 of its 128 experts, 1 layer
+BIG = dict(n_layer=1, n_embd=4096, n_head=64, n_head_kv=4, head_dim=128, n_vocab=2048, n_expert=16, n_expert_used=8,
+           n_ff_exp=1536, n_ctx_train=4096, rms_eps=1e-6, rope_freq_base=1000000.0)
+
 _w = {}
 
 
 def weights(name):
     if name not in _w:
-        hp, wtype, seed = {"tiny": (TINY, 8, 1234), "mid": (MID, 12, 99)}[name]
+        hp, wtype, seed = {"tiny": (TINY, 8, 1234), "mid": (MID, 12, 99), "big": (BIG, 12, 235)}[name]
         _w[name] = (hp, synth.qwen3_weights(np.random.default_rng(seed), hp, wtype=wtype))
     return _w[name]
 
@@ -169,6 +177,24 @@ def test_30b_shaped_layers(lstk, dev):
         err = float(np.max(np.abs(gl - rl)))
         print(f"[30b-shaped step {step}] max|dlogit| {err:.2e} (logit std {np.std(rl):.3f})", flush=True)
         assert err <= LOGITS_TOL
+        assert np.argmax(gl) == np.argmax(rl)
+        np.testing.assert_array_equal(gt, rt)
+        feed = np.array([np.argmax(rl)], np.int32)
+
+
+def test_235b_attention_shape(lstk, dev):
+    """h 4096 and 64 / 4 heads: single-token GEMVs over 4096 and 8192 columns, 16-row query tiles per
+    KV head, two row blocks at 8 tokens."""
+    hp, w = weights("big")
+    _, model = build(lstk, dev, hp, w, n_batch=8, kv_size=512)
+    ref = oracle.Qwen3(hp, w, 64)
+    feed = prompt(17, 8, hp["n_vocab"])
+    for step in range(4):
+        rl, rt = ref.decode(feed, want_trace=True)
+        gl, gt = run(model, 0, feed, hp, dev)
+        err = float(np.max(np.abs(gl - rl)))
+        print(f"[235b-shaped step {step} T={len(feed)}] max|dlogit| {err:.2e} (logit std {np.std(rl):.3f})", flush=True)
+        assert err <= BIG_TOL
         assert np.argmax(gl) == np.argmax(rl)
         np.testing.assert_array_equal(gt, rt)
         feed = np.array([np.argmax(rl)], np.int32)
