@@ -113,6 +113,13 @@ int32_t lstk_model_seq_len(const lstk_model *model, int32_t seq);
  * at that KV length without a prefill; it has no counterpart in the reference. */
 int lstk_model_fill_context(lstk_model *model, int32_t seq, int n_cells, uint64_t seed, lstk_stream_t stream);
 
+/* Engine::set_routing_trace (src/engine.cpp:179-186): with a path, creates the file and writes the
+ * trace header ("LSTKRTE1", n_layer, n_expert, n_expert_used as little-endian int32); every later step
+ * of lstk_model_decode then appends its token count and its router ids ([n_layer][n_tokens][k] int32,
+ * -1 for rows the last layer skips), read back from the device after the step (a synchronisation per
+ * step, as the reference's). NULL closes the file. Steps run through prepare / forward are not traced. */
+int lstk_model_set_trace(lstk_model *model, const char *path);
+
 /* Per-stage device time of the forward pass's own kernels, recorded like lstk_pool_timing:
  * stage 0 = norms + embedding, 1 = Q/K/V + QK-norm + RoPE + KV store, 2 = attention,
  * 3 = o-proj + residual, 4 = output head. The MoE block's stages are read with lstk_pool_timing. */

@@ -104,6 +104,7 @@ SIGNATURES = {
     "lstk_model_prepare": (_I, [_P, ctypes.c_int32, _P, _I, ctypes.POINTER(ctypes.c_int32), _P]),
     "lstk_model_forward": (_I, [_P, ctypes.c_int32, _I, ctypes.c_int32, _P, _P, _P]),
     "lstk_model_fill_context": (_I, [_P, ctypes.c_int32, _I, ctypes.c_uint64, _P]),
+    "lstk_model_set_trace": (_I, [_P, ctypes.c_char_p]),
     "lstk_model_remove_seq": (_I, [_P, ctypes.c_int32]),
     "lstk_model_truncate_seq": (_I, [_P, ctypes.c_int32, ctypes.c_int32]),
     "lstk_model_seq_len": (ctypes.c_int32, [_P, ctypes.c_int32]),
@@ -393,6 +394,10 @@ class Qwen3Model:
     def fill_context(self, seq, n_cells, seed=0, stream=None):
         """Appends n_cells synthetic positions (seeded random K/V, no tokens run) to sequence seq."""
         _check(lib().lstk_model_fill_context(self._h, int(seq), int(n_cells), int(seed), _stream(stream)))
+
+    def set_trace(self, path):
+        """Routing trace to `path` (LSTKRTE1, read by localstack_amd.trace); None closes it."""
+        _check(lib().lstk_model_set_trace(self._h, None if path is None else os.fsencode(path)))
 
     def remove_seq(self, seq):
         _check(lib().lstk_model_remove_seq(self._h, int(seq)))

@@ -20,6 +20,7 @@
 
 #include <algorithm>
 #include <cmath>
+#include <cstdio>
 #include <cstring>
 #include <map>
 #include <string>
@@ -168,6 +169,10 @@ struct lstk_model {
     // timing
     bool timing = false;
     std::vector<TimedLaunch> launched[kStages];
+    // routing trace
+    FILE *trace = nullptr;
+    int32_t *trace_dev = nullptr; // [n_layer][n_batch][k] when the caller passes no trace buffer
+    std::vector<int32_t> trace_host;
 };
 
 namespace {
@@ -189,6 +194,8 @@ hipError_t timed(lstk_model *M, int stage, F &&launch) {
 
 void destroy(lstk_model *M) {
     if (!M) return;
+    if (M->trace) fclose(M->trace);
+    if (M->trace_dev) (void) hipFree(M->trace_dev);
     if (M->mem) (void) hipFree(M->mem);
     if (M->h_in) (void) hipHostFree(M->h_in);
     if (M->in_free) (void) hipEventDestroy(M->in_free);
@@ -500,8 +507,22 @@ int lstk_model_decode(lstk_model *model, int32_t seq, const int32_t *tokens, int
     try {
         for (int done = 0; done < n_tokens;) {
             const int n = std::min(model->n_batch, n_tokens - done);
-            const int rc = step(model, seq, tokens + done, n, d_logits, d_trace, st);
+            int32_t *tr = d_trace ? d_trace : model->trace ? model->trace_dev : nullptr;
+            const int rc = step(model, seq, tokens + done, n, d_logits, tr, st);
             if (rc != LSTK_OK) return rc;
+            if (model->trace) {
+                // Engine::step_resident's trace write (src/engine.cpp:299-316): token count, then each layer's ids
+                const size_t cnt = (size_t) model->hp.n_layer * n * model->hp.n_expert_used;
+                model->trace_host.resize(cnt);
+                hipError_t e;
+                if ((e = hipMemcpyAsync(model->trace_host.data(), tr, cnt * 4, hipMemcpyDeviceToHost, st)) != hipSuccess ||
+                    (e = hipStreamSynchronize(st)) != hipSuccess)
+                    return hip_fail(e, "trace download");
+                const int32_t n32 = n;
+                if (fwrite(&n32, 4, 1, model->trace) != 1 || fwrite(model->trace_host.data(), 4, cnt, model->trace) != cnt ||
+                    fflush(model->trace) != 0)
+                    return set_error(LSTK_E_IO, "routing trace write failed");
+            }
             done += n;
         }
     } catch (const std::exception &ex) {
@@ -561,6 +582,30 @@ int lstk_model_fill_context(lstk_model *model, int32_t seq, int n_cells, uint64_
     } catch (const std::exception &ex) {
         return set_error(LSTK_E_NOMEM, std::string("lstk_model_fill_context: ") + ex.what());
     }
+    return LSTK_OK;
+}
+
+int lstk_model_set_trace(lstk_model *model, const char *path) {
+    if (!model) return set_error(LSTK_E_INVALID, "null model");
+    if (model->trace) {
+        fclose(model->trace);
+        model->trace = nullptr;
+    }
+    if (!path) return LSTK_OK;
+    if (!model->trace_dev) {
+        const size_t bytes = (size_t) model->hp.n_layer * model->n_batch * model->hp.n_expert_used * 4;
+        const hipError_t e = hipMalloc(&model->trace_dev, bytes);
+        if (e != hipSuccess) {
+            model->trace_dev = nullptr;
+            return set_error(LSTK_E_NOMEM, "hipMalloc of the trace buffer failed");
+        }
+    }
+    model->trace = fopen(path, "wb");
+    if (!model->trace) return set_error(LSTK_E_IO, std::string("cannot write ") + path);
+    static const char magic[8] = {'L', 'S', 'T', 'K', 'R', 'T', 'E', '1'};
+    const int32_t header[3] = {model->hp.n_layer, model->hp.n_expert, model->hp.n_expert_used};
+    if (fwrite(magic, 1, 8, model->trace) != 8 || fwrite(header, 4, 3, model->trace) != 3 || fflush(model->trace) != 0)
+        return set_error(LSTK_E_IO, "routing trace write failed");
     return LSTK_OK;
 }
 

@@ -254,6 +254,32 @@ def test_model_loaded_from_gguf_matches(lstk, dev, tmp_path):
         feed = np.array([np.argmax(a)], np.int32)
 
 
+def test_routing_trace_file(lstk, dev, tmp_path):
+    """set_trace writes the reference's LSTKRTE1 file: the header, then per step the token count and
+    the same ids the trace buffer receives (chunked steps each get their own record)."""
+    from localstack_amd import trace
+    hp, w = weights("tiny")
+    _, model = build(lstk, dev, hp, w, n_batch=8)
+    path = tmp_path / "route.bin"
+    model.set_trace(path)
+    want = []
+    toks = prompt(41, 12, hp["n_vocab"])
+    model.decode(0, toks)  # two steps of 8 + 4 tokens
+    feed = np.array([np.argmax(model.logits.cpu().numpy())], np.int32)
+    for _ in range(3):
+        _, tr = run(model, 0, feed, hp, dev)
+        want.append(tr)
+        feed = np.array([np.argmax(model.logits.cpu().numpy())], np.int32)
+    model.set_trace(None)
+    n_layer, n_expert, k, steps = trace.parse_trace(path.read_bytes())
+    assert (n_layer, n_expert, k) == (hp["n_layer"], hp["n_expert"], hp["n_expert_used"])
+    assert [s.shape[1] for s in steps] == [8, 4, 1, 1, 1]
+    for got, ref in zip(steps[2:], want):
+        np.testing.assert_array_equal(got, ref)
+    for s_ in steps[:2]:
+        assert (s_[-1][:-1] == -1).all() and (s_[:-1] >= 0).all() and (s_[-1][-1] >= 0).all()
+
+
 def test_errors_are_reported(lstk, dev):
     hp, w = weights("tiny")
     _, model = build(lstk, dev, hp, w, kv_size=32)
