@@ -342,10 +342,12 @@ def model30b_leg(torch, L, n_layer, ctx, steps, warmup, t_list=(1, 8, 32)):
     tok = (rng.standard_normal((hp["n_vocab"], H), dtype=np.float32) * np.float32(0.02)).astype(np.float16)
     w = {"tok_embd": tok, "output_norm": np.ones(H, np.float32), "output": None, "layers": [L0] * n_layer}
     t_max = max(t_list)
-    store = L.ExpertStore(n_layer, H, F, E, K, t_max, [(L0["types"], L0["up"], L0["gate"], L0["down"])] * n_layer)
+    n_prefill = 512
+    nb = max(t_max, n_prefill)
+    store = L.ExpertStore(n_layer, H, F, E, K, nb, [(L0["types"], L0["up"], L0["gate"], L0["down"])] * n_layer)
     kv = (ctx + t_max * (steps + warmup + 3) + 255) // 256 * 256
     dev = torch.device("cuda:0")
-    model = L.Qwen3Model(hp, w, store, kv, t_max, device=dev)
+    model = L.Qwen3Model(hp, w, store, kv, nb, device=dev)
     del tok
     log(f"[bench] 30B model: {n_layer} layers built in {time.time() - t0:.1f}s, experts {store.total_bytes() / 1e9:.1f} GB, "
         f"KV cache {kv} cells")
@@ -411,6 +413,19 @@ def model30b_leg(torch, L, n_layer, ctx, steps, warmup, t_list=(1, 8, 32)):
         log(f"[bench] 30B model T={T}: {json.dumps(r)}")
         del graph
         model.remove_seq(seq)
+    # prompt processing: one 512-token step into an empty cache (eager: the step's host work included)
+    prompt = rng.integers(0, hp["n_vocab"], n_prefill).astype(np.int32)
+    times = []
+    for rep in range(3):
+        torch.cuda.synchronize()
+        t0 = time.time()
+        model.decode(1000 + rep, prompt, logits=logits)
+        torch.cuda.synchronize()
+        times.append(time.time() - t0)
+        model.remove_seq(1000 + rep)
+    ms = 1e3 * min(times[1:])
+    res["prefill512"] = {"tok_s": n_prefill * 1000.0 / ms, "ms": ms}
+    log(f"[bench] 30B model prefill {n_prefill}: {json.dumps(res['prefill512'])}")
     model.close()
     store.close()
     return res

@@ -66,7 +66,9 @@ def build(verbose=False):
         with ThreadPoolExecutor(max_workers=min(len(cmds), 8)) as ex:
             list(ex.map(lambda c: _run(c, verbose), cmds))
         tmp = LIB + ".tmp"
-        _run([hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", tmp] + objs + ["-lpthread"], verbose)
+        rocm_lib = os.path.join(os.environ.get("ROCM_PATH", "/opt/rocm"), "lib")
+        _run([hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", tmp] + objs +
+             ["-L", rocm_lib, "-lrocblas", "-Wl,-rpath," + rocm_lib, "-lpthread"], verbose)
         os.replace(tmp, LIB)
     finally:
         shutil.rmtree(tmpdir, ignore_errors=True)

@@ -22,6 +22,7 @@ struct NormParams {
     float *y;
     int rows, n;
     float eps;
+    uint16_t *y16; // when set, also y rounded to fp16 (the input of an F16 matrix product)
 };
 
 // One F16 weight matrix of a GEMV launch: y[t * ldy + r] = sum_i fp16(x[t][i]) * w[r][i] (+ add[t * ldy + r]).
@@ -83,6 +84,7 @@ struct AttnParams {
     float scale;
     float *part; // [T][n_head][n_chunk][hd + 4]: max, sum, 2 unused, unnormalised output
     float *out;  // [T][n_head * hd]
+    uint16_t *out16; // when set, also out rounded to fp16
 };
 
 // Writes v to n int32 values (the trace rows the last layer does not compute).

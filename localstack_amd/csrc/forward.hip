@@ -67,7 +67,9 @@ __global__ __launch_bounds__(kNormBlock) void rmsnorm_kernel(NormParams P) {
         const int i = tid + k * kNormBlock;
         if (i < P.n) {
             if (e) P.x_out[off + i] = v[k];
-            P.y[off + i] = (v[k] * scale) * w[k];
+            const float y = (v[k] * scale) * w[k];
+            P.y[off + i] = y;
+            if (P.y16) P.y16[off + i] = f2h(y);
         }
     }
 }
@@ -483,7 +485,12 @@ __global__ __launch_bounds__(kAtBlock) void attn_kernel(AttnParams P) {
             if (P.n_chunk == 1) {
                 const float inv_l = s_L[rl];
 #pragma unroll
-                for (int dt = 0; dt < DT; dt++) P.out[((size_t) t * P.n_head + h) * HD + (w * DT + dt) * 16 + lr] = O[rt][dt][v] / inv_l;
+                for (int dt = 0; dt < DT; dt++) {
+                    const size_t o = ((size_t) t * P.n_head + h) * HD + (w * DT + dt) * 16 + lr;
+                    const float y = O[rt][dt][v] / inv_l;
+                    P.out[o] = y;
+                    if (P.out16) P.out16[o] = f2h(y);
+                }
             } else {
                 float *pp = P.part + (((size_t) t * P.n_head + h) * P.n_chunk + c) * (HD + 4);
 #pragma unroll
@@ -550,7 +557,9 @@ __global__ __launch_bounds__(kBlock) void attn_combine_kernel(AttnParams P) {
     if (tid < hd) {
         float o = 0.0f;
         for (int i = 0; i < CL; i++) o += s_o[i * hd + tid];
-        P.out[((size_t) t * P.n_head + h) * hd + tid] = o / L;
+        const size_t oi = ((size_t) t * P.n_head + h) * hd + tid;
+        P.out[oi] = o / L;
+        if (P.out16) P.out16[oi] = f2h(o / L);
     }
 }
 

@@ -13,10 +13,14 @@
 //     MoE block: lstk_moe_block (resident pool) or route -> acquire -> lstk_moe_ffn (streaming pool)
 //     the last layer runs its FFN on the output row only (src/qwen3.cpp:233-237)
 //   output_norm + head on the last row                  (rmsnorm_kernel, gemv_kernel)
+// With several tokens per step the projections are plain F16 matrix products: the normalised rows and
+// the attention output are also written as fp16 (ggml rounds the activations of an F16 mat-mul to
+// fp16) and rocBLAS multiplies them with f32 accumulation (rocblas_gemm_ex, f16 x f16 -> f32).
 // The KV cache keeps the reference's block table (32-cell blocks handed out per sequence, cell_seq /
 // cell_pos per cell) on the host; the device holds the cells' fp16 K and V in layouts chosen for
 // coalesced reads (forward.h) and a copy of cell_seq / cell_pos that the step's RoPE launch updates.
 #include <hip/hip_runtime.h>
+#include <rocblas/rocblas.h>
 
 #include <algorithm>
 #include <cmath>
@@ -35,6 +39,7 @@ namespace {
 using lstk::set_error;
 
 constexpr int kStages = 5;
+constexpr int kBlasMinTokens = 2; // steps of at least this many tokens take the library GEMM
 constexpr uint32_t kCellBlock = 32; // KvCache::block_size (src/kv_cache.h:27)
 
 int hip_fail(hipError_t e, const char *what) { return set_error(LSTK_E_DEVICE, std::string(what) + ": " + hipGetErrorString(e)); }
@@ -163,6 +168,8 @@ struct lstk_model {
     float *x = nullptr, *hn = nullptr, *q = nullptr, *k = nullptr, *v = nullptr, *qr = nullptr, *attn = nullptr,
           *part = nullptr, *weights = nullptr;
     int32_t *ids = nullptr, *slots = nullptr, *in = nullptr; // in = tokens | cells | positions
+    uint16_t *hn16 = nullptr, *attn16 = nullptr;             // fp16 inputs of the multi-token products
+    rocblas_handle blas = nullptr;
     // pinned host staging
     int32_t *h_in = nullptr, *h_ids = nullptr, *h_slots = nullptr;
     hipEvent_t in_free = nullptr;
@@ -194,6 +201,7 @@ hipError_t timed(lstk_model *M, int stage, F &&launch) {
 
 void destroy(lstk_model *M) {
     if (!M) return;
+    if (M->blas) (void) rocblas_destroy_handle(M->blas);
     if (M->trace) fclose(M->trace);
     if (M->trace_dev) (void) hipFree(M->trace_dev);
     if (M->mem) (void) hipFree(M->mem);
@@ -272,6 +280,8 @@ int create(const lstk_qwen3_hparams *hpp, const lstk_qwen3_weights *w, lstk_pool
         {(void **) &M->ids, nb * k * 4},
         {(void **) &M->slots, nb * k * 4},
         {(void **) &M->in, 3 * nb * 4},
+        {(void **) &M->hn16, nb * h * 2},
+        {(void **) &M->attn16, nb * hq * 2},
         {(void **) &M->cell_seq, (size_t) kv_size * 4},
         {(void **) &M->cell_pos, (size_t) kv_size * 4},
     };
@@ -301,6 +311,11 @@ int create(const lstk_qwen3_hparams *hpp, const lstk_qwen3_weights *w, lstk_pool
         destroy(M);
         return set_error(LSTK_E_NOMEM, "hipHostMalloc of the step staging failed");
     }
+    if (rocblas_create_handle(&M->blas) != rocblas_status_success) {
+        M->blas = nullptr;
+        destroy(M);
+        return set_error(LSTK_E_DEVICE, "rocblas_create_handle failed");
+    }
     M->h_ids = M->h_in + 3 * nb;
     M->h_slots = M->h_ids + nb * k;
     if ((e = hipEventCreateWithFlags(&M->in_free, hipEventDisableTiming)) != hipSuccess ||
@@ -310,6 +325,35 @@ int create(const lstk_qwen3_hparams *hpp, const lstk_qwen3_weights *w, lstk_pool
     }
     *out = M;
     return LSTK_OK;
+}
+
+// Records the time of `f`'s work on the stream with events around it (library calls launch kernels of
+// their own, which per-launch events cannot see).
+template <typename F>
+int timed_span(lstk_model *M, int stage, hipStream_t st, F &&f) {
+    if (!M->timing) return f();
+    TimedLaunch t{};
+    if (hipEventCreate(&t.start) != hipSuccess || hipEventCreate(&t.end) != hipSuccess ||
+        hipEventRecord(t.start, st) != hipSuccess)
+        return set_error(LSTK_E_DEVICE, "timing events");
+    const int rc = f();
+    if (hipEventRecord(t.end, st) != hipSuccess) return set_error(LSTK_E_DEVICE, "timing events");
+    M->launched[stage].push_back(t);
+    return rc;
+}
+
+// Y[t][r] (+)= sum_c X16[t][c] W[r][c] for T tokens: one rocBLAS f16 x f16 -> f32 product in column-major
+// terms, Y^T (rows x T, ld ldy) = W^T-op(A) (rows x cols) . X16^T (cols x T).
+int blas_gemm(lstk_model *M, const uint16_t *W, int rows, int cols, const uint16_t *X16, int T, float *Y, int ldy,
+              bool accumulate, hipStream_t st) {
+    const float alpha = 1.0f, beta = accumulate ? 1.0f : 0.0f;
+    rocblas_status s = rocblas_set_stream(M->blas, st);
+    if (s == rocblas_status_success)
+        s = rocblas_gemm_ex(M->blas, rocblas_operation_transpose, rocblas_operation_none, rows, T, cols, &alpha, W,
+                            rocblas_datatype_f16_r, cols, X16, rocblas_datatype_f16_r, cols, &beta, Y, rocblas_datatype_f32_r,
+                            ldy, Y, rocblas_datatype_f32_r, ldy, rocblas_datatype_f32_r, rocblas_gemm_algo_standard, 0, 0);
+    return s == rocblas_status_success ? LSTK_OK
+                                       : set_error(LSTK_E_DEVICE, std::string("rocblas_gemm_ex: ") + rocblas_status_to_string(s));
 }
 
 // Copies the host bookkeeping of the cells to the device (after removals; rare, synchronous).
@@ -374,6 +418,7 @@ int forward(lstk_model *M, int32_t seq, int T, int n_cells, float *d_logits, int
     const int hq = hp.n_head * hd, hk = hp.n_head_kv * hd;
     hipError_t e;
     const int32_t *d_tok = M->in, *d_cells = M->in + nb, *d_pos = M->in + 2 * nb;
+    const bool blas = T >= kBlasMinTokens;
 
     for (int l = 0; l < hp.n_layer; l++) {
         const lstk_qwen3_layer &L = M->layers[l];
@@ -396,13 +441,23 @@ int forward(lstk_model *M, int32_t seq, int T, int n_cells, float *d_logits, int
                 gp.x_out = M->x;
             }
         } else {
-            lstk::NormParams np{M->x, l == 0 ? M->tok_embd : nullptr, d_tok, M->x, L.attn_norm, M->hn, T, h, hp.rms_eps};
+            lstk::NormParams np{M->x, l == 0 ? M->tok_embd : nullptr, d_tok, M->x, L.attn_norm, M->hn, T, h, hp.rms_eps,
+                                blas ? M->hn16 : nullptr};
             if ((e = timed(M, 0, [&](const lstk::LaunchTiming *tm) { return lstk::launch_rmsnorm(np, st, tm); })) != hipSuccess)
                 return hip_fail(e, "attn_norm launch");
             gp.x = M->hn;
         }
-        if ((e = timed(M, 1, [&](const lstk::LaunchTiming *tm) { return lstk::launch_gemv(gp, st, tm); })) != hipSuccess)
+        if (blas) {
+            const int rc = timed_span(M, 1, st, [&] {
+                int r = blas_gemm(M, L.wq, hq, h, M->hn16, T, M->q, hq, false, st);
+                if (r == LSTK_OK) r = blas_gemm(M, L.wk, hk, h, M->hn16, T, M->k, hk, false, st);
+                if (r == LSTK_OK) r = blas_gemm(M, L.wv, hk, h, M->hn16, T, M->v, hk, false, st);
+                return r;
+            });
+            if (rc != LSTK_OK) return rc;
+        } else if ((e = timed(M, 1, [&](const lstk::LaunchTiming *tm) { return lstk::launch_gemv(gp, st, tm); })) != hipSuccess) {
             return hip_fail(e, "qkv launch");
+        }
         uint16_t *kc = M->kcache + M->layer_elems * l, *vc = M->vcache + M->layer_elems * l;
         lstk::RopeParams rp{M->q, M->k, M->v, L.q_norm, L.k_norm, hp.rms_eps, d_pos, d_cells, seq, M->cell_seq, M->cell_pos,
                             T, hp.n_head, hp.n_head_kv, hd, (int) M->kv.size, M->theta_scale, M->qr, kc, vc};
@@ -425,6 +480,7 @@ int forward(lstk_model *M, int32_t seq, int T, int n_cells, float *d_logits, int
         ap.scale = 1.0f / sqrtf((float) hd);
         ap.part = M->part;
         ap.out = M->attn;
+        ap.out16 = blas ? M->attn16 : nullptr;
         lstk::attn_plan(ap);
         if ((e = timed(M, 2, [&](const lstk::LaunchTiming *tm) { return lstk::launch_attn(ap, st, tm); })) != hipSuccess ||
             (ap.n_chunk > 1 &&
@@ -437,8 +493,12 @@ int forward(lstk_model *M, int32_t seq, int T, int n_cells, float *d_logits, int
         op.cols = hq;
         op.x = M->attn;
         op.T = T;
-        if ((e = timed(M, 3, [&](const lstk::LaunchTiming *tm) { return lstk::launch_gemv(op, st, tm); })) != hipSuccess)
+        if (blas) {
+            const int rc = timed_span(M, 3, st, [&] { return blas_gemm(M, L.wo, h, hq, M->attn16, T, M->x, h, true, st); });
+            if (rc != LSTK_OK) return rc;
+        } else if ((e = timed(M, 3, [&](const lstk::LaunchTiming *tm) { return lstk::launch_gemv(op, st, tm); })) != hipSuccess) {
             return hip_fail(e, "o-proj launch");
+        }
         // after the last attention only the output row goes on (src/qwen3.cpp:233-237)
         const bool last = l == hp.n_layer - 1;
         const int rows = last ? 1 : T;

@@ -4,9 +4,9 @@ Bar (the tiny-model workload: 2 layers, h 256, 4 / 2 heads of 64, vocab 1024, 8 
 f 512, Q8_0 experts; 16-token prefill of seeded uniform ids, then 32 greedy steps):
 logits within LOGITS_TOL max-abs of the oracle at every step, top-1 agreement on every step (the
 99.9% bar over 33 choices), and the router's expert ids of every layer and step bit-exact.
-Invariants of the device path itself are held exactly: chunked prefill, interleaved sequences,
-truncation, a streaming pool, graph replay and a model loaded from a GGUF file all reproduce the plain
-run bit for bit.
+Invariants of the device path itself: interleaved sequences, truncation, a streaming pool, graph replay
+and a model loaded from a GGUF file reproduce the plain run bit for bit; a prompt cut into steps of
+another size agrees to f32 summation order (multi-token steps multiply through the library GEMM).
 
 Why the logits differ at all: both sides quantize activations to Q8_0 / Q8_K before the expert
 products, so an f32 rounding difference upstream can move a value across a quantization step. The
@@ -92,15 +92,25 @@ def test_tiny_model_greedy_parity(lstk, dev):
     print(f"[tiny] 33 steps: worst max|dlogit| {worst:.2e}, top-1 agreement {agree}/{steps}", flush=True)
 
 
-def test_chunked_prefill_is_bit_identical(lstk, dev):
+def test_chunked_prefill_matches_one_step(lstk, dev):
+    """A 16-token prompt in one step and in steps of 5, 5, 5, 1: the last token's row goes through the
+    library GEMM in one case and the single-token GEMV in the other, so only the f32 summation order
+    differs (measured 2.9e-6)."""
     hp, w = weights("tiny")
     toks = prompt(7, 16, hp["n_vocab"])
     _, one = build(lstk, dev, hp, w)
     a, _ = run(one, 0, toks, hp, dev)
     _, chunked = build(lstk, dev, hp, w, n_batch=5)
     b, _ = run(chunked, 0, toks, hp, dev)
-    np.testing.assert_array_equal(a, b)
+    assert np.max(np.abs(a - b)) <= 1e-4
+    assert np.argmax(a) == np.argmax(b)
     assert chunked.seq_len(0) == 16
+    # the next single-token step routes identically and agrees as closely
+    nxt = np.array([np.argmax(a)], np.int32)
+    a2, ta = run(one, 0, nxt, hp, dev)
+    b2, tb = run(chunked, 0, nxt, hp, dev)
+    np.testing.assert_array_equal(ta, tb)
+    assert np.max(np.abs(a2 - b2)) <= 1e-4
 
 
 def test_sequences_are_isolated_and_removable(lstk, dev):
@@ -227,6 +237,31 @@ def test_graph_replay_matches_eager(lstk, dev):
         np.testing.assert_array_equal(logits.cpu().numpy(), ea, err_msg=f"replay {step}")
         feed = np.array([np.argmax(ea)], np.int32)
     assert gm.seq_len(0) == eager.seq_len(0) == 22
+
+
+def test_graph_replay_multi_token(lstk, dev):
+    """Steps of 4 tokens (library GEMM projections) captured once and replayed: every replay equals the
+    eager step, with the eager model's own work and synchronisations between replays."""
+    import torch
+    hp, w = weights("tiny")
+    _, eager = build(lstk, dev, hp, w)
+    _, gm = build(lstk, dev, hp, w)
+    toks = prompt(23, 40, hp["n_vocab"]).reshape(10, 4)
+    stream = torch.cuda.Stream()
+    logits = torch.zeros(hp["n_vocab"], dtype=torch.float32, device=dev)
+    graph = None
+    for step in range(10):
+        ea, _ = run(eager, 0, toks[step], hp, dev)
+        with torch.cuda.stream(stream):
+            n = gm.prepare(0, toks[step], stream=stream)
+            if graph is None:
+                graph = torch.cuda.CUDAGraph()
+                with torch.cuda.graph(graph, stream=stream):
+                    gm.forward(0, 4, 256, logits=logits, stream=stream)
+            assert n <= 256
+            graph.replay()
+        torch.cuda.synchronize()
+        np.testing.assert_array_equal(logits.cpu().numpy(), ea, err_msg=f"replay {step}")
 
 
 def test_model_loaded_from_gguf_matches(lstk, dev, tmp_path):
