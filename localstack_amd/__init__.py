@@ -230,10 +230,11 @@ class ExpertStore:
                                       int(min_slots), flags, ctypes.byref(h)))
         self._h = h
         self._keep = None  # the pool copied what it needs
+        self._destroy = lib().lstk_pool_destroy  # held, so that closing works during interpreter shutdown
 
     def close(self):
         if getattr(self, "_h", None):
-            lib().lstk_pool_destroy(self._h)
+            self._destroy(self._h)
             self._h = None
 
     def __del__(self):
@@ -356,11 +357,12 @@ class Qwen3Model:
         _check(lib().lstk_model_create(ctypes.byref(self._hp), ctypes.byref(self._w), store._h, int(kv_size),
                                        int(n_batch), ctypes.byref(h)))
         self._h = h
+        self._destroy = lib().lstk_model_destroy
         self.logits = torch.empty(self.hp["n_vocab"], dtype=torch.float32, device=self.device)
 
     def close(self):
         if getattr(self, "_h", None):
-            lib().lstk_model_destroy(self._h)
+            self._destroy(self._h)
             self._h = None
 
     def __del__(self):
@@ -424,21 +426,22 @@ _GGML_NAME = {0: "F32", 1: "F16", 8: "Q8_0", 12: "Q4_K", 14: "Q6_K", 30: "BF16"}
 
 
 class GgufFile:
-    """A memory-mapped GGUF file (include/lstk_gguf.h), mirroring GgufModel (src/gguf_model.h:31-60)."""
+    """A memory-mapped GGUF file (include/lstk_gguf.h), mirroring GgufModel (src/gguf_model.h:31-60).
+
+    The mapping lives as long as this object or any array view taken from it (tensor_bytes /
+    tensor_array keep the object alive), so a view never outlives the memory it reads."""
 
     def __init__(self, path):
         h = ctypes.c_void_p()
         _check(lib().lstk_gguf_open(os.fsencode(path), ctypes.byref(h)))
         self._h = h
+        self._destroy = lib().lstk_gguf_close
         self.path = path
 
-    def close(self):
-        if getattr(self, "_h", None):
-            lib().lstk_gguf_close(self._h)
-            self._h = None
-
     def __del__(self):
-        self.close()
+        if getattr(self, "_h", None):
+            self._destroy(self._h)
+            self._h = None
 
     @property
     def arch(self):
@@ -486,6 +489,7 @@ class GgufFile:
         """A read-only uint8 view of the tensor's bytes in the mapping (valid while the file is open)."""
         info = self.tensor_info(name)
         buf = (ctypes.c_uint8 * info["nbytes"]).from_address(info["data"])
+        buf._owner = self  # the view keeps the mapping alive
         a = np.ctypeslib.as_array(buf)
         a.flags.writeable = False
         return a

@@ -118,6 +118,14 @@ def test_qwen3_hparams_and_experts(lstk, tiny_file):
         g.tensor_info("output.weight")  # tied head
 
 
+def test_views_keep_the_mapping_alive(lstk, tiny_file):
+    import gc
+    p, w = tiny_file
+    a = lstk.GgufFile(p).tensor_array("token_embd.weight")  # the file object is dropped at once
+    gc.collect()
+    np.testing.assert_array_equal(a, w["tok_embd"])
+
+
 def corrupt(path, fn):
     b = bytearray(path.read_bytes())
     fn(b)
