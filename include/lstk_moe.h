@@ -91,7 +91,7 @@ int lstk_abi_version(void);
  * (up, gate, down) type triple, each group gets pool_bytes * n_layers_in_group / n_layer, shards hold
  * at most 1024 slots and at least min_slots; the full expert table is copied once into pinned host
  * memory (the host tier, standing in for the GGUF file) and misses are served from it with
- * hipMemcpyAsync on the pool's side stream. Layers that pass the same three host pointers (and
+ * hipMemcpyAsync on the pool's side streams. Layers that pass the same three host pointers (and
  * types) share one host-tier copy.
  * The layers' host pointers are only read during this call. */
 int lstk_pool_create(const lstk_moe_dims *dims, const lstk_expert_layer *layers, size_t pool_bytes,
@@ -100,7 +100,8 @@ void lstk_pool_destroy(lstk_pool *pool);
 
 /* ExpertStore::acquire (src/expert_store.cpp:232-286): makes `n` experts of `layer` resident and
  * writes their slot numbers to `slots` (host arrays), pinning them until lstk_pool_release_all().
- * Hits pin; misses evict the LRU head and queue the three matrix copies on the side stream; `stream`
+ * Hits pin; misses evict the LRU head and queue the three matrix copies on a side stream (misses
+ * round-robin over the pool's side streams, one expert's copies on one stream); `stream`
  * (the compute stream) is made to wait for those copies, so the host never blocks on them.
  * Fails with LSTK_E_EXHAUSTED when the layer needs more slots than its shard has. */
 int lstk_pool_acquire(lstk_pool *pool, int layer, const int32_t *experts, int n, int32_t *slots,

@@ -6,8 +6,9 @@
 //     Q4_K expert table whole), slot s of a layer = expert s;
 //   - streaming pools keep the reference's slot bookkeeping exactly (type-triple classes, shards of
 //     at most 1024 slots, pin counts, intrusive LRU, hits/misses/bytes_read/acquires stats), with the
-//     GGUF file replaced by a pinned host tier and pread() by hipMemcpyAsync on a side stream that the
-//     compute stream waits on through an event, so acquire() never blocks the host on a copy;
+//     GGUF file replaced by a pinned host tier and pread() by hipMemcpyAsync on side streams (a layer's
+//     misses round-robin over LSTK_SIDE_STREAMS of them) that the compute stream waits on through
+//     events, so acquire() never blocks the host on a copy;
 //   - a copy that fails unmaps its slot and fails the acquire (the reference only logs a short read,
 //     src/expert_store.cpp:62-66, and leaves the slot holding garbage).
 // It also owns the per-call device scratch (quantized activations, logits, permutation, SwiGLU rows,
@@ -107,6 +108,13 @@ constexpr int kStages = 4; // router (+ top-k), gate_up, down, combine
 
 }  // namespace
 
+// Side streams that carry host-tier copies: a layer's misses go round-robin over them (all three matrices
+// of one expert on one stream), so several DMA engines can serve one acquire.
+#ifndef LSTK_SIDE_STREAMS
+#define LSTK_SIDE_STREAMS 4
+#endif
+constexpr int kSides = LSTK_SIDE_STREAMS;
+
 struct lstk_pool {
     lstk_moe_dims dims{};
     bool streaming = false, dry = false;
@@ -119,8 +127,8 @@ struct lstk_pool {
     // streaming host tier: per layer, the layer's experts in pool layout, in pinned memory
     uint8_t *tier = nullptr;
     std::vector<std::array<uint8_t *, 3>> tier_of;
-    hipStream_t side = nullptr;
-    hipEvent_t copy_done = nullptr, release_ev = nullptr;
+    hipStream_t side[kSides] = {};
+    hipEvent_t copy_done[kSides] = {}, release_ev = nullptr;
     int fail_copies = 0;
     lstk_pool_stats_t stats{};
     // scratch
@@ -235,9 +243,11 @@ void destroy(lstk_pool *P) {
         }
         if (P->tier) (void) hipHostFree(P->tier);
         if (P->scratch) (void) hipFree(P->scratch);
-        if (P->copy_done) (void) hipEventDestroy(P->copy_done);
+        for (int i = 0; i < kSides; i++) {
+            if (P->copy_done[i]) (void) hipEventDestroy(P->copy_done[i]);
+            if (P->side[i]) (void) hipStreamDestroy(P->side[i]);
+        }
         if (P->release_ev) (void) hipEventDestroy(P->release_ev);
-        if (P->side) (void) hipStreamDestroy(P->side);
         for (auto &v : P->launched)
             for (TimedLaunch &t : v) {
                 (void) hipEventDestroy(t.start);
@@ -408,11 +418,12 @@ int create(const lstk_moe_dims *dims, const lstk_expert_layer *layers, size_t po
                 return rc;
             }
         }
-        if ((e = hipStreamCreateWithFlags(&P->side, hipStreamNonBlocking)) != hipSuccess ||
-            (e = hipEventCreateWithFlags(&P->copy_done, hipEventDisableTiming)) != hipSuccess ||
-            (e = hipEventCreateWithFlags(&P->release_ev, hipEventDisableTiming)) != hipSuccess) {
+        for (int i = 0; i < kSides && e == hipSuccess; i++)
+            if ((e = hipStreamCreateWithFlags(&P->side[i], hipStreamNonBlocking)) == hipSuccess)
+                e = hipEventCreateWithFlags(&P->copy_done[i], hipEventDisableTiming);
+        if (e != hipSuccess || (e = hipEventCreateWithFlags(&P->release_ev, hipEventDisableTiming)) != hipSuccess) {
             destroy(P);
-            return hip_fail(e, "side stream / events");
+            return hip_fail(e, "side streams / events");
         }
     } else {
         // resident: repack each layer's experts on the host and upload them once
@@ -449,8 +460,8 @@ int create(const lstk_moe_dims *dims, const lstk_expert_layer *layers, size_t po
     return LSTK_OK;
 }
 
-// Issues the three host-tier -> HBM copies of a miss on the side stream.
-int copy_in(lstk_pool *P, int layer, const Shard &s, int32_t slot, int32_t expert) {
+// Issues the three host-tier -> HBM copies of a miss on side stream `side`.
+int copy_in(lstk_pool *P, int layer, const Shard &s, int32_t slot, int32_t expert, hipStream_t side) {
     if (P->fail_copies > 0) {
         P->fail_copies--;
         return fail(LSTK_E_IO, "expert copy failed (injected) for layer " + std::to_string(layer) + " expert " +
@@ -462,7 +473,7 @@ int copy_in(lstk_pool *P, int layer, const Shard &s, int32_t slot, int32_t exper
     uint8_t *dst[3] = {s.d_up, s.d_gate, s.d_down};
     for (int m = 0; m < 3; m++) {
         const hipError_t e = hipMemcpyAsync(dst[m] + (size_t) slot * b[m], t[m] + (size_t) expert * b[m], b[m],
-                                            hipMemcpyHostToDevice, P->side);
+                                            hipMemcpyHostToDevice, side);
         if (e != hipSuccess)
             return fail(LSTK_E_IO, std::string("expert copy failed for layer ") + std::to_string(layer) + ": " +
                                        hipGetErrorString(e));
@@ -522,11 +533,13 @@ int acquire(lstk_pool *P, int layer, const int32_t *experts, int n, int32_t *slo
     }
     if (!misses.empty()) {
         hipError_t e = hipSuccess;
+        const int n_used = std::min<int>(kSides, (int) misses.size());
         // a slot released by earlier compute may only be overwritten once that compute has finished
-        if (!P->dry) e = hipStreamWaitEvent(P->side, P->release_ev, 0);
+        for (int i = 0; i < n_used && !P->dry && e == hipSuccess; i++) e = hipStreamWaitEvent(P->side[i], P->release_ev, 0);
         if (e != hipSuccess) rc = hip_fail(e, "hipStreamWaitEvent(side)");
-        for (const auto &[s, ex] : misses) {
-            const int crc = copy_in(P, layer, p, s, ex);
+        for (size_t mi = 0; mi < misses.size(); mi++) {
+            const auto &[s, ex] = misses[mi];
+            const int crc = copy_in(P, layer, p, s, ex, P->side[mi % n_used]);
             if (crc != LSTK_OK) {
                 // the slot holds no valid expert: unmap it rather than serve garbage
                 P->slot_of[(size_t) layer * d.n_expert + ex] = -1;
@@ -535,10 +548,12 @@ int acquire(lstk_pool *P, int layer, const int32_t *experts, int n, int32_t *slo
                 rc = crc;
             }
         }
-        if (!P->dry) {
-            if ((e = hipEventRecord(P->copy_done, P->side)) != hipSuccess ||
-                (e = hipStreamWaitEvent(stream, P->copy_done, 0)) != hipSuccess)
+        for (int i = 0; i < n_used && !P->dry; i++) {
+            if ((e = hipEventRecord(P->copy_done[i], P->side[i])) != hipSuccess ||
+                (e = hipStreamWaitEvent(stream, P->copy_done[i], 0)) != hipSuccess) {
                 rc = hip_fail(e, "copy event");
+                break;
+            }
         }
     }
     P->stats.wait_ms += std::chrono::duration<double, std::milli>(std::chrono::steady_clock::now() - t0).count();
