@@ -236,7 +236,9 @@ def stack235_leg(torch, L, n_layer, pool_gib, steps, warmup, stream_tokens):
       streaming  the pool capped at pool_gib GiB (ExpertStore::init's slot split); per layer, in the
                  order of Engine::run_segment (src/engine.cpp:343-399): router on the device, ids to
                  the host, acquire (hits pin, misses evict the LRU head and are copied from the pinned
-                 host tier on the pool's side stream), experts on the slots, release_all.
+                 host tier on the pool's side streams), experts on the slots, release_all;
+                 then the same with the acquire on the device (no host round trip), eager and as a
+                 captured graph per token.
     One layer's expert bytes are generated and passed for every layer (the host tier then holds one
     copy); every layer has its own HBM slots, router weights and hnorm rows."""
     from localstack_amd import synth
@@ -319,6 +321,56 @@ def stack235_leg(torch, L, n_layer, pool_gib, steps, warmup, stream_tokens):
                         "tok_s": stream_tokens / el, "ms_per_token": el * 1e3 / stream_tokens,
                         "hit_rate": hits / max(1, hits + misses), "misses_per_token": misses / stream_tokens,
                         "host_to_hbm_gbs": rd / el / 1e9, "bytes_read_per_token": rd / stream_tokens}
+    store.close()
+    torch.cuda.synchronize()
+    # (iii) streaming with the acquire on the device: the same pool size and token sequence, route ->
+    # lstk_pool_acquire_device (resolve + copy kernels) -> experts, no host round trip; timed eager
+    # and as one captured graph per token (the token's hnorm rows copied into the graph's inputs)
+    store = L.ExpertStore(n_layer, H5, F5, E, K, 1, layers, pool_bytes=pool_gib << 30, min_slots=2 * K + 2,
+                          streaming=True, device_lru=True)
+    xs_g = [torch.zeros((1, H5), dtype=torch.float32, device=dev) for _ in range(n_layer)]
+
+    def token_dev(xt):
+        for l in range(n_layer):
+            store.route(l, xt[l], routers[l], 1, ids[l], w[l])
+            store.acquire_device(l, ids[l], slots_d[l:l + 1])
+            store.ffn(l, xt[l], slots_d[l:l + 1], w[l], resid[l], out[l])
+
+    def timed_tokens(run):
+        for i in range(2):
+            run(xs_tok[i])
+        torch.cuda.synchronize()
+        s0 = store.stats()
+        t0 = time.time()
+        for i in range(stream_tokens):
+            run(xs_tok[2 + i])
+        torch.cuda.synchronize()
+        el = time.time() - t0
+        s1 = store.stats()
+        h_, m_ = s1["hits"] - s0["hits"], s1["misses"] - s0["misses"]
+        rd_ = s1["bytes_read"] - s0["bytes_read"]
+        return {"tok_s": stream_tokens / el, "ms_per_token": el * 1e3 / stream_tokens,
+                "hit_rate": h_ / max(1, h_ + m_), "misses_per_token": m_ / stream_tokens,
+                "host_to_hbm_gbs": rd_ / el / 1e9}
+
+    res["streaming_device"] = timed_tokens(token_dev)
+    store.check()
+    store.close()
+    # a fresh pool for the graph run, so it sees the same misses as the eager run
+    store = L.ExpertStore(n_layer, H5, F5, E, K, 1, layers, pool_bytes=pool_gib << 30, min_slots=2 * K + 2,
+                          streaming=True, device_lru=True)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        token_dev(xs_g)
+
+    def token_graph(xt):
+        for l in range(n_layer):
+            xs_g[l].copy_(xt[l])
+        graph.replay()
+
+    res["streaming_device_graph"] = timed_tokens(token_graph)
+    store.check()
+    del graph
     store.close()
     return res
 

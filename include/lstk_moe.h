@@ -80,6 +80,8 @@ typedef struct lstk_pool_stats_t {
 /* Pool flags. */
 #define LSTK_POOL_STREAMING 1 /* slots < experts: misses are copied from the pinned host tier */
 #define LSTK_POOL_DRY 2       /* bookkeeping only: no device memory, no HIP calls (CPU tests) */
+#define LSTK_POOL_DEVICE_LRU 4 /* streaming only: the slot bookkeeping lives on the device, acquires go
+                                  through lstk_pool_acquire_device */
 
 const char *lstk_last_error(void);
 int lstk_abi_version(void);
@@ -109,6 +111,21 @@ int lstk_pool_acquire(lstk_pool *pool, int layer, const int32_t *experts, int n,
 /* ExpertStore::release_all (src/expert_store.cpp:289-295). Slots released here are not overwritten
  * before the work already queued on `stream` has finished with them. */
 int lstk_pool_release_all(lstk_pool *pool, lstk_stream_t stream);
+/* ExpertStore::acquire followed by release_all (src/expert_store.cpp:232-295), run on the device for a
+ * pool created with LSTK_POOL_DEVICE_LRU, so the host never sees the router's choice (the per-layer
+ * CPU round trip of src/engine.cpp:343-392 and docs/decisions.md:14 goes away, and a forward pass over
+ * a streaming pool can be captured in a graph). d_experts [n] (device) are resolved in order with the
+ * same LRU as lstk_pool_acquire + lstk_pool_release_all: the same slots, hits and misses for the same
+ * sequence of calls. d_slots [n] (device) receives the slots; the misses are copied from the pinned
+ * host tier by a kernel reading it over PCIe. Both kernels run on `stream`: work queued on `stream`
+ * after this call sees the experts, and the slots stay valid until the next acquire_device on the pool.
+ * Calls on one pool must be ordered on one stream. n <= n_batch * n_expert_used <= 4096; every shard
+ * needs at least min(n_batch * n_expert_used, n_expert) slots (checked at creation), so a call never
+ * runs out of slots. An expert id out of range is clamped and reported by lstk_pool_check. */
+int lstk_pool_acquire_device(lstk_pool *pool, int layer, const int32_t *d_experts, int n, int32_t *d_slots,
+                             lstk_stream_t stream);
+/* For an LSTK_POOL_DEVICE_LRU pool the counters are read from the device (the call waits for the
+ * device; wait_ms stays 0). */
 int lstk_pool_stats(const lstk_pool *pool, lstk_pool_stats_t *out);
 size_t lstk_pool_total_bytes(const lstk_pool *pool);   /* ExpertStore::total_bytes */
 uint32_t lstk_pool_total_slots(const lstk_pool *pool); /* ExpertStore::total_slots */

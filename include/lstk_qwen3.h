@@ -97,7 +97,9 @@ int lstk_model_decode(lstk_model *model, int32_t seq, const int32_t *tokens, int
  *   lstk_model_decode). With a resident pool it makes no host synchronisation and no allocation, so it
  *   may be captured; a captured forward replays correctly after each prepare of the same seq,
  *   n_tokens and n_cells (n_cells changes only when the sequence crosses a multiple of 256 cells).
- *   With a streaming pool it synchronises the stream once per layer (the router's ids go to the host). */
+ *   With a streaming pool it synchronises the stream once per layer (the router's ids go to the host),
+ *   unless the pool was created with LSTK_POOL_DEVICE_LRU: then the experts are acquired on the device
+ *   (lstk_pool_acquire_device), nothing waits on the host and the forward may be captured too. */
 int lstk_model_prepare(lstk_model *model, int32_t seq, const int32_t *tokens, int n_tokens, int32_t *n_cells,
                        lstk_stream_t stream);
 int lstk_model_forward(lstk_model *model, int32_t seq, int n_tokens, int32_t n_cells, float *d_logits,

@@ -25,7 +25,7 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(HERE, "liblstk_moe.so")
 
 TYPE_F32, TYPE_F16, TYPE_Q8_0, TYPE_Q4_K = 0, 1, 8, 12
-POOL_STREAMING, POOL_DRY = 1, 2
+POOL_STREAMING, POOL_DRY, POOL_DEVICE_LRU = 1, 2, 4
 E_INVALID, E_NOMEM, E_EXHAUSTED, E_DEVICE, E_IO, E_BADID = -1, -2, -3, -4, -5, -6
 
 
@@ -80,6 +80,7 @@ SIGNATURES = {
     "lstk_pool_create": (_I, [ctypes.POINTER(MoeDims), _P, _SZ, ctypes.c_uint32, ctypes.c_uint32, ctypes.POINTER(_P)]),
     "lstk_pool_destroy": (None, [_P]),
     "lstk_pool_acquire": (_I, [_P, _I, _P, _I, _P, _P]),
+    "lstk_pool_acquire_device": (_I, [_P, _I, _P, _I, _P, _P]),
     "lstk_pool_release_all": (_I, [_P, _P]),
     "lstk_pool_stats": (_I, [_P, ctypes.POINTER(PoolStats)]),
     "lstk_pool_total_bytes": (_SZ, [_P]),
@@ -210,7 +211,7 @@ class ExpertStore:
     """
 
     def __init__(self, n_layer, n_embd, n_ff_exp, n_expert, n_expert_used, n_batch, layers, pool_bytes=0,
-                 min_slots=0, streaming=False, dry=False):
+                 min_slots=0, streaming=False, dry=False, device_lru=False):
         self.dims = MoeDims(n_layer, n_embd, n_ff_exp, n_expert, n_expert_used, n_batch)
         arr = (ExpertLayer * n_layer)()
         self._keep = []
@@ -224,7 +225,7 @@ class ExpertStore:
                     self._keep.append(a)
                     ptrs.append(a.ctypes.data)
             arr[l] = ExpertLayer(types[0], types[1], types[2], *ptrs)
-        flags = (POOL_STREAMING if streaming else 0) | (POOL_DRY if dry else 0)
+        flags = (POOL_STREAMING if streaming else 0) | (POOL_DRY if dry else 0) | (POOL_DEVICE_LRU if device_lru else 0)
         h = ctypes.c_void_p()
         _check(lib().lstk_pool_create(ctypes.byref(self.dims), ctypes.cast(arr, ctypes.c_void_p), int(pool_bytes),
                                       int(min_slots), flags, ctypes.byref(h)))
@@ -246,6 +247,12 @@ class ExpertStore:
         slots = np.zeros(e.size, np.int32)
         _check(lib().lstk_pool_acquire(self._h, layer, e.ctypes.data, e.size, slots.ctypes.data, _stream(stream)))
         return slots.reshape(np.shape(experts))
+
+    def acquire_device(self, layer, experts, slots, n=None, stream=None):
+        """Device-side acquire + release of one segment (pools made with device_lru=True): experts and
+        slots are int32 device tensors."""
+        n = experts.numel() if n is None else n
+        _check(lib().lstk_pool_acquire_device(self._h, layer, _ptr(experts), n, _ptr(slots), _stream(stream)))
 
     def release_all(self, stream=None):
         _check(lib().lstk_pool_release_all(self._h, _stream(stream)))
@@ -513,7 +520,8 @@ class GgufFile:
         return [((L.type_up, L.type_gate, L.type_down), L.host_up, L.host_gate, L.host_down) for L in arr]
 
 
-def load_qwen3_gguf(path, n_batch=64, kv_size=4096, device="cuda", pool_bytes=0, min_slots=0, streaming=False):
+def load_qwen3_gguf(path, n_batch=64, kv_size=4096, device="cuda", pool_bytes=0, min_slots=0, streaming=False,
+                    device_lru=False):
     """qwen3_load_hparams + qwen3_map_weights + the expert pool (src/qwen3.cpp:16-109,
     src/engine.cpp:31-173) from a qwen3moe GGUF: returns (hparams, ExpertStore, Qwen3Model, GgufFile).
     The experts go to the pool straight from the mapping; the dense tensors must be F16 (embedding,
@@ -542,6 +550,7 @@ def load_qwen3_gguf(path, n_batch=64, kv_size=4096, device="cuda", pool_bytes=0,
             "k_norm": dense(p + "attn_k_norm.weight", (0,), optional=True),
             "ffn_norm": dense(p + "ffn_norm.weight", (0,)), "gate_inp": dense(p + "ffn_gate_inp.weight", (0, 1))})
     store = ExpertStore(hp["n_layer"], hp["n_embd"], hp["n_ff_exp"], hp["n_expert"], hp["n_expert_used"], n_batch,
-                        experts, pool_bytes=pool_bytes, min_slots=min_slots, streaming=streaming)
+                        experts, pool_bytes=pool_bytes, min_slots=min_slots, streaming=streaming,
+                        device_lru=device_lru)
     model = Qwen3Model(hp, w, store, kv_size, n_batch, device=device)
     return hp, store, model, g

@@ -15,7 +15,7 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 ROOT = os.path.dirname(HERE)
 CSRC = os.path.join(HERE, "csrc")
 LIB = os.path.join(HERE, "liblstk_moe.so")
-SOURCES = ["kernels.hip", "grouped.hip", "fused.hip", "forward.hip", "pool.cpp", "repack.cpp", "model.cpp", "gguf.cpp"]
+SOURCES = ["kernels.hip", "grouped.hip", "fused.hip", "forward.hip", "pool.cpp", "repack.cpp", "model.cpp", "gguf.cpp", "tier.hip"]
 ARCH = os.environ.get("LSTK_OFFLOAD_ARCH", "gfx950")
 
 

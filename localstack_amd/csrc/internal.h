@@ -13,5 +13,7 @@ int set_error(int code, const std::string &msg);
 const lstk_moe_dims &pool_dims(const lstk_pool *pool);
 bool pool_streaming(const lstk_pool *pool);
 bool pool_dry(const lstk_pool *pool);
+// Whether the pool's bookkeeping lives on the device (LSTK_POOL_DEVICE_LRU).
+bool pool_device_lru(const lstk_pool *pool);
 
 }  // namespace lstk

@@ -180,6 +180,45 @@ hipError_t launch_combine(const CombineParams &p, hipStream_t s, const LaunchTim
 bool down_combine_supported(int h, int f, int k);
 hipError_t launch_down_combine(const DownCombineParams &p, hipStream_t s, const LaunchTiming *t);
 
+// streaming pool bookkeeping on the device, tier.hip
+constexpr int kTierMaxSlots = 1024;  // slots per shard (the pool's shard limit)
+constexpr int kTierMaxExperts = 256; // n_expert
+constexpr int kTierMaxIds = 4096;    // experts requested per call (n_batch * n_expert_used)
+constexpr int kTierCopyGrid = 1024;  // work-groups of a copy launch
+
+// Device copy of the streaming pool's bookkeeping: slot_of [n_layer][n_expert] (-1 = not resident);
+// per slot (all shards back to back) the LRU links and the owner; per shard {head, tail, n_in_lru, 0};
+// counters {hits, misses, bytes_read, acquires}.
+struct TierLru {
+    int32_t *slot_of, *prev, *next, *owner_layer, *owner_expert, *hdr;
+    unsigned long long *stats;
+};
+
+struct TierResolveParams {
+    TierLru lru;
+    int layer, E, shard, slot_base, n_slots;
+    unsigned long long slab; // bytes of one expert (up + gate + down)
+    const int32_t *experts;
+    int n;
+    int32_t *slots;  // [n] out
+    int32_t *miss;   // [2 * n] out: (slot, expert) of each miss
+    int32_t *n_miss; // out
+    int32_t *err;    // bit 1: expert id out of range (clamped); bit 8: shard exhausted
+};
+
+struct TierCopyParams {
+    const int32_t *miss, *n_miss;
+    int max_miss, n_slots, E;
+    const uint8_t *src[3]; // the layer's host-tier matrices (device-visible pinned memory), expert-major
+    uint8_t *dst[3];       // the shard's slot arrays
+    size_t bytes[3];       // bytes of one expert's matrix (multiples of 16)
+    int chunks[3];         // tier_copy_chunks(bytes)
+};
+
+int tier_copy_chunks(size_t bytes);
+hipError_t launch_tier_resolve(const TierResolveParams &p, hipStream_t s, const LaunchTiming *t);
+hipError_t launch_tier_copy(const TierCopyParams &p, hipStream_t s, const LaunchTiming *t);
+
 // grouped (prefill) path, grouped.hip
 #ifndef LSTK_GROUPED_CHUNK
 #define LSTK_GROUPED_CHUNK 32

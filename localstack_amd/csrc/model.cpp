@@ -10,7 +10,8 @@
 //     attention over the step's n_kv cells              (attn_kernel [+ attn_combine_kernel])
 //     o-proj + residual                                 (gemv_kernel with add)
 //     ffn_norm on the rows the FFN needs                (rmsnorm_kernel)
-//     MoE block: lstk_moe_block (resident pool) or route -> acquire -> lstk_moe_ffn (streaming pool)
+//     MoE block: lstk_moe_block (resident pool) or route -> acquire -> lstk_moe_ffn (streaming pool;
+//     the acquire runs on the device for an LSTK_POOL_DEVICE_LRU pool)
 //     the last layer runs its FFN on the output row only (src/qwen3.cpp:233-237)
 //   output_norm + head on the last row                  (rmsnorm_kernel, gemv_kernel)
 // With several tokens per step the projections are plain F16 matrix products: the normalised rows and
@@ -156,7 +157,7 @@ struct lstk_model {
     const uint16_t *tok_embd = nullptr, *output = nullptr;
     const float *output_norm = nullptr;
     lstk_pool *pool = nullptr;
-    bool streaming = false;
+    bool streaming = false, device_lru = false;
     int n_batch = 0;
     float theta_scale = 0.0f;
     KvBook kv;
@@ -254,6 +255,7 @@ int create(const lstk_qwen3_hparams *hpp, const lstk_qwen3_weights *w, lstk_pool
     M->output_norm = w->output_norm;
     M->pool = pool;
     M->streaming = lstk::pool_streaming(pool);
+    M->device_lru = lstk::pool_device_lru(pool);
     M->n_batch = (int) n_batch;
     M->theta_scale = powf(hp.rope_freq_base, -2.0f / (float) hp.head_dim);
     M->kv.init(kv_size);
@@ -372,10 +374,16 @@ int moe(lstk_model *M, int l, int rows, float *xr, int32_t *ids, hipStream_t st)
     if (!M->streaming)
         return lstk_moe_block(M->pool, l, M->hn, L.gate_inp, L.gate_inp_type, xr, xr, ids, M->weights, rows, st);
     // Engine::run_segment (src/engine.cpp:343-392): the host sees the router's choice, acquires the
-    // experts (misses are copied on the pool's side stream) and the experts run on their slots.
+    // experts (misses are copied on the pool's side streams) and the experts run on their slots.
+    // With the bookkeeping on the device the same acquire runs as two kernels on `st` instead, and
+    // the host never waits.
     const int k = M->hp.n_expert_used;
     int rc = lstk_moe_route(M->pool, l, M->hn, rows, L.gate_inp, L.gate_inp_type, ids, M->weights, st);
     if (rc != LSTK_OK) return rc;
+    if (M->device_lru) {
+        if ((rc = lstk_pool_acquire_device(M->pool, l, ids, rows * k, M->slots, st)) != LSTK_OK) return rc;
+        return lstk_moe_ffn(M->pool, l, M->hn, M->slots, M->weights, xr, xr, rows, st);
+    }
     hipError_t e;
     if ((e = hipMemcpyAsync(M->h_ids, ids, (size_t) rows * k * 4, hipMemcpyDeviceToHost, st)) != hipSuccess ||
         (e = hipStreamSynchronize(st)) != hipSuccess)
@@ -411,7 +419,8 @@ int prepare(lstk_model *M, int32_t seq, const int32_t *tokens, int T, int *n_cel
 }
 
 // The kernels of one step (qwen3_build_graph, src/qwen3.cpp:223-259) over the inputs prepare() uploaded.
-// With a resident pool this makes no host synchronisation, so a caller may capture it in a HIP graph.
+// With a resident pool (or a streaming pool that acquires on the device) this makes no host
+// synchronisation, so a caller may capture it in a HIP graph.
 int forward(lstk_model *M, int32_t seq, int T, int n_cells, float *d_logits, int32_t *d_trace, hipStream_t st) {
     const lstk_qwen3_hparams &hp = M->hp;
     const int nb = M->n_batch, h = hp.n_embd, hd = hp.head_dim, k = hp.n_expert_used;

@@ -51,6 +51,7 @@ int hip_fail(hipError_t e, const char *what) {
 }
 
 constexpr uint32_t kMaxSlotsPerShard = 1024; // kMaxSlotsPerPool, src/expert_store.h:80
+static_assert(kMaxSlotsPerShard <= (uint32_t) lstk::kTierMaxSlots, "the device-side acquire stages a shard in LDS");
 
 const char *type_name(int t) {
     switch (t) {
@@ -130,6 +131,14 @@ struct lstk_pool {
     hipStream_t side[kSides] = {};
     hipEvent_t copy_done[kSides] = {}, release_ev = nullptr;
     int fail_copies = 0;
+    // LSTK_POOL_DEVICE_LRU: the bookkeeping lives on the device (tier.hip); the host copy above
+    // only holds the initial state
+    bool device_lru = false;
+    void *dlru_mem = nullptr;
+    lstk::TierLru dlru{};
+    std::vector<int> slot_base;   // per shard: first slot in the device LRU arrays
+    int32_t *d_miss = nullptr, *d_n_miss = nullptr;
+    std::vector<std::array<const uint8_t *, 3>> tier_dev; // per layer: device-visible host-tier matrices
     lstk_pool_stats_t stats{};
     // scratch
     void *scratch = nullptr;
@@ -248,6 +257,7 @@ void destroy(lstk_pool *P) {
             if (P->side[i]) (void) hipStreamDestroy(P->side[i]);
         }
         if (P->release_ev) (void) hipEventDestroy(P->release_ev);
+        if (P->dlru_mem) (void) hipFree(P->dlru_mem);
         for (auto &v : P->launched)
             for (TimedLaunch &t : v) {
                 (void) hipEventDestroy(t.start);
@@ -299,6 +309,64 @@ int plan_streaming(lstk_pool *P, size_t pool_bytes, uint32_t min_slots) {
     return LSTK_OK;
 }
 
+// Uploads the streaming pool's bookkeeping (all slots free, in LRU order) for the device-side acquire,
+// and maps the host tier into the device's address space.
+int init_device_lru(lstk_pool *P) {
+    const lstk_moe_dims &d = P->dims;
+    size_t n_slots = 0;
+    for (const Shard &s : P->shards) {
+        P->slot_base.push_back((int) n_slots);
+        n_slots += s.n_slots;
+    }
+    const size_t n_map = (size_t) d.n_layer * d.n_expert, n_sh = P->shards.size(), n_ids = (size_t) d.n_batch * d.n_expert_used;
+    size_t off = 0;
+    auto take = [&](size_t bytes) {
+        const size_t o = off;
+        off = align_up(off + bytes, 256);
+        return o;
+    };
+    const size_t o_map = take(n_map * 4), o_prev = take(n_slots * 4), o_next = take(n_slots * 4), o_ol = take(n_slots * 4),
+                 o_oe = take(n_slots * 4), o_hdr = take(n_sh * 16), o_stats = take(4 * 8), o_miss = take(n_ids * 8),
+                 o_nmiss = take(16);
+    hipError_t e = hipMalloc(&P->dlru_mem, off);
+    if (e != hipSuccess) return hip_fail(e, "hipMalloc(device LRU)");
+    std::vector<uint8_t> init(off, 0);
+    auto put = [&](size_t o, const int32_t *v, size_t n) { std::memcpy(init.data() + o, v, n * 4); };
+    put(o_map, P->slot_of.data(), n_map);
+    std::vector<int32_t> hdr(n_sh * 4, 0);
+    for (size_t i = 0; i < n_sh; i++) {
+        const Shard &s = P->shards[i];
+        const size_t b = (size_t) P->slot_base[i];
+        put(o_prev + b * 4, s.prev.data(), s.n_slots);
+        put(o_next + b * 4, s.next.data(), s.n_slots);
+        put(o_ol + b * 4, s.owner_layer.data(), s.n_slots);
+        put(o_oe + b * 4, s.owner_expert.data(), s.n_slots);
+        hdr[i * 4 + 0] = s.lru_head;
+        hdr[i * 4 + 1] = s.lru_tail;
+        hdr[i * 4 + 2] = (int32_t) s.n_in_lru;
+    }
+    put(o_hdr, hdr.data(), hdr.size());
+    if ((e = hipMemcpy(P->dlru_mem, init.data(), off, hipMemcpyHostToDevice)) != hipSuccess)
+        return hip_fail(e, "device LRU upload");
+    uint8_t *b = static_cast<uint8_t *>(P->dlru_mem);
+    P->dlru.slot_of = reinterpret_cast<int32_t *>(b + o_map);
+    P->dlru.prev = reinterpret_cast<int32_t *>(b + o_prev);
+    P->dlru.next = reinterpret_cast<int32_t *>(b + o_next);
+    P->dlru.owner_layer = reinterpret_cast<int32_t *>(b + o_ol);
+    P->dlru.owner_expert = reinterpret_cast<int32_t *>(b + o_oe);
+    P->dlru.hdr = reinterpret_cast<int32_t *>(b + o_hdr);
+    P->dlru.stats = reinterpret_cast<unsigned long long *>(b + o_stats);
+    P->d_miss = reinterpret_cast<int32_t *>(b + o_miss);
+    P->d_n_miss = reinterpret_cast<int32_t *>(b + o_nmiss);
+    void *tier_dev = nullptr;
+    if ((e = hipHostGetDevicePointer(&tier_dev, P->tier, 0)) != hipSuccess) return hip_fail(e, "hipHostGetDevicePointer(host tier)");
+    const ptrdiff_t shift = static_cast<uint8_t *>(tier_dev) - P->tier;
+    P->tier_dev.resize(d.n_layer);
+    for (int l = 0; l < d.n_layer; l++)
+        for (int m = 0; m < 3; m++) P->tier_dev[l][m] = P->tier_of[l][m] + shift;
+    return LSTK_OK;
+}
+
 int create(const lstk_moe_dims *dims, const lstk_expert_layer *layers, size_t pool_bytes, uint32_t min_slots,
            uint32_t flags, lstk_pool **out) {
     if (!dims || !layers || !out) return fail(LSTK_E_INVALID, "null argument");
@@ -309,6 +377,11 @@ int create(const lstk_moe_dims *dims, const lstk_expert_layer *layers, size_t po
     P->dims = d;
     P->streaming = (flags & LSTK_POOL_STREAMING) != 0;
     P->dry = (flags & LSTK_POOL_DRY) != 0;
+    P->device_lru = (flags & LSTK_POOL_DEVICE_LRU) != 0;
+    if (P->device_lru && (!P->streaming || P->dry)) {
+        destroy(P);
+        return fail(LSTK_E_INVALID, "LSTK_POOL_DEVICE_LRU needs a streaming pool with device memory (not LSTK_POOL_DRY)");
+    }
     P->layer_shard.assign(d.n_layer, -1);
     P->types.resize(d.n_layer);
     for (int l = 0; l < d.n_layer; l++) {
@@ -329,7 +402,7 @@ int create(const lstk_moe_dims *dims, const lstk_expert_layer *layers, size_t po
             return fail(LSTK_E_INVALID, "layer " + std::to_string(l) + ": missing expert bytes");
         }
     }
-    int rc;
+    int rc = LSTK_OK;
     if (P->streaming) {
         rc = plan_streaming(P, pool_bytes, min_slots);
         if (rc != LSTK_OK) {
@@ -358,6 +431,28 @@ int create(const lstk_moe_dims *dims, const lstk_expert_layer *layers, size_t po
     if (bad[0]) {
         destroy(P);
         return fail(LSTK_E_INVALID, bad);
+    }
+    if (P->device_lru) {
+        const int ids = d.n_batch * d.n_expert_used;
+        if (ids > lstk::kTierMaxIds)
+            rc = fail(LSTK_E_INVALID, "LSTK_POOL_DEVICE_LRU: n_batch * n_expert_used must be at most " +
+                                          std::to_string(lstk::kTierMaxIds));
+        // one call pins at most min(n_batch * k, n_expert) distinct experts, so a shard of that many
+        // slots never runs out inside the device-side acquire
+        const int need = std::min(ids, d.n_expert);
+        for (const Shard &s : P->shards) {
+            if (rc != LSTK_OK) break;
+            if ((int) s.n_slots < need)
+                rc = fail(LSTK_E_INVALID, "LSTK_POOL_DEVICE_LRU: every shard needs at least min(n_batch * n_expert_used, "
+                                          "n_expert) = " + std::to_string(need) + " slots (a shard has " +
+                                              std::to_string(s.n_slots) + "); raise the pool size or lower n_batch");
+            else if (s.up_bytes % 16 || s.gate_bytes % 16 || s.down_bytes % 16)
+                rc = fail(LSTK_E_INVALID, "LSTK_POOL_DEVICE_LRU: expert matrices must be multiples of 16 bytes");
+        }
+        if (rc != LSTK_OK) {
+            destroy(P);
+            return rc;
+        }
     }
     if (P->dry) {
         *out = P;
@@ -452,7 +547,7 @@ int create(const lstk_moe_dims *dims, const lstk_expert_layer *layers, size_t po
             }
         }
     }
-    if ((rc = alloc_scratch(P)) != LSTK_OK) {
+    if ((rc = alloc_scratch(P)) != LSTK_OK || (P->device_lru && (rc = init_device_lru(P)) != LSTK_OK)) {
         destroy(P);
         return rc;
     }
@@ -490,6 +585,7 @@ int acquire(lstk_pool *P, int layer, const int32_t *experts, int n, int32_t *slo
     for (int i = 0; i < n; i++)
         if (experts[i] < 0 || experts[i] >= d.n_expert)
             return fail(LSTK_E_INVALID, "acquire: expert id " + std::to_string(experts[i]) + " out of range");
+    if (P->device_lru) return fail(LSTK_E_INVALID, "this pool keeps its bookkeeping on the device: use lstk_pool_acquire_device");
     const auto t0 = std::chrono::steady_clock::now();
     P->stats.acquires++;
     if (!P->streaming) {
@@ -573,6 +669,55 @@ int release_all(lstk_pool *P, hipStream_t stream) {
     return LSTK_OK;
 }
 
+bool aligned(const void *p, size_t a) { return (reinterpret_cast<uintptr_t>(p) % a) == 0; }
+
+// ExpertStore::acquire + release_all of one segment on the device (tier.hip): resolve, then copy the
+// misses from the host tier. Nothing waits on the host.
+int acquire_device(lstk_pool *P, int layer, const int32_t *d_experts, int n, int32_t *d_slots, hipStream_t st) {
+    const lstk_moe_dims &d = P->dims;
+    if (!P->device_lru) return fail(LSTK_E_INVALID, "lstk_pool_acquire_device needs a pool created with LSTK_POOL_DEVICE_LRU");
+    if (layer < 0 || layer >= d.n_layer) return fail(LSTK_E_INVALID, "acquire_device: bad layer");
+    if (n < 0 || n > d.n_batch * d.n_expert_used)
+        return fail(LSTK_E_INVALID, "acquire_device: n must be in [0, n_batch * n_expert_used]");
+    if (n == 0) return LSTK_OK;
+    if (!d_experts || !d_slots || !aligned(d_experts, 4) || !aligned(d_slots, 4))
+        return fail(LSTK_E_INVALID, "acquire_device: experts and slots must be non-null device arrays");
+    const int sh = P->layer_shard[layer];
+    const Shard &s = P->shards[sh];
+    lstk::TierResolveParams rp{};
+    rp.lru = P->dlru;
+    rp.layer = layer;
+    rp.E = d.n_expert;
+    rp.shard = sh;
+    rp.slot_base = P->slot_base[sh];
+    rp.n_slots = (int) s.n_slots;
+    rp.slab = s.slab;
+    rp.experts = d_experts;
+    rp.n = n;
+    rp.slots = d_slots;
+    rp.miss = P->d_miss;
+    rp.n_miss = P->d_n_miss;
+    rp.err = P->err;
+    hipError_t e = lstk::launch_tier_resolve(rp, st, nullptr);
+    if (e != hipSuccess) return hip_fail(e, "tier resolve launch");
+    lstk::TierCopyParams cp{};
+    cp.miss = P->d_miss;
+    cp.n_miss = P->d_n_miss;
+    cp.max_miss = n;
+    cp.n_slots = (int) s.n_slots;
+    cp.E = d.n_expert;
+    const size_t b[3] = {s.up_bytes, s.gate_bytes, s.down_bytes};
+    uint8_t *dst[3] = {s.d_up, s.d_gate, s.d_down};
+    for (int m = 0; m < 3; m++) {
+        cp.src[m] = P->tier_dev[layer][m];
+        cp.dst[m] = dst[m];
+        cp.bytes[m] = b[m];
+        cp.chunks[m] = lstk::tier_copy_chunks(b[m]);
+    }
+    e = lstk::launch_tier_copy(cp, st, nullptr);
+    return e == hipSuccess ? LSTK_OK : hip_fail(e, "tier copy launch");
+}
+
 // Runs one launch; with timing on, the launch records its own start/stop timestamps.
 template <typename F>
 hipError_t timed(lstk_pool *P, int stage, F &&launch) {
@@ -589,7 +734,6 @@ hipError_t timed(lstk_pool *P, int stage, F &&launch) {
     return le;
 }
 
-bool aligned(const void *p, size_t a) { return (reinterpret_cast<uintptr_t>(p) % a) == 0; }
 
 int check_call(lstk_pool *P, int layer, int T) {
     if (!P) return fail(LSTK_E_INVALID, "null pool");
@@ -837,6 +981,7 @@ int set_error(int code, const std::string &msg) { return fail(code, msg); }
 const lstk_moe_dims &pool_dims(const lstk_pool *pool) { return pool->dims; }
 bool pool_streaming(const lstk_pool *pool) { return pool->streaming; }
 bool pool_dry(const lstk_pool *pool) { return pool->dry; }
+bool pool_device_lru(const lstk_pool *pool) { return pool->device_lru; }
 }  // namespace lstk
 
 extern "C" {
@@ -860,6 +1005,12 @@ int lstk_pool_acquire(lstk_pool *pool, int layer, const int32_t *experts, int n,
     return acquire(pool, layer, experts, n, slots, static_cast<hipStream_t>(stream));
 }
 
+int lstk_pool_acquire_device(lstk_pool *pool, int layer, const int32_t *d_experts, int n, int32_t *d_slots,
+                             lstk_stream_t stream) {
+    if (!pool) return fail(LSTK_E_INVALID, "null pool");
+    return acquire_device(pool, layer, d_experts, n, d_slots, static_cast<hipStream_t>(stream));
+}
+
 int lstk_pool_release_all(lstk_pool *pool, lstk_stream_t stream) {
     if (!pool) return fail(LSTK_E_INVALID, "null pool");
     return release_all(pool, static_cast<hipStream_t>(stream));
@@ -868,6 +1019,15 @@ int lstk_pool_release_all(lstk_pool *pool, lstk_stream_t stream) {
 int lstk_pool_stats(const lstk_pool *pool, lstk_pool_stats_t *out) {
     if (!pool || !out) return fail(LSTK_E_INVALID, "null argument");
     *out = pool->stats;
+    if (pool->device_lru) {
+        unsigned long long c[4];
+        const hipError_t e = hipMemcpy(c, pool->dlru.stats, sizeof(c), hipMemcpyDeviceToHost);
+        if (e != hipSuccess) return hip_fail(e, "device LRU counters");
+        out->hits = c[0];
+        out->misses = c[1];
+        out->bytes_read = c[2];
+        out->acquires = c[3];
+    }
     return LSTK_OK;
 }
 
@@ -987,6 +1147,7 @@ int lstk_pool_check(lstk_pool *pool, lstk_stream_t stream) {
         if (flag & 1) msg += " an expert/slot id out of range (clamped)";
         if (flag & 2) msg += std::string(flag & 1 ? " and" : "") + " an expert repeated within one token";
         if (flag & 4) msg += std::string(flag & 3 ? " and" : "") + " a fused stage that timed out waiting for another work-group";
+        if (flag & 8) msg += std::string(flag & 7 ? " and" : "") + " a device-side acquire with no free slot";
         return fail(LSTK_E_BADID, msg);
     }
     return LSTK_OK;
@@ -1040,6 +1201,7 @@ int lstk_unpack_matrix(int type, int rows, int cols, const void *packed, void *g
 // Test hook: makes the next n host-tier copies fail, to exercise the LSTK_E_IO path.
 int lstk_pool_debug_fail_copies(lstk_pool *pool, int n) {
     if (!pool) return fail(LSTK_E_INVALID, "null pool");
+    if (pool->device_lru) return fail(LSTK_E_INVALID, "copy failures cannot be injected into device-side acquires");
     pool->fail_copies = n;
     return LSTK_OK;
 }

@@ -49,10 +49,11 @@ def weights(name):
     return _w[name]
 
 
-def build(lstk, dev, hp, w, n_batch=64, kv_size=1024, streaming=False, pool_bytes=0, min_slots=0):
+def build(lstk, dev, hp, w, n_batch=64, kv_size=1024, streaming=False, pool_bytes=0, min_slots=0, device_lru=False):
     layers = [(L["types"], L["up"], L["gate"], L["down"]) for L in w["layers"]]
     store = lstk.ExpertStore(hp["n_layer"], hp["n_embd"], hp["n_ff_exp"], hp["n_expert"], hp["n_expert_used"], n_batch,
-                             layers, pool_bytes=pool_bytes, min_slots=min_slots, streaming=streaming)
+                             layers, pool_bytes=pool_bytes, min_slots=min_slots, streaming=streaming,
+                             device_lru=device_lru)
     return store, lstk.Qwen3Model(hp, w, store, kv_size, n_batch, device=dev)
 
 
@@ -157,6 +158,63 @@ def test_streaming_pool_matches_resident(lstk, dev):
     s = store.stats()
     print(f"[streaming tiny] {s}", flush=True)
     assert s["misses"] > 8  # the two layers share 8 slots, so experts were copied in again
+
+
+def test_device_lru_streaming_matches_resident(lstk, dev):
+    """A streaming pool that acquires on the device decodes exactly like the resident pool and counts
+    the same hits and misses as the host-side acquire."""
+    hp, w = weights("tiny")
+    _, res = build(lstk, dev, hp, w)
+    slab = 3 * 512 * 256 // 32 * 34
+    hstore, hm = build(lstk, dev, hp, w, streaming=True, pool_bytes=8 * slab, min_slots=8)
+    dstore, dm = build(lstk, dev, hp, w, streaming=True, pool_bytes=8 * slab, min_slots=8, device_lru=True)
+    feed = prompt(5, 16, 1024)  # a prompt whose experts overflow the 8 slots the two layers share
+    for step in range(9):
+        a, ta = run(res, 0, feed, hp, dev)
+        b, tb = run(hm, 0, feed, hp, dev)
+        c, tc = run(dm, 0, feed, hp, dev)
+        np.testing.assert_array_equal(a, c)
+        np.testing.assert_array_equal(ta, tc)
+        np.testing.assert_array_equal(b, c)
+        feed = np.array([np.argmax(a)], np.int32)
+    hs, ds = hstore.stats(), dstore.stats()
+    print(f"[device lru tiny] host {hs} device {ds}", flush=True)
+    for key in ("hits", "misses", "bytes_read", "acquires"):
+        assert hs[key] == ds[key], key
+    assert ds["misses"] > 8
+
+
+def test_graph_replay_device_lru_streaming(lstk, dev):
+    """With the acquire on the device a streaming forward can be captured: every replay (misses copied
+    by the captured kernels) equals the eager resident step."""
+    import torch
+    hp, w = weights("tiny")
+    _, eager = build(lstk, dev, hp, w)
+    slab = 3 * 512 * 256 // 32 * 34
+    store, gm = build(lstk, dev, hp, w, streaming=True, pool_bytes=8 * slab, min_slots=8, device_lru=True)
+    toks = prompt(25, 16, hp["n_vocab"])
+    a, _ = run(eager, 0, toks, hp, dev)
+    b, _ = run(gm, 0, toks, hp, dev)
+    np.testing.assert_array_equal(a, b)
+    feed = np.array([np.argmax(a)], np.int32)
+    stream = torch.cuda.Stream()
+    logits = torch.zeros(hp["n_vocab"], dtype=torch.float32, device=dev)
+    graph = None
+    m0 = store.stats()["misses"]
+    for step in range(6):
+        ea, _ = run(eager, 0, feed, hp, dev)
+        with torch.cuda.stream(stream):
+            n = gm.prepare(0, feed, stream=stream)
+            if graph is None:
+                graph = torch.cuda.CUDAGraph()
+                with torch.cuda.graph(graph, stream=stream):
+                    gm.forward(0, 1, n, logits=logits, stream=stream)
+            graph.replay()
+        torch.cuda.synchronize()
+        np.testing.assert_array_equal(logits.cpu().numpy(), ea, err_msg=f"replay {step}")
+        feed = np.array([np.argmax(ea)], np.int32)
+    store.check()
+    assert store.stats()["misses"] > m0  # the replays evicted and copied experts in
 
 
 def test_long_context_splits_attention(lstk, dev):
