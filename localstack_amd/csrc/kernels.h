@@ -184,7 +184,10 @@ hipError_t launch_down_combine(const DownCombineParams &p, hipStream_t s, const 
 constexpr int kTierMaxSlots = 1024;  // slots per shard (the pool's shard limit)
 constexpr int kTierMaxExperts = 256; // n_expert
 constexpr int kTierMaxIds = 4096;    // experts requested per call (n_batch * n_expert_used)
-constexpr int kTierCopyGrid = 1024;  // work-groups of a copy launch
+#ifndef LSTK_TIER_COPY_GRID
+#define LSTK_TIER_COPY_GRID 256
+#endif
+constexpr int kTierCopyGrid = LSTK_TIER_COPY_GRID; // work-groups of a copy launch (64-512 all reach the same PCIe rate; 1024 and more lose 3-6%)
 
 // Device copy of the streaming pool's bookkeeping: slot_of [n_layer][n_expert] (-1 = not resident);
 // per slot (all shards back to back) the LRU links and the owner; per shard {head, tail, n_in_lru, 0};

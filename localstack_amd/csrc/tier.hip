@@ -18,9 +18,12 @@
 namespace lstk {
 namespace {
 
+#ifndef LSTK_TIER_COPY_VEC
+#define LSTK_TIER_COPY_VEC 4
+#endif
 constexpr int kCopyThreads = 256;
-constexpr int kCopyVec = 4;                                 // 16-byte vectors per thread per chunk
-constexpr int kCopyChunk = kCopyThreads * kCopyVec * 16;    // 16 KiB
+constexpr int kCopyVec = LSTK_TIER_COPY_VEC;                // 16-byte vectors per thread per chunk
+constexpr int kCopyChunk = kCopyThreads * kCopyVec * 16;    // 16 KiB at 4 vectors
 
 __global__ __launch_bounds__(256) void lru_resolve_kernel(TierResolveParams P) {
     __shared__ int32_t prv[kTierMaxSlots], nxt[kTierMaxSlots], own_l[kTierMaxSlots], own_e[kTierMaxSlots],
