@@ -25,33 +25,6 @@ struct NormParams {
     uint16_t *y16; // when set, also y rounded to fp16 (the input of an F16 matrix product)
 };
 
-// One F16 weight matrix of a GEMV launch: y[t * ldy + r] = sum_i fp16(x[t][i]) * w[r][i] (+ add[t * ldy + r]).
-struct GemvSeg {
-    const uint16_t *w;
-    float *y;
-    const float *add;
-    int rows;
-    int ldy;
-};
-
-// Up to three matrices with the same input (Q, K and V) in one launch; rows of the segments are
-// numbered one after the other. For a single token (T == 1) the input row may be normalised on the way
-// in: with norm_w set, x is replaced by rms_norm(x) * norm_w (the reference's attn_norm before Q/K/V),
-// and with emb set, x is first gathered from the F16 embedding row tokens[0] and written to x_out.
-struct GemvParams {
-    GemvSeg seg[3];
-    int nseg;
-    int rows_total;
-    int cols;
-    const float *x; // [T][cols]
-    int T;
-    const float *norm_w;
-    float eps;
-    const uint16_t *emb;
-    const int32_t *tokens;
-    float *x_out;
-};
-
 // Per-head RMSNorm (optional), NEOX RoPE and the KV-cache store of one step.
 // The cache layouts are the operand fragments of the attention's matrix-core products (16 x 16 x 16
 // fp16): K [n_head_kv][head_dim / 4][kv_size][4] (4 consecutive dims of a cell, 16 cells side by side)
@@ -68,6 +41,41 @@ struct RopeParams {
     float theta_scale; // freq_base^(-2 / hd)
     float *q_out;      // [T][n_head][hd]
     uint16_t *kc, *vc; // this layer's caches
+};
+
+// One F16 weight matrix of a GEMV launch: y[t * ldy + r] = sum_i fp16(x[t][i]) * w[r][i] (+ add[t * ldy + r]).
+struct GemvSeg {
+    const uint16_t *w;
+    float *y;
+    const float *add;
+    int rows;
+    int ldy;
+};
+
+// Up to three matrices with the same input (Q, K and V) in one launch; rows of the segments are
+// numbered one after the other. For a single token (T == 1) the input row may be normalised on the way
+// in: with norm_w set, x is replaced by rms_norm(x) * norm_w (the reference's attn_norm before Q/K/V),
+// and with emb set, x is first gathered from the F16 embedding row tokens[0] and written to x_out.
+//
+// A single-token Q/K/V launch may also finish the RoPE step in its last work-groups (fuse = 1): the
+// last of the work-groups that produce one head's rows (counted in cnt[head], n_head + 2 n_head_kv
+// slots that are zero before the launch and zero again after it) runs rope_kernel's work for that
+// head - QK-norm, RoPE and the K / V cache store - reading the rows back with device-coherent loads.
+struct GemvParams {
+    GemvSeg seg[3];
+    int nseg;
+    int rows_total;
+    int cols;
+    const float *x; // [T][cols]
+    int T;
+    const float *norm_w;
+    float eps;
+    const uint16_t *emb;
+    const int32_t *tokens;
+    float *x_out;
+    int fuse;
+    int *cnt;
+    RopeParams rope;
 };
 
 // Causal attention of one step over cells [0, n_cells) of one layer's cache. The query rows of a KV head

@@ -74,6 +74,77 @@ __global__ __launch_bounds__(kNormBlock) void rmsnorm_kernel(NormParams P) {
     }
 }
 
+
+
+// ------------------------------------------------------------------------------------------------
+// QK-norm + NEOX RoPE + KV store: one wavefront per (token, head) of Q, K and V
+// ------------------------------------------------------------------------------------------------
+
+__device__ __forceinline__ size_t k_index(int head, int d, int cell, int hd, int kv_size) {
+    return (((size_t) head * (hd / 4) + d / 4) * kv_size + cell) * 4 + (d & 3);
+}
+__device__ __forceinline__ size_t v_index(int head, int d, int cell, int hd, int kv_size) {
+    return (((size_t) head * (kv_size / 4) + cell / 4) * hd + d) * 4 + (cell & 3);
+}
+
+// Head j (Q heads, then K heads, then V heads) of token t by one wavefront (lanes = threadIdx.x % 64).
+// COH: q / k / v were written in this launch by other work-groups (device-coherent loads).
+template <bool COH>
+__device__ __forceinline__ void rope_head(const RopeParams &P, int t, int j) {
+    const int lane = threadIdx.x & (kWave - 1);
+    const int hd = P.hd, half = hd / 2;
+    auto ld = [](const float *a) { return COH ? ld_dev(a) : *a; };
+    const int cell = P.cells[t];
+    if (j == 0 && lane == 0) {
+        P.cell_seq[cell] = P.seq;
+        P.cell_pos[cell] = P.pos[t];
+    }
+    if (j >= P.n_head + P.n_kv) {
+        const int head = j - P.n_head - P.n_kv;
+        const float *src = P.v + ((size_t) t * P.n_kv + head) * hd;
+        for (int d = lane; d < hd; d += kWave) P.vc[v_index(head, d, cell, hd, P.kv_size)] = f2h(ld(src + d));
+        return;
+    }
+    const bool is_q = j < P.n_head;
+    const int head = is_q ? j : j - P.n_head;
+    const float *src = is_q ? P.q + ((size_t) t * P.n_head + head) * hd : P.k + ((size_t) t * P.n_kv + head) * hd;
+    const float *nw = is_q ? P.q_norm : P.k_norm;
+    float scale = 1.0f;
+    if (nw) {
+        double s = 0.0;
+        for (int d = lane; d < hd; d += kWave) {
+            const float v = ld(src + d);
+            s += (double) (v * v);
+        }
+        s = wave_sum_d(s);
+        const float mean = (float) (s / (double) hd);
+        scale = 1.0f / sqrtf(mean + P.eps);
+    }
+    const float p = (float) P.pos[t];
+    for (int i = lane; i < half; i += kWave) {
+        float x0 = ld(src + i), x1 = ld(src + i + half);
+        if (nw) {
+            x0 = (x0 * scale) * nw[i];
+            x1 = (x1 * scale) * nw[i + half];
+        }
+        float theta = p;
+        for (int s = 0; s < i; s++) theta *= P.theta_scale;
+        const float c = cosf(theta), sn = sinf(theta);
+        const float y0 = x0 * c - x1 * sn;
+        const float y1 = x0 * sn + x1 * c;
+        if (is_q) {
+            float *dst = P.q_out + ((size_t) t * P.n_head + head) * hd;
+            dst[i] = y0;
+            dst[i + half] = y1;
+        } else {
+            P.kc[k_index(head, i, cell, hd, P.kv_size)] = f2h(y0);
+            P.kc[k_index(head, i + half, cell, hd, P.kv_size)] = f2h(y1);
+        }
+    }
+}
+
+__global__ __launch_bounds__(kWave) void rope_kernel(RopeParams P) { rope_head<false>(P, blockIdx.x, blockIdx.y); }
+
 // ------------------------------------------------------------------------------------------------
 // F16 GEMV over up to 3 matrices: each wavefront owns kGvRows rows, lanes stride the row in 16-byte
 // chunks (a 1 KiB coalesced load per row per step), the TG tokens of a group sit in LDS as fp16 pairs
@@ -256,71 +327,30 @@ __global__ __launch_bounds__(kGvWaves *kWave) void gemv1_kernel(GemvParams P) {
 #pragma unroll
     for (int rr = 0; rr < RW; rr++) {
         const float sum = wave_sum_tree(acc[rr]);
-        if (lane == 0 && on[rr]) yr[rr][0] = ar[rr] ? sum + ar[rr][0] : sum;
-    }
-}
-
-// ------------------------------------------------------------------------------------------------
-// QK-norm + NEOX RoPE + KV store: one wavefront per (token, head) of Q, K and V
-// ------------------------------------------------------------------------------------------------
-
-__device__ __forceinline__ size_t k_index(int head, int d, int cell, int hd, int kv_size) {
-    return (((size_t) head * (hd / 4) + d / 4) * kv_size + cell) * 4 + (d & 3);
-}
-__device__ __forceinline__ size_t v_index(int head, int d, int cell, int hd, int kv_size) {
-    return (((size_t) head * (kv_size / 4) + cell / 4) * hd + d) * 4 + (cell & 3);
-}
-
-__global__ __launch_bounds__(kWave) void rope_kernel(RopeParams P) {
-    const int t = blockIdx.x, j = blockIdx.y, lane = threadIdx.x;
-    const int hd = P.hd, half = hd / 2;
-    const int cell = P.cells[t];
-    if (j == 0 && lane == 0) {
-        P.cell_seq[cell] = P.seq;
-        P.cell_pos[cell] = P.pos[t];
-    }
-    if (j >= P.n_head + P.n_kv) {
-        const int head = j - P.n_head - P.n_kv;
-        const float *src = P.v + ((size_t) t * P.n_kv + head) * hd;
-        for (int d = lane; d < hd; d += kWave) P.vc[v_index(head, d, cell, hd, P.kv_size)] = f2h(src[d]);
-        return;
-    }
-    const bool is_q = j < P.n_head;
-    const int head = is_q ? j : j - P.n_head;
-    const float *src = is_q ? P.q + ((size_t) t * P.n_head + head) * hd : P.k + ((size_t) t * P.n_kv + head) * hd;
-    const float *nw = is_q ? P.q_norm : P.k_norm;
-    float scale = 1.0f;
-    if (nw) {
-        double s = 0.0;
-        for (int d = lane; d < hd; d += kWave) {
-            const float v = src[d];
-            s += (double) (v * v);
-        }
-        s = wave_sum_d(s);
-        const float mean = (float) (s / (double) hd);
-        scale = 1.0f / sqrtf(mean + P.eps);
-    }
-    const float p = (float) P.pos[t];
-    for (int i = lane; i < half; i += kWave) {
-        float x0 = src[i], x1 = src[i + half];
-        if (nw) {
-            x0 = (x0 * scale) * nw[i];
-            x1 = (x1 * scale) * nw[i + half];
-        }
-        float theta = p;
-        for (int s = 0; s < i; s++) theta *= P.theta_scale;
-        const float c = cosf(theta), sn = sinf(theta);
-        const float y0 = x0 * c - x1 * sn;
-        const float y1 = x0 * sn + x1 * c;
-        if (is_q) {
-            float *dst = P.q_out + ((size_t) t * P.n_head + head) * hd;
-            dst[i] = y0;
-            dst[i + half] = y1;
-        } else {
-            P.kc[k_index(head, i, cell, hd, P.kv_size)] = f2h(y0);
-            P.kc[k_index(head, i + half, cell, hd, P.kv_size)] = f2h(y1);
+        if (lane == 0 && on[rr]) {
+            const float y = ar[rr] ? sum + ar[rr][0] : sum;
+            if (P.fuse) st_dev(yr[rr], y);
+            else yr[rr][0] = y;
         }
     }
+    if (!P.fuse) return;
+    // The work-groups that produced the rows the fused step reads count themselves in once their
+    // device-coherent stores have completed; the one that brings the count to n_in runs the step,
+    // reading those rows with device-coherent loads (no cache flush or invalidation is needed, and
+    // nothing waits for another work-group).
+    __shared__ int s_last;
+    const int per_wg = kGvWaves * RW;
+    const int slot = blockIdx.x * per_wg / P.rope.hd, n_in = P.rope.hd / per_wg;
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();
+    if (tid == 0) {
+        const int old = __hip_atomic_fetch_add(P.cnt + slot, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        s_last = old == n_in - 1;
+        if (s_last) __hip_atomic_store(P.cnt + slot, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    __syncthreads();
+    if (!s_last) return;
+    if (wv == 0) rope_head<true>(P.rope, 0, slot);
 }
 
 // ------------------------------------------------------------------------------------------------
@@ -642,6 +672,13 @@ hipError_t launch_gemv1_t(const GemvParams &P, hipStream_t st, const LaunchTimin
 
 hipError_t launch_gemv(const GemvParams &P, hipStream_t st, const LaunchTiming *tm) {
     if (P.T == 0 || P.rows_total == 0) return hipSuccess;
+    if (P.fuse) {
+        // fused RoPE: single token; the Q/K/V rows are whole heads of a work-group multiple (every RW
+        // below gives 4, 8 or 16 rows per work-group, dividing head_dim 64, 128 and 256)
+        if (P.fuse != 1 || P.T != 1 || !P.cnt || !attn_supported(P.rope.hd) || P.rope.T != 1 ||
+            P.rows_total != (P.rope.n_head + 2 * P.rope.n_kv) * P.rope.hd)
+            return hipErrorInvalidValue;
+    }
     if (P.T == 1) {
         // 16-byte chunks per lane per row; fewer rows per wavefront for long rows keep the weight
         // registers at 16 chunks and the grid above 256 work-groups

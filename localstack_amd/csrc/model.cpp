@@ -41,6 +41,7 @@ using lstk::set_error;
 
 constexpr int kStages = 5;
 constexpr int kBlasMinTokens = 2; // steps of at least this many tokens take the library GEMM
+
 constexpr uint32_t kCellBlock = 32; // KvCache::block_size (src/kv_cache.h:27)
 
 int hip_fail(hipError_t e, const char *what) { return set_error(LSTK_E_DEVICE, std::string(what) + ": " + hipGetErrorString(e)); }
@@ -170,6 +171,7 @@ struct lstk_model {
           *part = nullptr, *weights = nullptr;
     int32_t *ids = nullptr, *slots = nullptr, *in = nullptr; // in = tokens | cells | positions
     uint16_t *hn16 = nullptr, *attn16 = nullptr;             // fp16 inputs of the multi-token products
+    int *fuse_cnt = nullptr; // single-token Q/K/V launches: finished work-groups per head (RoPE in the last)
     rocblas_handle blas = nullptr;
     // pinned host staging
     int32_t *h_in = nullptr, *h_ids = nullptr, *h_slots = nullptr;
@@ -286,6 +288,7 @@ int create(const lstk_qwen3_hparams *hpp, const lstk_qwen3_weights *w, lstk_pool
         {(void **) &M->attn16, nb * hq * 2},
         {(void **) &M->cell_seq, (size_t) kv_size * 4},
         {(void **) &M->cell_pos, (size_t) kv_size * 4},
+        {(void **) &M->fuse_cnt, (size_t) (hp.n_head + 2 * hp.n_head_kv) * 4},
     };
     size_t total = 0;
     for (const Piece &p : pieces) total += (p.bytes + 255) / 256 * 256;
@@ -305,7 +308,8 @@ int create(const lstk_qwen3_hparams *hpp, const lstk_qwen3_weights *w, lstk_pool
     if ((e = hipMemset(M->kcache, 0, 2 * M->layer_elems * hp.n_layer * sizeof(uint16_t))) != hipSuccess ||
         (e = hipMemset(M->cell_seq, 0xff, (size_t) kv_size * 4)) != hipSuccess ||
         (e = hipMemset(M->cell_pos, 0xff, (size_t) kv_size * 4)) != hipSuccess ||
-        (e = hipMemset(M->in, 0, (size_t) 3 * nb * 4)) != hipSuccess) {
+        (e = hipMemset(M->in, 0, (size_t) 3 * nb * 4)) != hipSuccess ||
+        (e = hipMemset(M->fuse_cnt, 0, (size_t) (hp.n_head + 2 * hp.n_head_kv) * 4)) != hipSuccess) {
         destroy(M);
         return hip_fail(e, "hipMemset");
     }
@@ -456,6 +460,16 @@ int forward(lstk_model *M, int32_t seq, int T, int n_cells, float *d_logits, int
                 return hip_fail(e, "attn_norm launch");
             gp.x = M->hn;
         }
+        uint16_t *kc = M->kcache + M->layer_elems * l, *vc = M->vcache + M->layer_elems * l;
+        lstk::RopeParams rp{M->q, M->k, M->v, L.q_norm, L.k_norm, hp.rms_eps, d_pos, d_cells, seq, M->cell_seq, M->cell_pos,
+                            T, hp.n_head, hp.n_head_kv, hd, (int) M->kv.size, M->theta_scale, M->qr, kc, vc};
+        const bool fuse_rope = T == 1;
+        if (fuse_rope) {
+            // QK-norm, RoPE and the K / V store run in the last work-group of each head
+            gp.fuse = 1;
+            gp.cnt = M->fuse_cnt;
+            gp.rope = rp;
+        }
         if (blas) {
             const int rc = timed_span(M, 1, st, [&] {
                 int r = blas_gemm(M, L.wq, hq, h, M->hn16, T, M->q, hq, false, st);
@@ -467,10 +481,7 @@ int forward(lstk_model *M, int32_t seq, int T, int n_cells, float *d_logits, int
         } else if ((e = timed(M, 1, [&](const lstk::LaunchTiming *tm) { return lstk::launch_gemv(gp, st, tm); })) != hipSuccess) {
             return hip_fail(e, "qkv launch");
         }
-        uint16_t *kc = M->kcache + M->layer_elems * l, *vc = M->vcache + M->layer_elems * l;
-        lstk::RopeParams rp{M->q, M->k, M->v, L.q_norm, L.k_norm, hp.rms_eps, d_pos, d_cells, seq, M->cell_seq, M->cell_pos,
-                            T, hp.n_head, hp.n_head_kv, hd, (int) M->kv.size, M->theta_scale, M->qr, kc, vc};
-        if ((e = timed(M, 1, [&](const lstk::LaunchTiming *tm) { return lstk::launch_rope(rp, st, tm); })) != hipSuccess)
+        if (!fuse_rope && (e = timed(M, 1, [&](const lstk::LaunchTiming *tm) { return lstk::launch_rope(rp, st, tm); })) != hipSuccess)
             return hip_fail(e, "rope launch");
         lstk::AttnParams ap{};
         ap.q = M->qr;
@@ -502,17 +513,17 @@ int forward(lstk_model *M, int32_t seq, int T, int n_cells, float *d_logits, int
         op.cols = hq;
         op.x = M->attn;
         op.T = T;
+        // after the last attention only the output row goes on (src/qwen3.cpp:233-237)
+        const bool last = l == hp.n_layer - 1;
+        const int rows = last ? 1 : T;
+        float *xr = M->x + (size_t) (T - rows) * h;
+        lstk::NormParams fp{xr, nullptr, nullptr, nullptr, L.ffn_norm, M->hn, rows, h, hp.rms_eps};
         if (blas) {
             const int rc = timed_span(M, 3, st, [&] { return blas_gemm(M, L.wo, h, hq, M->attn16, T, M->x, h, true, st); });
             if (rc != LSTK_OK) return rc;
         } else if ((e = timed(M, 3, [&](const lstk::LaunchTiming *tm) { return lstk::launch_gemv(op, st, tm); })) != hipSuccess) {
             return hip_fail(e, "o-proj launch");
         }
-        // after the last attention only the output row goes on (src/qwen3.cpp:233-237)
-        const bool last = l == hp.n_layer - 1;
-        const int rows = last ? 1 : T;
-        float *xr = M->x + (size_t) (T - rows) * h;
-        lstk::NormParams fp{xr, nullptr, nullptr, nullptr, L.ffn_norm, M->hn, rows, h, hp.rms_eps};
         if ((e = timed(M, 0, [&](const lstk::LaunchTiming *tm) { return lstk::launch_rmsnorm(fp, st, tm); })) != hipSuccess)
             return hip_fail(e, "ffn_norm launch");
         int32_t *ids = d_trace ? d_trace + ((size_t) l * T + (T - rows)) * k : M->ids;
