@@ -136,6 +136,20 @@ def time_steps(torch, fn, steps, warmup):
     return s.elapsed_time(e) / steps
 
 
+def step_percentiles(torch, fn, steps):
+    """p10 / p50 / p90 of single-step times, from an event pair around each of `steps` further steps
+    (a pass of its own, so the per-step events do not touch the timed run)."""
+    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(steps)]
+    torch.cuda.synchronize()
+    for a, b in ev:
+        a.record()
+        fn()
+        b.record()
+    torch.cuda.synchronize()
+    t = np.array([a.elapsed_time(b) for a, b in ev])
+    return [float(np.percentile(t, q)) for q in (10, 50, 90)]
+
+
 def measure(torch, st, T, steps, warmup, use_graph):
     st.inputs(T, seed=1000 + T)
     graph = None
@@ -149,6 +163,7 @@ def measure(torch, st, T, steps, warmup, use_graph):
     else:
         fn = st.step
     ms = time_steps(torch, fn, steps, warmup)
+    pct = step_percentiles(torch, fn, steps)
     st.store.check()
     # stage timing (eager, events around every launch on the launch stream)
     st.store.set_timing(True)
@@ -163,7 +178,7 @@ def measure(torch, st, T, steps, warmup, use_graph):
     dn_bytes = distinct.mean() * 1671168 + T * K * (F * 4 + H * 4) + T * H * 8
     rt_bytes = E * H * 2 + T * H * 4
     avg = [stage_ms[i] / max(1, launches[i]) for i in range(4)]
-    res = dict(T=T, ms_per_step=ms, tok_s=T * 1000.0 / ms, graph=use_graph,
+    res = dict(T=T, ms_per_step=ms, tok_s=T * 1000.0 / ms, graph=use_graph, ms_per_step_p10_p50_p90=pct,
                stage_avg_us={"route": avg[0] * 1e3, "gate_up": avg[1] * 1e3, "down": avg[2] * 1e3,
                              "combine": avg[3] * 1e3},
                stage_launches=launches, distinct_experts_per_layer=float(distinct.mean()),
@@ -610,8 +625,10 @@ def main():
                      "kernel_avg_us": main_res["stage_avg_us"]["gate_up"],
                      "bytes_per_launch": main_res["gate_up_bytes"]},
         "stack_gbs": main_res["layer_gbs"],
+        "ms_per_step_p10_p50_p90": main_res["ms_per_step_p10_p50_p90"],
         "stage_avg_us": main_res["stage_avg_us"],
         "t8": None if extra is None else {"tok_s": extra["tok_s"], "ms_per_step": extra["ms_per_step"],
+                                          "ms_per_step_p10_p50_p90": extra["ms_per_step_p10_p50_p90"],
                                           "stack_gbs": extra["layer_gbs"], "stage_avg_us": extra["stage_avg_us"],
                                           "distinct_experts_per_layer": extra["distinct_experts_per_layer"]},
         "prefill": pre,

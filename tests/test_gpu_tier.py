@@ -88,14 +88,15 @@ def test_device_lru_equals_host_lru_on_recorded_trace(lstk, dev, n_batch, slots_
     assert hs["misses"] > 0 and hs["hits"] > 0
 
 
-@pytest.mark.parametrize("types,h,f,E,k", [((Q8_0,) * 3, 256, 512, 8, 2), ((Q4_K, Q4_K, Q8_0), 256, 768, 16, 4),
-                                           ((Q4_K,) * 3, 4096, 1536, 16, 8)])
-def test_device_acquire_ffn_equals_resident(orc, lstk, dev, types, h, f, E, k):
+@pytest.mark.parametrize("types,h,f,E,k,T", [((Q8_0,) * 3, 256, 512, 8, 2, 8), ((Q4_K, Q4_K, Q8_0), 256, 768, 16, 4, 8),
+                                             ((Q4_K,) * 3, 4096, 1536, 16, 8, 8), ((Q4_K,) * 3, 1024, 512, 32, 4, 64)])
+def test_device_acquire_ffn_equals_resident(orc, lstk, dev, types, h, f, E, k, T):
     """route -> acquire_device -> ffn on a pool that evicts constantly gives exactly the resident block's
-    output (the copy kernel moves whole expert matrices, Q8_0 / Q4_K and partial 16 KiB chunks)."""
+    output (the copy kernel moves whole expert matrices, Q8_0 / Q4_K and partial 16 KiB chunks; at 64
+    tokens the grouped matrix-core path runs on the slots)."""
     import torch
     import localstack_amd as L
-    n_layer, T = 2, 8
+    n_layer = 2
     rng = np.random.default_rng(510 + h + E)
     layers = [(types, synth.experts(rng, types[0], E, f, h), synth.experts(rng, types[1], E, f, h),
                synth.experts(rng, types[2], E, h, f)) for _ in range(n_layer)]
