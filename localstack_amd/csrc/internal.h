@@ -1,6 +1,8 @@
 // internal.h - what the forward pass (model.cpp) needs from the pool (pool.cpp) beyond the C ABI.
 #pragma once
 
+#include <hip/hip_runtime.h>
+
 #include <string>
 
 #include "../../include/lstk_moe.h"
@@ -15,5 +17,10 @@ bool pool_streaming(const lstk_pool *pool);
 bool pool_dry(const lstk_pool *pool);
 // Whether the pool's bookkeeping lives on the device (LSTK_POOL_DEVICE_LRU).
 bool pool_device_lru(const lstk_pool *pool);
+// lstk_moe_block for one token of a resident pool whose hnorm row the router launch computes itself as
+// rms_norm(x) * norm_w (bit-identical to the RMSNorm kernel's row; also stored to d_hnorm).
+int moe_block_normed(lstk_pool *pool, int layer, const float *d_x, const float *d_norm_w, float eps, float *d_hnorm,
+                     const void *d_gate_inp, int gate_type, const float *d_resid, float *d_out, int32_t *d_ids,
+                     float *d_weights, hipStream_t st);
 
 }  // namespace lstk

@@ -33,6 +33,14 @@ struct RouteParams {
     float *logits; // [T][E]
     int qtype;     // 0: none, 8: Q8_0 rows, 12: Q8_K rows (for Q4_K weights)
     ActBuf xq;
+    // One token only: with x_raw set, the launch first computes the row itself as the layer's
+    // ffn_norm of x_raw - (x * s) * norm_w with s = 1 / sqrtf(mean + eps), the mean from a double sum
+    // of x * x taken in the RMSNorm kernel's order, so the row is bit-identical to that kernel's - and
+    // stores it to hnorm_out (hnorm is then unused).
+    const float *x_raw;
+    const float *norm_w;
+    float eps;
+    float *hnorm_out;
 };
 
 // softmax + top-k + renormalisation from logits, one wavefront per token.

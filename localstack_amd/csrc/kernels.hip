@@ -48,6 +48,32 @@ constexpr int kGuRouteBlock = 512;
 // router logits
 // ------------------------------------------------------------------------------------------------
 
+// One row's RMSNorm by the kBlock threads of a work-group, in the RMSNorm kernel's order (forward.hip):
+// thread i holds x[i + 256 k] for k < NG, sums (double) (x * x) over k, then over the wavefront
+// (wave_sum_d) and the four wavefronts as (w0 + w1) + (w2 + w3). Returns the row's
+// (x * scale) * w values of this thread.
+template <int NG>
+__device__ __forceinline__ void norm_row(const float *x, const float *wn, int n, float eps, float (&y)[NG], double *s_part) {
+    const int tid = threadIdx.x;
+    float v[NG], w[NG];
+#pragma unroll
+    for (int k = 0; k < NG; k++) {
+        v[k] = x[tid + k * kBlock];
+        w[k] = wn[tid + k * kBlock];
+    }
+    double s = 0.0;
+#pragma unroll
+    for (int k = 0; k < NG; k++) s += (double) (v[k] * v[k]);
+    s = wave_sum_d(s);
+    if ((tid & (kWave - 1)) == 0) s_part[tid / kWave] = s;
+    __syncthreads();
+    const double tot = (s_part[0] + s_part[1]) + (s_part[2] + s_part[3]);
+    const float mean = (float) (tot / (double) n);
+    const float scale = 1.0f / sqrtf(mean + eps);
+#pragma unroll
+    for (int k = 0; k < NG; k++) y[k] = (v[k] * scale) * w[k];
+}
+
 // Dot products of a tile of tokens with kRouteEG experts. Lane l of a wavefront owns elements
 // 256 g + 4 l + q (g ascending, then q) and accumulates them with fmaf from 0; the 64 partials are
 // summed by wave_sum_tree. The oracle evaluates the same expression in the same order, so the
@@ -55,7 +81,7 @@ constexpr int kGuRouteBlock = 512;
 // ggml's CPU mul_mat converts src1 to the F16 vec_dot_type (src/qwen3.cpp:178).
 // The wavefront's two weight rows are loaded before the activations are staged.
 template <int GT, int NG>
-__device__ __forceinline__ void route_tile(const RouteParams &P, int b, float *xs, int tt, int ns) {
+__device__ __forceinline__ void route_tile(const RouteParams &P, int b, float *xs, int tt, int ns, double *s_part) {
     const int n_eg = (P.E + kRouteEG - 1) / kRouteEG;
     const int tile = b / n_eg, eg = b - tile * n_eg;
     constexpr int h = NG * 256;
@@ -88,6 +114,35 @@ __device__ __forceinline__ void route_tile(const RouteParams &P, int b, float *x
     }
     // the work-group's ns stages of tt tokens: stage s + 1 is loaded into registers while the
     // tokens of stage s are multiplied from LDS
+    if (P.x_raw) {
+        // one token, normalised here from the raw row while the router rows stream in
+        float y[NG];
+        norm_row<NG>(P.x_raw, P.norm_w, h, P.eps, y, s_part);
+#pragma unroll
+        for (int k = 0; k < NG; k++) xs[threadIdx.x + k * kBlock] = GT == kTypeF16 ? round_f16(y[k]) : y[k];
+        __syncthreads();
+        float acc[kRouteEPW];
+#pragma unroll
+        for (int ee = 0; ee < kRouteEPW; ee++) acc[ee] = 0.0f;
+#pragma unroll
+        for (int g = 0; g < NG; g++) {
+            const float4 x = *reinterpret_cast<const float4 *>(xs + 256 * g + 4 * lane);
+#pragma unroll
+            for (int ee = 0; ee < kRouteEPW; ee++) {
+                acc[ee] = fmaf(x.x, w[ee][g][0], acc[ee]);
+                acc[ee] = fmaf(x.y, w[ee][g][1], acc[ee]);
+                acc[ee] = fmaf(x.z, w[ee][g][2], acc[ee]);
+                acc[ee] = fmaf(x.w, w[ee][g][3], acc[ee]);
+            }
+        }
+#pragma unroll
+        for (int ee = 0; ee < kRouteEPW; ee++) {
+            const int e = eg * kRouteEG + wave * kRouteEPW + ee;
+            const float sum = wave_sum_tree(acc[ee]);
+            if (lane == 0 && e < P.E) P.logits[e] = sum;
+        }
+        return;
+    }
     const int tbase = tile * tt * ns;
     float4 pre[kPre];
     auto load = [&](int s) {
@@ -152,11 +207,25 @@ __device__ __forceinline__ void route_tile(const RouteParams &P, int b, float *x
 template <int GT, int NG>
 __global__ __launch_bounds__(kBlock) void route_kernel(RouteParams P, int n_route_wg, int n_quant_wg, int route_tt, int route_ns) {
     extern __shared__ __align__(16) float lds[];
+    __shared__ double s_part[kBlock / kWave];
     const int b = blockIdx.x;
     if (b < n_route_wg) {
-        route_tile<GT, NG>(P, b, lds, route_tt, route_ns);
+        route_tile<GT, NG>(P, b, lds, route_tt, route_ns, s_part);
     } else if (P.qtype != 0) {
         const int h = P.h;
+        if (P.x_raw) {
+            // one token: this work-group normalises the row, stores it, and quantizes what it stored
+            float y[NG];
+            norm_row<NG>(P.x_raw, P.norm_w, h, P.eps, y, s_part);
+#pragma unroll
+            for (int k = 0; k < NG; k++) P.hnorm_out[threadIdx.x + k * kBlock] = y[k];
+            __syncthreads();
+            if (P.qtype == kTypeQ8_0)
+                quantize_row<kTypeQ8_0>(P.hnorm_out, h, P.xq.qs, P.xq.d, P.xq.bs);
+            else
+                quantize_row<kTypeQ4_K>(P.hnorm_out, h, P.xq.qs, P.xq.d, P.xq.bs);
+            return;
+        }
         for (int t = b - n_route_wg; t < P.T; t += n_quant_wg) {
             if (P.qtype == kTypeQ8_0)
                 quantize_row<kTypeQ8_0>(P.hnorm + (size_t) t * h, h, P.xq.qs + (size_t) t * h, P.xq.d + (size_t) t * (h / 32),
@@ -794,6 +863,8 @@ size_t align16(size_t x) { return (x + 15) / 16 * 16; }
 
 template <int GT, int NG>
 hipError_t launch_route_t(const RouteParams &P, hipStream_t st, const LaunchTiming *tm) {
+    // the in-launch normalisation serves one token and needs the quantizing work-group to store the row
+    if (P.x_raw && (P.T != 1 || !P.norm_w || !P.hnorm_out || !P.qtype)) return hipErrorInvalidValue;
     int n_route = 0, tt = 1, ns = 1;
     if (P.do_route) {
         tt = route_tile_tokens(P.h);

@@ -3,13 +3,15 @@
 // lstk_model plays the part of the reference's Engine + qwen3_build_graph + KvCache
 // (src/engine.cpp:193-341, src/qwen3.cpp:128-259, src/kv_cache.cpp:59-150) for one GPU and one
 // stream. Instead of building a ggml graph per step it launches a fixed kernel sequence:
-//   layer 0:  embedding gather + attn_norm             (rmsnorm_kernel)
+//   layer 0:  embedding gather + attn_norm             (rmsnorm_kernel; inside the Q/K/V launch at T = 1)
 //   each layer l:
-//     Q, K, V projections in one launch                 (gemv_kernel, 3 segments)
-//     QK-norm + NEOX RoPE + K/V store into the cache    (rope_kernel)
+//     Q, K, V projections in one launch                 (gemv_kernel, 3 segments; gemv1_kernel at T = 1)
+//     QK-norm + NEOX RoPE + K/V store into the cache    (rope_kernel; at T = 1 the last work-group of
+//                                                        each head of the Q/K/V launch)
 //     attention over the step's n_kv cells              (attn_kernel [+ attn_combine_kernel])
 //     o-proj + residual                                 (gemv_kernel with add)
-//     ffn_norm on the rows the FFN needs                (rmsnorm_kernel)
+//     ffn_norm on the rows the FFN needs                (rmsnorm_kernel; at T = 1 with a resident pool
+//                                                        the router launch normalises the row itself)
 //     MoE block: lstk_moe_block (resident pool) or route -> acquire -> lstk_moe_ffn (streaming pool;
 //     the acquire runs on the device for an LSTK_POOL_DEVICE_LRU pool)
 //     the last layer runs its FFN on the output row only (src/qwen3.cpp:233-237)
@@ -373,8 +375,13 @@ int sync_cells(lstk_model *M) {
 }
 
 // The MoE block of layer l on `rows` rows of hn, added into the residual rows xr in place.
-int moe(lstk_model *M, int l, int rows, float *xr, int32_t *ids, hipStream_t st) {
+// With ffn_norm set (one token, resident pool) the router launch computes hn = rms_norm(xr) * ffn_norm
+// itself, so the step needs no RMSNorm launch before the block.
+int moe(lstk_model *M, int l, int rows, float *xr, int32_t *ids, hipStream_t st, const float *ffn_norm) {
     const lstk_qwen3_layer &L = M->layers[l];
+    if (!M->streaming && ffn_norm)
+        return lstk::moe_block_normed(M->pool, l, xr, ffn_norm, M->hp.rms_eps, M->hn, L.gate_inp, L.gate_inp_type, xr, xr,
+                                      ids, M->weights, st);
     if (!M->streaming)
         return lstk_moe_block(M->pool, l, M->hn, L.gate_inp, L.gate_inp_type, xr, xr, ids, M->weights, rows, st);
     // Engine::run_segment (src/engine.cpp:343-392): the host sees the router's choice, acquires the
@@ -524,14 +531,16 @@ int forward(lstk_model *M, int32_t seq, int T, int n_cells, float *d_logits, int
         } else if ((e = timed(M, 3, [&](const lstk::LaunchTiming *tm) { return lstk::launch_gemv(op, st, tm); })) != hipSuccess) {
             return hip_fail(e, "o-proj launch");
         }
-        if ((e = timed(M, 0, [&](const lstk::LaunchTiming *tm) { return lstk::launch_rmsnorm(fp, st, tm); })) != hipSuccess)
+        const bool norm_in_router = rows == 1 && T == 1 && !M->streaming;
+        if (!norm_in_router &&
+            (e = timed(M, 0, [&](const lstk::LaunchTiming *tm) { return lstk::launch_rmsnorm(fp, st, tm); })) != hipSuccess)
             return hip_fail(e, "ffn_norm launch");
         int32_t *ids = d_trace ? d_trace + ((size_t) l * T + (T - rows)) * k : M->ids;
         if (last && d_trace && T > 1) {
             lstk::FillParams fl{d_trace + (size_t) l * T * k, (T - 1) * k, -1};
             if ((e = lstk::launch_fill(fl, st, nullptr)) != hipSuccess) return hip_fail(e, "trace fill launch");
         }
-        const int rc = moe(M, l, rows, xr, ids, st);
+        const int rc = moe(M, l, rows, xr, ids, st, norm_in_router ? L.ffn_norm : nullptr);
         if (rc != LSTK_OK) return rc;
     }
     lstk::NormParams onp{M->x + (size_t) (T - 1) * h, nullptr, nullptr, nullptr, M->output_norm, M->hn, 1, h, hp.rms_eps};

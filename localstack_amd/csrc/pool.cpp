@@ -867,16 +867,28 @@ int run_fused(lstk_pool *P, const Shard &s, int mode, const float *d_hnorm, cons
 
 // Router (optional) + experts + combine of one layer. mode 0: ffn with caller slots / weights;
 // mode 1: resident block, routing from gate_inp, ids / weights written to d_ids / d_weights.
+// The ffn_norm input of a one-token block whose router launch normalises the row itself.
+struct NormIn {
+    const float *x, *w;
+    float eps;
+};
+
 int run_block(lstk_pool *P, int layer, int mode, const float *d_hnorm, const void *d_gate_inp, int gate_type,
               const int32_t *d_slots, int32_t *d_ids, float *d_weights, const float *d_resid, float *d_out, int T,
-              hipStream_t st) {
+              hipStream_t st, const NormIn *norm = nullptr) {
     const lstk_moe_dims &d = P->dims;
     const Shard &s = P->shards[P->layer_shard[layer]];
     const int k = d.n_expert_used;
-    if (T == 1 && use_fused(P, s, mode == 1 ? gate_type : lstk::kTypeF16))
+    if (T == 1 && !norm && use_fused(P, s, mode == 1 ? gate_type : lstk::kTypeF16))
         return run_fused(P, s, mode, d_hnorm, d_gate_inp, gate_type, d_slots, d_ids, d_weights, d_resid, d_out, st);
     lstk::RouteParams rp{};
     rp.hnorm = d_hnorm;
+    if (norm) {
+        rp.x_raw = norm->x;
+        rp.norm_w = norm->w;
+        rp.eps = norm->eps;
+        rp.hnorm_out = const_cast<float *>(d_hnorm);
+    }
     rp.T = T;
     rp.h = d.n_embd;
     rp.do_route = mode == 1;
@@ -982,6 +994,22 @@ const lstk_moe_dims &pool_dims(const lstk_pool *pool) { return pool->dims; }
 bool pool_streaming(const lstk_pool *pool) { return pool->streaming; }
 bool pool_dry(const lstk_pool *pool) { return pool->dry; }
 bool pool_device_lru(const lstk_pool *pool) { return pool->device_lru; }
+
+int moe_block_normed(lstk_pool *pool, int layer, const float *d_x, const float *d_norm_w, float eps, float *d_hnorm,
+                     const void *d_gate_inp, int gate_type, const float *d_resid, float *d_out, int32_t *d_ids,
+                     float *d_weights, hipStream_t st) {
+    int rc;
+    if ((rc = check_call(pool, layer, 1)) != LSTK_OK) return rc;
+    if (pool->streaming) return fail(LSTK_E_INVALID, "moe_block_normed needs a resident pool");
+    if ((rc = check_router_args(d_gate_inp, gate_type)) != LSTK_OK || (rc = check_act(d_x, "x")) != LSTK_OK ||
+        (rc = check_act(d_norm_w, "norm_w")) != LSTK_OK || (rc = check_act(d_hnorm, "hnorm")) != LSTK_OK ||
+        (rc = check_act(d_resid, "resid")) != LSTK_OK || (rc = check_act(d_out, "out")) != LSTK_OK)
+        return rc;
+    if (!d_ids || !d_weights) return fail(LSTK_E_INVALID, "ids and weights must be non-null");
+    const NormIn norm{d_x, d_norm_w, eps};
+    return run_block(pool, layer, 1, d_hnorm, d_gate_inp, gate_type, nullptr, d_ids, d_weights, d_resid, d_out, 1, st,
+                     &norm);
+}
 }  // namespace lstk
 
 extern "C" {
