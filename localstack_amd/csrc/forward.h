@@ -41,6 +41,7 @@ struct RopeParams {
     float theta_scale; // freq_base^(-2 / hd)
     float *q_out;      // [T][n_head][hd]
     uint16_t *kc, *vc; // this layer's caches
+    const float *cs;   // [T][hd / 2][2]: cos and sin of each pair's angle (launch_rope_table), or null
 };
 
 // One F16 weight matrix of a GEMV launch: y[t * ldy + r] = sum_i fp16(x[t][i]) * w[r][i] (+ add[t * ldy + r]).
@@ -57,10 +58,6 @@ struct GemvSeg {
 // in: with norm_w set, x is replaced by rms_norm(x) * norm_w (the reference's attn_norm before Q/K/V),
 // and with emb set, x is first gathered from the F16 embedding row tokens[0] and written to x_out.
 //
-// A single-token Q/K/V launch may also finish the RoPE step in its last work-groups (fuse = 1): the
-// last of the work-groups that produce one head's rows (counted in cnt[head], n_head + 2 n_head_kv
-// slots that are zero before the launch and zero again after it) runs rope_kernel's work for that
-// head - QK-norm, RoPE and the K / V cache store - reading the rows back with device-coherent loads.
 struct GemvParams {
     GemvSeg seg[3];
     int nseg;
@@ -73,9 +70,6 @@ struct GemvParams {
     const uint16_t *emb;
     const int32_t *tokens;
     float *x_out;
-    int fuse;
-    int *cnt;
-    RopeParams rope;
 };
 
 // Causal attention of one step over cells [0, n_cells) of one layer's cache. The query rows of a KV head
@@ -93,6 +87,11 @@ struct AttnParams {
     float *part; // [T][n_head][n_chunk][hd + 4]: max, sum, 2 unused, unnormalised output
     float *out;  // [T][n_head * hd]
     uint16_t *out16; // when set, also out rounded to fp16
+    // One token: with rope_in set the launch does rope_kernel's work itself (q above is then unused):
+    // every work-group rotates its query rows from rope.q, and the one whose chunk holds the token's
+    // cell stores that cell's K / V (and cell-table entries) of its KV head before reading the chunk.
+    int rope_in;
+    RopeParams rope;
 };
 
 // Writes v to n int32 values (the trace rows the last layer does not compute).
@@ -127,6 +126,9 @@ size_t attn_part_rows(int n_batch, int n_head);
 hipError_t launch_rmsnorm(const NormParams &P, hipStream_t st, const LaunchTiming *tm);
 hipError_t launch_gemv(const GemvParams &P, hipStream_t st, const LaunchTiming *tm);
 hipError_t launch_rope(const RopeParams &P, hipStream_t st, const LaunchTiming *tm);
+// Fills cs_out [T][hd / 2][2] with the cos and sin of the step's angles (pos[t] * theta_scale^i, by
+// repeated multiplication), the values every layer's RoPE uses (P.cs is ignored).
+hipError_t launch_rope_table(const RopeParams &P, float *cs_out, hipStream_t st);
 hipError_t launch_attn(const AttnParams &P, hipStream_t st, const LaunchTiming *tm);
 hipError_t launch_attn_combine(const AttnParams &P, hipStream_t st, const LaunchTiming *tm);
 hipError_t launch_fill(const FillParams &P, hipStream_t st, const LaunchTiming *tm);

@@ -87,15 +87,34 @@ __device__ __forceinline__ size_t v_index(int head, int d, int cell, int hd, int
     return (((size_t) head * (kv_size / 4) + cell / 4) * hd + d) * 4 + (cell & 3);
 }
 
+// cos and sin of pair i's angle at position p: p * theta_scale^i, the power built by repeated
+// multiplication (ggml's rope cache), then cosf / sinf.
+__device__ __forceinline__ void rope_angle(float p, float theta_scale, int i, float &c, float &sn) {
+    float theta = p;
+    for (int s = 0; s < i; s++) theta *= theta_scale;
+    c = cosf(theta);
+    sn = sinf(theta);
+}
+
+__global__ __launch_bounds__(kWave) void rope_table_kernel(RopeParams P, float *cs) {
+    const int t = blockIdx.x, half = P.hd / 2;
+    const float p = (float) P.pos[t];
+    for (int i = threadIdx.x; i < half; i += kWave) {
+        float c, sn;
+        rope_angle(p, P.theta_scale, i, c, sn);
+        reinterpret_cast<float2 *>(cs)[(size_t) t * half + i] = make_float2(c, sn);
+    }
+}
+
 // Head j (Q heads, then K heads, then V heads) of token t by one wavefront (lanes = threadIdx.x % 64).
-// COH: q / k / v were written in this launch by other work-groups (device-coherent loads).
-template <bool COH>
-__device__ __forceinline__ void rope_head(const RopeParams &P, int t, int j) {
+// A Q head's rotated row goes to q_dst (hd floats) or, when that is null, to its row of P.q_out;
+// with cells set, the wavefront also records the token's cell in the cell tables.
+__device__ __forceinline__ void rope_head(const RopeParams &P, int t, int j, float *q_dst, bool cells) {
     const int lane = threadIdx.x & (kWave - 1);
     const int hd = P.hd, half = hd / 2;
-    auto ld = [](const float *a) { return COH ? ld_dev(a) : *a; };
+    auto ld = [](const float *a) { return *a; };
     const int cell = P.cells[t];
-    if (j == 0 && lane == 0) {
+    if (cells && lane == 0) {
         P.cell_seq[cell] = P.seq;
         P.cell_pos[cell] = P.pos[t];
     }
@@ -127,13 +146,18 @@ __device__ __forceinline__ void rope_head(const RopeParams &P, int t, int j) {
             x0 = (x0 * scale) * nw[i];
             x1 = (x1 * scale) * nw[i + half];
         }
-        float theta = p;
-        for (int s = 0; s < i; s++) theta *= P.theta_scale;
-        const float c = cosf(theta), sn = sinf(theta);
+        float c, sn;
+        if (P.cs) {
+            const float2 v = reinterpret_cast<const float2 *>(P.cs)[(size_t) t * half + i];
+            c = v.x;
+            sn = v.y;
+        } else {
+            rope_angle(p, P.theta_scale, i, c, sn);
+        }
         const float y0 = x0 * c - x1 * sn;
         const float y1 = x0 * sn + x1 * c;
         if (is_q) {
-            float *dst = P.q_out + ((size_t) t * P.n_head + head) * hd;
+            float *dst = q_dst ? q_dst : P.q_out + ((size_t) t * P.n_head + head) * hd;
             dst[i] = y0;
             dst[i + half] = y1;
         } else {
@@ -143,7 +167,9 @@ __device__ __forceinline__ void rope_head(const RopeParams &P, int t, int j) {
     }
 }
 
-__global__ __launch_bounds__(kWave) void rope_kernel(RopeParams P) { rope_head<false>(P, blockIdx.x, blockIdx.y); }
+__global__ __launch_bounds__(kWave) void rope_kernel(RopeParams P) {
+    rope_head(P, blockIdx.x, blockIdx.y, nullptr, blockIdx.y == 0);
+}
 
 // ------------------------------------------------------------------------------------------------
 // F16 GEMV over up to 3 matrices: each wavefront owns kGvRows rows, lanes stride the row in 16-byte
@@ -327,30 +353,8 @@ __global__ __launch_bounds__(kGvWaves *kWave) void gemv1_kernel(GemvParams P) {
 #pragma unroll
     for (int rr = 0; rr < RW; rr++) {
         const float sum = wave_sum_tree(acc[rr]);
-        if (lane == 0 && on[rr]) {
-            const float y = ar[rr] ? sum + ar[rr][0] : sum;
-            if (P.fuse) st_dev(yr[rr], y);
-            else yr[rr][0] = y;
-        }
+        if (lane == 0 && on[rr]) yr[rr][0] = ar[rr] ? sum + ar[rr][0] : sum;
     }
-    if (!P.fuse) return;
-    // The work-groups that produced the rows the fused step reads count themselves in once their
-    // device-coherent stores have completed; the one that brings the count to n_in runs the step,
-    // reading those rows with device-coherent loads (no cache flush or invalidation is needed, and
-    // nothing waits for another work-group).
-    __shared__ int s_last;
-    const int per_wg = kGvWaves * RW;
-    const int slot = blockIdx.x * per_wg / P.rope.hd, n_in = P.rope.hd / per_wg;
-    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-    __syncthreads();
-    if (tid == 0) {
-        const int old = __hip_atomic_fetch_add(P.cnt + slot, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        s_last = old == n_in - 1;
-        if (s_last) __hip_atomic_store(P.cnt + slot, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    }
-    __syncthreads();
-    if (!s_last) return;
-    if (wv == 0) rope_head<true>(P.rope, 0, slot);
 }
 
 // ------------------------------------------------------------------------------------------------
@@ -384,6 +388,7 @@ __global__ __launch_bounds__(kAtBlock) void attn_kernel(AttnParams P) {
     __shared__ uint16_t s_Ph[RB][PS], s_Pl[RB][PS];
     __shared__ float s_M[RB], s_L[RB], s_f[RB];
     __shared__ int s_pos[RB];
+    __shared__ float s_q[NRT == 1 ? 16 * HD : 1]; // rotated Q rows when this launch applies RoPE
     const int tid = threadIdx.x, w = tid / kWave, l = tid & (kWave - 1), lr = l & 15, lq = l >> 4;
     const int grp = P.n_head / P.n_kv;
     const int g = blockIdx.x % P.n_kv, rest = blockIdx.x / P.n_kv;
@@ -395,13 +400,27 @@ __global__ __launch_bounds__(kAtBlock) void attn_kernel(AttnParams P) {
         s_M[tid] = -INFINITY;
         s_L[tid] = 0.0f;
     }
+    const int begin = c * P.chunk, end = min(begin + P.chunk, P.n_cells), last4 = P.kv_size - 4;
+    if (NRT == 1 && P.rope_in) {
+        // one token: every work-group rotates its own query rows (rope_kernel's work, bit for bit),
+        // and the work-group whose chunk holds the token's cell first stores that cell's K and V of
+        // KV head g and its cell-table entries, so its reads below see them
+        const int cell0 = P.rope.cells[0];
+        if (cell0 >= begin && cell0 < end) {
+            if (w == 0) rope_head(P.rope, 0, P.n_head + g, nullptr, true);
+            else if (w == 1) rope_head(P.rope, 0, P.n_head + P.n_kv + g, nullptr, false);
+        }
+        for (int r = w; r < grp; r += kAtBlock / kWave) rope_head(P.rope, 0, g * grp + r, s_q + r * HD, false);
+        __syncthreads();
+    }
     // Q fragments (A operand): row rt*16 + lr, dims ks*16 + 4 lq .. +3
     half4v qa[NRT][NK];
 #pragma unroll
     for (int rt = 0; rt < NRT; rt++) {
         const int r = row0 + rt * 16 + lr;
         const bool on = r < rows;
-        const float *q = P.q + ((size_t) (on ? r / grp : 0) * P.n_head + g * grp + (on ? r % grp : 0)) * HD;
+        const float *q = NRT == 1 && P.rope_in ? s_q + (on ? r % grp : 0) * HD
+                                               : P.q + ((size_t) (on ? r / grp : 0) * P.n_head + g * grp + (on ? r % grp : 0)) * HD;
 #pragma unroll
         for (int ks = 0; ks < NK; ks++) {
             const float4 v = on ? *reinterpret_cast<const float4 *>(q + ks * 16 + 4 * lq) : make_float4(0, 0, 0, 0);
@@ -416,7 +435,6 @@ __global__ __launch_bounds__(kAtBlock) void attn_kernel(AttnParams P) {
     __syncthreads();
 
     const uint16_t *kb = P.kc + (size_t) g * (HD / 4) * P.kv_size * 4;
-    const int begin = c * P.chunk, end = min(begin + P.chunk, P.n_cells), last4 = P.kv_size - 4;
     for (int c0 = begin; c0 < end; c0 += kFaCells) {
         // V fragments of this pass (B operand of O += P V): cells kc*16 + 4 lq .. +3, dim (w*DT + dt)*16 + lr
         half4v vf[4][DT];
@@ -672,13 +690,6 @@ hipError_t launch_gemv1_t(const GemvParams &P, hipStream_t st, const LaunchTimin
 
 hipError_t launch_gemv(const GemvParams &P, hipStream_t st, const LaunchTiming *tm) {
     if (P.T == 0 || P.rows_total == 0) return hipSuccess;
-    if (P.fuse) {
-        // fused RoPE: single token; the Q/K/V rows are whole heads of a work-group multiple (every RW
-        // below gives 4, 8 or 16 rows per work-group, dividing head_dim 64, 128 and 256)
-        if (P.fuse != 1 || P.T != 1 || !P.cnt || !attn_supported(P.rope.hd) || P.rope.T != 1 ||
-            P.rows_total != (P.rope.n_head + 2 * P.rope.n_kv) * P.rope.hd)
-            return hipErrorInvalidValue;
-    }
     if (P.T == 1) {
         // 16-byte chunks per lane per row; fewer rows per wavefront for long rows keep the weight
         // registers at 16 chunks and the grid above 256 work-groups
@@ -700,6 +711,11 @@ hipError_t launch_gemv(const GemvParams &P, hipStream_t st, const LaunchTiming *
     return launch(gemv_kernel<8>, grid, block, gemv_lds<8>(P.cols), st, tm, P);
 }
 
+hipError_t launch_rope_table(const RopeParams &P, float *cs_out, hipStream_t st) {
+    if (P.T == 0) return hipSuccess;
+    return launch(rope_table_kernel, dim3(P.T), dim3(kWave), 0, st, nullptr, P, cs_out);
+}
+
 hipError_t launch_rope(const RopeParams &P, hipStream_t st, const LaunchTiming *tm) {
     if (P.T == 0) return hipSuccess;
     return launch(rope_kernel, dim3(P.T, P.n_head + 2 * P.n_kv), dim3(kWave), 0, st, tm, P);
@@ -715,6 +731,9 @@ hipError_t launch_attn_hd(const AttnParams &P, hipStream_t st, const LaunchTimin
 
 hipError_t launch_attn(const AttnParams &P, hipStream_t st, const LaunchTiming *tm) {
     if (P.T == 0) return hipSuccess;
+    // RoPE inside the launch: one token, whose query rows fit one 16-row tile
+    if (P.rope_in && (P.T != 1 || P.rb_rows != 16 || P.n_rowblk != 1 || P.rope.T != 1 || P.rope.hd != P.hd))
+        return hipErrorInvalidValue;
     switch (P.hd) {
     case 64: return launch_attn_hd<64>(P, st, tm);
     case 128: return launch_attn_hd<128>(P, st, tm);

@@ -6,8 +6,8 @@
 //   layer 0:  embedding gather + attn_norm             (rmsnorm_kernel; inside the Q/K/V launch at T = 1)
 //   each layer l:
 //     Q, K, V projections in one launch                 (gemv_kernel, 3 segments; gemv1_kernel at T = 1)
-//     QK-norm + NEOX RoPE + K/V store into the cache    (rope_kernel; at T = 1 the last work-group of
-//                                                        each head of the Q/K/V launch)
+//     QK-norm + NEOX RoPE + K/V store into the cache    (rope_kernel; at T = 1 inside the attention
+//                                                        launch)
 //     attention over the step's n_kv cells              (attn_kernel [+ attn_combine_kernel])
 //     o-proj + residual                                 (gemv_kernel with add)
 //     ffn_norm on the rows the FFN needs                (rmsnorm_kernel; at T = 1 with a resident pool
@@ -173,7 +173,7 @@ struct lstk_model {
           *part = nullptr, *weights = nullptr;
     int32_t *ids = nullptr, *slots = nullptr, *in = nullptr; // in = tokens | cells | positions
     uint16_t *hn16 = nullptr, *attn16 = nullptr;             // fp16 inputs of the multi-token products
-    int *fuse_cnt = nullptr; // single-token Q/K/V launches: finished work-groups per head (RoPE in the last)
+    float *rope_cs = nullptr; // [n_batch][head_dim / 2][2] cos / sin of the step's RoPE angles
     rocblas_handle blas = nullptr;
     // pinned host staging
     int32_t *h_in = nullptr, *h_ids = nullptr, *h_slots = nullptr;
@@ -290,7 +290,7 @@ int create(const lstk_qwen3_hparams *hpp, const lstk_qwen3_weights *w, lstk_pool
         {(void **) &M->attn16, nb * hq * 2},
         {(void **) &M->cell_seq, (size_t) kv_size * 4},
         {(void **) &M->cell_pos, (size_t) kv_size * 4},
-        {(void **) &M->fuse_cnt, (size_t) (hp.n_head + 2 * hp.n_head_kv) * 4},
+        {(void **) &M->rope_cs, nb * (size_t) hp.head_dim * 4},
     };
     size_t total = 0;
     for (const Piece &p : pieces) total += (p.bytes + 255) / 256 * 256;
@@ -310,8 +310,7 @@ int create(const lstk_qwen3_hparams *hpp, const lstk_qwen3_weights *w, lstk_pool
     if ((e = hipMemset(M->kcache, 0, 2 * M->layer_elems * hp.n_layer * sizeof(uint16_t))) != hipSuccess ||
         (e = hipMemset(M->cell_seq, 0xff, (size_t) kv_size * 4)) != hipSuccess ||
         (e = hipMemset(M->cell_pos, 0xff, (size_t) kv_size * 4)) != hipSuccess ||
-        (e = hipMemset(M->in, 0, (size_t) 3 * nb * 4)) != hipSuccess ||
-        (e = hipMemset(M->fuse_cnt, 0, (size_t) (hp.n_head + 2 * hp.n_head_kv) * 4)) != hipSuccess) {
+        (e = hipMemset(M->in, 0, (size_t) 3 * nb * 4)) != hipSuccess) {
         destroy(M);
         return hip_fail(e, "hipMemset");
     }
@@ -439,6 +438,15 @@ int forward(lstk_model *M, int32_t seq, int T, int n_cells, float *d_logits, int
     hipError_t e;
     const int32_t *d_tok = M->in, *d_cells = M->in + nb, *d_pos = M->in + 2 * nb;
     const bool blas = T >= kBlasMinTokens;
+    {
+        // the step's RoPE angles, shared by every layer
+        lstk::RopeParams tp{};
+        tp.pos = d_pos;
+        tp.T = T;
+        tp.hd = hd;
+        tp.theta_scale = M->theta_scale;
+        if ((e = lstk::launch_rope_table(tp, M->rope_cs, st)) != hipSuccess) return hip_fail(e, "rope table launch");
+    }
 
     for (int l = 0; l < hp.n_layer; l++) {
         const lstk_qwen3_layer &L = M->layers[l];
@@ -469,14 +477,10 @@ int forward(lstk_model *M, int32_t seq, int T, int n_cells, float *d_logits, int
         }
         uint16_t *kc = M->kcache + M->layer_elems * l, *vc = M->vcache + M->layer_elems * l;
         lstk::RopeParams rp{M->q, M->k, M->v, L.q_norm, L.k_norm, hp.rms_eps, d_pos, d_cells, seq, M->cell_seq, M->cell_pos,
-                            T, hp.n_head, hp.n_head_kv, hd, (int) M->kv.size, M->theta_scale, M->qr, kc, vc};
-        const bool fuse_rope = T == 1;
-        if (fuse_rope) {
-            // QK-norm, RoPE and the K / V store run in the last work-group of each head
-            gp.fuse = 1;
-            gp.cnt = M->fuse_cnt;
-            gp.rope = rp;
-        }
+                            T, hp.n_head, hp.n_head_kv, hd, (int) M->kv.size, M->theta_scale, M->qr, kc, vc, M->rope_cs};
+        // one token (its query rows in one 16-row tile): QK-norm, RoPE and the K / V store run inside
+        // the attention launch
+        const bool rope_in_attn = T == 1 && hp.n_head / hp.n_head_kv <= 16;
         if (blas) {
             const int rc = timed_span(M, 1, st, [&] {
                 int r = blas_gemm(M, L.wq, hq, h, M->hn16, T, M->q, hq, false, st);
@@ -488,7 +492,7 @@ int forward(lstk_model *M, int32_t seq, int T, int n_cells, float *d_logits, int
         } else if ((e = timed(M, 1, [&](const lstk::LaunchTiming *tm) { return lstk::launch_gemv(gp, st, tm); })) != hipSuccess) {
             return hip_fail(e, "qkv launch");
         }
-        if (!fuse_rope && (e = timed(M, 1, [&](const lstk::LaunchTiming *tm) { return lstk::launch_rope(rp, st, tm); })) != hipSuccess)
+        if (!rope_in_attn && (e = timed(M, 1, [&](const lstk::LaunchTiming *tm) { return lstk::launch_rope(rp, st, tm); })) != hipSuccess)
             return hip_fail(e, "rope launch");
         lstk::AttnParams ap{};
         ap.q = M->qr;
@@ -508,6 +512,8 @@ int forward(lstk_model *M, int32_t seq, int T, int n_cells, float *d_logits, int
         ap.part = M->part;
         ap.out = M->attn;
         ap.out16 = blas ? M->attn16 : nullptr;
+        ap.rope_in = rope_in_attn ? 1 : 0;
+        ap.rope = rp;
         lstk::attn_plan(ap);
         if ((e = timed(M, 2, [&](const lstk::LaunchTiming *tm) { return lstk::launch_attn(ap, st, tm); })) != hipSuccess ||
             (ap.n_chunk > 1 &&
