@@ -51,7 +51,9 @@ typedef struct lstk_qwen3_layer {
     const float *attn_norm;  /* [n_embd] */
     const uint16_t *wq;      /* F16 [n_head * head_dim][n_embd] */
     const uint16_t *wk;      /* F16 [n_head_kv * head_dim][n_embd] */
-    const uint16_t *wv;      /* F16 [n_head_kv * head_dim][n_embd] */
+    const uint16_t *wv;      /* F16 [n_head_kv * head_dim][n_embd]; when wk starts where wq ends and wv
+                                where wk ends (one [q | k | v] block), multi-token steps take one
+                                library product for all three instead of three */
     const uint16_t *wo;      /* F16 [n_embd][n_head * head_dim] */
     const float *q_norm;     /* [head_dim] or NULL */
     const float *k_norm;     /* [head_dim] or NULL */

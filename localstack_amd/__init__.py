@@ -328,7 +328,7 @@ class Qwen3Model:
     `store`, an ExpertStore of matching dims created by the caller (resident or streaming).
     """
 
-    def __init__(self, hp, weights, store, kv_size, n_batch, device="cuda"):
+    def __init__(self, hp, weights, store, kv_size, n_batch, device="cuda", join_qkv=True):
         import torch
         self.hp = dict(hp)
         self.store = store
@@ -345,6 +345,15 @@ class Qwen3Model:
             self._keep.append(t)
             return t.data_ptr()
 
+        def up_joined(arrs, dtype):
+            """The arrays one after the other in one device buffer (Q, K and V weights, so the model can
+            multiply all three in one product); returns each one's device pointer."""
+            flat = [np.ascontiguousarray(a).view(dtype).ravel() for a in arrs]
+            t = torch.from_numpy(np.concatenate(flat)).to(self.device)
+            self._keep.append(t)
+            offs = np.cumsum([0] + [a.size for a in flat[:-1]])
+            return [t.data_ptr() + int(o) * t.element_size() for o in offs]
+
         f16, f32 = np.uint16, np.float32
         self._hp = Qwen3HParams(*(int(self.hp[n]) for n in ("n_layer", "n_embd", "n_head", "n_head_kv", "head_dim",
                                                              "n_vocab", "n_expert", "n_expert_used", "n_ff_exp")),
@@ -353,7 +362,11 @@ class Qwen3Model:
         n_layer = self.hp["n_layer"]
         self._layers = (Qwen3Layer * n_layer)()
         for l, L in enumerate(weights["layers"]):
-            self._layers[l] = Qwen3Layer(up(L["attn_norm"], f32), up(L["wq"], f16), up(L["wk"], f16), up(L["wv"], f16),
+            if join_qkv:
+                wq, wk, wv = up_joined((L["wq"], L["wk"], L["wv"]), f16)
+            else:
+                wq, wk, wv = up(L["wq"], f16), up(L["wk"], f16), up(L["wv"], f16)
+            self._layers[l] = Qwen3Layer(up(L["attn_norm"], f32), wq, wk, wv,
                                          up(L["wo"], f16), up(L.get("q_norm"), f32), up(L.get("k_norm"), f32),
                                          up(L["ffn_norm"], f32),
                                          up(L["gate_inp"], f32 if L["gate_inp"].dtype == np.float32 else f16),

@@ -31,7 +31,7 @@ struct NormParams {
 // and V [n_head_kv][kv_size / 4][head_dim][4] (4 consecutive cells of a dim, 16 dims side by side), so
 // every fragment a lane needs is one 8-byte load and 16 lanes read 128 contiguous bytes.
 struct RopeParams {
-    const float *q, *k, *v; // [T][n_head * hd], [T][n_head_kv * hd] x 2
+    const float *q, *k, *v; // token t's rows at q + t * ld (n_head * hd), k + t * ld, v + t * ld (n_head_kv * hd)
     const float *q_norm, *k_norm;
     float eps;
     const int32_t *pos, *cells; // [T]
@@ -42,6 +42,7 @@ struct RopeParams {
     float *q_out;      // [T][n_head][hd]
     uint16_t *kc, *vc; // this layer's caches
     const float *cs;   // [T][hd / 2][2]: cos and sin of each pair's angle (launch_rope_table), or null
+    int ld;            // row stride of q, k and v (floats)
 };
 
 // One F16 weight matrix of a GEMV launch: y[t * ldy + r] = sum_i fp16(x[t][i]) * w[r][i] (+ add[t * ldy + r]).

@@ -120,13 +120,13 @@ __device__ __forceinline__ void rope_head(const RopeParams &P, int t, int j, flo
     }
     if (j >= P.n_head + P.n_kv) {
         const int head = j - P.n_head - P.n_kv;
-        const float *src = P.v + ((size_t) t * P.n_kv + head) * hd;
+        const float *src = P.v + (size_t) t * P.ld + head * hd;
         for (int d = lane; d < hd; d += kWave) P.vc[v_index(head, d, cell, hd, P.kv_size)] = f2h(ld(src + d));
         return;
     }
     const bool is_q = j < P.n_head;
     const int head = is_q ? j : j - P.n_head;
-    const float *src = is_q ? P.q + ((size_t) t * P.n_head + head) * hd : P.k + ((size_t) t * P.n_kv + head) * hd;
+    const float *src = (is_q ? P.q : P.k) + (size_t) t * P.ld + head * hd;
     const float *nw = is_q ? P.q_norm : P.k_norm;
     float scale = 1.0f;
     if (nw) {

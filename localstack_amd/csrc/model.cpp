@@ -173,6 +173,8 @@ struct lstk_model {
           *part = nullptr, *weights = nullptr;
     int32_t *ids = nullptr, *slots = nullptr, *in = nullptr; // in = tokens | cells | positions
     uint16_t *hn16 = nullptr, *attn16 = nullptr;             // fp16 inputs of the multi-token products
+    int ld_qkv = 0; // row stride of q | k | v (one buffer: token t's Q, K and V rows side by side)
+    std::vector<char> qkv_joined; // per layer: wk follows wq and wv follows wk in memory
     float *rope_cs = nullptr; // [n_batch][head_dim / 2][2] cos / sin of the step's RoPE angles
     rocblas_handle blas = nullptr;
     // pinned host staging
@@ -276,11 +278,9 @@ int create(const lstk_qwen3_hparams *hpp, const lstk_qwen3_weights *w, lstk_pool
         {(void **) &M->kcache, 2 * M->layer_elems * hp.n_layer * sizeof(uint16_t)},
         {(void **) &M->x, nb * h * 4},
         {(void **) &M->hn, nb * h * 4},
-        {(void **) &M->q, nb * hq * 4},
+        {(void **) &M->q, nb * (hq + 2 * hk) * 4},
         {(void **) &M->qr, nb * hq * 4},
         {(void **) &M->attn, nb * hq * 4},
-        {(void **) &M->k, nb * hk * 4},
-        {(void **) &M->v, nb * hk * 4},
         {(void **) &M->part, part_rows * (hp.head_dim + 4) * 4},
         {(void **) &M->weights, nb * k * 4},
         {(void **) &M->ids, nb * k * 4},
@@ -305,6 +305,14 @@ int create(const lstk_qwen3_hparams *hpp, const lstk_qwen3_weights *w, lstk_pool
         off += (p.bytes + 255) / 256 * 256;
     }
     M->vcache = M->kcache + M->layer_elems * hp.n_layer;
+    M->ld_qkv = (int) (hq + 2 * hk);
+    M->k = M->q + hq;
+    M->v = M->k + hk;
+    M->qkv_joined.resize(hp.n_layer);
+    for (int l = 0; l < hp.n_layer; l++) {
+        const lstk_qwen3_layer &L = w->layers[l];
+        M->qkv_joined[l] = L.wk == L.wq + hq * h && L.wv == L.wk + hk * h;
+    }
     // zero K/V (a masked cell is never read, but keep the cache free of stale NaNs as the reference
     // does, src/kv_cache.cpp:31) and mark every cell empty
     if ((e = hipMemset(M->kcache, 0, 2 * M->layer_elems * hp.n_layer * sizeof(uint16_t))) != hipSuccess ||
@@ -451,9 +459,9 @@ int forward(lstk_model *M, int32_t seq, int T, int n_cells, float *d_logits, int
     for (int l = 0; l < hp.n_layer; l++) {
         const lstk_qwen3_layer &L = M->layers[l];
         lstk::GemvParams gp{};
-        gp.seg[0] = {L.wq, M->q, nullptr, hq, hq};
-        gp.seg[1] = {L.wk, M->k, nullptr, hk, hk};
-        gp.seg[2] = {L.wv, M->v, nullptr, hk, hk};
+        gp.seg[0] = {L.wq, M->q, nullptr, hq, M->ld_qkv};
+        gp.seg[1] = {L.wk, M->k, nullptr, hk, M->ld_qkv};
+        gp.seg[2] = {L.wv, M->v, nullptr, hk, M->ld_qkv};
         gp.nseg = 3;
         gp.rows_total = hq + 2 * hk;
         gp.cols = h;
@@ -477,15 +485,18 @@ int forward(lstk_model *M, int32_t seq, int T, int n_cells, float *d_logits, int
         }
         uint16_t *kc = M->kcache + M->layer_elems * l, *vc = M->vcache + M->layer_elems * l;
         lstk::RopeParams rp{M->q, M->k, M->v, L.q_norm, L.k_norm, hp.rms_eps, d_pos, d_cells, seq, M->cell_seq, M->cell_pos,
-                            T, hp.n_head, hp.n_head_kv, hd, (int) M->kv.size, M->theta_scale, M->qr, kc, vc, M->rope_cs};
+                            T, hp.n_head, hp.n_head_kv, hd, (int) M->kv.size, M->theta_scale, M->qr, kc, vc, M->rope_cs,
+                            M->ld_qkv};
         // one token (its query rows in one 16-row tile): QK-norm, RoPE and the K / V store run inside
         // the attention launch
         const bool rope_in_attn = T == 1 && hp.n_head / hp.n_head_kv <= 16;
         if (blas) {
             const int rc = timed_span(M, 1, st, [&] {
-                int r = blas_gemm(M, L.wq, hq, h, M->hn16, T, M->q, hq, false, st);
-                if (r == LSTK_OK) r = blas_gemm(M, L.wk, hk, h, M->hn16, T, M->k, hk, false, st);
-                if (r == LSTK_OK) r = blas_gemm(M, L.wv, hk, h, M->hn16, T, M->v, hk, false, st);
+                // Q, K and V rows side by side in the output; one product when the weights are too
+                if (M->qkv_joined[l]) return blas_gemm(M, L.wq, hq + 2 * hk, h, M->hn16, T, M->q, M->ld_qkv, false, st);
+                int r = blas_gemm(M, L.wq, hq, h, M->hn16, T, M->q, M->ld_qkv, false, st);
+                if (r == LSTK_OK) r = blas_gemm(M, L.wk, hk, h, M->hn16, T, M->k, M->ld_qkv, false, st);
+                if (r == LSTK_OK) r = blas_gemm(M, L.wv, hk, h, M->hn16, T, M->v, M->ld_qkv, false, st);
                 return r;
             });
             if (rc != LSTK_OK) return rc;
