@@ -30,8 +30,10 @@
 namespace lstk {
 namespace {
 
-constexpr int kRouteEPW = 2;      // experts per wavefront in the router tile
-constexpr int kRouteEG = 8;       // experts per router work-group (4 wavefronts x 2)
+// Experts per wavefront in the router tile: 2 when a work-group serves several tokens (its router
+// rows stay in registers over them), 1 for a single token, where twice the work-groups each wait
+// on half the rows. A work-group takes 4 EPW experts (4 wavefronts).
+constexpr int kRouteEPWMax = 2;
 constexpr int kRouteMaxNG = 16;   // n_embd <= 4096: 16 groups of 256 per lane
 constexpr int kDnRows = 64;       // rows per down work-group
 constexpr int kTC = 8;            // tokens staged per pass
@@ -79,9 +81,10 @@ __device__ __forceinline__ void norm_row(const float *x, const float *wn, int n,
 // summed by wave_sum_tree. The oracle evaluates the same expression in the same order, so the
 // logits agree bit for bit and so does the top-k. F16 weights see fp16-rounded activations, as
 // ggml's CPU mul_mat converts src1 to the F16 vec_dot_type (src/qwen3.cpp:178).
-// The wavefront's two weight rows are loaded before the activations are staged.
-template <int GT, int NG>
+// The wavefront's kRouteEPW weight rows are loaded before the activations are staged.
+template <int GT, int NG, int kRouteEPW>
 __device__ __forceinline__ void route_tile(const RouteParams &P, int b, float *xs, int tt, int ns, double *s_part) {
+    constexpr int kRouteEG = 4 * kRouteEPW;
     const int n_eg = (P.E + kRouteEG - 1) / kRouteEG;
     const int tile = b / n_eg, eg = b - tile * n_eg;
     constexpr int h = NG * 256;
@@ -204,13 +207,13 @@ __device__ __forceinline__ void route_tile(const RouteParams &P, int b, float *x
     }
 }
 
-template <int GT, int NG>
+template <int GT, int NG, int EPW>
 __global__ __launch_bounds__(kBlock) void route_kernel(RouteParams P, int n_route_wg, int n_quant_wg, int route_tt, int route_ns) {
     extern __shared__ __align__(16) float lds[];
     __shared__ double s_part[kBlock / kWave];
     const int b = blockIdx.x;
     if (b < n_route_wg) {
-        route_tile<GT, NG>(P, b, lds, route_tt, route_ns, s_part);
+        route_tile<GT, NG, EPW>(P, b, lds, route_tt, route_ns, s_part);
     } else if (P.qtype != 0) {
         const int h = P.h;
         if (P.x_raw) {
@@ -866,16 +869,18 @@ hipError_t launch_route_t(const RouteParams &P, hipStream_t st, const LaunchTimi
     // the in-launch normalisation serves one token and needs the quantizing work-group to store the row
     if (P.x_raw && (P.T != 1 || !P.norm_w || !P.hnorm_out || !P.qtype)) return hipErrorInvalidValue;
     int n_route = 0, tt = 1, ns = 1;
+    const int epw = P.T == 1 ? 1 : kRouteEPWMax;
     if (P.do_route) {
         tt = route_tile_tokens(P.h);
         // many tokens: each work-group keeps its router rows in registers over 4 stages of tokens
         ns = P.T > 8 * tt ? 4 : 1;
-        n_route = ((P.T + tt * ns - 1) / (tt * ns)) * ((P.E + kRouteEG - 1) / kRouteEG);
+        n_route = ((P.T + tt * ns - 1) / (tt * ns)) * ((P.E + 4 * epw - 1) / (4 * epw));
     }
     const int n_quant = P.qtype ? std::min(P.T, 256) : 0;
     const int grid = std::max(1, n_route + n_quant);
     const size_t lds = P.do_route ? (size_t) tt * P.h * 4 : 16;
-    return launch(route_kernel<GT, NG>, dim3(grid), dim3(kBlock), lds, st, tm, P, n_route, n_quant, tt, ns);
+    if (epw == 1) return launch(route_kernel<GT, NG, 1>, dim3(grid), dim3(kBlock), lds, st, tm, P, n_route, n_quant, tt, ns);
+    return launch(route_kernel<GT, NG, kRouteEPWMax>, dim3(grid), dim3(kBlock), lds, st, tm, P, n_route, n_quant, tt, ns);
 }
 
 template <int GT>
