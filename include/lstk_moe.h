@@ -163,6 +163,22 @@ int lstk_moe_block(lstk_pool *pool, int layer, const float *d_hnorm, const void 
                    const float *d_resid, float *d_out, int32_t *d_ids, float *d_weights, int n_tokens,
                    lstk_stream_t stream);
 
+/* No counterpart in the reference: lstk_moe_block for callers that cannot allocate device memory
+ * (code under HIP graph capture, tight serving loops, harnesses that forbid hipMalloc). The call's
+ * scratch (quantized activations, router logits, SwiGLU rows, per-pair outputs) comes from a fixed
+ * array of LSTK_NOALLOC_SCRATCH_BYTES in the library, one copy per device, held until the process
+ * ends; the call allocates nothing and creates no events. Same arguments, kernels and results as
+ * lstk_moe_block, except that it never takes the fused or the grouped (matrix-core prefill) path and
+ * keeps no stage timing. Fails with LSTK_E_INVALID when n_tokens needs more scratch than the array
+ * holds: n_tokens * (n_embd * (1.25 + 4 k) + 4 E + 4 k n_ff_exp) bytes, each part rounded up to 256
+ * (up to 180 tokens at the 30B-A3B shape, 90 at the 235B-A22B shape; n_batch of the pool still applies). Every call on a device shares that device's
+ * array, which keeps the last call's contents: calls that overlap on one device race, whatever pool
+ * or stream they use. */
+#define LSTK_NOALLOC_SCRATCH_BYTES ((size_t) 16 << 20)
+int lstk_moe_block_noalloc(lstk_pool *pool, int layer, const float *d_hnorm, const void *d_gate_inp, int gate_type,
+                           const float *d_resid, float *d_out, int32_t *d_ids, float *d_weights, int n_tokens,
+                           lstk_stream_t stream);
+
 /* The token-to-expert grouping of ggml's CPU mul_mat_id (the three calls at src/qwen3.cpp:201-204) on
  * the device: the n_tokens * n_expert_used pairs (t, j), pair index t * n_expert_used + j, are sorted by
  * bin d_bins[t][j] in [0, n_bins), bins ascending and each bin's pairs in token-major order (a stable

@@ -90,6 +90,7 @@ SIGNATURES = {
     "lstk_moe_route": (_I, [_P, _I, _P, _I, _P, _I, _P, _P, _P]),
     "lstk_moe_ffn": (_I, [_P, _I, _P, _P, _P, _P, _P, _I, _P]),
     "lstk_moe_block": (_I, [_P, _I, _P, _P, _I, _P, _P, _P, _P, _I, _P]),
+    "lstk_moe_block_noalloc": (_I, [_P, _I, _P, _P, _I, _P, _P, _P, _P, _I, _P]),
     "lstk_moe_permute": (_I, [_P, _P, _I, _I, _P, _P, _P, _P]),
     "lstk_pool_check": (_I, [_P, _P]),
     "lstk_pool_set_timing": (_I, [_P, _I]),
@@ -297,6 +298,12 @@ class ExpertStore:
         T = hnorm.shape[0] if n_tokens is None else n_tokens
         _check(lib().lstk_moe_block(self._h, layer, _ptr(hnorm), _ptr(gate_inp), gate_type, _ptr(resid), _ptr(out),
                                     _ptr(ids), _ptr(weights), T, _stream(stream)))
+
+    def block_noalloc(self, layer, hnorm, gate_inp, gate_type, resid, out, ids, weights, n_tokens=None, stream=None):
+        """block() with the call's scratch in the library's fixed per-device array (allocates nothing)."""
+        T = hnorm.shape[0] if n_tokens is None else n_tokens
+        _check(lib().lstk_moe_block_noalloc(self._h, layer, _ptr(hnorm), _ptr(gate_inp), gate_type, _ptr(resid),
+                                            _ptr(out), _ptr(ids), _ptr(weights), T, _stream(stream)))
 
     def permute(self, bins, n_bins, counts, offsets, perm, n_tokens=None, stream=None):
         """Stable grouping of the (token, slot) pairs by bin, as ggml's CPU mul_mat_id walks them."""
