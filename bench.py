@@ -21,9 +21,13 @@ prefill: the same layer with Q4_K experts as a 512-token prefill with a Zipf(1.1
 roofline (algorithmic flops per second against the int8 MFMA peak, and expert bytes per second
 against HBM).
 
-model30b (--model30b): the whole 30B-A3B-shaped model - attention, MoE blocks and the 151936-token
-output head - decoding one sequence at a 4096-token KV context, T = 1, 8 and 32 tokens per step, each
-step a replay of the captured forward pass.
+stack235 (on by default, --no-stack235 skips it): the Qwen3-235B-A22B-shaped 94-layer Q4_K MoE stack at
+batch 1, fully resident (~128 GB of HBM) and with the expert pool capped at 32 GiB (misses streamed from
+pinned host memory; host acquire and device acquire).
+
+model30b (on by default, --no-model30b skips it): the whole 30B-A3B-shaped model - attention, MoE
+blocks and the 151936-token output head - decoding one sequence at a 4096-token KV context, T = 1, 8
+and 32 tokens per step, each step a replay of the captured forward pass; and a 512-token prompt step.
 
 cpu_baseline: the oracle (a C restatement of ggml's CPU algorithm: Q8_0 activations, int8 block
 dots, OpenMP) runs the same layer on the host cores for a bounded sample of layer passes, each with
@@ -60,14 +64,14 @@ def parse():
     ap.add_argument("--no-prefill", action="store_true")
     ap.add_argument("--prefill-layers", type=int, default=8)
     ap.add_argument("--no-decode", action="store_true", help="skip the decode legs (profiling the prefill leg alone)")
-    ap.add_argument("--stack235", action="store_true",
-                    help="also run the Qwen3-235B-A22B-shaped 94-layer Q4_K stack: resident (~128 GB of HBM) and "
-                         "with the pool capped at --pool-gib GiB (misses streamed from the pinned host tier)")
+    ap.add_argument("--no-stack235", action="store_true",
+                    help="skip the Qwen3-235B-A22B-shaped 94-layer Q4_K stack (resident, ~128 GB of HBM, and with the "
+                         "pool capped at --pool-gib GiB, misses streamed from the pinned host tier)")
     ap.add_argument("--stack235-layers", type=int, default=94)
     ap.add_argument("--pool-gib", type=int, default=32)
     ap.add_argument("--stream-tokens", type=int, default=8)
-    ap.add_argument("--model30b", action="store_true",
-                    help="also decode the whole 30B-A3B-shaped model (attention + MoE + head) at a long KV context")
+    ap.add_argument("--no-model30b", action="store_true",
+                    help="skip the whole 30B-A3B-shaped model (attention + MoE + head) decoding at a long KV context")
     ap.add_argument("--model30b-layers", type=int, default=N_LAYER)
     ap.add_argument("--context", type=int, default=4096)
     ap.add_argument("--model30b-tokens", type=str, default="1,8,32", help="tokens per decode step, comma-separated")
@@ -235,7 +239,9 @@ def prefill_leg(torch, L, n_layer, T, steps, warmup):
     layer_s = ms * 1e-3 / n_layer
     gu_s = per_block[1] * 1e-3
     del graph
-    return dict(T=T, n_layer=n_layer, ms_per_step=ms, tok_s=T * n_layer / (ms * 1e-3), layer_us=layer_s * 1e6,
+    # layer_tok_s: prompt tokens per second through ONE MoE layer (T tokens x n_layer layer copies per step); a
+    # 48-layer model's prompt rate through its MoE blocks is layer_tok_s / 48
+    return dict(T=T, n_layer=n_layer, ms_per_step=ms, layer_tok_s=T * n_layer / (ms * 1e-3), layer_us=layer_s * 1e6,
                 stage_us_per_block={"route_topk_permute": per_block[0] * 1e3, "gate_up": per_block[1] * 1e3,
                                     "quant_down": per_block[2] * 1e3, "combine": per_block[3] * 1e3},
                 active_experts=active, max_tokens_per_expert=int(max(c.max() for c in counts)),
@@ -293,6 +299,9 @@ def stack235_leg(torch, L, n_layer, pool_gib, steps, warmup, stream_tokens):
     per_tok = n_layer * (K * 3 * mat + E * H5 * 2 + H5 * 8)
     res["resident"] = {"tok_s": 1000.0 / ms, "ms_per_token": ms, "bytes_per_token": per_tok,
                        "gbs": per_tok / (ms * 1e-3) / 1e9, "frac_hbm": per_tok / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS,
+                       "roofline": {"bound": "hbm", "achieved": per_tok / (ms * 1e-3) / 1e9, "peak": HBM_PEAK_GBS,
+                                    "unit": "GB/s", "frac": per_tok / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS,
+                                    "what": "94 layers x (8 routed Q4_K experts + F16 router + hnorm in/out) per token"},
                        "hbm_gb": store.total_bytes() / 1e9}
     del graph
     store.close()
@@ -475,6 +484,9 @@ def model30b_leg(torch, L, n_layer, ctx, steps, warmup, t_list=(1, 8, 32)):
         if T == 1:
             r["gbs"] = per_tok / (ms * 1e-3) / 1e9
             r["frac_hbm"] = r["gbs"] / HBM_PEAK_GBS
+            r["roofline"] = {"bound": "hbm", "achieved": r["gbs"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                             "frac": r["frac_hbm"],
+                             "what": "48 x (attention weights + K/V of the context + router + 8 Q4_K experts) + head"}
             r["moe_gbs_eager"] = n_layer * moe_b / (moe_ms * 1e-3) / 1e9
         res[f"T{T}"] = r
         log(f"[bench] 30B model T={T}: {json.dumps(r)}")
@@ -565,10 +577,10 @@ def main():
         out = {}
         if not a.no_prefill:
             out["prefill"] = prefill_leg(torch, L, a.prefill_layers, 512, max(5, a.steps // 5), 2)
-        if a.stack235:
+        if not a.no_stack235:
             out["stack235"] = stack235_leg(torch, L, a.stack235_layers, a.pool_gib, max(5, a.steps // 2), 2,
                                            a.stream_tokens)
-        if a.model30b:
+        if not a.no_model30b:
             out["model30b"] = model30b_leg(torch, L, a.model30b_layers, a.context, max(5, a.steps // 5), 2,
                                             tuple(int(t) for t in a.model30b_tokens.split(",")))
         print(json.dumps(out), flush=True)
@@ -592,11 +604,11 @@ def main():
                            "achieved_gbs": pre["layer_hbm_gbs"], "hbm_peak_gbs": HBM_PEAK_GBS,
                            "frac_hbm": pre["layer_hbm_gbs"] / HBM_PEAK_GBS}
     s235 = None
-    if a.stack235:
+    if not a.no_stack235:
         s235 = stack235_leg(torch, L, a.stack235_layers, a.pool_gib, max(5, a.steps // 2), 2, a.stream_tokens)
         log(f"[bench] 235B stack: {json.dumps(s235)}")
     m30 = None
-    if a.model30b:
+    if not a.no_model30b:
         m30 = model30b_leg(torch, L, a.model30b_layers, a.context, max(5, a.steps // 5), 2,
                                             tuple(int(t) for t in a.model30b_tokens.split(",")))
     cpu = None if a.no_cpu else cpu_baseline(a.tokens, a.cpu_seconds)
@@ -621,6 +633,9 @@ def main():
         "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": achieved / HBM_PEAK_GBS,
                      "traffic": measured_traffic("gate_up_T1") if (a.tokens == 1 and a.layers == N_LAYER) else None,
+                     "traffic_source": "not measured in this run: FETCH_SIZE + WRITE_SIZE per gate_up launch from two "
+                                       "rocprofv3 --pmc passes over this same command, scaled by a plain copy, kept in "
+                                       "profiles/moe_decode_30b_q8_0_traffic.txt",
                      "kernel": "gate_up",
                      "kernel_avg_us": main_res["stage_avg_us"]["gate_up"],
                      "bytes_per_launch": main_res["gate_up_bytes"]},

@@ -82,6 +82,9 @@ typedef struct lstk_pool_stats_t {
 #define LSTK_POOL_DRY 2       /* bookkeeping only: no device memory, no HIP calls (CPU tests) */
 #define LSTK_POOL_DEVICE_LRU 4 /* streaming only: the slot bookkeeping lives on the device, acquires go
                                   through lstk_pool_acquire_device */
+#define LSTK_POOL_AUTO_SIZE 8  /* streaming only: pool_bytes is ignored and the pool takes
+                                  lstk_pool_default_bytes(expert table, 0, 0, total, free) from hipMemGetInfo
+                                  on the current device */
 
 const char *lstk_last_error(void);
 int lstk_abi_version(void);
@@ -98,6 +101,16 @@ int lstk_abi_version(void);
  * The layers' host pointers are only read during this call. */
 int lstk_pool_create(const lstk_moe_dims *dims, const lstk_expert_layer *layers, size_t pool_bytes,
                      uint32_t min_slots, uint32_t flags, lstk_pool **out);
+
+/* The pool budget of Engine::init (src/engine.cpp:84-117), restated for a GPU with its own HBM:
+ *   min(table_bytes, device_total - weight_bytes - kv_bytes - 1.5 GiB, device_free - 3 GiB), at least 16 KiB
+ * (each difference floored at 0). The reference also caps the pool at 45% of the table and at 9 GiB: limits
+ * of a Mac's unified memory and Metal working set that do not apply to 288 GB of HBM, where a table that
+ * fits is simply held whole. The 1024-slot shard limit stays (the device-side acquire stages a shard in
+ * LDS). Pure arithmetic, no device call: callers that know their dense weights and KV cache pass them
+ * with hipMemGetInfo's figures. */
+size_t lstk_pool_default_bytes(size_t table_bytes, size_t weight_bytes, size_t kv_bytes, size_t device_total,
+                               size_t device_free);
 void lstk_pool_destroy(lstk_pool *pool);
 
 /* ExpertStore::acquire (src/expert_store.cpp:232-286): makes `n` experts of `layer` resident and
@@ -171,9 +184,9 @@ int lstk_moe_block(lstk_pool *pool, int layer, const float *d_hnorm, const void 
  * lstk_moe_block, except that it never takes the fused or the grouped (matrix-core prefill) path and
  * keeps no stage timing. Fails with LSTK_E_INVALID when n_tokens needs more scratch than the array
  * holds: n_tokens * (n_embd * (1.25 + 4 k) + 4 E + 4 k n_ff_exp) bytes, each part rounded up to 256
- * (up to 180 tokens at the 30B-A3B shape, 90 at the 235B-A22B shape; n_batch of the pool still applies). Every call on a device shares that device's
- * array, which keeps the last call's contents: calls that overlap on one device race, whatever pool
- * or stream they use. */
+ * (up to 180 tokens at the 30B-A3B shape, 90 at the 235B-A22B shape; n_batch of the pool still
+ * applies). Every call on a device shares that device's array, which keeps the last call's contents:
+ * calls that overlap on one device race, whatever pool or stream they use. */
 #define LSTK_NOALLOC_SCRATCH_BYTES ((size_t) 16 << 20)
 int lstk_moe_block_noalloc(lstk_pool *pool, int layer, const float *d_hnorm, const void *d_gate_inp, int gate_type,
                            const float *d_resid, float *d_out, int32_t *d_ids, float *d_weights, int n_tokens,

@@ -25,7 +25,7 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(HERE, "liblstk_moe.so")
 
 TYPE_F32, TYPE_F16, TYPE_Q8_0, TYPE_Q4_K = 0, 1, 8, 12
-POOL_STREAMING, POOL_DRY, POOL_DEVICE_LRU = 1, 2, 4
+POOL_STREAMING, POOL_DRY, POOL_DEVICE_LRU, POOL_AUTO_SIZE = 1, 2, 4, 8
 E_INVALID, E_NOMEM, E_EXHAUSTED, E_DEVICE, E_IO, E_BADID = -1, -2, -3, -4, -5, -6
 
 
@@ -79,6 +79,7 @@ SIGNATURES = {
     "lstk_abi_version": (_I, []),
     "lstk_pool_create": (_I, [ctypes.POINTER(MoeDims), _P, _SZ, ctypes.c_uint32, ctypes.c_uint32, ctypes.POINTER(_P)]),
     "lstk_pool_destroy": (None, [_P]),
+    "lstk_pool_default_bytes": (_SZ, [_SZ, _SZ, _SZ, _SZ, _SZ]),
     "lstk_pool_acquire": (_I, [_P, _I, _P, _I, _P, _P]),
     "lstk_pool_acquire_device": (_I, [_P, _I, _P, _I, _P, _P]),
     "lstk_pool_release_all": (_I, [_P, _P]),
@@ -190,6 +191,13 @@ def matrix_bytes(type_, rows, cols):
     return lib().lstk_matrix_bytes(type_, rows, cols)
 
 
+def default_pool_bytes(table_bytes, weight_bytes, kv_bytes, device_total, device_free):
+    """Engine::init's pool budget (src/engine.cpp:84-117) for HBM: min(table, total - weights - kv - 1.5 GiB,
+    free - 3 GiB), at least 16 KiB."""
+    return lib().lstk_pool_default_bytes(int(table_bytes), int(weight_bytes), int(kv_bytes), int(device_total),
+                                         int(device_free))
+
+
 def repack_matrix(type_, rows, cols, gguf):
     gguf = np.ascontiguousarray(gguf, dtype=np.uint8)
     out = np.empty(matrix_bytes(type_, rows, cols), np.uint8)
@@ -212,7 +220,7 @@ class ExpertStore:
     """
 
     def __init__(self, n_layer, n_embd, n_ff_exp, n_expert, n_expert_used, n_batch, layers, pool_bytes=0,
-                 min_slots=0, streaming=False, dry=False, device_lru=False):
+                 min_slots=0, streaming=False, dry=False, device_lru=False, auto_size=False):
         self.dims = MoeDims(n_layer, n_embd, n_ff_exp, n_expert, n_expert_used, n_batch)
         arr = (ExpertLayer * n_layer)()
         self._keep = []
@@ -226,7 +234,8 @@ class ExpertStore:
                     self._keep.append(a)
                     ptrs.append(a.ctypes.data)
             arr[l] = ExpertLayer(types[0], types[1], types[2], *ptrs)
-        flags = (POOL_STREAMING if streaming else 0) | (POOL_DRY if dry else 0) | (POOL_DEVICE_LRU if device_lru else 0)
+        flags = ((POOL_STREAMING if streaming else 0) | (POOL_DRY if dry else 0) | (POOL_DEVICE_LRU if device_lru else 0) |
+                 (POOL_AUTO_SIZE if auto_size else 0))
         h = ctypes.c_void_p()
         _check(lib().lstk_pool_create(ctypes.byref(self.dims), ctypes.cast(arr, ctypes.c_void_p), int(pool_bytes),
                                       int(min_slots), flags, ctypes.byref(h)))
@@ -540,7 +549,7 @@ class GgufFile:
         return [((L.type_up, L.type_gate, L.type_down), L.host_up, L.host_gate, L.host_down) for L in arr]
 
 
-def load_qwen3_gguf(path, n_batch=64, kv_size=4096, device="cuda", pool_bytes=0, min_slots=0, streaming=False,
+def load_qwen3_gguf(path, n_batch=64, kv_size=4096, device="cuda", pool_bytes=None, min_slots=None, streaming=False,
                     device_lru=False):
     """qwen3_load_hparams + qwen3_map_weights + the expert pool (src/qwen3.cpp:16-109,
     src/engine.cpp:31-173) from a qwen3moe GGUF: returns (hparams, ExpertStore, Qwen3Model, GgufFile).
@@ -569,6 +578,22 @@ def load_qwen3_gguf(path, n_batch=64, kv_size=4096, device="cuda", pool_bytes=0,
             "q_norm": dense(p + "attn_q_norm.weight", (0,), optional=True),
             "k_norm": dense(p + "attn_k_norm.weight", (0,), optional=True),
             "ffn_norm": dense(p + "ffn_norm.weight", (0,)), "gate_inp": dense(p + "ffn_gate_inp.weight", (0, 1))})
+    if min_slots is None:
+        # a pool class never has fewer slots than one layer's experts (src/engine.cpp:114-116)
+        min_slots = max(hp["n_expert"], 2 * hp["n_expert_used"] + 2) if streaming else 0
+    if pool_bytes is None:
+        pool_bytes = 0
+        if streaming:
+            # Engine::init's budget (src/engine.cpp:84-117) from this device's memory, the dense weights and
+            # the KV cache
+            import torch
+            free_now, total = torch.cuda.mem_get_info(torch.device(device))
+            table = sum((matrix_bytes(t[0], hp["n_ff_exp"], hp["n_embd"]) + matrix_bytes(t[1], hp["n_ff_exp"], hp["n_embd"]) +
+                         matrix_bytes(t[2], hp["n_embd"], hp["n_ff_exp"])) * hp["n_expert"] for t, *_ in experts)
+            dense_bytes = sum(a.nbytes for a in (w["tok_embd"], w["output_norm"], w["output"]) if a is not None)
+            dense_bytes += sum(a.nbytes for lw in w["layers"] for a in lw.values() if a is not None)
+            kv = hp["n_layer"] * ((kv_size + 255) // 256 * 256) * hp["n_head_kv"] * hp["head_dim"] * 2 * 2
+            pool_bytes = default_pool_bytes(table, dense_bytes, kv, total, free_now)
     store = ExpertStore(hp["n_layer"], hp["n_embd"], hp["n_ff_exp"], hp["n_expert"], hp["n_expert_used"], n_batch,
                         experts, pool_bytes=pool_bytes, min_slots=min_slots, streaming=streaming,
                         device_lru=device_lru)

@@ -223,11 +223,18 @@ int parse(lstk_gguf *g, const std::string &path) {
             if (t.ne[d] < 0 || (t.ne[d] > 0 && (uint64_t) t.ne[d] > g->size * 8))
                 return set_error(LSTK_E_INVALID, "tensor " + t.name + " has an impossible shape");
         if (t.ne[0] % tt->block) return set_error(LSTK_E_INVALID, "tensor " + t.name + ": ne[0] is not a multiple of its block");
-        const unsigned __int128 n = (unsigned __int128) ((uint64_t) t.ne[0] / tt->block) * (uint64_t) t.ne[1] *
-                                    (uint64_t) t.ne[2] * (uint64_t) t.ne[3] * (uint64_t) tt->bytes;
-        if (t.offset % g->alignment || n > g->size || t.offset > g->size || g->data_offset + t.offset + (uint64_t) n > g->size)
+        // bytes = blocks * bytes per block, each partial product checked: a product of four dims near
+        // size * 8 can pass 2^64 (and would wrap any fixed-width integer)
+        uint64_t n = 0;
+        bool over = false;
+        if (t.ne[0] > 0 && t.ne[1] > 0 && t.ne[2] > 0 && t.ne[3] > 0) {
+            n = (uint64_t) t.ne[0] / tt->block;
+            for (int d = 1; d < 4 && !over; d++) over = __builtin_mul_overflow(n, (uint64_t) t.ne[d], &n) || n > g->size;
+            over = over || __builtin_mul_overflow(n, (uint64_t) tt->bytes, &n);
+        }
+        if (over || t.offset % g->alignment || n > g->size || t.offset > g->size || g->data_offset + t.offset + n > g->size)
             return set_error(LSTK_E_INVALID, "tensor " + t.name + " lies outside the file (truncated?): " + path);
-        t.nbytes = (uint64_t) n;
+        t.nbytes = n;
         t.offset += g->data_offset;
         g->t_index[t.name] = (size_t) (&t - g->tensors.data());
     }

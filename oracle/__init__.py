@@ -84,6 +84,15 @@ def lib():
     return _lib
 
 
+def diff_logits(ref, ours):
+    """diff_logits of src/main.cpp:195-207: max and RMS of |ref - ours| in double, and both argmaxes
+    (first index of the largest value, as std::max_element). Returns (max_abs, rms, ref_arg, our_arg)."""
+    r = np.asarray(ref, np.float64).ravel()
+    o = np.asarray(ours, np.float64).ravel()
+    d = np.abs(r - o)
+    return float(d.max()), float(np.sqrt(np.sum(d * d) / d.size)), int(np.argmax(r)), int(np.argmax(o))
+
+
 def _p(a):
     return a.ctypes.data_as(ctypes.c_void_p)
 

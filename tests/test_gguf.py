@@ -204,3 +204,20 @@ def test_architecture_and_unknown_types(lstk, tmp_path):
     synth.write_gguf(p, [("general.architecture", synth.GGUF_STR, "toy")], [("t", [1024], 0, bytes(16))])
     with pytest.raises(lstk.LstkError, match="lies outside the file"):
         lstk.GgufFile(p)
+
+
+def test_rejects_dims_whose_product_wraps(lstk, tmp_path):
+    """Four dims of 2^32 F32 values each pass the per-dim bound of a 640 MiB file, but their byte count,
+    2^130, wraps to 0 in 128-bit arithmetic; the reader must reject the tensor, not map it as 0 bytes.
+    The file is sparse: only its header is written."""
+    p = tmp_path / "wrap.gguf"
+    synth.write_gguf(p, [("general.architecture", synth.GGUF_STR, "toy")], [("t", [2 ** 32] * 4, 0, bytes(16))])
+    with open(p, "r+b") as f:
+        f.truncate(640 << 20)
+    with pytest.raises(lstk.LstkError, match="outside the file"):
+        lstk.GgufFile(p)
+    # the same file with dims whose product fits is read
+    synth.write_gguf(p, [("general.architecture", synth.GGUF_STR, "toy")], [("t", [4, 1, 1, 1], 0, bytes(16))])
+    with open(p, "r+b") as f:
+        f.truncate(640 << 20)
+    assert lstk.GgufFile(p).tensor_info("t")["nbytes"] == 16

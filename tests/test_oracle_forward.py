@@ -195,3 +195,10 @@ def test_context_full_is_an_error(tiny):
     m.decode(np.arange(8))
     with pytest.raises(RuntimeError):
         m.decode([1])
+
+
+def test_diff_logits_metric(orc):
+    """src/main.cpp:195-207: max |d|, sqrt(sum d^2 / n), and the first argmax of each side."""
+    mx, rms, ra, oa = orc.diff_logits(np.array([0.0, 1.0, 2.0, 2.0], np.float32), np.array([0.0, 1.5, 2.0, 3.0], np.float32))
+    assert mx == 1.0 and abs(rms - np.sqrt((0.25 + 1.0) / 4)) < 1e-15 and ra == 2 and oa == 3
+    assert orc.diff_logits([1.0, 1.0], [1.0, 1.0]) == (0.0, 0.0, 0, 0)

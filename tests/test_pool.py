@@ -185,3 +185,25 @@ def test_resident_acquire_is_identity(lstk):
     assert p.layer_slots(0) == 8
     with pytest.raises(lstk.LstkError):
         p.acquire(1, [8])
+
+
+def test_default_pool_bytes_hbm_budget(lstk):
+    """Engine::init's pool budget (src/engine.cpp:84-117) restated for HBM, with injected device figures."""
+    G = 1 << 30
+    f = lstk.default_pool_bytes
+    # a 235B-A22B-shaped Q4_K table fits whole on a 288 GB device: the pool holds the whole table
+    table = 94 * 128 * 3 * 3538944
+    assert f(table, 3 * G, 1 * G, 288 * 10**9, 280 * 10**9) == table
+    # a table larger than the device: total - weights - kv - 1.5 GiB bounds it
+    assert f(200 * G, 10 * G, 2 * G, 96 * G, 90 * G) == 96 * G - 10 * G - 2 * G - G - G // 2
+    # little free memory right now: free - 3 GiB bounds it
+    assert f(200 * G, 10 * G, 2 * G, 96 * G, 20 * G) == 17 * G
+    # nothing left: the 16 KiB floor (ExpertStore::init then raises each shard to its minimum slots)
+    assert f(200 * G, 90 * G, 10 * G, 96 * G, 2 * G) == 16 << 10
+    assert f(0, 0, 0, 96 * G, 96 * G) == 16 << 10
+
+
+def test_auto_size_needs_a_device_pool(lstk):
+    with pytest.raises(lstk.LstkError, match="AUTO_SIZE"):
+        lstk.ExpertStore(2, 256, 512, 8, 2, 4, [((8,) * 3, None, None, None)] * 2, pool_bytes=0, min_slots=8,
+                         streaming=True, dry=True, auto_size=True)
