@@ -445,7 +445,10 @@ def model30b_leg(torch, L, n_layer, ctx, steps, warmup, t_list=(1, 8, 32)):
         # past a sequence's end are masked), so one capture serves the whole run
         n_cells = (ctx + T * (steps + warmup + 3) + 255) // 256 * 256
         toks = rng.integers(0, hp["n_vocab"], (steps + warmup + 4, T)).astype(np.int32)
-        # per-stage device time from two eager steps
+        # per-stage device time from two eager steps (after one untimed step: the first multi-token step
+        # loads the library GEMM's kernels)
+        model.decode(seq, toks[-1], logits=logits)
+        model.truncate_seq(seq, ctx)
         model.set_timing(True)
         store.set_timing(True)
         for i in range(2):

@@ -117,6 +117,13 @@ int32_t lstk_model_seq_len(const lstk_model *model, int32_t seq);
  * at that KV length without a prefill; it has no counterpart in the reference. */
 int lstk_model_fill_context(lstk_model *model, int32_t seq, int n_cells, uint64_t seed, lstk_stream_t stream);
 
+/* Test hook (no counterpart in the reference): with d_states set, every forward also copies the residual
+ * stream after each layer l, [T][n_embd] f32, to d_states + l * T * n_embd (a device buffer of at least
+ * n_layer * n_batch * n_embd floats) on its stream, so a test can compare the model layer by layer with
+ * a reference fed the same layer inputs; NULL turns it off. After the last layer only the output row has
+ * been through the MoE block. */
+int lstk_model_debug_capture(lstk_model *model, float *d_states);
+
 /* Engine::set_routing_trace (src/engine.cpp:179-186): with a path, creates the file and writes the
  * trace header ("LSTKRTE1", n_layer, n_expert, n_expert_used as little-endian int32); every later step
  * of lstk_model_decode then appends its token count and its router ids ([n_layer][n_tokens][k] int32,

@@ -108,6 +108,7 @@ SIGNATURES = {
     "lstk_model_forward": (_I, [_P, ctypes.c_int32, _I, ctypes.c_int32, _P, _P, _P]),
     "lstk_model_fill_context": (_I, [_P, ctypes.c_int32, _I, ctypes.c_uint64, _P]),
     "lstk_model_set_trace": (_I, [_P, ctypes.c_char_p]),
+    "lstk_model_debug_capture": (_I, [_P, _P]),
     "lstk_model_remove_seq": (_I, [_P, ctypes.c_int32]),
     "lstk_model_truncate_seq": (_I, [_P, ctypes.c_int32, ctypes.c_int32]),
     "lstk_model_seq_len": (ctypes.c_int32, [_P, ctypes.c_int32]),
@@ -432,6 +433,12 @@ class Qwen3Model:
     def fill_context(self, seq, n_cells, seed=0, stream=None):
         """Appends n_cells synthetic positions (seeded random K/V, no tokens run) to sequence seq."""
         _check(lib().lstk_model_fill_context(self._h, int(seq), int(n_cells), int(seed), _stream(stream)))
+
+    def debug_capture(self, states):
+        """Test hook: every forward copies the residual stream after each layer into the device tensor
+        states ([n_layer][T][n_embd] f32, T the step's tokens); None turns it off."""
+        self._capture = states
+        _check(lib().lstk_model_debug_capture(self._h, None if states is None else _ptr(states)))
 
     def set_trace(self, path):
         """Routing trace to `path` (LSTKRTE1, read by localstack_amd.trace); None closes it."""

@@ -183,6 +183,8 @@ struct lstk_model {
     // timing
     bool timing = false;
     std::vector<TimedLaunch> launched[kStages];
+    // test hook: the residual stream after every layer, [n_layer][T][n_embd] (lstk_model_debug_capture)
+    float *capture = nullptr;
     // routing trace
     FILE *trace = nullptr;
     int32_t *trace_dev = nullptr; // [n_layer][n_batch][k] when the caller passes no trace buffer
@@ -559,6 +561,9 @@ int forward(lstk_model *M, int32_t seq, int T, int n_cells, float *d_logits, int
         }
         const int rc = moe(M, l, rows, xr, ids, st, norm_in_router ? L.ffn_norm : nullptr);
         if (rc != LSTK_OK) return rc;
+        if (M->capture && (e = hipMemcpyAsync(M->capture + (size_t) l * T * h, M->x, (size_t) T * h * sizeof(float),
+                                              hipMemcpyDeviceToDevice, st)) != hipSuccess)
+            return hip_fail(e, "capture copy");
     }
     lstk::NormParams onp{M->x + (size_t) (T - 1) * h, nullptr, nullptr, nullptr, M->output_norm, M->hn, 1, h, hp.rms_eps};
     if ((e = timed(M, 0, [&](const lstk::LaunchTiming *tm) { return lstk::launch_rmsnorm(onp, st, tm); })) != hipSuccess)
@@ -688,6 +693,12 @@ int lstk_model_fill_context(lstk_model *model, int32_t seq, int n_cells, uint64_
     } catch (const std::exception &ex) {
         return set_error(LSTK_E_NOMEM, std::string("lstk_model_fill_context: ") + ex.what());
     }
+    return LSTK_OK;
+}
+
+int lstk_model_debug_capture(lstk_model *model, float *d_states) {
+    if (!model) return set_error(LSTK_E_INVALID, "null model");
+    model->capture = d_states;
     return LSTK_OK;
 }
 

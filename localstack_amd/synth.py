@@ -91,6 +91,16 @@ def experts(rng, wtype, n_expert, rows, cols, std=0.02, centered=False):
     return np.concatenate(parts)
 
 
+def f16_spread(rng, rows, cols):
+    """rows x cols fp16 values drawn straight as bit patterns (fast for full-size models): a random sign, a
+    random 10-bit mantissa and a binary exponent in [-10, -6], so |w| lies in [2^-10, 2^-5) (std about
+    0.01, zero mean). Stands in for N(0, 0.02) dense weights where generating normals would dominate."""
+    r = rng.integers(0, 65536, size=(rows, cols), dtype=np.uint16)
+    exp = ((r >> np.uint16(10)) & np.uint16(0x1F)) % np.uint16(5) + np.uint16(5)
+    bits = (r & np.uint16(0x83FF)) | (exp << np.uint16(10))
+    return bits.view(np.float16)
+
+
 def router_f16(rng, n_expert, n_embd, std=0.02):
     """ffn_gate_inp [n_expert][n_embd] as fp16."""
     return (rng.standard_normal((n_expert, n_embd), dtype=np.float32) * np.float32(std)).astype(np.float16)

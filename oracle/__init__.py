@@ -66,6 +66,7 @@ def lib():
             "or_pool_slot_owner": (i32, [P, i32, i32, P, P]),
             "or_pool_lru": (i32, [P, i32, P, i32]),
             "or_dot_f16": (f32, [P, P, i32]),
+            "or_set_f16_double": (None, [i32]),
             "or_matmul_f16": (None, [P, i32, i32, P, i32, P]),
             "or_rms_norm": (None, [P, i32, P, f32, P]),
             "or_rope_neox": (None, [P, i32, i32, f32, P]),
@@ -75,6 +76,9 @@ def lib():
             "or_qwen3_decode": (i32, [P, P, i32, P, P]),
             "or_qwen3_len": (i32, [P]),
             "or_qwen3_truncate": (None, [P, i32]),
+            "or_qwen3_run_layer": (i32, [P, i32, P, i32, P]),
+            "or_qwen3_head": (None, [P, P, P]),
+            "or_qwen3_advance": (None, [P, i32]),
         }
         for name, (res, args) in sig.items():
             fn = getattr(L, name)
@@ -82,6 +86,12 @@ def lib():
             fn.argtypes = args
         _lib = L
     return _lib
+
+
+def set_f16_double(on):
+    """Sums every F16 dot product of the oracle in double (True) or in ggml's f32 SIMD order (False, the
+    default): the oracle's own sensitivity to a legitimate reordering."""
+    lib().or_set_f16_double(1 if on else 0)
 
 
 def diff_logits(ref, ours):
@@ -377,6 +387,26 @@ class Qwen3:
         if rc != 0:
             raise RuntimeError("context full")
         return (logits, trace) if want_trace else logits
+
+    def run_layer(self, l, x):
+        """Layer l on x [T][n_embd] (f32) at the current positions, K / V written there, position unchanged;
+        returns (x after the layer, router ids [T][k], -1 for rows the last layer skips)."""
+        xx = np.array(x, dtype=np.float32, order="C", copy=True)
+        T = xx.shape[0]
+        ids = np.zeros((T, self.hp["n_expert_used"]), np.int32)
+        if lib().or_qwen3_run_layer(self._h, int(l), _p(xx), T, _p(ids)) != 0:
+            raise RuntimeError("context full or bad layer")
+        return xx, ids
+
+    def head(self, x_row):
+        """The final RMSNorm and output head of one row: logits [n_vocab]."""
+        xr = _c(np.ravel(x_row), np.float32)
+        logits = np.zeros(self.hp["n_vocab"], np.float32)
+        lib().or_qwen3_head(self._h, _p(xr), _p(logits))
+        return logits
+
+    def advance(self, T):
+        lib().or_qwen3_advance(self._h, int(T))
 
     def __len__(self):
         return lib().or_qwen3_len(self._h)

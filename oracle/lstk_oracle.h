@@ -133,6 +133,8 @@ typedef struct or_qwen3_layer {
 } or_qwen3_layer;
 typedef struct or_qwen3 or_qwen3;
 
+/* Test hook: 1 sums every F16 dot in double (the oracle's own sensitivity to summation order). */
+void or_set_f16_double(int on);
 float or_dot_f16(const uint16_t *w, const uint16_t *x, int n);                                /* ggml_vec_dot_f16 */
 void or_matmul_f16(const uint16_t *W, int rows, int cols, const float *x, int T, float *y);     /* y [T][rows] */
 void or_rms_norm(const float *x, int n, const float *w, float eps, float *y);                  /* rms_norm (+ mul) */
@@ -143,6 +145,11 @@ or_qwen3 *or_qwen3_create(const or_qwen3_hparams *hp, const or_qwen3_layer *laye
                           const float *output_norm, const uint16_t *output, int max_ctx);
 void or_qwen3_destroy(or_qwen3 *m);
 int or_qwen3_decode(or_qwen3 *m, const int32_t *tokens, int T, float *logits, int32_t *trace);
+/* One layer on x [T][n_embd] in place (K / V written at len .. len + T - 1, len unchanged), the final
+ * norm + head of one row, and the position advance: or_qwen3_decode is these three in sequence. */
+int or_qwen3_run_layer(or_qwen3 *m, int l, float *x, int T, int32_t *ids);
+void or_qwen3_head(const or_qwen3 *m, const float *x, float *logits);
+void or_qwen3_advance(or_qwen3 *m, int T);
 int or_qwen3_len(const or_qwen3 *m);
 void or_qwen3_truncate(or_qwen3 *m, int keep);
 

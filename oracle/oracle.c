@@ -8,6 +8,7 @@
  */
 #include "lstk_oracle.h"
 
+#include <immintrin.h>
 #include <math.h>
 #include <stdio.h>
 #include <stdlib.h>
@@ -669,13 +670,30 @@ int or_pool_lru(const or_pool *P, int shard, int32_t *out, int cap) {
  * fp16, ggml's vec_dot_type for F16 weights); 4 accumulators of 8 lanes over steps of 32 values,
  * reduced x0+x2, x1+x3, then x0+x1, then the two 128-bit halves, then two horizontal adds; the tail
  * (n % 32 values) is summed in double. The fp16 products are exact in f32. */
+/* Sensitivity probe for the tests: with or_set_f16_double(1) every F16 dot is summed in double instead (a
+ * legitimate reordering that ggml itself could make), which shows how far the forward pass's logits move
+ * under rounding-level changes of its inputs alone. */
+static int g_f16_double = 0;
+void or_set_f16_double(int on) { g_f16_double = on; }
+
 float or_dot_f16(const uint16_t *w, const uint16_t *x, int n) {
+    if (g_f16_double) {
+        double s = 0.0;
+        for (int i = 0; i < n; i++) s += (double) h2f(w[i]) * (double) h2f(x[i]);
+        return (float) s;
+    }
+    /* acc[a][l] = acc[a][l] + w * x per lane, each multiply and add rounded on its own (8-lane AVX
+     * vectors of the same expression; F16C converts fp16 exactly) */
     float acc[4][8];
-    memset(acc, 0, sizeof(acc));
+    __m256 va[4] = {_mm256_setzero_ps(), _mm256_setzero_ps(), _mm256_setzero_ps(), _mm256_setzero_ps()};
     const int np = n & ~31;
     for (int i = 0; i < np; i += 32)
-        for (int a = 0; a < 4; a++)
-            for (int l = 0; l < 8; l++) acc[a][l] = acc[a][l] + h2f(w[i + 8 * a + l]) * h2f(x[i + 8 * a + l]);
+        for (int a = 0; a < 4; a++) {
+            const __m256 wv = _mm256_cvtph_ps(_mm_loadu_si128((const __m128i *) (w + i + 8 * a)));
+            const __m256 xv = _mm256_cvtph_ps(_mm_loadu_si128((const __m128i *) (x + i + 8 * a)));
+            va[a] = _mm256_add_ps(va[a], _mm256_mul_ps(wv, xv));
+        }
+    for (int a = 0; a < 4; a++) _mm256_storeu_ps(acc[a], va[a]);
     for (int l = 0; l < 8; l++) {
         acc[0][l] = acc[0][l] + acc[2][l];
         acc[1][l] = acc[1][l] + acc[3][l];
@@ -795,17 +813,17 @@ void or_qwen3_truncate(or_qwen3 *m, int keep) {
     if (keep < m->len) m->len = keep < 0 ? 0 : keep;
 }
 
-/* One Engine step of one sequence (qwen3_build_graph, src/qwen3.cpp:223-259): T tokens at positions
- * len .. len+T-1, each attending to every earlier position and itself; the last layer runs its FFN on
- * the last row only; logits [n_vocab] of the last token. trace (optional) [n_layer][T][k] receives the
- * router ids, -1 for the rows the last layer skips. Returns 0, or -1 when the context is full. */
-int or_qwen3_decode(or_qwen3 *m, const int32_t *tokens, int T, float *logits, int32_t *trace) {
+/* Layer l of the forward pass (src/qwen3.cpp:128-171 attention + residual, then the MoE block,
+ * :239-250) for T tokens at positions len .. len + T - 1: x [T][n_embd] is updated in place and the
+ * layer's K / V rows are written at those positions. The last layer runs its MoE block on the last row
+ * only (src/qwen3.cpp:233-238); ids [T][k] (optional) receive the router ids, -1 for rows it skips.
+ * Does not advance len (or_qwen3_advance does). Returns 0, or -1 when the context is full. */
+int or_qwen3_run_layer(or_qwen3 *m, int l, float *x, int T, int32_t *ids_out) {
     const or_qwen3_hparams *hp = &m->hp;
-    if (T < 1 || m->len + T > m->max_ctx) return -1;
+    if (T < 1 || l < 0 || l >= hp->n_layer || m->len + T > m->max_ctx) return -1;
     const int h = hp->n_embd, hd = hp->head_dim, nh = hp->n_head, nkv = hp->n_head_kv, k = hp->n_expert_used;
     const int hq = nh * hd, hk = nkv * hd, E = hp->n_expert, f = hp->n_ff_exp;
     const float kq_scale = 1.0f / sqrtf((float) hd);
-    float *x = (float *) malloc(sizeof(float) * (size_t) T * h);
     float *hn = (float *) malloc(sizeof(float) * (size_t) T * h);
     float *q = (float *) malloc(sizeof(float) * (size_t) T * hq);
     float *kk = (float *) malloc(sizeof(float) * (size_t) T * hk);
@@ -815,61 +833,52 @@ int or_qwen3_decode(or_qwen3 *m, const int32_t *tokens, int T, float *logits, in
     float *tmp = (float *) malloc(sizeof(float) * (size_t) (hd > h ? hd : h));
     float *wts = (float *) malloc(sizeof(float) * (size_t) T * k);
     int32_t *ids = (int32_t *) malloc(sizeof(int32_t) * (size_t) T * k);
-    for (int t = 0; t < T; t++)
-        for (int i = 0; i < h; i++) x[(size_t) t * h + i] = h2f(m->tok_embd[(size_t) tokens[t] * h + i]);
-    for (int l = 0; l < hp->n_layer; l++) {
-        const or_qwen3_layer *L = &m->layers[l];
-        for (int t = 0; t < T; t++) or_rms_norm(x + (size_t) t * h, h, L->attn_norm, hp->rms_eps, hn + (size_t) t * h);
-        or_matmul_f16(L->wq, hq, h, hn, T, q);
-        or_matmul_f16(L->wk, hk, h, hn, T, kk);
-        or_matmul_f16(L->wv, hk, h, hn, T, vv);
-        uint16_t *Kl = m->K + (size_t) l * m->max_ctx * hk, *Vl = m->V + (size_t) l * m->max_ctx * hk;
-        for (int t = 0; t < T; t++) {
-            const int pos = m->len + t;
-            for (int j = 0; j < nh; j++) {
-                float *qh = q + (size_t) t * hq + (size_t) j * hd;
-                if (L->q_norm) or_rms_norm(qh, hd, L->q_norm, hp->rms_eps, qh);
-                or_rope_neox(qh, hd, pos, m->theta_scale, tmp);
-                memcpy(qh, tmp, sizeof(float) * (size_t) hd);
-            }
-            for (int j = 0; j < nkv; j++) {
-                float *kh = kk + (size_t) t * hk + (size_t) j * hd;
-                if (L->k_norm) or_rms_norm(kh, hd, L->k_norm, hp->rms_eps, kh);
-                or_rope_neox(kh, hd, pos, m->theta_scale, tmp);
-                for (int d = 0; d < hd; d++) {
-                    Kl[(size_t) pos * hk + (size_t) j * hd + d] = or_fp32_to_fp16(tmp[d]);
-                    Vl[(size_t) pos * hk + (size_t) j * hd + d] = or_fp32_to_fp16(vv[(size_t) t * hk + (size_t) j * hd + d]);
-                }
-            }
+    const or_qwen3_layer *L = &m->layers[l];
+    for (int t = 0; t < T; t++) or_rms_norm(x + (size_t) t * h, h, L->attn_norm, hp->rms_eps, hn + (size_t) t * h);
+    or_matmul_f16(L->wq, hq, h, hn, T, q);
+    or_matmul_f16(L->wk, hk, h, hn, T, kk);
+    or_matmul_f16(L->wv, hk, h, hn, T, vv);
+    uint16_t *Kl = m->K + (size_t) l * m->max_ctx * hk, *Vl = m->V + (size_t) l * m->max_ctx * hk;
+    for (int t = 0; t < T; t++) {
+        const int pos = m->len + t;
+        for (int j = 0; j < nh; j++) {
+            float *qh = q + (size_t) t * hq + (size_t) j * hd;
+            if (L->q_norm) or_rms_norm(qh, hd, L->q_norm, hp->rms_eps, qh);
+            or_rope_neox(qh, hd, pos, m->theta_scale, tmp);
+            memcpy(qh, tmp, sizeof(float) * (size_t) hd);
         }
-#pragma omp parallel for collapse(2) schedule(static)
-        for (int t = 0; t < T; t++)
-            for (int j = 0; j < nh; j++) {
-                const int g = j / (nh / nkv);
-                or_attn_row(q + (size_t) t * hq + (size_t) j * hd, Kl + (size_t) g * hd, Vl + (size_t) g * hd, m->len + t + 1, hd,
-                            hk, kq_scale, att + (size_t) t * hq + (size_t) j * hd);
+        for (int j = 0; j < nkv; j++) {
+            float *kh = kk + (size_t) t * hk + (size_t) j * hd;
+            if (L->k_norm) or_rms_norm(kh, hd, L->k_norm, hp->rms_eps, kh);
+            or_rope_neox(kh, hd, pos, m->theta_scale, tmp);
+            for (int d = 0; d < hd; d++) {
+                Kl[(size_t) pos * hk + (size_t) j * hd + d] = or_fp32_to_fp16(tmp[d]);
+                Vl[(size_t) pos * hk + (size_t) j * hd + d] = or_fp32_to_fp16(vv[(size_t) t * hk + (size_t) j * hd + d]);
             }
-        or_matmul_f16(L->wo, h, hq, att, T, o);
-        for (size_t i = 0; i < (size_t) T * h; i++) x[i] = o[i] + x[i];
-        const int last = l == hp->n_layer - 1;
-        const int rows = last ? 1 : T;
-        float *xr = x + (size_t) (T - rows) * h;
-        for (int t = 0; t < rows; t++) or_rms_norm(xr + (size_t) t * h, h, L->ffn_norm, hp->rms_eps, hn + (size_t) t * h);
-        or_router(hn, rows, h, L->gate_inp, 1, E, k, ids, wts, NULL, NULL);
-        const size_t su = or_row_bytes(L->type_up, h) * f, sg = or_row_bytes(L->type_gate, h) * f,
-                     sd = or_row_bytes(L->type_down, f) * h;
-        or_moe_ffn(hn, rows, h, f, k, ids, wts, xr, L->up, L->gate, L->down, su, sg, sd, L->type_up, L->type_gate,
-                   L->type_down, xr, NULL, 8);
-        if (trace) {
-            int32_t *tr = trace + (size_t) l * T * k;
-            for (int i = 0; i < (T - rows) * k; i++) tr[i] = -1;
-            memcpy(tr + (size_t) (T - rows) * k, ids, sizeof(int32_t) * (size_t) rows * k);
         }
     }
-    or_rms_norm(x + (size_t) (T - 1) * h, h, m->output_norm, hp->rms_eps, tmp);
-    or_matmul_f16(m->output, hp->n_vocab, h, tmp, 1, logits);
-    m->len += T;
-    free(x);
+#pragma omp parallel for collapse(2) schedule(static)
+    for (int t = 0; t < T; t++)
+        for (int j = 0; j < nh; j++) {
+            const int g = j / (nh / nkv);
+            or_attn_row(q + (size_t) t * hq + (size_t) j * hd, Kl + (size_t) g * hd, Vl + (size_t) g * hd, m->len + t + 1, hd,
+                        hk, kq_scale, att + (size_t) t * hq + (size_t) j * hd);
+        }
+    or_matmul_f16(L->wo, h, hq, att, T, o);
+    for (size_t i = 0; i < (size_t) T * h; i++) x[i] = o[i] + x[i];
+    const int last = l == hp->n_layer - 1;
+    const int rows = last ? 1 : T;
+    float *xr = x + (size_t) (T - rows) * h;
+    for (int t = 0; t < rows; t++) or_rms_norm(xr + (size_t) t * h, h, L->ffn_norm, hp->rms_eps, hn + (size_t) t * h);
+    or_router(hn, rows, h, L->gate_inp, 1, E, k, ids, wts, NULL, NULL);
+    const size_t su = or_row_bytes(L->type_up, h) * f, sg = or_row_bytes(L->type_gate, h) * f,
+                 sd = or_row_bytes(L->type_down, f) * h;
+    or_moe_ffn(hn, rows, h, f, k, ids, wts, xr, L->up, L->gate, L->down, su, sg, sd, L->type_up, L->type_gate,
+               L->type_down, xr, NULL, 8);
+    if (ids_out) {
+        for (int i = 0; i < (T - rows) * k; i++) ids_out[i] = -1;
+        memcpy(ids_out + (size_t) (T - rows) * k, ids, sizeof(int32_t) * (size_t) rows * k);
+    }
     free(hn);
     free(q);
     free(kk);
@@ -879,5 +888,33 @@ int or_qwen3_decode(or_qwen3 *m, const int32_t *tokens, int T, float *logits, in
     free(tmp);
     free(wts);
     free(ids);
+    return 0;
+}
+
+/* The final RMSNorm and the output head of one row x [n_embd] (src/qwen3.cpp:252-258). */
+void or_qwen3_head(const or_qwen3 *m, const float *x, float *logits) {
+    const or_qwen3_hparams *hp = &m->hp;
+    float *tmp = (float *) malloc(sizeof(float) * (size_t) hp->n_embd);
+    or_rms_norm(x, hp->n_embd, m->output_norm, hp->rms_eps, tmp);
+    or_matmul_f16(m->output, hp->n_vocab, hp->n_embd, tmp, 1, logits);
+    free(tmp);
+}
+
+void or_qwen3_advance(or_qwen3 *m, int T) { m->len += T; }
+
+/* One step of the forward pass (src/qwen3.cpp:223-259) over T tokens: embedding, every layer (the last on
+ * the last row only), logits [n_vocab] of the last token. trace (optional) [n_layer][T][k] receives the
+ * router ids, -1 for the rows the last layer skips. Returns 0, or -1 when the context is full. */
+int or_qwen3_decode(or_qwen3 *m, const int32_t *tokens, int T, float *logits, int32_t *trace) {
+    const or_qwen3_hparams *hp = &m->hp;
+    if (T < 1 || m->len + T > m->max_ctx) return -1;
+    const int h = hp->n_embd, k = hp->n_expert_used;
+    float *x = (float *) malloc(sizeof(float) * (size_t) T * h);
+    for (int t = 0; t < T; t++)
+        for (int i = 0; i < h; i++) x[(size_t) t * h + i] = h2f(m->tok_embd[(size_t) tokens[t] * h + i]);
+    for (int l = 0; l < hp->n_layer; l++) or_qwen3_run_layer(m, l, x, T, trace ? trace + (size_t) l * T * k : NULL);
+    or_qwen3_head(m, x + (size_t) (T - 1) * h, logits);
+    m->len += T;
+    free(x);
     return 0;
 }

@@ -202,3 +202,24 @@ def test_diff_logits_metric(orc):
     mx, rms, ra, oa = orc.diff_logits(np.array([0.0, 1.0, 2.0, 2.0], np.float32), np.array([0.0, 1.5, 2.0, 3.0], np.float32))
     assert mx == 1.0 and abs(rms - np.sqrt((0.25 + 1.0) / 4)) < 1e-15 and ra == 2 and oa == 3
     assert orc.diff_logits([1.0, 1.0], [1.0, 1.0]) == (0.0, 0.0, 0, 0)
+
+
+def test_layer_by_layer_equals_decode(orc):
+    """run_layer over every layer + head + advance reproduces decode() bit for bit (ids too), so a
+    layer-by-layer comparison checks the same oracle the whole-model tests use."""
+    hp = dict(n_layer=2, n_embd=256, n_head=4, n_head_kv=2, head_dim=64, n_vocab=1024, n_expert=8, n_expert_used=2,
+              n_ff_exp=512, n_ctx_train=1024, rms_eps=1e-6, rope_freq_base=10000.0)
+    w = synth.qwen3_weights(np.random.default_rng(8), hp, wtype=8)
+    a, b = orc.Qwen3(hp, w, 32), orc.Qwen3(hp, w, 32)
+    feed = np.random.default_rng(9).integers(0, 1024, 6).astype(np.int32)
+    for _ in range(3):
+        la, ta = a.decode(feed, want_trace=True)
+        x = w["tok_embd"][feed].astype(np.float32)
+        tb = []
+        for l in range(hp["n_layer"]):
+            x, ids = b.run_layer(l, x)
+            tb.append(ids)
+        lb = b.head(x[-1])
+        b.advance(len(feed))
+        assert np.array_equal(la, lb) and np.array_equal(ta, np.array(tb)) and len(a) == len(b)
+        feed = np.array([np.argmax(la)], np.int32)
