@@ -654,13 +654,25 @@ bool gemv_supported(int cols) { return cols > 0 && cols % 8 == 0 && cols <= 8192
 bool attn_supported(int hd) { return hd == 64 || hd == 128 || hd == 256; }
 
 // Rows of a work-group: 16, 32 or 64 (one, two or four 16-row tiles). Chunks are whole 64-cell passes,
-// as many as bring the launch to about 512 work-groups. Then T * n_head * n_chunk <= 32768 + T * n_head.
+// as many as bring the launch to about kAttnTarget work-groups. Then T * n_head * n_chunk <= 32768 +
+// T * n_head. With rope_in (one token) every chunk is one pass while n_head * passes <= 32768 (65536
+// cells at 32 query heads, 32768 at 64): the RoPE prologue has only been run with single-pass chunks on
+// the device. Past that, rope_in is cleared (the caller runs rope_kernel) and chunks take several passes.
+constexpr int kAttnTarget = 512;
 void attn_plan(AttnParams &P) {
     const int rows = P.T * (P.n_head / P.n_kv);
     P.rb_rows = rows <= 16 ? 16 : rows <= 32 ? 32 : 64;
     P.n_rowblk = (rows + P.rb_rows - 1) / P.rb_rows;
     const int passes = (P.n_cells + kFaCells - 1) / kFaCells;
-    int want = (512 + P.n_kv * P.n_rowblk - 1) / (P.n_kv * P.n_rowblk);
+    if (P.rope_in) {
+        if ((long) P.n_head * passes <= 32768) {
+            P.chunk = kFaCells;
+            P.n_chunk = passes;
+            return;
+        }
+        P.rope_in = 0;
+    }
+    int want = (kAttnTarget + P.n_kv * P.n_rowblk - 1) / (P.n_kv * P.n_rowblk);
     want = want < 1 ? 1 : (want > passes ? passes : want);
     P.chunk = (passes + want - 1) / want * kFaCells;
     P.n_chunk = (P.n_cells + P.chunk - 1) / P.chunk;

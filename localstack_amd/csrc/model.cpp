@@ -505,8 +505,6 @@ int forward(lstk_model *M, int32_t seq, int T, int n_cells, float *d_logits, int
         } else if ((e = timed(M, 1, [&](const lstk::LaunchTiming *tm) { return lstk::launch_gemv(gp, st, tm); })) != hipSuccess) {
             return hip_fail(e, "qkv launch");
         }
-        if (!rope_in_attn && (e = timed(M, 1, [&](const lstk::LaunchTiming *tm) { return lstk::launch_rope(rp, st, tm); })) != hipSuccess)
-            return hip_fail(e, "rope launch");
         lstk::AttnParams ap{};
         ap.q = M->qr;
         ap.kc = kc;
@@ -527,7 +525,9 @@ int forward(lstk_model *M, int32_t seq, int T, int n_cells, float *d_logits, int
         ap.out16 = blas ? M->attn16 : nullptr;
         ap.rope_in = rope_in_attn ? 1 : 0;
         ap.rope = rp;
-        lstk::attn_plan(ap);
+        lstk::attn_plan(ap); // clears rope_in when the context is too long for one pass per chunk
+        if (!ap.rope_in && (e = timed(M, 1, [&](const lstk::LaunchTiming *tm) { return lstk::launch_rope(rp, st, tm); })) != hipSuccess)
+            return hip_fail(e, "rope launch");
         if ((e = timed(M, 2, [&](const lstk::LaunchTiming *tm) { return lstk::launch_attn(ap, st, tm); })) != hipSuccess ||
             (ap.n_chunk > 1 &&
              (e = timed(M, 2, [&](const lstk::LaunchTiming *tm) { return lstk::launch_attn_combine(ap, st, tm); })) != hipSuccess))

@@ -1,0 +1,184 @@
+"""CPU replay of the attention launch plan and of every index the attention kernels compute
+(localstack_amd/csrc/forward.hip: attn_plan, attn_kernel, attn_combine_kernel; buffers sized as
+model.cpp allocates them), for work-group targets of 512 (the build's), 256 and 128, over the shapes the
+tests and the benchmark run and past them: every global index stays inside its buffer, every LDS index
+inside its array, and the partial rows inside attn_part_rows. No GPU.
+
+Also a restatement of the kernel's online softmax over 64-cell passes (running max, sum and rescale per
+row, P split into fp16 hi + lo parts, passes in which a row sees no cell) against a direct softmax, and of
+the chunk combine, so the multi-pass arithmetic is checked on the CPU.
+"""
+import numpy as np
+import pytest
+
+FA_CELLS = 64       # kFaCells
+AT_BLOCK = 256      # kAtBlock: 4 wavefronts
+BLOCK = 256         # kBlock (attn_combine_kernel)
+LDS_MAX = 65536
+
+
+def plan(T, n_head, n_kv, n_cells, target=512, rope_in=False):
+    """attn_plan (forward.hip): rows per work-group, row blocks, chunk (cells), chunks; rope_in kept or not."""
+    rows = T * (n_head // n_kv)
+    rb_rows = 16 if rows <= 16 else 32 if rows <= 32 else 64
+    n_rowblk = (rows + rb_rows - 1) // rb_rows
+    passes = (n_cells + FA_CELLS - 1) // FA_CELLS
+    if rope_in:
+        if n_head * passes <= 32768:
+            return rb_rows, n_rowblk, FA_CELLS, passes, True
+        rope_in = False
+    want = (target + n_kv * n_rowblk - 1) // (n_kv * n_rowblk)
+    want = max(1, min(want, passes))
+    chunk = (passes + want - 1) // want * FA_CELLS
+    n_chunk = (n_cells + chunk - 1) // chunk
+    return rb_rows, n_rowblk, chunk, n_chunk, rope_in
+
+
+def part_rows(n_batch, n_head):
+    return 32768 + n_batch * n_head  # attn_part_rows
+
+
+def check_launch(T, n_head, n_kv, hd, kv_size, n_cells, n_batch, target, rope_in):
+    """Every access of one attention launch (and its combine) against the buffers' sizes."""
+    assert 1 <= T <= n_batch and 1 <= n_cells <= kv_size and kv_size % 256 == 0
+    grp = n_head // n_kv
+    rb_rows, n_rowblk, chunk, n_chunk, rope_in = plan(T, n_head, n_kv, n_cells, target, rope_in)
+    NRT = rb_rows // 16
+    RB, NK = 16 * NRT, hd // 16
+    DT = NK // 4
+    rows = T * grp
+    if rope_in:  # launch_attn's own condition
+        assert T == 1 and rb_rows == 16 and n_rowblk == 1 and grp <= 16
+    grid = n_kv * n_chunk * n_rowblk
+    wg = np.arange(grid)
+    g, rest = wg % n_kv, wg // n_kv
+    c, rb = rest % n_chunk, rest // n_chunk
+    assert c.max() < n_chunk and rb.max() < n_rowblk and g.max() < n_kv
+    begin = c * chunk
+    end = np.minimum(begin + chunk, n_cells)
+    assert (begin < end).all(), "a chunk without cells"
+    row0 = rb * rb_rows
+    # s_pos / Q rows: r < rows reads pos[r / grp] and q[(r / grp) * n_head + g * grp + r % grp]
+    r = row0[:, None] + np.arange(RB)[None, :]
+    on = r < rows
+    assert (r[on] // grp < T).all()
+    qrow = (r // grp) * n_head + g[:, None] * grp + r % grp
+    assert (qrow[on] < T * n_head).all() and (qrow[on] >= 0).all()
+    # RoPE prologue: rotated rows r < grp into s_q [16 * hd]
+    if rope_in:
+        assert grp * hd <= 16 * hd
+    # passes: cells c0 .. c0 + 63; V fragments at min(c0 + kc * 16 + 4 lq, kv_size - 4) + 0..3,
+    # K fragments and cell tables at min(cell, kv_size - 1)
+    last4 = kv_size - 4
+    kv_elems = n_kv * (hd // 4) * kv_size * 4
+    for b0, e0, gg in zip(begin, end, g):
+        c0 = np.arange(b0, e0, FA_CELLS)
+        cg = np.minimum(c0[:, None] + (np.arange(4)[:, None] * 16 + 4 * np.arange(4)[None, :]).ravel()[None, :], last4)
+        assert cg.min() >= 0 and (cg % 4 == 0).all()
+        d = np.arange(hd)
+        vi_max = ((gg * (kv_size // 4) + cg.max() // 4) * hd + d.max()) * 4 + 3
+        assert vi_max < kv_elems
+        cell = c0[:, None] + np.arange(FA_CELLS)[None, :]
+        cc = np.minimum(cell, kv_size - 1)
+        ki_max = ((gg * (hd // 4) + (hd // 4 - 1)) * kv_size + cc.max()) * 4 + 3
+        assert cc.max() < kv_size and ki_max < kv_elems
+    # LDS of attn_kernel: s_S [RB][64] f32, s_Ph / s_Pl [RB][72] u16, s_M / s_L / s_f [RB], s_pos [RB],
+    # s_q [16 hd] (NRT = 1) f32
+    lds = RB * FA_CELLS * 4 + 2 * RB * (FA_CELLS + 8) * 2 + 3 * RB * 4 + RB * 4 + (16 * hd if NRT == 1 else 1) * 4
+    assert lds <= LDS_MAX
+    # outputs: n_chunk == 1 writes out[(t * n_head + h) * hd + d]; else part rows
+    if n_chunk > 1:
+        t = r // grp
+        h = g[:, None] * grp + r % grp
+        prow = (t * n_head + h) * n_chunk + c[:, None]
+        assert (prow[on] < part_rows(n_batch, n_head)).all()
+        assert T * n_head * n_chunk <= part_rows(n_batch, n_head)
+        # attn_combine_kernel: grid (n_head, T), LDS [n_chunk rounded to 4] factors + [BLOCK / (hd / 4)][hd]
+        clds = (((n_chunk + 3) & ~3) + BLOCK // (hd // 4) * hd) * 4
+        assert clds <= LDS_MAX
+        assert ((T - 1) * n_head + n_head - 1) * n_chunk + n_chunk - 1 < part_rows(n_batch, n_head)
+    return rb_rows, n_rowblk, chunk, n_chunk, rope_in
+
+
+SHAPES = {"tiny": (4, 2, 64), "30b": (32, 4, 128), "235b": (64, 4, 128)}
+CELLS = [256, 512, 4352, 8192, 8256, 16384, 32768, 65536, 131072]
+
+
+@pytest.mark.parametrize("target", [512, 256, 128])
+@pytest.mark.parametrize("shape", list(SHAPES))
+def test_every_attention_index_in_bounds(target, shape):
+    n_head, n_kv, hd = SHAPES[shape]
+    grp = n_head // n_kv
+    plans = 0
+    for n_cells in CELLS:
+        kv_size = (n_cells + 255) // 256 * 256
+        for T in (1, 2, 8, 32, 64, 256, 512):
+            for n_batch in sorted({T, 64, 512}):
+                if T > n_batch:
+                    continue
+                rope = T == 1 and grp <= 16
+                check_launch(T, n_head, n_kv, hd, kv_size, n_cells, n_batch, target, rope)
+                plans += 1
+    assert plans > 100
+
+
+def test_rope_in_keeps_single_pass_chunks():
+    # one token at the 30B shape: one pass per chunk up to 65536 cells, then RoPE leaves the launch
+    assert plan(1, 32, 4, 4352, rope_in=True)[2:] == (64, 68, True)
+    assert plan(1, 32, 4, 65536, rope_in=True)[2:] == (64, 1024, True)
+    rb, nrb, chunk, n_chunk, rope = plan(1, 32, 4, 65600, rope_in=True)
+    assert not rope and chunk > 64
+    # the committed plan without RoPE: several passes per chunk once the target is reached
+    assert plan(32, 32, 4, 4352)[2] == 3 * 64
+    assert plan(512, 32, 4, 512)[2:4] == (4 * 64, 2)  # a 512-token prompt: 64 row blocks x 4 KV heads x 2
+
+
+def softmax_passes(s, T_rows, pass_cells=FA_CELLS):
+    """The kernel's online softmax for rows of scores s [rows][cells] (-inf = masked) over passes of
+    pass_cells: per pass m_new = max(m_old, max s), p = exp(s - m_new) split into fp16 hi + lo, f =
+    exp(m_old - m_new) (0 while m_old = -inf), L = L f + sum p, O = O f + (hi + lo) V. Returns
+    (m, L, O) per row for V = identity columns (O = the unnormalised weights)."""
+    rows, n = s.shape
+    m = np.full(rows, -np.inf, np.float32)
+    L = np.zeros(rows, np.float32)
+    O = np.zeros((rows, n), np.float32)
+    for c0 in range(0, n, pass_cells):
+        sv = s[:, c0:c0 + pass_cells]
+        mx = np.max(sv, axis=1)
+        m_new = np.maximum(m, mx)
+        with np.errstate(invalid="ignore"):
+            p = np.where(sv == -np.inf, 0.0, np.exp(sv - m_new[:, None])).astype(np.float32)
+        hi = p.astype(np.float16).astype(np.float32)
+        lo = (p - hi).astype(np.float16).astype(np.float32)
+        with np.errstate(invalid="ignore"):
+            f = np.where(m == -np.inf, 0.0, np.exp(m - m_new)).astype(np.float32)
+        L = L * f + p.sum(axis=1, dtype=np.float32)
+        O = O * f[:, None]
+        O[:, c0:c0 + pass_cells] += hi + lo
+        m = m_new
+    return m, L, O
+
+
+def test_online_softmax_over_passes_and_chunks_matches_direct():
+    rng = np.random.default_rng(5)
+    rows, n = 48, 1024
+    s = (rng.standard_normal((rows, n)) * 4).astype(np.float32)
+    # causal-like masks, rows that see nothing in early passes, one row that sees a single cell
+    for r in range(rows):
+        s[r, : (r * 37) % 700] = -np.inf
+        s[r, 900 + r:] = -np.inf
+    s[0, :] = -np.inf
+    s[0, 777] = 1.5
+    direct = np.exp(s.astype(np.float64) - np.max(s, axis=1, keepdims=True))
+    direct /= direct.sum(axis=1, keepdims=True)
+    m, L, O = softmax_passes(s, rows)
+    assert np.max(np.abs(O / L[:, None] - direct)) < 2e-6
+    assert O[0, 777] / L[0] == 1.0
+    # the same scores cut into chunks of 3 passes, each with its own (m, L, O), merged as the combine
+    # kernel merges them: out = sum_c O_c e^(m_c - M) / sum_c L_c e^(m_c - M)
+    parts = [softmax_passes(s[:, c0:c0 + 192], rows) for c0 in range(0, n, 192)]
+    M = np.max([p[0] for p in parts], axis=0)
+    fs = [np.where(p[0] == -np.inf, 0.0, np.exp(p[0] - M)) for p in parts]
+    Ls = sum(p[1] * f for p, f in zip(parts, fs))
+    Os = np.concatenate([p[2] * f[:, None] for p, f in zip(parts, fs)], axis=1)
+    assert np.max(np.abs(Os / Ls[:, None] - direct)) < 2e-6
