@@ -29,9 +29,10 @@ model30b (on by default, --no-model30b skips it): the whole 30B-A3B-shaped model
 blocks and the 151936-token output head - decoding one sequence at a 4096-token KV context, T = 1, 8
 and 32 tokens per step, each step a replay of the captured forward pass; and a 512-token prompt step.
 
-cpu_baseline: the oracle (a C restatement of ggml's CPU algorithm: Q8_0 activations, int8 block
-dots, OpenMP) runs the same layer on the host cores for a bounded sample of layer passes, each with
-new hnorm rows (so new experts).
+cpu_baseline: a CPU restatement of ggml semantics (oracle/cpu_ggml.c: Q8_0 / Q8_K activations, int8
+block dots with AVX-512 VNNI, OpenMP over (expert, row block); checked against the oracle by
+tests/test_cpu_ggml.py) runs the same decode layer on the host cores for a bounded sample of layer
+passes, each with new hnorm rows (so new experts), and the 512-token prefill layer for a few passes.
 """
 import argparse
 import json
@@ -513,35 +514,64 @@ def model30b_leg(torch, L, n_layer, ctx, steps, warmup, t_list=(1, 8, 32)):
     return res
 
 
+def cpu_model():
+    try:
+        with open("/proc/cpuinfo") as fh:
+            for line in fh:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
 def cpu_baseline(T, seconds):
-    """Times the oracle on this host over whole layer passes of the same workload."""
-    import oracle
+    """The CPU restatement of ggml semantics (oracle/cpu_ggml.c: Q8_0 / Q8_K activation quantization,
+    int8 block dots with AVX-512 VNNI where the host has it, OpenMP over (expert, 16-row block)) on this
+    host's cores: the decode layer (Q8_0, T tokens) for `seconds`, each pass with new hnorm rows so new
+    experts stream from DRAM; then the 512-token Q4_K Zipf prefill layer for a few passes."""
+    from oracle import cpu_ggml
     from localstack_amd import synth
     rng = np.random.default_rng(7)
+    cores = len(os.sched_getaffinity(0))
     gate_inp = synth.router_f16(rng, E, H)
-    # a different hnorm per pass, so each pass routes to other experts and the 642 MB expert table
-    # is streamed from DRAM rather than replayed from the host's last-level cache
     xs = [synth.activations(rng, T, H) for _ in range(64)]
     resid = synth.activations(rng, T, H)
-    up, gate, down = (synth.experts(rng, Q8_0, E, F, H).reshape(E, -1), synth.experts(rng, Q8_0, E, F, H).reshape(E, -1),
-                      synth.experts(rng, Q8_0, E, H, F).reshape(E, -1))
-    cores = len(os.sched_getaffinity(0))
-    os.environ.setdefault("OMP_NUM_THREADS", str(cores))
+    up, gate, down = (synth.experts(rng, Q8_0, E, F, H), synth.experts(rng, Q8_0, E, F, H),
+                      synth.experts(rng, Q8_0, E, H, F))
+    cpu_ggml.moe_block(xs[0], gate_inp, up, gate, down, Q8_0, resid, E, F, K, n_threads=cores)
     n = 0
     t0 = time.time()
     while True:
-        x = xs[n % len(xs)]
-        ids, w, _, _ = oracle.router(x, gate_inp, 1, K)
-        oracle.moe_ffn(x, ids, w, resid, up, gate, down, (Q8_0,) * 3, F, n_threads=cores)
+        cpu_ggml.moe_block(xs[n % len(xs)], gate_inp, up, gate, down, Q8_0, resid, E, F, K, n_threads=cores)
         n += 1
         el = time.time() - t0
         if el >= seconds or n >= 100000:
             break
     per_layer = el / n
+    del up, gate, down
+    # prefill: 512 tokens, Q4_K experts, Zipf(1.1)-biased router (the GPU prefill leg's workload)
+    up4, gate4, down4 = (synth.experts(rng, Q4_K, E, F, H), synth.experts(rng, Q4_K, E, F, H),
+                         synth.experts(rng, Q4_K, E, H, F))
+    zr = synth.zipf_router_f16(rng, E, H)
+    xp = [synth.activations(rng, 512, H, bias_unit=True) for _ in range(2)]
+    rp = synth.activations(rng, 512, H)
+    m = 0
+    t0 = time.time()
+    while True:
+        cpu_ggml.moe_block(xp[m % 2], zr, up4, gate4, down4, Q4_K, rp, E, F, K, n_threads=cores)
+        m += 1
+        pel = time.time() - t0
+        if pel >= seconds / 2 or m >= 50:
+            break
+    pre_layer = pel / m
     return dict(value=T / (per_layer * N_LAYER), unit="tok/s", cores=cores, kind="port",
-                sample=f"{n} passes of one Qwen3-30B-A3B MoE layer (router + Q8_0 experts, T={T}) by the oracle "
-                       f"(C restatement of ggml's CPU algorithm, OpenMP {cores} threads), scaled to 48 layers; "
-                       f"{per_layer * 1e3:.2f} ms per layer")
+                label="CPU restatement of ggml semantics", cpu_model=cpu_model(), isa=cpu_ggml.isa(),
+                sample=f"{n} passes of one Qwen3-30B-A3B MoE layer (router + Q8_0 experts, T={T}, new hnorm rows "
+                       f"each pass) by oracle/cpu_ggml.c on {cores} threads, scaled to 48 layers; "
+                       f"{per_layer * 1e3:.3f} ms per layer",
+                prefill={"layer_tok_s": 512 / pre_layer, "ms_per_layer": pre_layer * 1e3, "passes": m,
+                         "what": "512-token Q4_K Zipf(1.1) prefill through one MoE layer"})
 
 
 def measured_traffic(key):
