@@ -2,7 +2,7 @@
 // each expert. ggml's CPU mul_mat_id groups the (token, slot) pairs by expert and runs each expert's
 // matrix over its rows (src/qwen3.cpp:201-204); here that is:
 //   permute    one work-group: per-bin counts, exclusive offsets, the stable token-major pair order
-//              and the work list of 64-pair chunks (full chunks first, then the partial ones).
+//              and the work list of 32-pair chunks, expert-major (each expert's chunks in order).
 //   gate_up    per (chunk, 64-row block): Q4_K gate and up rows x Q8_K token rows on
 //              v_mfma_i32_32x32x32_i8, fused SwiGLU (src/qwen3.cpp:201-203).
 //   act_quant  the SwiGLU rows to Q8_K, the activation type ggml pairs with Q4_K down weights.
@@ -72,7 +72,7 @@ __global__ __launch_bounds__(kPermThreads) void permute_kernel(PermuteParams P) 
     __shared__ unsigned seg[kPermSeg][kGroupedMaxBins / 2];
     __shared__ int16_t bl[kPermMaxPairs];
     __shared__ int cnt[kGroupedMaxBins];
-    __shared__ int wsum[3][kPermSeg];
+    __shared__ int wsum[2][kPermSeg];
     const int tid = threadIdx.x, lane = tid % kWave, w = tid / kWave;
     const int np = P.np, nb = P.n_bins;
     for (int i = tid; i < kPermSeg * (kGroupedMaxBins / 2); i += kPermThreads) (&seg[0][0])[i] = 0u;
@@ -114,39 +114,36 @@ __global__ __launch_bounds__(kPermThreads) void permute_kernel(PermuteParams P) 
     __syncthreads();
     // offsets and the work list: one bin per thread (n_bins <= 1024)
     const int c = tid < nb ? cnt[tid] : 0;
-    const int full = c / P.chunk, part = (c % P.chunk) ? 1 : 0;
-    const int v0 = wave_incl_scan(c), v1 = wave_incl_scan(full), v2 = wave_incl_scan(part);
+    const int nch = (c + P.chunk - 1) / P.chunk; // the bin's work items: its chunks in order
+    const int v0 = wave_incl_scan(c), v1 = wave_incl_scan(nch);
     if (lane == kWave - 1) {
         wsum[0][w] = v0;
         wsum[1][w] = v1;
-        wsum[2][w] = v2;
     }
     __syncthreads();
-    int b0 = 0, b1 = 0, b2 = 0, tot0 = 0, tot1 = 0, tot2 = 0;
+    int b0 = 0, b1 = 0, tot0 = 0, tot1 = 0;
     for (int s = 0; s < kPermSeg; s++) {
         if (s < w) {
             b0 += wsum[0][s];
             b1 += wsum[1][s];
-            b2 += wsum[2][s];
         }
         tot0 += wsum[0][s];
         tot1 += wsum[1][s];
-        tot2 += wsum[2][s];
     }
     const int off = b0 + v0 - c;
     if (tid < nb) {
         P.counts[tid] = c;
         P.offsets[tid] = off;
         if (P.items) {
-            const int fb = b1 + v1 - full, pb = tot1 + b2 + v2 - part;
-            for (int i = 0; i < full; i++) P.items[fb + i] = make_int4(tid, off + i * P.chunk, P.chunk, 0);
-            if (part) P.items[pb] = make_int4(tid, off + full * P.chunk, c - full * P.chunk, 0);
+            // expert-major: a bin's chunks are consecutive items (XCD-aware mapping keeps them on one XCD)
+            const int fb = b1 + v1 - nch;
+            for (int i = 0; i < nch; i++) P.items[fb + i] = make_int4(tid, off + i * P.chunk, min(P.chunk, c - i * P.chunk), 0);
         }
         cnt[tid] = off;
     }
     if (tid == 0) {
         P.offsets[nb] = tot0;
-        if (P.n_items) *P.n_items = tot1 + tot2;
+        if (P.n_items) *P.n_items = tot1;
     }
     __syncthreads();
     for (int base = s0; base < s1; base += kWave) {
@@ -232,6 +229,7 @@ __device__ __forceinline__ GLds g_lds(unsigned char *base) {
 // the wave-uniform bases): kAInstr activation pieces, the row scale, 5 weight chunk pairs.
 struct DmaOffs {
     unsigned a[kAInstr], dx, w[5];
+    unsigned live; // bit i: activation piece i is a real row of the chunk (t < n); bit 31: the lane's scale is
 };
 
 __device__ __forceinline__ DmaOffs dma_offsets(const GroupedParams &P, const GLds &g, int n, int row0) {
@@ -242,8 +240,11 @@ __device__ __forceinline__ DmaOffs dma_offsets(const GroupedParams &P, const GLd
         const int s = (wave * kAInstr + i) * kWave + lane;
         const int t = s >> 4, part = (s & 15) ^ (t & 15);
         o.a[i] = (unsigned) g.src[min(t, n - 1)] * (unsigned) P.K + part * 16;
+        if (i == 0) o.live = 0u;
+        if (t < n) o.live |= 1u << i;
     }
     o.dx = (unsigned) g.src[min(lane, n - 1)] * (unsigned) (P.K / 32) * 4;
+    if (lane < n) o.live |= 1u << 31;
 #pragma unroll
     for (int i = 0; i < 5; i++) {
         const int c = min(2 * i + (lane >> 5), 8);
@@ -260,8 +261,11 @@ __device__ __forceinline__ void issue_stage(const GroupedParams &P, const GLds &
     unsigned char *st = g.ring + (size_t) slot * kStageBytes;
     const uint8_t *xa = reinterpret_cast<const uint8_t *>(P.xqs) + sb * 256;
 #pragma unroll
-    for (int i = 0; i < kAInstr; i++) dma16(xa + o.a[i], st + (wave * kAInstr + i) * 1024);
-    if (wave == 0 && lane < kGroupedChunk) dma4(reinterpret_cast<const uint8_t *>(P.xd) + sb * 32 + o.dx, st + kABytes);
+    // rows past the chunk's n pairs are not loaded: their LDS rows hold stale bytes, and the products of
+    // those rows are never stored
+    for (int i = 0; i < kAInstr; i++)
+        if (o.live & (1u << i)) dma16(xa + o.a[i], st + (wave * kAInstr + i) * 1024);
+    if (wave == 0 && lane < kGroupedChunk && (o.live >> 31)) dma4(reinterpret_cast<const uint8_t *>(P.xd) + sb * 32 + o.dx, st + kABytes);
     const uint8_t *wb = w + (size_t) sb * kChunksQ4_K * P.rows * 16;
     unsigned char *wl = st + kABytes + kDXBytes + wave * kWWaveBytes;
 #pragma unroll
@@ -372,10 +376,17 @@ __device__ __forceinline__ void q4k_rows(const GroupedParams &P, const GLds &g, 
     }
 }
 
-// Reads the work item of this work-group; false when it has none.
-__device__ __forceinline__ bool g_item(const GroupedParams &P, int n_rb, const GLds &g, int4 &it) {
-    const int item = blockIdx.x / n_rb;
-    if (item >= *P.n_items) return false;
+// Work-group b -> (item, row block), XCD-aware: the dispatcher deals work-groups to the 8 XCDs in turn
+// (b goes to XCD b % 8), so XCD x takes the items [x per, (x + 1) per) of the expert-major work list, all
+// row blocks of an item before the next. The row blocks that share an item's activation rows, and the
+// chunks that share an expert's weight rows, then meet in one XCD's L2.
+constexpr int kXcds = 8;
+// Reads the work item and row block of this work-group; false when it has none.
+__device__ __forceinline__ bool g_item(const GroupedParams &P, int n_rb, const GLds &g, int4 &it, int &rb) {
+    const int n_items = *P.n_items, per = (n_items + kXcds - 1) / kXcds;
+    const int local = blockIdx.x / kXcds, item = (blockIdx.x % kXcds) * per + local / n_rb;
+    if (local / n_rb >= per || item >= n_items) return false;
+    rb = local % n_rb;
     it = P.items[item];
     const int tid = threadIdx.x;
     if (tid < kGroupedChunk) {
@@ -394,8 +405,9 @@ __global__ __launch_bounds__(kGThreads) void gate_up_grouped_kernel(GroupedParam
     const GLds g = g_lds(smem);
     const int n_rb = P.rows / 64;
     int4 it;
-    if (!g_item(P, n_rb, g, it)) return;
-    const int rb = blockIdx.x % n_rb, e = it.x, n = it.z;
+    int rb;
+    if (!g_item(P, n_rb, g, it, rb)) return;
+    const int e = it.x, n = it.z;
     const int wave = threadIdx.x / kWave, lane = threadIdx.x % kWave;
     const int m = wave & 1, row0 = rb * 64 + 32 * (wave >> 1);
     const uint8_t *w = m ? P.w1 + (size_t) e * P.stride1 : P.w0 + (size_t) e * P.stride0;
@@ -432,8 +444,9 @@ __global__ __launch_bounds__(kGThreads) void down_grouped_kernel(GroupedParams P
     const GLds g = g_lds(smem);
     const int n_rb = P.rows / 128;
     int4 it;
-    if (!g_item(P, n_rb, g, it)) return;
-    const int rb = blockIdx.x % n_rb, e = it.x, n = it.z;
+    int rb;
+    if (!g_item(P, n_rb, g, it, rb)) return;
+    const int e = it.x, n = it.z;
     const int wave = threadIdx.x / kWave, lane = threadIdx.x % kWave, h = lane / 32;
     const int row0 = rb * 128 + 32 * wave;
     float acc[kMT][16];
@@ -487,13 +500,15 @@ hipError_t allow_lds() {
 hipError_t launch_gate_up_grouped(const GroupedParams &P, int max_items, hipStream_t st, const LaunchTiming *tm) {
     if (max_items <= 0) return hipSuccess;
     if (const hipError_t e = allow_lds(); e != hipSuccess) return e;
-    return launch(gate_up_grouped_kernel, dim3(max_items * (P.rows / 64)), dim3(kGThreads), kGLdsBytes, st, tm, P);
+    const int per = (max_items + kXcds - 1) / kXcds;
+    return launch(gate_up_grouped_kernel, dim3(kXcds * per * (P.rows / 64)), dim3(kGThreads), kGLdsBytes, st, tm, P);
 }
 
 hipError_t launch_down_grouped(const GroupedParams &P, int max_items, hipStream_t st, const LaunchTiming *tm) {
     if (max_items <= 0) return hipSuccess;
     if (const hipError_t e = allow_lds(); e != hipSuccess) return e;
-    return launch(down_grouped_kernel, dim3(max_items * (P.rows / 128)), dim3(kGThreads), kGLdsBytes, st, tm, P);
+    const int per = (max_items + kXcds - 1) / kXcds;
+    return launch(down_grouped_kernel, dim3(kXcds * per * (P.rows / 128)), dim3(kGThreads), kGLdsBytes, st, tm, P);
 }
 
 hipError_t launch_act_quant(const float *act, int f, int np, const ActBuf &aq, hipStream_t st, const LaunchTiming *tm) {

@@ -120,7 +120,7 @@ struct PermuteParams {
     int32_t *counts;  // [n_bins]
     int32_t *offsets; // [n_bins + 1] exclusive scan of counts
     int32_t *perm;    // [np] sorted position -> pair index
-    int4 *items;      // [max_items] {bin, first position, pairs, 0}: full chunks first; may be null
+    int4 *items;      // [max_items] {bin, first position, pairs, 0}: each bin's chunks in order, bins ascending; may be null
     int32_t *n_items; // may be null
     int32_t *err;
 };
