@@ -69,6 +69,15 @@ int lstk_gguf_qwen3_hparams(const lstk_gguf *g, lstk_qwen3_hparams *hp);
  * pool stores (Q8_0, Q4_K): anything else fails with a message naming the layer, tensor and type. */
 int lstk_gguf_qwen3_experts(const lstk_gguf *g, const lstk_qwen3_hparams *hp, lstk_expert_layer *layers);
 
+/* Dense tensors for the forward pass, which multiplies F16 matrices: n values of a tensor of ggml type
+ * `type` at src (GGUF bytes, n a multiple of the type's block) to fp16 at dst, round to nearest even.
+ * F32, F16, Q8_0 (d q), Q4_K (d sc q - dmin m), Q5_K (d sc (q + 16 h) - dmin m) and Q6_K (d sc (q - 32),
+ * sc a signed 8-bit scale per 16 values) - ggml's dequantize_row_* for each format (the reference maps such
+ * tensors into its graph whatever their type, src/qwen3.cpp:52-89). Each value is formed in f32 in ggml's
+ * order, then rounded to fp16 once; the forward pass then differs from ggml's quantized dot products by the
+ * fp16 rounding of the weights. LSTK_E_INVALID for any other type or a bad n. Host memory only. */
+int lstk_dequant_f16(int type, const void *src, size_t n, uint16_t *dst);
+
 #ifdef __cplusplus
 }
 #endif

@@ -126,6 +126,7 @@ SIGNATURES = {
     "lstk_gguf_find_tensor": (_I, [_P, ctypes.c_char_p, ctypes.POINTER(GgufTensor)]),
     "lstk_gguf_qwen3_hparams": (_I, [_P, ctypes.POINTER(Qwen3HParams)]),
     "lstk_gguf_qwen3_experts": (_I, [_P, ctypes.POINTER(Qwen3HParams), _P]),
+    "lstk_dequant_f16": (_I, [_I, _P, ctypes.c_size_t, _P]),
     "lstk_model_set_timing": (_I, [_P, _I]),
     "lstk_model_timing": (_I, [_P, ctypes.POINTER(ctypes.c_double), ctypes.POINTER(ctypes.c_int64)]),
 }
@@ -465,7 +466,22 @@ class Qwen3Model:
 
 
 _GGML_NP = {0: np.float32, 1: np.float16}
-_GGML_NAME = {0: "F32", 1: "F16", 8: "Q8_0", 12: "Q4_K", 14: "Q6_K", 30: "BF16"}
+_GGML_NAME = {0: "F32", 1: "F16", 8: "Q8_0", 12: "Q4_K", 13: "Q5_K", 14: "Q6_K", 15: "Q8_K", 30: "BF16"}
+# types lstk_dequant_f16 expands, with (values, bytes) per block
+DEQUANT_TYPES = {0: (1, 4), 1: (1, 2), 8: (32, 34), 12: (256, 144), 13: (256, 176), 14: (256, 210)}
+
+
+def dequant_f16(type_, data, n):
+    """n values of ggml type type_ (bytes-like or uint8 array) to a float16 numpy array (lstk_dequant_f16)."""
+    if type_ not in DEQUANT_TYPES:
+        raise LstkError(E_INVALID, f"no dequantizer for {_GGML_NAME.get(type_, type_)}")
+    per, nb = DEQUANT_TYPES[type_]
+    src = np.ascontiguousarray(np.frombuffer(data, np.uint8) if not isinstance(data, np.ndarray) else data.view(np.uint8).ravel())
+    if n % per or src.nbytes < n // per * nb:
+        raise LstkError(E_INVALID, f"{n} values of {_GGML_NAME[type_]} need {-(-n // per) * nb} bytes, got {src.nbytes}")
+    out = np.empty(n, np.float16)
+    _check(lib().lstk_dequant_f16(type_, src.ctypes.data, n, out.ctypes.data))
+    return out
 
 
 class GgufFile:
@@ -544,6 +560,15 @@ class GgufFile:
             raise LstkError(E_INVALID, f"tensor {name} is {_GGML_NAME.get(info['type'], info['type'])}, not F32/F16")
         return self.tensor_bytes(name).view(_GGML_NP[info["type"]]).reshape(tuple(reversed(info["ne"])))
 
+    def tensor_f16(self, name):
+        """Any type lstk_dequant_f16 expands (F32, F16, Q8_0, Q4_K, Q5_K, Q6_K) as a float16 array shaped
+        [ne[n-1]]...[ne[0]]; F16 stays a view of the mapping, the others are dequantized copies."""
+        info = self.tensor_info(name)
+        if info["type"] == 1:
+            return self.tensor_array(name)
+        n = int(np.prod(info["ne"]))
+        return dequant_f16(info["type"], self.tensor_bytes(name), n).reshape(tuple(reversed(info["ne"])))
+
     def qwen3_hparams(self):
         hp = Qwen3HParams()
         _check(lib().lstk_gguf_qwen3_hparams(self._h, ctypes.byref(hp)))
@@ -556,24 +581,24 @@ class GgufFile:
         return [((L.type_up, L.type_gate, L.type_down), L.host_up, L.host_gate, L.host_down) for L in arr]
 
 
-def load_qwen3_gguf(path, n_batch=64, kv_size=4096, device="cuda", pool_bytes=None, min_slots=None, streaming=False,
-                    device_lru=False):
-    """qwen3_load_hparams + qwen3_map_weights + the expert pool (src/qwen3.cpp:16-109,
-    src/engine.cpp:31-173) from a qwen3moe GGUF: returns (hparams, ExpertStore, Qwen3Model, GgufFile).
-    The experts go to the pool straight from the mapping; the dense tensors must be F16 (embedding,
-    attention, output) and F32 (norms), the router F16 or F32 - other types are rejected."""
-    g = GgufFile(path)
-    hp = g.qwen3_hparams()
-    experts = g.qwen3_experts(hp)
+def qwen3_dense_weights(g, hp):
+    """The non-expert tensors of a qwen3moe GGUF as the forward pass takes them (qwen3_map_weights,
+    src/qwen3.cpp:52-89): {"tok_embd", "output_norm", "output" (None when the head is tied), "layers": [...]}.
+    Norms must be F32; the router is taken as F16 or F32 as stored; the matrices the forward pass multiplies
+    in F16 (embedding, attention, output) are taken as stored when F16 and dequantized to F16 from F32, Q8_0,
+    Q4_K, Q5_K or Q6_K (lstk_dequant_f16); other types are rejected with the tensor's name."""
+    names = {t["name"] for t in g.tensors()}
 
-    def dense(name, types=(1,), optional=False):
-        if optional and not any(t["name"] == name for t in g.tensors()):
+    def dense(name, types=tuple(DEQUANT_TYPES), optional=False):
+        if optional and name not in names:
             return None
         t = g.tensor_info(name)
         if t["type"] not in types:
             want = "/".join(_GGML_NAME[x] for x in types)
             raise LstkError(E_INVALID, f"tensor {name} is {_GGML_NAME.get(t['type'], t['type'])}; the forward pass takes {want}")
-        return g.tensor_array(name)
+        if types == (0,) or (types == (0, 1) and t["type"] in types):
+            return g.tensor_array(name)
+        return g.tensor_f16(name)
 
     w = {"tok_embd": dense("token_embd.weight"), "output_norm": dense("output_norm.weight", (0,)),
          "output": dense("output.weight", optional=True), "layers": []}
@@ -585,6 +610,18 @@ def load_qwen3_gguf(path, n_batch=64, kv_size=4096, device="cuda", pool_bytes=No
             "q_norm": dense(p + "attn_q_norm.weight", (0,), optional=True),
             "k_norm": dense(p + "attn_k_norm.weight", (0,), optional=True),
             "ffn_norm": dense(p + "ffn_norm.weight", (0,)), "gate_inp": dense(p + "ffn_gate_inp.weight", (0, 1))})
+    return w
+
+
+def load_qwen3_gguf(path, n_batch=64, kv_size=4096, device="cuda", pool_bytes=None, min_slots=None, streaming=False,
+                    device_lru=False):
+    """qwen3_load_hparams + qwen3_map_weights + the expert pool (src/qwen3.cpp:16-109,
+    src/engine.cpp:31-173) from a qwen3moe GGUF: returns (hparams, ExpertStore, Qwen3Model, GgufFile).
+    The experts go to the pool straight from the mapping; the dense tensors as qwen3_dense_weights takes them."""
+    g = GgufFile(path)
+    hp = g.qwen3_hparams()
+    experts = g.qwen3_experts(hp)
+    w = qwen3_dense_weights(g, hp)
     if min_slots is None:
         # a pool class never has fewer slots than one layer's experts (src/engine.cpp:114-116)
         min_slots = max(hp["n_expert"], 2 * hp["n_expert_used"] + 2) if streaming else 0

@@ -403,3 +403,139 @@ int lstk_gguf_qwen3_experts(const lstk_gguf *g, const lstk_qwen3_hparams *hp, ls
 }
 
 }  // extern "C"
+
+namespace {
+
+float half_to_float(uint16_t h) {
+    const uint32_t sign = (uint32_t) (h & 0x8000u) << 16, e = (h >> 10) & 0x1fu, m = h & 0x3ffu;
+    uint32_t bits;
+    if (e == 0) {
+        if (m == 0) {
+            bits = sign;
+        } else { // subnormal: normalise
+            int ee = -1;
+            uint32_t mm = m;
+            do {
+                ee++;
+                mm <<= 1;
+            } while ((mm & 0x400u) == 0);
+            bits = sign | ((uint32_t) (127 - 15 - ee) << 23) | ((mm & 0x3ffu) << 13);
+        }
+    } else if (e == 31) {
+        bits = sign | 0x7f800000u | (m << 13);
+    } else {
+        bits = sign | ((e + 112) << 23) | (m << 13);
+    }
+    float f;
+    std::memcpy(&f, &bits, 4);
+    return f;
+}
+
+// f32 -> fp16, round to nearest even (overflow to infinity, NaN kept quiet)
+uint16_t float_to_half(float f) {
+    uint32_t x;
+    std::memcpy(&x, &f, 4);
+    const uint32_t sign = (x >> 16) & 0x8000u;
+    x &= 0x7fffffffu;
+    if (x > 0x7f800000u) return (uint16_t) (sign | 0x7e00u);
+    if (x >= 0x477ff000u) return (uint16_t) (sign | 0x7c00u); // rounds to above 65504
+    if (x < 0x38800000u) {                                      // subnormal or zero in fp16
+        if (x < 0x33000000u) return (uint16_t) sign;            // below half the smallest subnormal
+        const uint32_t m = (x & 0x7fffffu) | 0x800000u;
+        const int shift = 126 - (int) (x >> 23); // 14 .. 24
+        const uint32_t q = m >> shift, rem = m & ((1u << shift) - 1u), half = 1u << (shift - 1);
+        return (uint16_t) (sign | (q + (rem > half || (rem == half && (q & 1u)))));
+    }
+    const uint32_t q = ((x - 0x38000000u) >> 13), rem = x & 0x1fffu;
+    return (uint16_t) (sign | (q + (rem > 0x1000u || (rem == 0x1000u && (q & 1u)))));
+}
+
+void scale_min_k4(int j, const uint8_t *q, int &sc, int &m) {
+    if (j < 4) {
+        sc = q[j] & 63;
+        m = q[j + 4] & 63;
+    } else {
+        sc = (q[j + 4] & 0xF) | ((q[j - 4] >> 6) << 4);
+        m = (q[j + 4] >> 4) | ((q[j] >> 6) << 4);
+    }
+}
+
+}  // namespace
+
+extern "C" int lstk_dequant_f16(int type, const void *src, size_t n, uint16_t *dst) {
+    if (!src || !dst) return set_error(LSTK_E_INVALID, "lstk_dequant_f16: null argument");
+    const uint8_t *b = static_cast<const uint8_t *>(src);
+    auto h16 = [](const uint8_t *p) { return (uint16_t) (p[0] | (p[1] << 8)); };
+    switch (type) {
+    case 0: // F32
+        for (size_t i = 0; i < n; i++) {
+            float f;
+            std::memcpy(&f, b + 4 * i, 4);
+            dst[i] = float_to_half(f);
+        }
+        return LSTK_OK;
+    case 1: // F16
+        std::memcpy(dst, src, n * 2);
+        return LSTK_OK;
+    case 8: // Q8_0: {fp16 d, int8 q[32]}
+        if (n % 32) break;
+        for (size_t blk = 0; blk < n / 32; blk++, b += 34) {
+            const float d = half_to_float(h16(b));
+            for (int i = 0; i < 32; i++) dst[blk * 32 + i] = float_to_half((float) (int8_t) b[2 + i] * d);
+        }
+        return LSTK_OK;
+    case 12: // Q4_K: {fp16 d, dmin, scales[12], qs[128]}
+    case 13: // Q5_K: {fp16 d, dmin, scales[12], qh[32], qs[128]}
+        if (n % 256) break;
+        for (size_t blk = 0; blk < n / 256; blk++) {
+            const bool five = type == 13;
+            const float d = half_to_float(h16(b)), dmin = half_to_float(h16(b + 2));
+            const uint8_t *sc = b + 4, *qh = b + 16, *ql = five ? b + 48 : b + 16;
+            uint16_t *y = dst + blk * 256;
+            for (int c = 0; c < 4; c++) { // 64 values: sub-blocks 2c (low nibbles) and 2c + 1 (high)
+                int s0, m0, s1, m1;
+                scale_min_k4(2 * c, sc, s0, m0);
+                scale_min_k4(2 * c + 1, sc, s1, m1);
+                const float d1 = d * (float) s0, mm1 = dmin * (float) m0, d2 = d * (float) s1, mm2 = dmin * (float) m1;
+                for (int l = 0; l < 32; l++) {
+                    int q0 = ql[32 * c + l] & 0xF, q1 = ql[32 * c + l] >> 4;
+                    if (five) {
+                        q0 += (qh[l] >> (2 * c)) & 1 ? 16 : 0;
+                        q1 += (qh[l] >> (2 * c + 1)) & 1 ? 16 : 0;
+                    }
+                    y[64 * c + l] = float_to_half(d1 * (float) q0 - mm1);
+                    y[64 * c + 32 + l] = float_to_half(d2 * (float) q1 - mm2);
+                }
+            }
+            b += five ? 176 : 144;
+        }
+        return LSTK_OK;
+    case 14: // Q6_K: {ql[128], qh[64], int8 scales[16], fp16 d}
+        if (n % 256) break;
+        for (size_t blk = 0; blk < n / 256; blk++, b += 210) {
+            const uint8_t *ql = b, *qh = b + 128;
+            const int8_t *sc = reinterpret_cast<const int8_t *>(b + 192);
+            const float d = half_to_float(h16(b + 208));
+            uint16_t *y = dst + blk * 256;
+            for (int half = 0; half < 2; half++) { // 128 values each
+                const uint8_t *l8 = ql + 64 * half, *h8 = qh + 32 * half;
+                const int8_t *s8 = sc + 8 * half;
+                for (int l = 0; l < 32; l++) {
+                    const int is = l / 16;
+                    const int q1 = (int) ((l8[l] & 0xF) | ((h8[l] & 3) << 4)) - 32;
+                    const int q2 = (int) ((l8[l + 32] & 0xF) | (((h8[l] >> 2) & 3) << 4)) - 32;
+                    const int q3 = (int) ((l8[l] >> 4) | (((h8[l] >> 4) & 3) << 4)) - 32;
+                    const int q4 = (int) ((l8[l + 32] >> 4) | (((h8[l] >> 6) & 3) << 4)) - 32;
+                    y[128 * half + l] = float_to_half(d * (float) s8[is] * (float) q1);
+                    y[128 * half + l + 32] = float_to_half(d * (float) s8[is + 2] * (float) q2);
+                    y[128 * half + l + 64] = float_to_half(d * (float) s8[is + 4] * (float) q3);
+                    y[128 * half + l + 96] = float_to_half(d * (float) s8[is + 6] * (float) q4);
+                }
+            }
+        }
+        return LSTK_OK;
+    default:
+        return set_error(LSTK_E_INVALID, "lstk_dequant_f16: unsupported type " + std::to_string(type));
+    }
+    return set_error(LSTK_E_INVALID, "lstk_dequant_f16: n is not a multiple of the type's block");
+}

@@ -195,8 +195,9 @@ def write_gguf(path, kv, tensors, align=32, version=3):
         f.write(body)
 
 
-def write_qwen3_gguf(path, hp, w, extra_kv=()):
-    """The model of qwen3_weights(hp) as a qwen3moe GGUF (tied head: no output.weight)."""
+def write_qwen3_gguf(path, hp, w, extra_kv=(), dense_override=None):
+    """The model of qwen3_weights(hp) as a qwen3moe GGUF (tied head: no output.weight). dense_override maps
+    a tensor name to (ggml type, bytes) stored in place of that tensor's data (same shape)."""
     a = "qwen3moe."
     kv = [("general.architecture", GGUF_STR, "qwen3moe"), ("general.name", GGUF_STR, "synthetic-qwen3moe"),
           (a + "block_count", GGUF_U32, hp["n_layer"]), (a + "context_length", GGUF_U32, hp.get("n_ctx_train", 1024)),
@@ -226,4 +227,7 @@ def write_qwen3_gguf(path, hp, w, extra_kv=()):
                (p + "ffn_up_exps.weight", [h, f, E], L["types"][0], b(L["up"])),
                (p + "ffn_gate_exps.weight", [h, f, E], L["types"][1], b(L["gate"])),
                (p + "ffn_down_exps.weight", [f, h, E], L["types"][2], b(L["down"]))]
+    for name, (gtype, data) in (dense_override or {}).items():
+        i = next(i for i, t in enumerate(ts) if t[0] == name)
+        ts[i] = (name, ts[i][1], gtype, b(data))
     write_gguf(path, kv, ts)
