@@ -198,10 +198,11 @@ constexpr int kTierMaxIds = 4096;    // experts requested per call (n_batch * n_
 constexpr int kTierCopyGrid = LSTK_TIER_COPY_GRID; // work-groups of a copy launch (64-512 all reach the same PCIe rate; 1024 and more lose 3-6%)
 
 // Device copy of the streaming pool's bookkeeping: slot_of [n_layer][n_expert] (-1 = not resident);
-// per slot (all shards back to back) the LRU links and the owner; per shard {head, tail, n_in_lru, 0};
+// per shard (shards back to back, slot_base apart) its slots in eviction order (order[0] the least
+// recently released; every slot is idle between calls) and each slot's owner (layer, expert);
 // counters {hits, misses, bytes_read, acquires}.
 struct TierLru {
-    int32_t *slot_of, *prev, *next, *owner_layer, *owner_expert, *hdr;
+    int32_t *slot_of, *order, *owner_layer, *owner_expert;
     unsigned long long *stats;
 };
 

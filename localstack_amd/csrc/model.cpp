@@ -48,102 +48,103 @@ constexpr uint32_t kCellBlock = 32; // KvCache::block_size (src/kv_cache.h:27)
 
 int hip_fail(hipError_t e, const char *what) { return set_error(LSTK_E_DEVICE, std::string(what) + ": " + hipGetErrorString(e)); }
 
-// KvCache's host bookkeeping (src/kv_cache.cpp:59-150): blocks of 32 cells handed out per sequence
-// from a free list that returns block 0 first, cell = blocks[pos / 32] * 32 + pos % 32.
+// The KV cache's cell table (KvCache, src/kv_cache.cpp:59-150). Cells come in blocks of kCellBlock
+// that a sequence takes as it grows; position p of a sequence lives in cell
+// blocks[p / kCellBlock] * kCellBlock + p % kCellBlock. Spare blocks form a stack whose top starts at
+// block 0, and freed blocks are pushed back in the order they are released, so the cell each step
+// gets is the reference's. A block holds consecutive positions of one sequence from its first cell,
+// so its occupied cells are its first fill[b]; the attended range ends after the last occupied cell.
 struct KvBook {
+    struct Seq {
+        std::vector<uint32_t> blocks;
+        int32_t len = 0;
+    };
     uint32_t size = 0;
-    std::vector<int32_t> cell_seq, cell_pos;
-    std::vector<uint32_t> free_blocks;
-    std::map<int32_t, std::vector<uint32_t>> seq_blocks;
-    std::map<int32_t, int32_t> seq_len;
-    uint32_t used_hwm = 0;
+    std::vector<int32_t> cell_seq, cell_pos; // per cell: sequence and position, -1 when free (mirrored to the device)
+    std::vector<uint32_t> spare;             // free blocks; the next one handed out is at the back
+    std::vector<uint32_t> fill;              // per block: occupied cells
+    std::map<int32_t, Seq> seqs;
 
     void init(uint32_t n) {
         size = n;
         cell_seq.assign(n, -1);
         cell_pos.assign(n, -1);
-        free_blocks.clear();
-        for (uint32_t b = n / kCellBlock; b > 0; b--) free_blocks.push_back(b - 1);
-        seq_blocks.clear();
-        seq_len.clear();
-        used_hwm = 0;
+        const uint32_t nb = n / kCellBlock;
+        fill.assign(nb, 0);
+        spare.resize(nb);
+        for (uint32_t i = 0; i < nb; i++) spare[i] = nb - 1 - i;
+        seqs.clear();
     }
+    int32_t length(int32_t seq) const {
+        const auto it = seqs.find(seq);
+        return it == seqs.end() ? 0 : it->second.len;
+    }
+    uint32_t cell_of(const Seq &q, int32_t p) const { return q.blocks[(uint32_t) p / kCellBlock] * kCellBlock + (uint32_t) p % kCellBlock; }
+    void clear_cell(uint32_t c) { cell_seq[c] = cell_pos[c] = -1; }
     bool alloc(int32_t seq, int n, std::vector<int32_t> &cells, std::vector<int32_t> &positions) {
-        std::vector<uint32_t> &blocks = seq_blocks[seq];
-        int32_t &len = seq_len[seq];
-        const uint32_t have = (uint32_t) blocks.size() * kCellBlock;
-        const uint32_t need = (uint32_t) len + (uint32_t) n;
-        const uint32_t extra = need > have ? (need - have + kCellBlock - 1) / kCellBlock : 0;
-        if (extra > free_blocks.size()) {
-            if (blocks.empty() && len == 0) {
-                seq_blocks.erase(seq);
-                seq_len.erase(seq);
-            }
+        const bool fresh = seqs.find(seq) == seqs.end();
+        Seq &q = seqs[seq];
+        const size_t blocks_after = ((size_t) q.len + (size_t) n + kCellBlock - 1) / kCellBlock;
+        if (blocks_after > q.blocks.size() + spare.size()) {
+            if (fresh) seqs.erase(seq);
             return false;
         }
-        for (uint32_t i = 0; i < extra; i++) {
-            blocks.push_back(free_blocks.back());
-            free_blocks.pop_back();
+        while (q.blocks.size() < blocks_after) {
+            q.blocks.push_back(spare.back());
+            spare.pop_back();
         }
         cells.resize(n);
         positions.resize(n);
         for (int i = 0; i < n; i++) {
-            const uint32_t cell = blocks[(uint32_t) len / kCellBlock] * kCellBlock + (uint32_t) len % kCellBlock;
-            cell_seq[cell] = seq;
-            cell_pos[cell] = len;
-            cells[i] = (int32_t) cell;
-            positions[i] = len;
-            used_hwm = std::max(used_hwm, cell + 1);
-            len++;
+            const int32_t p = q.len + i;
+            const uint32_t c = cell_of(q, p);
+            cell_seq[c] = seq;
+            cell_pos[c] = p;
+            fill[c / kCellBlock] = c % kCellBlock + 1;
+            cells[i] = (int32_t) c;
+            positions[i] = p;
         }
+        q.len += n;
         return true;
     }
-    void rescan() {
-        used_hwm = 0;
-        for (uint32_t c = 0; c < size; c++)
-            if (cell_seq[c] >= 0) used_hwm = c + 1;
+    // Frees the sequence's positions from `keep` on; blocks left empty go back to the spares, last first.
+    void shrink(std::map<int32_t, Seq>::iterator it, int32_t keep) {
+        Seq &q = it->second;
+        for (int32_t p = keep; p < q.len; p++) clear_cell(cell_of(q, p));
+        const size_t keep_blocks = ((size_t) keep + kCellBlock - 1) / kCellBlock;
+        while (q.blocks.size() > keep_blocks) {
+            fill[q.blocks.back()] = 0;
+            spare.push_back(q.blocks.back());
+            q.blocks.pop_back();
+        }
+        if (keep_blocks > 0) fill[q.blocks.back()] = (uint32_t) (keep - (int32_t) (keep_blocks - 1) * (int32_t) kCellBlock);
+        q.len = keep;
     }
     void remove_seq(int32_t seq) {
-        auto it = seq_blocks.find(seq);
-        if (it == seq_blocks.end()) return;
-        for (uint32_t b : it->second) {
-            for (uint32_t c = b * kCellBlock; c < (b + 1) * kCellBlock; c++) {
-                cell_seq[c] = -1;
-                cell_pos[c] = -1;
-            }
-            free_blocks.push_back(b);
+        const auto it = seqs.find(seq);
+        if (it == seqs.end()) return;
+        // every block of the sequence, first to last, back to the spares
+        Seq &q = it->second;
+        for (uint32_t b : q.blocks) {
+            for (uint32_t c = b * kCellBlock; c < b * kCellBlock + fill[b]; c++) clear_cell(c);
+            fill[b] = 0;
+            spare.push_back(b);
         }
-        seq_blocks.erase(it);
-        seq_len.erase(seq);
-        rescan();
+        seqs.erase(it);
     }
     void truncate_seq(int32_t seq, int32_t keep) {
-        auto it = seq_blocks.find(seq);
-        if (it == seq_blocks.end()) return;
-        if (keep <= 0) {
-            remove_seq(seq);
-            return;
-        }
-        std::vector<uint32_t> &blocks = it->second;
-        int32_t &len = seq_len[seq];
-        if (keep >= len) return;
-        for (int32_t p = keep; p < len; p++) {
-            const uint32_t cell = blocks[(uint32_t) p / kCellBlock] * kCellBlock + (uint32_t) p % kCellBlock;
-            cell_seq[cell] = -1;
-            cell_pos[cell] = -1;
-        }
-        const uint32_t keep_blocks = ((uint32_t) keep + kCellBlock - 1) / kCellBlock;
-        while (blocks.size() > keep_blocks) {
-            free_blocks.push_back(blocks.back());
-            blocks.pop_back();
-        }
-        len = keep;
-        rescan();
+        const auto it = seqs.find(seq);
+        if (it == seqs.end()) return;
+        if (keep <= 0) return remove_seq(seq);
+        if (keep < it->second.len) shrink(it, keep);
     }
-    // Engine::n_kv_for (src/engine.cpp:193-196) over the high-water mark after this step's cells
-    // were assigned: the attended cells, a multiple of 256 (at least 256) capped at the cache size.
+    // Engine::n_kv_for (src/engine.cpp:193-196): the cells up to the last occupied one, rounded up to a
+    // multiple of 256 (at least 256), capped at the cache size.
     int n_kv() const {
-        const uint32_t padded = (used_hwm + 255) / 256 * 256;
+        uint32_t end = 0;
+        for (uint32_t b = 0; b < (uint32_t) fill.size(); b++)
+            if (fill[b] > 0) end = std::max(end, b * kCellBlock + fill[b]);
+        const uint32_t padded = (end + 255) / 256 * 256;
         return (int) std::min<uint32_t>(size, std::max<uint32_t>(256, padded));
     }
 };
@@ -740,8 +741,7 @@ int lstk_model_truncate_seq(lstk_model *model, int32_t seq, int32_t keep) {
 
 int32_t lstk_model_seq_len(const lstk_model *model, int32_t seq) {
     if (!model) return 0;
-    auto it = model->kv.seq_len.find(seq);
-    return it == model->kv.seq_len.end() ? 0 : it->second;
+    return model->kv.length(seq);
 }
 
 int lstk_model_set_timing(lstk_model *model, int enable) {

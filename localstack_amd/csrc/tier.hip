@@ -3,11 +3,15 @@
 // ExpertStore::acquire + release_all (src/expert_store.cpp:232-295) of one segment, with the hit
 // resolution moved from the CPU to the device, so a streaming layer needs no host round trip between
 // its router and its experts (the per-layer CPU sync of docs/decisions.md:14):
-//   lru_resolve_kernel  one work-group: stages the shard's LRU (prev / next / owners) and the layer's
-//                       expert -> slot map in LDS, then one lane runs the acquire loop in request
-//                       order (hit: pin, unlinking an unpinned slot; miss: evict the LRU head, remap,
-//                       record (slot, expert)), then the release loop (a slot whose pin count returns
-//                       to 0 goes to the LRU tail, in acquisition order); the state is written back;
+//   lru_resolve_kernel  one work-group. The shard's slots are kept as an array in eviction order (the
+//                       least recently released first). A call's n requests are resolved in request
+//                       order by one lane against LDS copies: a resident expert is a hit (its slot is
+//                       marked used); otherwise the first unmarked entry of the order is taken, its
+//                       previous expert unmapped, and (slot, expert) recorded as a miss. Everything
+//                       else is done by the whole work-group in parallel: staging, the owners of the
+//                       entries a miss can reach (the first 2n), and the new order - the unmarked
+//                       entries in their order, then the call's slots by their last request (the order
+//                       in which release_all returns them), placed by two work-group prefix sums;
 //   tier_copy_kernel    copies the three matrices of every miss from the pinned host tier into the
 //                       miss's slot with 16-byte loads over PCIe, the misses' chunks spread over the
 //                       grid.
@@ -25,24 +29,50 @@ constexpr int kCopyThreads = 256;
 constexpr int kCopyVec = LSTK_TIER_COPY_VEC;                // 16-byte vectors per thread per chunk
 constexpr int kCopyChunk = kCopyThreads * kCopyVec * 16;    // 16 KiB at 4 vectors
 
-__global__ __launch_bounds__(256) void lru_resolve_kernel(TierResolveParams P) {
-    __shared__ int32_t prv[kTierMaxSlots], nxt[kTierMaxSlots], own_l[kTierMaxSlots], own_e[kTierMaxSlots],
-        pins[kTierMaxSlots];
-    __shared__ int32_t slot_of[kTierMaxExperts], ex[kTierMaxIds], got[kTierMaxIds];
+constexpr int kResolveThreads = 256;
+
+// Exclusive prefix sum over the work-group of one value per thread; *total gets the sum.
+__device__ __forceinline__ int block_excl_scan(int v, int *s_w, int *total) {
+    const int lane = threadIdx.x % kWave, w = threadIdx.x / kWave;
+    int x = v;
+#pragma unroll
+    for (int o = 1; o < kWave; o <<= 1) {
+        const int y = __shfl_up(x, o, kWave);
+        if (lane >= o) x += y;
+    }
+    if (lane == kWave - 1) s_w[w] = x;
+    __syncthreads();
+    int before = 0, sum = 0;
+#pragma unroll
+    for (int i = 0; i < kResolveThreads / kWave; i++) {
+        before += i < w ? s_w[i] : 0;
+        sum += s_w[i];
+    }
+    __syncthreads();
+    *total = sum;
+    return before + x - v;
+}
+
+__global__ __launch_bounds__(kResolveThreads) void lru_resolve_kernel(TierResolveParams P) {
+    __shared__ int32_t order[kTierMaxSlots], last[kTierMaxSlots], slot_of[kTierMaxExperts];
+    __shared__ int32_t front_l[2 * kTierMaxIds < kTierMaxSlots ? 2 * kTierMaxIds : kTierMaxSlots];
+    __shared__ int32_t front_e[2 * kTierMaxIds < kTierMaxSlots ? 2 * kTierMaxIds : kTierMaxSlots];
+    __shared__ int32_t ex[kTierMaxIds], got[kTierMaxIds];
+    __shared__ uint8_t used[kTierMaxSlots];
+    __shared__ int s_w[kResolveThreads / kWave];
     const int tid = threadIdx.x, ns = P.n_slots, E = P.E, n = P.n;
-    int32_t *g_prev = P.lru.prev + P.slot_base, *g_next = P.lru.next + P.slot_base;
+    const int reach = min(ns, 2 * n); // entries a miss can take: each request passes at most two
+    int32_t *g_order = P.lru.order + P.slot_base;
     int32_t *g_ol = P.lru.owner_layer + P.slot_base, *g_oe = P.lru.owner_expert + P.slot_base;
     int32_t *g_slot_of = P.lru.slot_of + (size_t) P.layer * E;
-    for (int i = tid; i < ns; i += blockDim.x) {
-        prv[i] = g_prev[i];
-        nxt[i] = g_next[i];
-        own_l[i] = g_ol[i];
-        own_e[i] = g_oe[i];
-        pins[i] = 0;
+    for (int i = tid; i < ns; i += kResolveThreads) {
+        order[i] = g_order[i];
+        last[i] = -1;
+        used[i] = 0;
     }
-    for (int i = tid; i < E; i += blockDim.x) slot_of[i] = g_slot_of[i];
+    for (int i = tid; i < E; i += kResolveThreads) slot_of[i] = g_slot_of[i];
     int bad = 0;
-    for (int i = tid; i < n; i += blockDim.x) {
+    for (int i = tid; i < n; i += kResolveThreads) {
         int e = P.experts[i];
         if (e < 0 || e >= E) {
             e = e < 0 ? 0 : E - 1;
@@ -52,66 +82,45 @@ __global__ __launch_bounds__(256) void lru_resolve_kernel(TierResolveParams P) {
     }
     if (bad) atomicOr(P.err, 1);
     __syncthreads();
+    for (int i = tid; i < reach; i += kResolveThreads) {
+        const int s = min(max(order[i], 0), ns - 1);
+        front_l[i] = g_ol[s];
+        front_e[i] = g_oe[s];
+    }
+    __syncthreads();
     if (tid == 0) {
-        int32_t *hdr = P.lru.hdr + 4 * P.shard;
-        int head = hdr[0], tail = hdr[1], n_in = hdr[2];
-        int hits = 0, misses = 0;
-        auto unlink = [&](int s) {
-            const int a = prv[s], b = nxt[s];
-            if (a >= 0) nxt[a] = b;
-            else head = b;
-            if (b >= 0) prv[b] = a;
-            else tail = a;
-            prv[s] = nxt[s] = -1;
-            n_in--;
-        };
-        auto push_tail = [&](int s) {
-            prv[s] = tail;
-            nxt[s] = -1;
-            if (tail >= 0) nxt[tail] = s;
-            tail = s;
-            if (head < 0) head = s;
-            n_in++;
-        };
+        int p = 0, hits = 0, misses = 0;
         for (int i = 0; i < n; i++) {
             const int e = ex[i];
             int s = slot_of[e];
             if (s >= 0) {
-                if (pins[s] == 0) unlink(s);
-                pins[s]++;
+                used[s] = 1;
                 got[i] = s;
                 hits++;
                 continue;
             }
-            s = head;
-            if (s < 0) {
-                // cannot happen: the host only launches calls of at most n_slots experts, and at
-                // most i slots are pinned here; flagged, and the request is served from slot 0 so
-                // nothing leaves the pool
+            while (p < reach && used[order[p]]) p++;
+            if (p == reach) {
+                // cannot happen: the host launches at most n_slots requests, and each passes at most
+                // two entries; flagged, and the request is served from slot 0 so nothing leaves the pool
                 atomicOr(P.err, 8);
                 got[i] = -1;
                 continue;
             }
-            unlink(s);
-            const int l0 = own_l[s], e0 = own_e[s];
+            s = order[p];
+            const int l0 = front_l[p], e0 = front_e[p];
+            p++;
             if (l0 == P.layer) slot_of[e0] = -1;
             else if (l0 >= 0) P.lru.slot_of[(size_t) l0 * E + e0] = -1;
-            own_l[s] = P.layer;
-            own_e[s] = e;
+            g_ol[s] = P.layer;
+            g_oe[s] = e;
             slot_of[e] = s;
-            pins[s] = 1;
+            used[s] = 1;
             got[i] = s;
             P.miss[2 * misses] = s;
             P.miss[2 * misses + 1] = e;
             misses++;
         }
-        for (int i = 0; i < n; i++) {
-            const int s = got[i];
-            if (s >= 0 && --pins[s] == 0) push_tail(s);
-        }
-        hdr[0] = head;
-        hdr[1] = tail;
-        hdr[2] = n_in;
         *P.n_miss = misses;
         P.lru.stats[0] += (unsigned long long) hits;
         P.lru.stats[1] += (unsigned long long) misses;
@@ -119,14 +128,25 @@ __global__ __launch_bounds__(256) void lru_resolve_kernel(TierResolveParams P) {
         P.lru.stats[3] += 1ull;
     }
     __syncthreads();
-    for (int i = tid; i < ns; i += blockDim.x) {
-        g_prev[i] = prv[i];
-        g_next[i] = nxt[i];
-        g_ol[i] = own_l[i];
-        g_oe[i] = own_e[i];
-    }
-    for (int i = tid; i < E; i += blockDim.x) g_slot_of[i] = slot_of[i];
-    for (int i = tid; i < n; i += blockDim.x) P.slots[i] = got[i] < 0 ? 0 : got[i];
+    for (int i = tid; i < n; i += kResolveThreads)
+        if (got[i] >= 0) atomicMax(&last[got[i]], i);
+    __syncthreads();
+    // new order: unmarked entries in order, then the used slots by their last request. Thread t owns
+    // the consecutive entries [t c, (t + 1) c) of each list.
+    const int ce = (ns + kResolveThreads - 1) / kResolveThreads, ci = (n + kResolveThreads - 1) / kResolveThreads;
+    int keep = 0, rel = 0;
+    for (int j = tid * ce; j < min(ns, (tid + 1) * ce); j++) keep += used[order[j]] ? 0 : 1;
+    for (int i = tid * ci; i < min(n, (tid + 1) * ci); i++) rel += (got[i] >= 0 && last[got[i]] == i) ? 1 : 0;
+    int n_keep, n_rel;
+    int at = block_excl_scan(keep, s_w, &n_keep);
+    int at_rel = n_keep + block_excl_scan(rel, s_w, &n_rel);
+    for (int j = tid * ce; j < min(ns, (tid + 1) * ce); j++)
+        if (!used[order[j]]) g_order[at++] = order[j];
+    for (int i = tid * ci; i < min(n, (tid + 1) * ci); i++)
+        if (got[i] >= 0 && last[got[i]] == i) g_order[at_rel++] = got[i];
+    if (tid == 0 && n_keep + n_rel != ns) atomicOr(P.err, 8);
+    for (int i = tid; i < E; i += kResolveThreads) g_slot_of[i] = slot_of[i];
+    for (int i = tid; i < n; i += kResolveThreads) P.slots[i] = got[i] < 0 ? 0 : got[i];
 }
 
 __global__ __launch_bounds__(kCopyThreads) void tier_copy_kernel(TierCopyParams P) {
@@ -171,7 +191,7 @@ __global__ __launch_bounds__(kCopyThreads) void tier_copy_kernel(TierCopyParams 
 int tier_copy_chunks(size_t bytes) { return (int) ((bytes + kCopyChunk - 1) / kCopyChunk); }
 
 hipError_t launch_tier_resolve(const TierResolveParams &P, hipStream_t st, const LaunchTiming *tm) {
-    return launch(lru_resolve_kernel, dim3(1), dim3(256), 0, st, tm, P);
+    return launch(lru_resolve_kernel, dim3(1), dim3(kResolveThreads), 0, st, tm, P);
 }
 
 hipError_t launch_tier_copy(const TierCopyParams &P, hipStream_t st, const LaunchTiming *tm) {
