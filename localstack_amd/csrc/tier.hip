@@ -8,8 +8,8 @@
 //                       order by one lane against LDS copies: a resident expert is a hit (its slot is
 //                       marked used); otherwise the first unmarked entry of the order is taken, its
 //                       previous expert unmapped, and (slot, expert) recorded as a miss. Everything
-//                       else is done by the whole work-group in parallel: staging, the owners of the
-//                       entries a miss can reach (the first 2n), and the new order - the unmarked
+//                       else is done by the whole work-group in parallel: staging (the order, the
+//                       owners and the layer's expert -> slot map, in one round) and the new order - the unmarked
 //                       entries in their order, then the call's slots by their last request (the order
 //                       in which release_all returns them), placed by two work-group prefix sums;
 //   tier_copy_kernel    copies the three matrices of every miss from the pinned host tier into the
@@ -55,18 +55,27 @@ __device__ __forceinline__ int block_excl_scan(int v, int *s_w, int *total) {
 
 __global__ __launch_bounds__(kResolveThreads) void lru_resolve_kernel(TierResolveParams P) {
     __shared__ int32_t order[kTierMaxSlots], last[kTierMaxSlots], slot_of[kTierMaxExperts];
-    __shared__ int32_t front_l[2 * kTierMaxIds < kTierMaxSlots ? 2 * kTierMaxIds : kTierMaxSlots];
-    __shared__ int32_t front_e[2 * kTierMaxIds < kTierMaxSlots ? 2 * kTierMaxIds : kTierMaxSlots];
+    __shared__ int32_t own_l[kTierMaxSlots], own_e[kTierMaxSlots];
     __shared__ int32_t ex[kTierMaxIds], got[kTierMaxIds];
     __shared__ uint8_t used[kTierMaxSlots];
     __shared__ int s_w[kResolveThreads / kWave];
     const int tid = threadIdx.x, ns = P.n_slots, E = P.E, n = P.n;
-    const int reach = min(ns, 2 * n); // entries a miss can take: each request passes at most two
+    const int reach = min(ns, 2 * n); // entries a miss can reach: each request passes at most two
+    // the counters, read before anything waits (lane 0 adds this call's figures at the end)
+    unsigned long long st0 = 0, st1 = 0, st2 = 0, st3 = 0;
+    if (tid == 0) {
+        st0 = P.lru.stats[0];
+        st1 = P.lru.stats[1];
+        st2 = P.lru.stats[2];
+        st3 = P.lru.stats[3];
+    }
     int32_t *g_order = P.lru.order + P.slot_base;
     int32_t *g_ol = P.lru.owner_layer + P.slot_base, *g_oe = P.lru.owner_expert + P.slot_base;
     int32_t *g_slot_of = P.lru.slot_of + (size_t) P.layer * E;
     for (int i = tid; i < ns; i += kResolveThreads) {
         order[i] = g_order[i];
+        own_l[i] = g_ol[i];
+        own_e[i] = g_oe[i];
         last[i] = -1;
         used[i] = 0;
     }
@@ -81,12 +90,6 @@ __global__ __launch_bounds__(kResolveThreads) void lru_resolve_kernel(TierResolv
         ex[i] = e;
     }
     if (bad) atomicOr(P.err, 1);
-    __syncthreads();
-    for (int i = tid; i < reach; i += kResolveThreads) {
-        const int s = min(max(order[i], 0), ns - 1);
-        front_l[i] = g_ol[s];
-        front_e[i] = g_oe[s];
-    }
     __syncthreads();
     if (tid == 0) {
         int p = 0, hits = 0, misses = 0;
@@ -107,9 +110,8 @@ __global__ __launch_bounds__(kResolveThreads) void lru_resolve_kernel(TierResolv
                 got[i] = -1;
                 continue;
             }
-            s = order[p];
-            const int l0 = front_l[p], e0 = front_e[p];
-            p++;
+            s = order[p++];
+            const int l0 = own_l[s], e0 = own_e[s];
             if (l0 == P.layer) slot_of[e0] = -1;
             else if (l0 >= 0) P.lru.slot_of[(size_t) l0 * E + e0] = -1;
             g_ol[s] = P.layer;
@@ -122,10 +124,10 @@ __global__ __launch_bounds__(kResolveThreads) void lru_resolve_kernel(TierResolv
             misses++;
         }
         *P.n_miss = misses;
-        P.lru.stats[0] += (unsigned long long) hits;
-        P.lru.stats[1] += (unsigned long long) misses;
-        P.lru.stats[2] += (unsigned long long) misses * P.slab;
-        P.lru.stats[3] += 1ull;
+        P.lru.stats[0] = st0 + (unsigned long long) hits;
+        P.lru.stats[1] = st1 + (unsigned long long) misses;
+        P.lru.stats[2] = st2 + (unsigned long long) misses * P.slab;
+        P.lru.stats[3] = st3 + 1ull;
     }
     __syncthreads();
     for (int i = tid; i < n; i += kResolveThreads)
