@@ -22,7 +22,8 @@ import os
 import numpy as np
 
 HERE = os.path.dirname(os.path.abspath(__file__))
-LIB_PATH = os.path.join(HERE, "liblstk_moe.so")
+# LSTK_LIBRARY names another build of the library (the sanitizer build of the CPU tests)
+LIB_PATH = os.environ.get("LSTK_LIBRARY") or os.path.join(HERE, "liblstk_moe.so")
 
 TYPE_F32, TYPE_F16, TYPE_Q8_0, TYPE_Q4_K = 0, 1, 8, 12
 POOL_STREAMING, POOL_DRY, POOL_DEVICE_LRU, POOL_AUTO_SIZE = 1, 2, 4, 8

@@ -9,7 +9,6 @@ import os
 import shutil
 import subprocess
 import sys
-import tempfile
 
 HERE = os.path.dirname(os.path.abspath(__file__))
 ROOT = os.path.dirname(HERE)
@@ -51,28 +50,68 @@ def _run(cmd, verbose):
         print(out)
 
 
+OBJ_DIR = os.path.join(HERE, "_build")  # objects of the last build (not shipped; the sanitizer build reuses the kernels')
+ASAN_LIB = os.path.join(OBJ_DIR, "liblstk_moe_asan.so")
+# host sources checked by the sanitizer build: the pool's bookkeeping, the GGUF reader, the repacker, the model's host side
+HOST_SOURCES = ["pool.cpp", "repack.cpp", "model.cpp", "gguf.cpp"]
+SANITIZE = ["-Xarch_host", "-fsanitize=address", "-Xarch_host", "-fsanitize=undefined",
+            "-Xarch_host", "-fno-omit-frame-pointer"]
+
+
+def _compile(sources, objdir, extra, verbose):
+    from concurrent.futures import ThreadPoolExecutor
+    os.makedirs(objdir, exist_ok=True)
+    cmds, objs = [], []
+    for s in sources:
+        o = os.path.join(objdir, s + ".o")
+        objs.append(o)
+        cmds.append([hipcc(), "-x", "hip", f"--offload-arch={ARCH}"] + COMMON + EXTRA.get(s, []) + extra.get(s, []) +
+                    ["-I", os.path.join(ROOT, "include"), "-c", os.path.join(CSRC, s), "-o", o])
+    with ThreadPoolExecutor(max_workers=min(len(cmds), 8)) as ex:
+        list(ex.map(lambda c: _run(c, verbose), cmds))
+    return objs
+
+
+def _link(objs, out, extra, verbose):
+    tmp = out + ".tmp"
+    rocm_lib = os.path.join(os.environ.get("ROCM_PATH", "/opt/rocm"), "lib")
+    _run([hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", tmp] + extra + objs +
+         ["-L", rocm_lib, "-lrocblas", "-Wl,-rpath," + rocm_lib, "-lpthread"], verbose)
+    os.replace(tmp, out)
+
+
 def build(verbose=False):
     """Compiles every source for gfx950 (in parallel) and links the shared library; always rebuilds."""
-    from concurrent.futures import ThreadPoolExecutor
-    tmpdir = tempfile.mkdtemp(prefix="lstk_build_")
-    try:
-        objs = []
-        cmds = []
-        for s in SOURCES:
-            o = os.path.join(tmpdir, s + ".o")
-            objs.append(o)
-            cmds.append([hipcc(), "-x", "hip", f"--offload-arch={ARCH}"] + COMMON + EXTRA.get(s, []) +
-                        ["-I", os.path.join(ROOT, "include"), "-c", os.path.join(CSRC, s), "-o", o])
-        with ThreadPoolExecutor(max_workers=min(len(cmds), 8)) as ex:
-            list(ex.map(lambda c: _run(c, verbose), cmds))
-        tmp = LIB + ".tmp"
-        rocm_lib = os.path.join(os.environ.get("ROCM_PATH", "/opt/rocm"), "lib")
-        _run([hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", tmp] + objs +
-             ["-L", rocm_lib, "-lrocblas", "-Wl,-rpath," + rocm_lib, "-lpthread"], verbose)
-        os.replace(tmp, LIB)
-    finally:
-        shutil.rmtree(tmpdir, ignore_errors=True)
+    objs = _compile(SOURCES, OBJ_DIR, {}, verbose)
+    _link(objs, LIB, [], verbose)
     return LIB
+
+
+def build_sanitized(verbose=False):
+    """A copy of the library whose host sources (HOST_SOURCES) are built with AddressSanitizer and
+    UndefinedBehaviorSanitizer on the host side only (the device code is unchanged), for the CPU tests of
+    the dry pool and the GGUF reader. The kernel sources' objects come from the last build() (compiled
+    here if there are none). Load it with the sanitizer runtime preloaded (asan_runtime())."""
+    kernels = [s for s in SOURCES if s not in HOST_SOURCES]
+    have = all(os.path.exists(os.path.join(OBJ_DIR, s + ".o")) for s in kernels)
+    kobjs = [os.path.join(OBJ_DIR, s + ".o") for s in kernels] if have else _compile(kernels, OBJ_DIR, {}, verbose)
+    sdir = os.path.join(OBJ_DIR, "asan")
+    hobjs = _compile(HOST_SOURCES, sdir, {s: ["-O1", "-g"] + SANITIZE for s in HOST_SOURCES}, verbose)
+    _link(kobjs + hobjs, ASAN_LIB, ["-Xarch_host", "-fsanitize=address", "-Xarch_host", "-fsanitize=undefined",
+                                    "-shared-libsan"], verbose)
+    return ASAN_LIB
+
+
+def asan_runtime():
+    """The clang AddressSanitizer runtime that the sanitized library links against, or None."""
+    root = os.path.join(os.environ.get("ROCM_PATH", "/opt/rocm"), "llvm", "lib", "clang")
+    if not os.path.isdir(root):
+        return None
+    for v in sorted(os.listdir(root), reverse=True):
+        p = os.path.join(root, v, "lib", "linux", "libclang_rt.asan-x86_64.so")
+        if os.path.exists(p):
+            return p
+    return None
 
 
 if __name__ == "__main__":
