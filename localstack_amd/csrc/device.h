@@ -14,6 +14,22 @@
 #include "kernels.h"
 
 namespace lstk {
+
+#ifndef LSTK_NT_WEIGHTS
+#define LSTK_NT_WEIGHTS 1
+#endif
+// Weights read once per call (the experts of one token, the dense matrices of one decode step) carry the
+// non-temporal hint, so they do not displace what the next launches read again (router rows,
+// activations, the KV cache) from the last-level cache. LSTK_NT_WEIGHTS=0 turns the hint off.
+__device__ __forceinline__ uint4 load_weights(const uint4 *p) {
+#if LSTK_NT_WEIGHTS
+    typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
+    const u32x4 v = __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(p));
+    return make_uint4(v.x, v.y, v.z, v.w);
+#else
+    return *p;
+#endif
+}
 namespace {
 
 constexpr int kWave = 64;

@@ -280,7 +280,7 @@ __global__ __launch_bounds__(kGvWaves *kWave) void gemv1_kernel(GemvParams P) {
     for (int j = 0; j < NJ; j++) {
         const int c = lane + kWave * j;
 #pragma unroll
-        for (int rr = 0; rr < RW; rr++) w[rr][j] = c < nc ? wr[rr][c] : make_uint4(0, 0, 0, 0);
+        for (int rr = 0; rr < RW; rr++) w[rr][j] = c < nc ? load_weights(wr[rr] + c) : make_uint4(0, 0, 0, 0);
     }
     float xv[NJ][8];
     const uint16_t *e = P.emb ? P.emb + (size_t) P.tokens[0] * cols : nullptr;
