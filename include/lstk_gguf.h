@@ -66,12 +66,14 @@ int lstk_gguf_qwen3_hparams(const lstk_gguf *g, lstk_qwen3_hparams *hp);
 /* qwen3_expert_infos: for each of hp->n_layer layers, the types and mapped host pointers of
  * blk.L.ffn_{up,gate,down}_exps.weight, ready for lstk_pool_create. The shapes must match hp (up and
  * gate [n_embd, n_ff_exp, n_expert], down [n_ff_exp, n_embd, n_expert]) and the types must be ones the
- * pool stores (Q8_0, Q4_K): anything else fails with a message naming the layer, tensor and type. */
+ * pool stores (Q8_0, Q2_K, Q3_K, Q4_K, Q5_K, Q6_K): anything else fails with a message naming the
+ * layer, tensor and type. */
 int lstk_gguf_qwen3_experts(const lstk_gguf *g, const lstk_qwen3_hparams *hp, lstk_expert_layer *layers);
 
 /* Dense tensors for the forward pass, which multiplies F16 matrices: n values of a tensor of ggml type
  * `type` at src (GGUF bytes, n a multiple of the type's block) to fp16 at dst, round to nearest even.
- * F32, F16, Q8_0 (d q), Q4_K (d sc q - dmin m), Q5_K (d sc (q + 16 h) - dmin m) and Q6_K (d sc (q - 32),
+ * F32, F16, Q8_0 (d q), Q2_K (d sc q - dmin m, 2-bit q, 4-bit sc / m per 16 values), Q3_K (d (sc - 32) (q - 4 h'),
+ * 3-bit q, 6-bit sc per 16), Q4_K (d sc q - dmin m), Q5_K (d sc (q + 16 h) - dmin m) and Q6_K (d sc (q - 32),
  * sc a signed 8-bit scale per 16 values) - ggml's dequantize_row_* for each format (the reference maps such
  * tensors into its graph whatever their type, src/qwen3.cpp:52-89). Each value is formed in f32 in ggml's
  * order, then rounded to fp16 once; the forward pass then differs from ggml's quantized dot products by the

@@ -34,6 +34,10 @@ extern "C" {
 #define LSTK_TYPE_F16 1
 #define LSTK_TYPE_Q8_0 8
 #define LSTK_TYPE_Q4_K 12
+#define LSTK_TYPE_Q2_K 10
+#define LSTK_TYPE_Q3_K 11
+#define LSTK_TYPE_Q5_K 13
+#define LSTK_TYPE_Q6_K 14
 
 /* Error codes. */
 #define LSTK_OK 0
@@ -61,7 +65,8 @@ typedef struct lstk_moe_dims {
 /* One layer's stacked expert tensors as they sit in a GGUF file: expert e of a matrix starts at
  * host_x + e * expert_stride (GgufTensorInfo::expert_stride, src/gguf_model.h:28).
  * up/gate are [n_expert][n_ff_exp rows][n_embd cols], down is [n_expert][n_embd rows][n_ff_exp cols],
- * each row a run of Q8_0 (34 B / 32 values) or Q4_K (144 B / 256 values) blocks.
+ * each row a run of Q8_0 (34 B / 32 values) or Q2_K / Q3_K / Q4_K / Q5_K / Q6_K (84 / 110 / 144 / 176 /
+ * 210 B per 256 values) blocks; gate and up share a type, down may differ.
  * Replaces ExpertLayerInfo (src/expert_store.h:32-36), with host memory in place of a file offset. */
 typedef struct lstk_expert_layer {
     int32_t type_up, type_gate, type_down;
@@ -219,8 +224,11 @@ int lstk_pool_timing(lstk_pool *pool, double ms[4], int64_t launches[4]);
 /* Host-side repacking between GGUF expert bytes and the pool's HBM layout (one expert matrix of
  * `rows` x `cols`). The pool layout is [cols/256][C][rows][16 B]: each 256-value super-block row is
  * split into C 16-byte chunks (Q8_0: 8 fp16 scales + 16 chunks of int8; Q4_K: {d, dmin, scales}
- * + 8 chunks of 4-bit pairs) and the chunks of neighbouring rows are adjacent, so a wavefront reading
- * one chunk of 64 rows issues one coalesced 1 KiB load. Sizes are unchanged. */
+ * + 8 chunks of 4-bit pairs; Q2_K, Q3_K, Q5_K and Q6_K unpacked to integers: {f32 d, f32 dmin},
+ * 16 int8 scales, 16 mins and 16 chunks of int8 quants, one per 16 values) and the chunks of
+ * neighbouring rows are adjacent, so a wavefront reading one chunk of 64 rows issues one coalesced
+ * 1 KiB load. lstk_matrix_bytes is the pool size (the GGUF size for Q8_0 and Q4_K, 304 B per
+ * super-block row for the other k-quants); lstk_unpack_matrix inverts Q8_0 and Q4_K only. */
 size_t lstk_matrix_bytes(int type, int rows, int cols);
 int lstk_repack_matrix(int type, int rows, int cols, const void *gguf, void *packed);
 int lstk_unpack_matrix(int type, int rows, int cols, const void *packed, void *gguf);

@@ -467,9 +467,10 @@ class Qwen3Model:
 
 
 _GGML_NP = {0: np.float32, 1: np.float16}
-_GGML_NAME = {0: "F32", 1: "F16", 8: "Q8_0", 12: "Q4_K", 13: "Q5_K", 14: "Q6_K", 15: "Q8_K", 30: "BF16"}
+_GGML_NAME = {0: "F32", 1: "F16", 8: "Q8_0", 10: "Q2_K", 11: "Q3_K", 12: "Q4_K", 13: "Q5_K", 14: "Q6_K", 15: "Q8_K", 30: "BF16"}
 # types lstk_dequant_f16 expands, with (values, bytes) per block
-DEQUANT_TYPES = {0: (1, 4), 1: (1, 2), 8: (32, 34), 12: (256, 144), 13: (256, 176), 14: (256, 210)}
+DEQUANT_TYPES = {0: (1, 4), 1: (1, 2), 8: (32, 34), 10: (256, 84), 11: (256, 110), 12: (256, 144), 13: (256, 176),
+                 14: (256, 210)}
 
 
 def dequant_f16(type_, data, n):
@@ -562,7 +563,7 @@ class GgufFile:
         return self.tensor_bytes(name).view(_GGML_NP[info["type"]]).reshape(tuple(reversed(info["ne"])))
 
     def tensor_f16(self, name):
-        """Any type lstk_dequant_f16 expands (F32, F16, Q8_0, Q4_K, Q5_K, Q6_K) as a float16 array shaped
+        """Any type lstk_dequant_f16 expands (F32, F16, Q8_0, Q2_K .. Q6_K) as a float16 array shaped
         [ne[n-1]]...[ne[0]]; F16 stays a view of the mapping, the others are dequantized copies."""
         info = self.tensor_info(name)
         if info["type"] == 1:
@@ -587,7 +588,7 @@ def qwen3_dense_weights(g, hp):
     src/qwen3.cpp:52-89): {"tok_embd", "output_norm", "output" (None when the head is tied), "layers": [...]}.
     Norms must be F32; the router is taken as F16 or F32 as stored; the matrices the forward pass multiplies
     in F16 (embedding, attention, output) are taken as stored when F16 and dequantized to F16 from F32, Q8_0,
-    Q4_K, Q5_K or Q6_K (lstk_dequant_f16); other types are rejected with the tensor's name."""
+    Q2_K, Q3_K, Q4_K, Q5_K or Q6_K (lstk_dequant_f16); other types are rejected with the tensor's name."""
     names = {t["name"] for t in g.tensors()}
 
     def dense(name, types=tuple(DEQUANT_TYPES), optional=False):

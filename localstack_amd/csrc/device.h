@@ -652,12 +652,45 @@ __device__ __forceinline__ float dot_sb_q4_K(const uint4 (&w)[kChunksQ4_K], cons
     return acc;
 }
 
+// KQ8 (Q2_K, Q3_K, Q5_K, Q6_K unpacked) x Q8_K: per 16-value group g, dot_g = q_g . x_g and bsum_g =
+// the sum of x_g (both exact int32 from v_dot4); isum = sum_g sc_g dot_g, imin = sum_g m_g bsum_g;
+// acc += (d_w d_x) isum, then acc -= (dmin_w d_x) imin.
+__device__ __forceinline__ float dot_sb_kq8(const uint4 (&w)[kChunksKQ8], const int8_t *x, const float *xd, float acc) {
+    const float dw = __uint_as_float(w[0].x), dmin = __uint_as_float(w[0].y);
+    int isum = 0, imin = 0;
+#pragma unroll
+    for (int g = 0; g < 16; g++) {
+        const int4 xv = *reinterpret_cast<const int4 *>(x + 16 * g);
+        const uint4 q = w[3 + g];
+        int s = __builtin_amdgcn_sdot4((int) q.x, xv.x, 0, false);
+        s = __builtin_amdgcn_sdot4((int) q.y, xv.y, s, false);
+        s = __builtin_amdgcn_sdot4((int) q.z, xv.z, s, false);
+        s = __builtin_amdgcn_sdot4((int) q.w, xv.w, s, false);
+        int b = __builtin_amdgcn_sdot4(0x01010101, xv.x, 0, false);
+        b = __builtin_amdgcn_sdot4(0x01010101, xv.y, b, false);
+        b = __builtin_amdgcn_sdot4(0x01010101, xv.z, b, false);
+        b = __builtin_amdgcn_sdot4(0x01010101, xv.w, b, false);
+        const unsigned scw = g < 4 ? w[1].x : g < 8 ? w[1].y : g < 12 ? w[1].z : w[1].w;
+        const unsigned mw = g < 4 ? w[2].x : g < 8 ? w[2].y : g < 12 ? w[2].z : w[2].w;
+        const int sc = (int) (int8_t) (scw >> (8 * (g % 4))), m = (int) ((mw >> (8 * (g % 4))) & 0xFFu);
+        isum += sc * s;
+        imin += m * b;
+    }
+    const float dx = xd[0];
+    acc += (dw * dx) * (float) isum;
+    acc -= (dmin * dx) * (float) imin;
+    return acc;
+}
+
 template <int WT>
 __device__ __forceinline__ float dot_sb(const uint4 (&w)[chunks_of(WT)], const int8_t *x, const float *xd,
                                         const int *xb, float acc) {
     if constexpr (WT == kTypeQ8_0) {
         (void) xb;
         return dot_sb_q8_0(w, x, xd, acc);
+    } else if constexpr (WT == kTypeKQ8) {
+        (void) xb;
+        return dot_sb_kq8(w, x, xd, acc);
     } else {
         return dot_sb_q4_K(w, x, xd, xb, acc);
     }

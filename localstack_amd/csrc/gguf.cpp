@@ -20,6 +20,7 @@
 #include <vector>
 
 #include "../../include/lstk_gguf.h"
+#include "formats.h"
 #include "internal.h"
 
 namespace {
@@ -389,9 +390,9 @@ int lstk_gguf_qwen3_experts(const lstk_gguf *g, const lstk_qwen3_hparams *hp, ls
                               t[2].ne[0] == hp->n_ff_exp && t[2].ne[1] == hp->n_embd && t[2].ne[2] == hp->n_expert;
         if (!shape_ok) return set_error(LSTK_E_INVALID, "expert tensor shapes do not match the hyperparameters for layer " + std::to_string(l));
         for (int m = 0; m < 3; m++)
-            if (t[m].type != LSTK_TYPE_Q8_0 && t[m].type != LSTK_TYPE_Q4_K)
+            if (!lstk::supported_weight_type(t[m].type))
                 return set_error(LSTK_E_INVALID, "layer " + std::to_string(l) + ": " + p + names[m] + " is " + type_name(t[m].type) +
-                                                     "; the expert pool stores Q8_0 and Q4_K");
+                                                     "; the expert pool stores Q8_0, Q2_K, Q3_K, Q4_K, Q5_K and Q6_K");
         layers[l].type_up = t[0].type;
         layers[l].type_gate = t[1].type;
         layers[l].type_down = t[2].type;
@@ -485,12 +486,10 @@ extern "C" int lstk_dequant_f16(int type, const void *src, size_t n, uint16_t *d
         }
         return LSTK_OK;
     case 12: // Q4_K: {fp16 d, dmin, scales[12], qs[128]}
-    case 13: // Q5_K: {fp16 d, dmin, scales[12], qh[32], qs[128]}
         if (n % 256) break;
-        for (size_t blk = 0; blk < n / 256; blk++) {
-            const bool five = type == 13;
+        for (size_t blk = 0; blk < n / 256; blk++, b += 144) {
             const float d = half_to_float(h16(b)), dmin = half_to_float(h16(b + 2));
-            const uint8_t *sc = b + 4, *qh = b + 16, *ql = five ? b + 48 : b + 16;
+            const uint8_t *sc = b + 4, *qs = b + 16;
             uint16_t *y = dst + blk * 256;
             for (int c = 0; c < 4; c++) { // 64 values: sub-blocks 2c (low nibbles) and 2c + 1 (high)
                 int s0, m0, s1, m1;
@@ -498,42 +497,30 @@ extern "C" int lstk_dequant_f16(int type, const void *src, size_t n, uint16_t *d
                 scale_min_k4(2 * c + 1, sc, s1, m1);
                 const float d1 = d * (float) s0, mm1 = dmin * (float) m0, d2 = d * (float) s1, mm2 = dmin * (float) m1;
                 for (int l = 0; l < 32; l++) {
-                    int q0 = ql[32 * c + l] & 0xF, q1 = ql[32 * c + l] >> 4;
-                    if (five) {
-                        q0 += (qh[l] >> (2 * c)) & 1 ? 16 : 0;
-                        q1 += (qh[l] >> (2 * c + 1)) & 1 ? 16 : 0;
-                    }
-                    y[64 * c + l] = float_to_half(d1 * (float) q0 - mm1);
-                    y[64 * c + 32 + l] = float_to_half(d2 * (float) q1 - mm2);
+                    y[64 * c + l] = float_to_half(d1 * (float) (qs[32 * c + l] & 0xF) - mm1);
+                    y[64 * c + 32 + l] = float_to_half(d2 * (float) (qs[32 * c + l] >> 4) - mm2);
                 }
             }
-            b += five ? 176 : 144;
         }
         return LSTK_OK;
-    case 14: // Q6_K: {ql[128], qh[64], int8 scales[16], fp16 d}
+    case 10: // Q2_K, Q3_K, Q5_K, Q6_K: the block as integers (kq8_unpack), then (d sc) q - dmin m as ggml forms it
+    case 11:
+    case 13:
+    case 14: {
+        const size_t bb = (size_t) lstk::gguf_superblock_bytes(type);
         if (n % 256) break;
-        for (size_t blk = 0; blk < n / 256; blk++, b += 210) {
-            const uint8_t *ql = b, *qh = b + 128;
-            const int8_t *sc = reinterpret_cast<const int8_t *>(b + 192);
-            const float d = half_to_float(h16(b + 208));
+        const bool mins = type == 10 || type == 13;
+        lstk::KQ8Block k;
+        for (size_t blk = 0; blk < n / 256; blk++, b += bb) {
+            lstk::kq8_unpack(type, b, k);
             uint16_t *y = dst + blk * 256;
-            for (int half = 0; half < 2; half++) { // 128 values each
-                const uint8_t *l8 = ql + 64 * half, *h8 = qh + 32 * half;
-                const int8_t *s8 = sc + 8 * half;
-                for (int l = 0; l < 32; l++) {
-                    const int is = l / 16;
-                    const int q1 = (int) ((l8[l] & 0xF) | ((h8[l] & 3) << 4)) - 32;
-                    const int q2 = (int) ((l8[l + 32] & 0xF) | (((h8[l] >> 2) & 3) << 4)) - 32;
-                    const int q3 = (int) ((l8[l] >> 4) | (((h8[l] >> 4) & 3) << 4)) - 32;
-                    const int q4 = (int) ((l8[l + 32] >> 4) | (((h8[l] >> 6) & 3) << 4)) - 32;
-                    y[128 * half + l] = float_to_half(d * (float) s8[is] * (float) q1);
-                    y[128 * half + l + 32] = float_to_half(d * (float) s8[is + 2] * (float) q2);
-                    y[128 * half + l + 64] = float_to_half(d * (float) s8[is + 4] * (float) q3);
-                    y[128 * half + l + 96] = float_to_half(d * (float) s8[is + 6] * (float) q4);
-                }
+            for (int v = 0; v < 256; v++) {
+                const float dl = k.d * (float) k.sc[v / 16], yv = dl * (float) k.q[v];
+                y[v] = float_to_half(mins ? yv - k.dmin * (float) k.m[v / 16] : yv);
             }
         }
         return LSTK_OK;
+    }
     default:
         return set_error(LSTK_E_INVALID, "lstk_dequant_f16: unsupported type " + std::to_string(type));
     }

@@ -572,7 +572,7 @@ __global__ __launch_bounds__(NT) void gate_up_kernel(GateUpParams P) {
 template <int WT, int S>
 __global__ __launch_bounds__(kDnRows * kMaxG) void down_kernel(DownParams P) {
     constexpr int C = chunks_of(WT);
-    constexpr int QT = WT == kTypeQ4_K ? kTypeQ4_K : kTypeQ8_0;
+    constexpr int QT = WT == kTypeQ8_0 ? kTypeQ8_0 : kTypeQ4_K; // Q8_K activations for every k-quant
     extern __shared__ __align__(16) unsigned char smem[];
     const int G = blockDim.x / kDnRows;
     const int tid = threadIdx.x, r = tid % kDnRows, g = tid / kDnRows;
@@ -712,7 +712,7 @@ __device__ __forceinline__ void q8k_block_lanes(const float (&v)[VPT], int lanes
 template <int WT, int NP, int R, int SEG>
 __global__ __launch_bounds__(kBlock) void down_combine_kernel(DownCombineParams P, int rd0) {
     constexpr int C = chunks_of(WT);
-    constexpr int QT = WT == kTypeQ4_K ? kTypeQ4_K : kTypeQ8_0;
+    constexpr int QT = WT == kTypeQ8_0 ? kTypeQ8_0 : kTypeQ4_K; // Q8_K activations for every k-quant
     extern __shared__ __align__(16) unsigned char smem[];
     const int tid = threadIdx.x, k = P.k, f = P.f, nsbf = f / 256, nact = k * f;
     // R rows per thread: local row ir * rd0 + rr of the work-group's rd = R * rd0 rows
@@ -955,7 +955,7 @@ template <int WT, int R>
 hipError_t launch_down_combine_r(const DownCombineParams &P, int rd0, int np, size_t lds, int threads, hipStream_t st,
                                  const LaunchTiming *tm) {
     const dim3 grid(P.h / (rd0 * R)), block(threads);
-    if (WT == kTypeQ4_K && threads == P.k * (P.f / 256) * rd0) {
+    if (WT != kTypeQ8_0 && threads == P.k * (P.f / 256) * rd0) {
         // one Q8_K block per (pair, super-block), quantized by that combination's rd0 threads
         switch (rd0) {
             case 4: return launch(down_combine_kernel<WT, 1, R, 64>, grid, block, lds, st, tm, P, rd0);
@@ -978,7 +978,7 @@ hipError_t launch_down_combine_t(const DownCombineParams &P, hipStream_t st, con
     const int threads = (P.k * nsbf * rd0 + kWave - 1) / kWave * kWave;
     const size_t lds = (size_t) nact + (size_t) nact / 32 * 8 + (size_t) P.k * nsbf * rd0 * R * 4 + (size_t) P.k * 4;
     // Q8_0: whole 32-value blocks per thread; Q8_K: passes of 8 values per thread
-    const int per = WT == kTypeQ4_K ? threads * 8 : threads * 32;
+    const int per = WT != kTypeQ8_0 ? threads * 8 : threads * 32;
     const int np = (nact + per - 1) / per;
     if (R == 4) return launch_down_combine_r<WT, 4>(P, rd0, np, lds, threads, st, tm);
     if (R == 2) return launch_down_combine_r<WT, 2>(P, rd0, np, lds, threads, st, tm);
@@ -997,7 +997,11 @@ bool down_combine_supported(int h, int f, int k) {
 
 hipError_t launch_down_combine(const DownCombineParams &P, hipStream_t st, const LaunchTiming *tm) {
     if (!down_combine_supported(P.h, P.f, P.k)) return hipErrorInvalidValue;
-    return P.type == kTypeQ8_0 ? launch_down_combine_t<kTypeQ8_0>(P, st, tm) : launch_down_combine_t<kTypeQ4_K>(P, st, tm);
+    switch (pool_format(P.type)) {
+        case kTypeQ8_0: return launch_down_combine_t<kTypeQ8_0>(P, st, tm);
+        case kTypeKQ8: return launch_down_combine_t<kTypeKQ8>(P, st, tm);
+        default: return launch_down_combine_t<kTypeQ4_K>(P, st, tm);
+    }
 }
 
 int decode_route_max_tokens() { return kDecodeRouteT; }
@@ -1047,6 +1051,10 @@ hipError_t launch_gate_up(const GateUpParams &P, hipStream_t st, const LaunchTim
         if (S == 1) return launch_gate_up_t<kTypeQ8_0, 1>(P, G, st, tm);
         return launch_gate_up_t<kTypeQ8_0, 2>(P, G, st, tm);
     }
+    if (pool_format(P.type) == kTypeKQ8) {
+        if (S == 1) return launch_gate_up_t<kTypeKQ8, 1>(P, G, st, tm);
+        return launch_gate_up_t<kTypeKQ8, 2>(P, G, st, tm);
+    }
     if (S == 1) return launch_gate_up_t<kTypeQ4_K, 1>(P, G, st, tm);
     return launch_gate_up_t<kTypeQ4_K, 2>(P, G, st, tm);
 }
@@ -1057,6 +1065,10 @@ hipError_t launch_down(const DownParams &P, hipStream_t st, const LaunchTiming *
     if (P.type == kTypeQ8_0) {
         if (S == 1) return launch_down_t<kTypeQ8_0, 1>(P, G, st, tm);
         return launch_down_t<kTypeQ8_0, 2>(P, G, st, tm);
+    }
+    if (pool_format(P.type) == kTypeKQ8) {
+        if (S == 1) return launch_down_t<kTypeKQ8, 1>(P, G, st, tm);
+        return launch_down_t<kTypeKQ8, 2>(P, G, st, tm);
     }
     if (S == 1) return launch_down_t<kTypeQ4_K, 1>(P, G, st, tm);
     return launch_down_t<kTypeQ4_K, 2>(P, G, st, tm);

@@ -77,15 +77,38 @@ def q4_k_centered(rng, rows, cols, std=0.02):
     return out.reshape(-1)
 
 
+# Q2_K, Q3_K, Q5_K, Q6_K: bytes per 256-value block, the fp16 fields' offsets and a d that keeps the
+# dequantized values' spread near 0.02 (mins, where the format has them, about centre the values)
+K_BLOCKS = {10: (84, (80, 82), 2.5e-3, 1.5), 11: (110, (108,), 5e-4, None), 13: (176, (0, 2), 6e-5, 15.5),
+            14: (210, (208,), 1.5e-5, None)}
+
+
+def k_quant_random(rng, wtype, rows, cols):
+    """rows x cols random blocks of Q2_K / Q3_K / Q5_K / Q6_K: random quants and scales, fp16 d drawn
+    around the type's scale (dmin = d times the type's centring factor)."""
+    size, offs, d0, dmin_f = K_BLOCKS[wtype]
+    nb = rows * (cols // 256)
+    out = rng.integers(0, 256, (nb, size), dtype=np.uint8)
+    d = (rng.uniform(0.5, 1.5, nb) * d0).astype(np.float16)
+    out[:, offs[0]:offs[0] + 2] = d.view(np.uint8).reshape(nb, 2)
+    if dmin_f is not None:
+        dmin = (d.astype(np.float32) * np.float32(dmin_f)).astype(np.float16)
+        out[:, offs[1]:offs[1] + 2] = dmin.view(np.uint8).reshape(nb, 2)
+    return out.reshape(-1)
+
+
 def experts(rng, wtype, n_expert, rows, cols, std=0.02, centered=False):
-    """Stacked expert tensor [n_expert][rows][cols] as GGUF bytes of wtype (8 = Q8_0, 12 = Q4_K).
-    Q4_K is q4_k_random unless centered (q4_k_centered with the given std)."""
+    """Stacked expert tensor [n_expert][rows][cols] as GGUF bytes of wtype (8 = Q8_0, 10 = Q2_K,
+    11 = Q3_K, 12 = Q4_K, 13 = Q5_K, 14 = Q6_K). Q4_K is q4_k_random unless centered (q4_k_centered
+    with the given std); the other k-quants are k_quant_random."""
     parts = []
     for _ in range(n_expert):
         if wtype == 8:
             parts.append(q8_0_from_normal(rng, rows, cols, std))
         elif wtype == 12:
             parts.append(q4_k_centered(rng, rows, cols, std) if centered else q4_k_random(rng, rows, cols))
+        elif wtype in K_BLOCKS:
+            parts.append(k_quant_random(rng, wtype, rows, cols))
         else:
             raise ValueError(f"unsupported expert type {wtype}")
     return np.concatenate(parts)

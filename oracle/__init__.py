@@ -48,6 +48,8 @@ def lib():
             "or_dequant_q8_0": (None, [P, i32, P]),
             "or_dequant_q4_K": (None, [P, i32, P]),
             "or_dequant_q8_K": (None, [P, i32, P]),
+            "or_dequant_k": (None, [i32, P, i32, P]),
+            "or_vec_dot_k_q8_K": (ctypes.c_float, [i32, i32, P, P]),
             "or_q4_K_scale_min": (None, [i32, P, P, P]),
             "or_vec_dot_q8_0_q8_0": (f32, [i32, P, P]),
             "or_vec_dot_q4_K_q8_K": (f32, [i32, P, P]),
@@ -145,6 +147,27 @@ def quantize_q8_0_act(x):
 
 def quantize_q8_K(x):
     return _quant(lib().or_quantize_q8_K, x, Q8_K_DTYPE, QK_K)
+
+
+# the other k-quants: ggml type id -> bytes per 256-value block
+K_QUANTS = {10: 84, 11: 110, 13: 176, 14: 210}
+
+
+def dequant_k(type_, raw, n):
+    """n values of Q2_K / Q3_K / Q5_K / Q6_K blocks (raw bytes) to f32 (dequantize_row_*)."""
+    raw = np.ascontiguousarray(np.frombuffer(raw, np.uint8) if not isinstance(raw, np.ndarray) else raw.view(np.uint8).ravel())
+    assert n % QK_K == 0 and raw.nbytes >= n // QK_K * K_QUANTS[type_]
+    out = np.zeros(n, np.float32)
+    lib().or_dequant_k(type_, _p(raw), n, _p(out))
+    return out
+
+
+def vec_dot_k(type_, raw, xq):
+    """ggml_vec_dot_<type>_q8_K of one row: raw k-quant bytes against Q8_K blocks xq."""
+    raw = np.ascontiguousarray(raw).view(np.uint8).ravel()
+    xq = np.ascontiguousarray(xq)
+    n = xq.size * QK_K
+    return float(lib().or_vec_dot_k_q8_K(type_, n, _p(raw), _p(xq)))
 
 
 def dequant(blocks, type_):

@@ -58,6 +58,34 @@ typedef struct {
     int16_t bsums[OR_QK_K / 16];
 } or_block_q8_K; /* 292 bytes */
 
+/* ggml's block_q2_K .. block_q6_K (ggml-common.h), the other k-quant expert formats */
+typedef struct {
+    uint8_t scales[OR_QK_K / 16]; /* per 16 values: 4-bit scale | 4-bit min << 4 */
+    uint8_t qs[OR_QK_K / 4];      /* 2-bit quants */
+    uint16_t d, dmin;             /* fp16 */
+} or_block_q2_K; /* 84 bytes */
+
+typedef struct {
+    uint8_t hmask[OR_QK_K / 8]; /* high bit of each 3-bit quant */
+    uint8_t qs[OR_QK_K / 4];    /* low 2 bits */
+    uint8_t scales[12];         /* 16 6-bit scales */
+    uint16_t d;                 /* fp16 */
+} or_block_q3_K; /* 110 bytes */
+
+typedef struct {
+    uint16_t d, dmin; /* fp16 */
+    uint8_t scales[12];
+    uint8_t qh[OR_QK_K / 8]; /* fifth bit of each quant */
+    uint8_t qs[OR_QK_K / 2]; /* low 4 bits */
+} or_block_q5_K; /* 176 bytes */
+
+typedef struct {
+    uint8_t ql[OR_QK_K / 2];      /* low 4 bits */
+    uint8_t qh[OR_QK_K / 4];      /* high 2 bits */
+    int8_t scales[OR_QK_K / 16];  /* per 16 values */
+    uint16_t d;                   /* fp16 */
+} or_block_q6_K; /* 210 bytes */
+
 /* ---- fp16 ---- */
 uint16_t or_fp32_to_fp16(float f); /* round to nearest even, like F16C / numpy */
 float or_fp16_to_fp32(uint16_t h);
@@ -73,6 +101,9 @@ void or_dequant_q8_K(const void *in, int n, float *y);
 void or_q4_K_scale_min(int j, const uint8_t *scales, uint8_t *sc, uint8_t *m); /* get_scale_min_k4 */
 float or_vec_dot_q8_0_q8_0(int n, const void *w, const void *x);
 float or_vec_dot_q4_K_q8_K(int n, const void *w, const void *x);
+/* Q2_K (10), Q3_K (11), Q5_K (13), Q6_K (14): dequantize_row_* and ggml_vec_dot_*_q8_K */
+void or_dequant_k(int type, const void *in, int n, float *y);
+float or_vec_dot_k_q8_K(int type, int n, const void *w, const void *x);
 
 /* ---- router (src/qwen3.cpp:175-192) ----
  * hnorm [T][h] f32; gate_inp [E][h] of gate_type (0 = F32, 1 = F16).

@@ -76,7 +76,11 @@ size_t or_row_bytes(int type, int n) {
         case 0: return (size_t) n * 4;
         case 1: return (size_t) n * 2;
         case 8: return (size_t) (n / OR_QK8_0) * sizeof(or_block_q8_0);
+        case 10: return (size_t) (n / OR_QK_K) * sizeof(or_block_q2_K);
+        case 11: return (size_t) (n / OR_QK_K) * sizeof(or_block_q3_K);
         case 12: return (size_t) (n / OR_QK_K) * sizeof(or_block_q4_K);
+        case 13: return (size_t) (n / OR_QK_K) * sizeof(or_block_q5_K);
+        case 14: return (size_t) (n / OR_QK_K) * sizeof(or_block_q6_K);
         case 15: return (size_t) (n / OR_QK_K) * sizeof(or_block_q8_K);
         default: return 0;
     }
@@ -241,6 +245,125 @@ float or_vec_dot_q4_K_q8_K(int n, const void *w, const void *x) {
     return sumf;
 }
 
+/* ---- Q2_K, Q3_K, Q5_K, Q6_K ---------------------------------------------------------------- */
+
+/* The 16 6-bit scales of a Q3_K block (dequantize_row_q3_K's kmask unpacking): scale i = 4a + b has
+ * low 4 bits from byte 4a + b (a < 2) or the high nibble of byte 4(a - 2) + b, and high 2 bits from
+ * bits 2a, 2a + 1 of byte 8 + b; the result is that 6-bit value - 32. */
+static int q3_K_scale(const uint8_t *s, int i) {
+    const int a = i / 4, b = i % 4;
+    const int lo = a < 2 ? s[4 * a + b] & 0xF : s[4 * (a - 2) + b] >> 4;
+    const int hi = (s[8 + b] >> (2 * a)) & 3;
+    return (lo | hi << 4) - 32;
+}
+
+/* Each k-quant block as 256 integer quants, 16 integer scales and 16 mins (one per 16 values) and the
+ * block's d / dmin, so that value v = (d * sc[v / 16]) * q[v] - dmin * m[v / 16] is ggml's dequantized
+ * value, and ggml's dot with a Q8_K block is (d * d_x) * sum_j sc_j * dot_j - (dmin * d_x) * sum_j
+ * m_j * bsums_j in integers per super-block. Layouts (ggml-common.h):
+ *   Q2_K  value 128 n + 32 j + l (n < 2, j < 4, l < 32): bits 2j of qs[32 n + l]; scales[8 n + 2 j + l / 16]
+ *         holds sc (low nibble) and m (high nibble).
+ *   Q3_K  same 2-bit layout; the third bit is bit 4 n + j of hmask[l], and a clear bit subtracts 4;
+ *         scale q3_K_scale(), no mins.
+ *   Q5_K  Q4_K's nibbles and 6-bit scale / min pairs per 32 values; bit 2 c + h of qh[l] (value
+ *         64 c + 32 h + l) adds 16.
+ *   Q6_K  value 128 n + 32 j + l: the low (j < 2) or high (j >= 2) nibble of ql[64 n + 32 (j % 2) + l]
+ *         and bits 2j, 2j + 1 of qh[32 n + l], minus 32; int8 scale per 16 values, no mins. */
+typedef struct {
+    float d, dmin;
+    int sc[16], m[16];
+    int q[256];
+} or_kblock;
+
+static void k_unpack(int type, const void *blk, or_kblock *o) {
+    memset(o, 0, sizeof(*o));
+    if (type == 10) {
+        const or_block_q2_K *b = (const or_block_q2_K *) blk;
+        o->d = h2f(b->d);
+        o->dmin = h2f(b->dmin);
+        for (int i = 0; i < 16; i++) {
+            o->sc[i] = b->scales[i] & 0xF;
+            o->m[i] = b->scales[i] >> 4;
+        }
+        for (int v = 0; v < 256; v++) {
+            const int n = v / 128, j = (v % 128) / 32, l = v % 32;
+            o->q[v] = (b->qs[32 * n + l] >> (2 * j)) & 3;
+        }
+    } else if (type == 11) {
+        const or_block_q3_K *b = (const or_block_q3_K *) blk;
+        o->d = h2f(b->d);
+        for (int i = 0; i < 16; i++) o->sc[i] = q3_K_scale(b->scales, i);
+        for (int v = 0; v < 256; v++) {
+            const int n = v / 128, j = (v % 128) / 32, l = v % 32;
+            o->q[v] = ((b->qs[32 * n + l] >> (2 * j)) & 3) - (((b->hmask[l] >> (4 * n + j)) & 1) ? 0 : 4);
+        }
+    } else if (type == 13) {
+        const or_block_q5_K *b = (const or_block_q5_K *) blk;
+        o->d = h2f(b->d);
+        o->dmin = h2f(b->dmin);
+        for (int j = 0; j < 8; j++) {
+            uint8_t sc, m;
+            or_q4_K_scale_min(j, b->scales, &sc, &m);
+            o->sc[2 * j] = o->sc[2 * j + 1] = sc;
+            o->m[2 * j] = o->m[2 * j + 1] = m;
+        }
+        for (int v = 0; v < 256; v++) {
+            const int c = v / 64, h = (v % 64) / 32, l = v % 32;
+            const int nib = h ? b->qs[32 * c + l] >> 4 : b->qs[32 * c + l] & 0xF;
+            o->q[v] = nib + (((b->qh[l] >> (2 * c + h)) & 1) ? 16 : 0);
+        }
+    } else { /* 14 */
+        const or_block_q6_K *b = (const or_block_q6_K *) blk;
+        o->d = h2f(b->d);
+        for (int i = 0; i < 16; i++) o->sc[i] = b->scales[i];
+        for (int v = 0; v < 256; v++) {
+            const int n = v / 128, j = (v % 128) / 32, l = v % 32;
+            const int lo = (b->ql[64 * n + 32 * (j % 2) + l] >> (4 * (j / 2))) & 0xF;
+            const int hi = (b->qh[32 * n + l] >> (2 * j)) & 3;
+            o->q[v] = (lo | hi << 4) - 32;
+        }
+    }
+}
+
+static size_t k_block_bytes(int type) { return or_row_bytes(type, OR_QK_K); }
+
+/* dequantize_row_q2_K / q3_K / q5_K / q6_K: (d * sc) * q - dmin * m, each product rounded in f32 as ggml
+ * forms it (dl = d * sc, ml = dmin * m, y = dl * q - ml; the types without mins subtract nothing). */
+void or_dequant_k(int type, const void *in, int n, float *y) {
+    or_kblock k;
+    for (int i = 0; i < n / OR_QK_K; i++) {
+        k_unpack(type, (const uint8_t *) in + (size_t) i * k_block_bytes(type), &k);
+        for (int v = 0; v < 256; v++) {
+            const float dl = k.d * (float) k.sc[v / 16];
+            const float yv = dl * (float) k.q[v];
+            y[(size_t) i * OR_QK_K + v] = (type == 10 || type == 13) ? yv - k.dmin * (float) k.m[v / 16] : yv;
+        }
+    }
+}
+
+/* ggml_vec_dot_q2_K_q8_K / q3_K / q5_K / q6_K (generic): per super-block the integer isum = sum_j sc_j *
+ * (sum of q * x over the 16 values of j) and imin = sum_j m_j * bsums_j; sumf += (d * d_x) * isum, then
+ * sumf -= (dmin * d_x) * imin; super-blocks in ascending order. ggml's own float order within a block
+ * differs by type (per-lane partial sums); the integers are exact either way. */
+float or_vec_dot_k_q8_K(int type, int n, const void *w, const void *x) {
+    const or_block_q8_K *b = (const or_block_q8_K *) x;
+    float sumf = 0.0f;
+    or_kblock k;
+    for (int i = 0; i < n / OR_QK_K; i++) {
+        k_unpack(type, (const uint8_t *) w + (size_t) i * k_block_bytes(type), &k);
+        int isum = 0, imin = 0;
+        for (int j = 0; j < 16; j++) {
+            int s = 0;
+            for (int l = 0; l < 16; l++) s += k.q[16 * j + l] * (int) b[i].qs[16 * j + l];
+            isum += k.sc[j] * s;
+            imin += k.m[j] * (int) b[i].bsums[j];
+        }
+        sumf += (k.d * b[i].d) * (float) isum;
+        sumf -= (k.dmin * b[i].d) * (float) imin;
+    }
+    return sumf;
+}
+
 /* ------------------------------------------------------------------------------------------ */
 /* router                                                                                      */
 /* ------------------------------------------------------------------------------------------ */
@@ -355,15 +478,18 @@ int or_permute(const int32_t *bins, int T, int k, int n_bins, int32_t *counts, i
 /* expert FFN                                                                                  */
 /* ------------------------------------------------------------------------------------------ */
 
-static int act_type_for(int wtype) { return wtype == 12 ? 15 : 8; }
+/* ggml's vec_dot_type: Q8_0 for Q8_0 weights, Q8_K for every k-quant */
+static int act_type_for(int wtype) { return wtype == 8 ? 8 : 15; }
 
 static void quantize_act(int wtype, const float *x, int n, void *out) {
-    if (wtype == 12) or_quantize_q8_K(x, n, out);
-    else or_quantize_q8_0_act(x, n, out);
+    if (wtype == 8) or_quantize_q8_0_act(x, n, out);
+    else or_quantize_q8_K(x, n, out);
 }
 
 static float dot_row(int wtype, int n, const void *w, const void *xq) {
-    return wtype == 12 ? or_vec_dot_q4_K_q8_K(n, w, xq) : or_vec_dot_q8_0_q8_0(n, w, xq);
+    if (wtype == 8) return or_vec_dot_q8_0_q8_0(n, w, xq);
+    if (wtype == 12) return or_vec_dot_q4_K_q8_K(n, w, xq);
+    return or_vec_dot_k_q8_K(wtype, n, w, xq);
 }
 
 /* moe_apply() src/qwen3.cpp:197-214 with ggml CPU mul_mat_id semantics, then the residual add

@@ -57,6 +57,37 @@ def test_repack_roundtrip_and_layout(lstk, wtype, rows, cols):
             assert np.array_equal(at(1 + 2 * i), b[i, 2:18]) and np.array_equal(at(2 + 2 * i), b[i, 18:34])
 
 
+@pytest.mark.parametrize("wtype", [10, 11, 13, 14])
+def test_repack_k_quants_to_kq8(lstk, wtype):
+    """Q2_K / Q3_K / Q5_K / Q6_K matrices enter the pool unpacked to KQ8 (19 chunks per super-block row:
+    {f32 d, f32 dmin}, 16 int8 scales, 16 mins, 16 x 16 int8 quants): the values (d * sc) * q - dmin * m
+    read back from the packed chunks equal the oracle's dequantize_row_* bit for bit (f32)."""
+    import oracle
+    rows, cols = 96, 512
+    rng = np.random.default_rng(wtype)
+    g = synth.experts(rng, wtype, 1, rows, cols)
+    assert g.size == rows * cols // 256 * oracle.K_QUANTS[wtype]
+    assert lstk.matrix_bytes(wtype, rows, cols) == rows * (cols // 256) * 19 * 16
+    p = lstk.repack_matrix(wtype, rows, cols, g)
+    C, nsb = 19, cols // 256
+    chunks = p.reshape(nsb, C, rows, 16)  # [sb][c][row][16 B]
+    d = chunks[:, 0, :, 0:4].copy().view(np.float32)[..., 0]    # [sb][row]
+    dmin = chunks[:, 0, :, 4:8].copy().view(np.float32)[..., 0]
+    sc = chunks[:, 1].view(np.int8).astype(np.float32)           # [sb][row][16]
+    m = chunks[:, 2].astype(np.float32)
+    q = chunks[:, 3:].view(np.int8).astype(np.float32)           # [sb][16][row][16]
+    q = q.transpose(0, 2, 1, 3).reshape(nsb, rows, 256)
+    dl = (d[..., None] * sc).astype(np.float32)                  # d * sc per 16 values, in f32
+    vals = np.repeat(dl, 16, axis=2) * q
+    if wtype in (10, 13):
+        vals = vals - np.repeat((dmin[..., None] * m).astype(np.float32), 16, axis=2)
+    got = vals.astype(np.float32).transpose(1, 0, 2).reshape(rows, cols)
+    want = oracle.dequant_k(wtype, g, rows * cols).reshape(rows, cols)
+    np.testing.assert_array_equal(got.view(np.uint32), want.view(np.uint32))
+    with pytest.raises(lstk.LstkError):
+        lstk.unpack_matrix(wtype, rows, cols, p)  # the unpacking is one-way
+
+
 def test_rejects_bad_shapes_and_types(lstk):
     Q8 = (8, 8, 8)
     cases = [

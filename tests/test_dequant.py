@@ -12,7 +12,11 @@ formats, so each format is pinned as follows:
   each of its 256 high bits, set alone, moves exactly one value by 16 d sc: value 32 j + l for bit j of
   qh[l] (ggml's block_q5_K layout);
 - Q6_K: d = 1 and unit scales give q - 32 exactly, which pins where each value's 4 low and 2 high bits
-  sit (every bit probed alone) and the 16-value scale groups; power-of-two d makes the products exact.
+  sit (every bit probed alone) and the 16-value scale groups; power-of-two d makes the products exact;
+- Q2_K and Q3_K: every quant bit, high-mask bit and scale-byte bit probed alone at unit scales, and the
+  scale / min nibbles of each 16-value group.
+The oracle's own k-quant dequantizers and dot products (used by the GPU parity tests of k-quant experts)
+are held against the probe-pinned product dequantizer and against float64 dots of dequantized values.
 """
 import numpy as np
 import pytest
@@ -20,7 +24,7 @@ import pytest
 import oracle
 from localstack_amd import synth
 
-F32, F16, Q8_0, Q4_K, Q5_K, Q6_K = 0, 1, 8, 12, 13, 14
+F32, F16, Q8_0, Q2_K, Q3_K, Q4_K, Q5_K, Q6_K = 0, 1, 8, 10, 11, 12, 13, 14
 
 
 def f16(lstk, type_, blocks, n):
@@ -249,3 +253,129 @@ def test_loader_dequantizes_dense_tensors(lstk, tmp_path):
     g = lstk.GgufFile(bad)
     with pytest.raises(lstk.LstkError, match="blk.1.ffn_norm.weight is Q4_K"):
         lstk.qwen3_dense_weights(g, g.qwen3_hparams())
+
+
+# ---- Q2_K and Q3_K ----------------------------------------------------------------------------------
+
+def q2_k_block(scales, qs, d, dmin):
+    return np.concatenate([np.asarray(scales, np.uint8), np.asarray(qs, np.uint8),
+                           np.array([d, dmin], np.float16).view(np.uint8)])
+
+
+def q3_k_block(hmask, qs, scales, d):
+    return np.concatenate([np.asarray(hmask, np.uint8), np.asarray(qs, np.uint8), np.asarray(scales, np.uint8),
+                           np.array([d], np.float16).view(np.uint8)])
+
+
+def test_q2_k_bit_layout(lstk):
+    # each qs bit alone (unit scales, no mins): value 128 n + 32 j + l takes bits 2j, 2j + 1 of qs[32 n + l]
+    ones = np.full(16, 0x01, np.uint8)
+    for byte in range(64):
+        for bit in range(8):
+            qs = np.zeros(64, np.uint8)
+            qs[byte] = 1 << bit
+            y = f16(lstk, Q2_K, q2_k_block(ones, qs, 1.0, 0.0), 256).astype(np.float32)
+            n, l, j = byte // 32, byte % 32, bit // 2
+            want = np.zeros(256, np.float32)
+            want[128 * n + 32 * j + l] = 1 << (bit % 2)
+            np.testing.assert_array_equal(y, want, err_msg=f"qs[{byte}] bit {bit}")
+    # every value q = 1: the low nibble of scales[i] is the scale of values 16 i .. 16 i + 15; the high
+    # nibble is the min, times dmin
+    rng = np.random.default_rng(9)
+    sc = rng.integers(0, 16, 16)
+    m = rng.integers(0, 16, 16)
+    y = f16(lstk, Q2_K, q2_k_block(sc | m << 4, np.full(64, 0x55, np.uint8), 1.0, 0.5), 256).astype(np.float32)
+    np.testing.assert_array_equal(y, (np.repeat(sc, 16) - 0.5 * np.repeat(m, 16)).astype(np.float32))
+
+
+def q3_scale_bytes(scale6):
+    """The 12 scale bytes holding 16 6-bit values, built bit by bit from the block_q3_K packing: the low
+    4 bits of scale i sit in byte i (i < 8, low nibble) or byte i - 8 (high nibble); its bits 4 and 5 in
+    byte 8 + i % 4, at bits 2 (i / 4) and 2 (i / 4) + 1."""
+    b = np.zeros(12, np.uint8)
+    for i, v in enumerate(scale6):
+        if i < 8:
+            b[i] |= v & 0xF
+        else:
+            b[i - 8] |= (v & 0xF) << 4
+        b[8 + i % 4] |= ((v >> 4) & 3) << (2 * (i // 4))
+    return b
+
+
+def test_q3_k_bit_layout(lstk):
+    unit = q3_scale_bytes([33] * 16)  # every scale 33 - 32 = 1
+    # all high bits set, no low bits: q = 0 everywhere
+    base = f16(lstk, Q3_K, q3_k_block(np.full(32, 0xFF), np.zeros(64), unit, 1.0), 256).astype(np.float32)
+    np.testing.assert_array_equal(base, np.zeros(256, np.float32))
+    for byte in range(64):
+        for bit in range(8):
+            qs = np.zeros(64, np.uint8)
+            qs[byte] = 1 << bit
+            y = f16(lstk, Q3_K, q3_k_block(np.full(32, 0xFF), qs, unit, 1.0), 256).astype(np.float32)
+            n, l, j = byte // 32, byte % 32, bit // 2
+            want = np.zeros(256, np.float32)
+            want[128 * n + 32 * j + l] = 1 << (bit % 2)
+            np.testing.assert_array_equal(y, want, err_msg=f"qs[{byte}] bit {bit}")
+    for byte in range(32):
+        for bit in range(8):
+            hm = np.full(32, 0xFF, np.uint8)
+            hm[byte] &= ~np.uint8(1 << bit)
+            y = f16(lstk, Q3_K, q3_k_block(hm, np.zeros(64), unit, 1.0), 256).astype(np.float32)
+            want = np.zeros(256, np.float32)
+            want[128 * (bit // 4) + 32 * (bit % 4) + byte] = -4.0  # a clear high bit subtracts 4
+            np.testing.assert_array_equal(y, want, err_msg=f"hmask[{byte}] bit {bit}")
+    # each scale byte bit alone, values q = 1: the 16-value group(s) it feeds move by its weight
+    for byte in range(12):
+        for bit in range(8):
+            sb = np.zeros(12, np.uint8)
+            sb[byte] = 1 << bit
+            y = f16(lstk, Q3_K, q3_k_block(np.full(32, 0xFF), np.full(64, 0x55), sb, 1.0), 256).astype(np.float32)
+            scale = np.full(16, -32.0)
+            if byte < 8:
+                scale[byte if bit < 4 else byte + 8] += 1 << (bit % 4)
+            else:
+                scale[4 * (bit // 2) + byte - 8] += 1 << (4 + bit % 2)
+            np.testing.assert_array_equal(y, np.repeat(scale, 16).astype(np.float32), err_msg=f"scales[{byte}] bit {bit}")
+    # the helper's packing agrees with the bit probes above on random scales
+    rng = np.random.default_rng(10)
+    s6 = rng.integers(0, 64, 16)
+    y = f16(lstk, Q3_K, q3_k_block(np.full(32, 0xFF), np.full(64, 0x55), q3_scale_bytes(s6), 2.0 ** -4), 256)
+    np.testing.assert_array_equal(y.astype(np.float32), np.repeat((s6 - 32) * 2.0 ** -4, 16).astype(np.float32))
+
+
+def random_k_blocks(rng, type_, nb):
+    """nb random blocks of a k-quant with finite, modest fp16 scales."""
+    size = oracle.K_QUANTS[type_]
+    b = rng.integers(0, 256, (nb, size), dtype=np.uint8)
+    offs = {10: (80, 82), 11: (108,), 13: (0, 2), 14: (208,)}[type_]
+    for o in offs:
+        b[:, o:o + 2] = rng.uniform(1e-4, 1e-2, nb).astype(np.float16).view(np.uint8).reshape(-1, 2)
+    return b.ravel()
+
+
+@pytest.mark.parametrize("type_", [10, 11, 13, 14])
+def test_oracle_k_dequant_matches_product(lstk, type_):
+    """The oracle's dequantize_row_* restatement against the product's (pinned by the bit probes above),
+    rounded once to fp16."""
+    rng = np.random.default_rng(type_)
+    raw = random_k_blocks(rng, type_, 40)
+    want = oracle.dequant_k(type_, raw, 40 * 256).astype(np.float16)
+    np.testing.assert_array_equal(f16(lstk, type_, raw, 40 * 256).view(np.uint16), want.view(np.uint16))
+
+
+@pytest.mark.parametrize("type_", [10, 11, 13, 14])
+def test_oracle_k_dot_equals_float64_dot_of_dequantized(type_):
+    """ggml_vec_dot_<type>_q8_K as the oracle restates it: integers exact, so the result equals the float64
+    dot of the dequantized weights and activations to f32 rounding."""
+    rng = np.random.default_rng(100 + type_)
+    nb = 8
+    for _ in range(6):
+        raw = random_k_blocks(rng, type_, nb)
+        x = rng.standard_normal(nb * 256).astype(np.float32)
+        xq = oracle.quantize_q8_K(x)
+        got = oracle.vec_dot_k(type_, raw, xq)
+        w64 = oracle.dequant_k(type_, raw, nb * 256).astype(np.float64)
+        x64 = oracle.dequant(xq, oracle.TYPE_Q8_K).astype(np.float64).ravel()
+        ref = float(np.dot(w64, x64))
+        scale = float(np.sum(np.abs(w64 * x64)))
+        assert abs(got - ref) <= 2e-6 * scale, (type_, got, ref)

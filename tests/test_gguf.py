@@ -173,12 +173,22 @@ def test_expert_checks(lstk, tmp_path):
 
     def q6(w):
         w["layers"][0]["types"] = (8, 8, 14)  # Q6_K down: bytes of the right size for the sizing rule
-        w["layers"][0]["down"] = np.zeros(small["n_expert"] * small["n_embd"] * (small["n_ff_exp"] // 256) * 210, np.uint8)
+        w["layers"][0]["down"] = np.arange(small["n_expert"] * small["n_embd"] * (small["n_ff_exp"] // 256) * 210).astype(np.uint8)
+
+    def q4_0(w):
+        w["layers"][0]["types"] = (8, 8, 2)  # Q4_0 (18 B per 32 values): not a type the pool stores
+        w["layers"][0]["down"] = np.zeros(small["n_expert"] * small["n_embd"] * (small["n_ff_exp"] // 32) * 18, np.uint8)
 
     g = lstk.GgufFile(write_variant(tmp_path, "q6.gguf", small, q6))
     hp = g.qwen3_hparams()
-    with pytest.raises(lstk.LstkError, match=r"layer 0: blk.0.ffn_down_exps.weight is Q6_K; the expert pool stores Q8_0 and Q4_K"):
-        g.qwen3_experts(hp)
+    types, _, _, down = g.qwen3_experts(hp)[0]  # the other k-quants are located like Q8_0 / Q4_K
+    assert types == (8, 8, 14)
+    nb = small["n_expert"] * small["n_embd"] * (small["n_ff_exp"] // 256) * 210
+    np.testing.assert_array_equal(np.ctypeslib.as_array((np.ctypeslib.ctypes.c_uint8 * nb).from_address(down)),
+                                  np.arange(nb).astype(np.uint8))
+    g = lstk.GgufFile(write_variant(tmp_path, "q4_0.gguf", small, q4_0))
+    with pytest.raises(lstk.LstkError, match=r"layer 0: blk.0.ffn_down_exps.weight is Q4_0; the expert pool stores Q8_0, Q2_K"):
+        g.qwen3_experts(g.qwen3_hparams())
     g = lstk.GgufFile(write_variant(tmp_path, "ok.gguf", small, lambda w: None))
     hp = g.qwen3_hparams()
     with pytest.raises(lstk.LstkError, match="expert tensor shapes do not match the hyperparameters for layer 0"):

@@ -12,7 +12,7 @@ from localstack_amd import synth
 
 pytestmark = pytest.mark.gpu
 
-Q8_0, Q4_K = 8, 12
+Q8_0, Q2_K, Q3_K, Q4_K, Q5_K, Q6_K = 8, 10, 11, 12, 13, 14
 FFN_TOL = 2e-3
 
 
@@ -40,6 +40,14 @@ def model(name):
         "mixed": dict(h=256, f=768, E=16, k=4, types=(Q4_K, Q4_K, Q8_0), n_layer=1, n_batch=64),
         # Qwen3-235B-A22B MoE layer shape (h 4096, f 1536, top-8, Q4_K) over 16 experts
         "235b_q4": dict(h=4096, f=1536, E=16, k=8, types=(Q4_K,) * 3, n_layer=1, n_batch=64),
+        # the other k-quants (stored unpacked, KQ8) at the 30B shape over 32 experts, in the mixes real
+        # files use: Q4_K_M (Q4_K gate/up, Q6_K down), Q5_K_M, and the 3- and 2-bit classes
+        "q4km": dict(h=2048, f=768, E=32, k=8, types=(Q4_K, Q4_K, Q6_K), n_layer=1, n_batch=64),
+        "q5km": dict(h=2048, f=768, E=32, k=8, types=(Q5_K, Q5_K, Q6_K), n_layer=1, n_batch=64),
+        "q3": dict(h=2048, f=768, E=32, k=8, types=(Q3_K, Q3_K, Q4_K), n_layer=1, n_batch=64),
+        "q2": dict(h=2048, f=768, E=32, k=8, types=(Q2_K, Q2_K, Q3_K), n_layer=1, n_batch=64),
+        # the 235B shape with k-quants in both kernels (two super-blocks per thread in gate/up)
+        "235b_q6": dict(h=4096, f=1536, E=16, k=8, types=(Q6_K, Q6_K, Q5_K), n_layer=1, n_batch=64),
     }[name]
     rng = np.random.default_rng(sum(map(ord, name)))
     layers = [layer_bytes(rng, cfg["types"], cfg["E"], cfg["h"], cfg["f"]) for _ in range(cfg["n_layer"])]
@@ -101,7 +109,9 @@ def test_route_f32_weights_and_zipf(orc, lstk, dev):
 
 @pytest.mark.parametrize("name,T", [("tiny", 1), ("tiny", 16), ("30b_q8", 1), ("30b_q8", 8), ("30b_q8", 32),
                                     ("30b_q4", 1), ("30b_q4", 8), ("30b_q4", 64), ("mixed", 5), ("235b_q4", 1),
-                                    ("235b_q4", 8), ("235b_q4", 64)])
+                                    ("235b_q4", 8), ("235b_q4", 64), ("q4km", 1), ("q4km", 8), ("q4km", 64),
+                                    ("q5km", 1), ("q5km", 16), ("q3", 1), ("q3", 8), ("q2", 1), ("q2", 8),
+                                    ("235b_q6", 1), ("235b_q6", 8)])
 def test_ffn_matches_oracle(orc, lstk, dev, name, T):
     import torch
     cfg, layers, routers, store = model(name)
@@ -120,7 +130,8 @@ def test_ffn_matches_oracle(orc, lstk, dev, name, T):
     assert err <= FFN_TOL
 
 
-@pytest.mark.parametrize("name,T", [("tiny", 16), ("30b_q8", 1), ("30b_q8", 8), ("30b_q4", 16), ("235b_q4", 1)])
+@pytest.mark.parametrize("name,T", [("tiny", 16), ("30b_q8", 1), ("30b_q8", 8), ("30b_q4", 16), ("235b_q4", 1),
+                                    ("q4km", 1), ("q5km", 1), ("q3", 1), ("q2", 1), ("235b_q6", 1), ("q4km", 64)])
 def test_block_matches_oracle(orc, lstk, dev, name, T):
     import torch
     cfg, layers, routers, store = model(name)
@@ -204,6 +215,57 @@ def test_streaming_pool_is_bit_identical_to_resident(orc, lstk, dev):
     assert chunked.stats()["misses"] > 0 and chunked.layer_slots(0) == 2 * k + 2
 
 
+def test_streaming_mixed_k_quant_classes(orc, lstk, dev):
+    """A Q4_K_M-style stack (layers of (Q4_K, Q4_K, Q6_K) and (Q4_K, Q4_K, Q4_K): two type classes, so two
+    shards) streamed through small pools with the host and the device acquire: bit-identical to resident,
+    and within FFN_TOL of the oracle."""
+    import torch
+    import localstack_amd as L
+    h, f, E, k, T = 2048, 768, 16, 8, 4
+    rng = np.random.default_rng(450)
+    tys = [(Q4_K, Q4_K, Q6_K), (Q4_K, Q4_K, Q4_K), (Q4_K, Q4_K, Q6_K), (Q4_K, Q4_K, Q4_K)]
+    layers = [(t,) + layer_bytes(rng, t, E, h, f) for t in tys]
+    routers = [synth.router_f16(rng, E, h) for _ in tys]
+    xs = [synth.activations(rng, T, h) for _ in tys]
+    resid = synth.activations(rng, T, h)
+    resident = L.ExpertStore(len(tys), h, f, E, k, T, layers)
+    host = L.ExpertStore(len(tys), h, f, E, k, T, layers, pool_bytes=1, min_slots=2 * k + 2, streaming=True)
+    devp = L.ExpertStore(len(tys), h, f, E, k, T, layers, pool_bytes=1, min_slots=2 * k + 2, streaming=True,
+                         device_lru=True)
+    assert host.describe().count("q6_K") >= 1
+    slots_d = torch.zeros((T, k), dtype=torch.int32, device=dev)
+    for rep in range(2):
+        for l in range(len(tys)):
+            rids, rw, _, _ = orc.router(xs[l], routers[l], 1, k)
+            args = (to_dev(xs[l], dev), None, to_dev(rw, dev), to_dev(resid, dev))
+            outs = []
+            for store in (resident, host, devp):
+                o = torch.zeros((T, h), dtype=torch.float32, device=dev)
+                if store is resident:
+                    slots = to_dev(rids, dev)
+                elif store is host:
+                    slots = to_dev(host.acquire(l, rids), dev)
+                else:
+                    devp.acquire_device(l, to_dev(rids, dev), slots_d)
+                    slots = slots_d
+                store.ffn(l, args[0], slots, args[2], args[3], o)
+                if store is host:
+                    host.release_all()
+                store.check()
+                outs.append(o.cpu().numpy())
+            assert np.array_equal(outs[1], outs[0]) and np.array_equal(outs[2], outs[0]), (rep, l)
+            lb = layers[l]
+            ref = orc.moe_ffn(xs[l], rids, rw, resid, lb[1].reshape(E, -1), lb[2].reshape(E, -1), lb[3].reshape(E, -1),
+                              tys[l], f)
+            err = ffn_err(outs[0], ref, resid)
+            print(f"[stream k-quants rep {rep} layer {l} {tys[l]}] rel max err {err:.3e}", flush=True)
+            assert err <= FFN_TOL
+    assert host.stats()["misses"] > 0 and host.stats()["hits"] > 0
+    assert (devp.stats()["hits"], devp.stats()["misses"]) == (host.stats()["hits"], host.stats()["misses"])
+    for st in (resident, host, devp):
+        st.close()
+
+
 def test_streaming_layers_sharing_host_matrices(orc, lstk, dev):
     # layers passed the same host matrices share one host-tier copy; every layer still owns its own
     # slots, and the result equals the resident pool's bit for bit
@@ -268,7 +330,7 @@ def test_stage_timing_counts_launches(orc, lstk, dev):
     assert n == [3 + 2, 4, 4, 1] and all(m > 0 for m in ms)
 
 
-@pytest.mark.parametrize("name", ["tiny", "30b_q8", "30b_q4", "mixed", "235b_q4"])
+@pytest.mark.parametrize("name", ["tiny", "30b_q8", "30b_q4", "mixed", "235b_q4", "q4km", "q2", "235b_q6"])
 def test_single_token_equals_batched_row(orc, lstk, dev, name):
     """A single token (gate_up ranking its experts, down + combine in one launch) gives the bits of
     the same token inside a batch (separate top-k, down and combine launches)."""
