@@ -115,6 +115,17 @@ struct FillKvParams {
     uint64_t seed;
 };
 
+// Y[t][r] (+)= sum_c X[t][c] W[r][c] for a few tokens (T <= 16): fp16 W [rows][cols] and X
+// [T][cols], f32 accumulation, Y [T][ldy]; with accumulate set the products are added to Y.
+struct Gemm16Params {
+    const uint16_t *w, *x;
+    float *y;
+    int rows, cols, T, ldy, accumulate;
+};
+// rows a multiple of 16, cols 2048 or 4096, 1 <= T <= 16
+bool gemm16_supported(int rows, int cols, int T);
+hipError_t launch_gemm16(const Gemm16Params &P, hipStream_t st, const LaunchTiming *tm);
+
 bool gemv_supported(int cols);
 bool rmsnorm_supported(int n);
 bool attn_supported(int hd);

@@ -18,7 +18,8 @@
 //   output_norm + head on the last row                  (rmsnorm_kernel, gemv_kernel)
 // With several tokens per step the projections are plain F16 matrix products: the normalised rows and
 // the attention output are also written as fp16 (ggml rounds the activations of an F16 mat-mul to
-// fp16) and rocBLAS multiplies them with f32 accumulation (rocblas_gemm_ex, f16 x f16 -> f32).
+// fp16) and they are multiplied with f32 accumulation: on the matrix cores by gemm16_kernel (forward.hip)
+// up to 16 tokens, by rocBLAS (rocblas_gemm_ex, f16 x f16 -> f32) for more.
 // The KV cache keeps the reference's block table (32-cell blocks handed out per sequence, cell_seq /
 // cell_pos per cell) on the host; the device holds the cells' fp16 K and V in layouts chosen for
 // coalesced reads (forward.h) and a copy of cell_seq / cell_pos that the step's RoPE launch updates.
@@ -374,6 +375,15 @@ int blas_gemm(lstk_model *M, const uint16_t *W, int rows, int cols, const uint16
                                        : set_error(LSTK_E_DEVICE, std::string("rocblas_gemm_ex: ") + rocblas_status_to_string(s));
 }
 
+// The same product on the matrix cores for up to 16 tokens (gemm16_kernel), rocBLAS beyond.
+int project(lstk_model *M, const uint16_t *W, int rows, int cols, const uint16_t *X16, int T, float *Y, int ldy,
+            bool accumulate, hipStream_t st) {
+    if (!lstk::gemm16_supported(rows, cols, T)) return blas_gemm(M, W, rows, cols, X16, T, Y, ldy, accumulate, st);
+    const lstk::Gemm16Params gp{W, X16, Y, rows, cols, T, ldy, accumulate ? 1 : 0};
+    const hipError_t e = lstk::launch_gemm16(gp, st, nullptr);
+    return e == hipSuccess ? LSTK_OK : hip_fail(e, "gemm16 launch");
+}
+
 // Copies the host bookkeeping of the cells to the device (after removals; rare, synchronous).
 int sync_cells(lstk_model *M) {
     hipError_t e;
@@ -496,10 +506,10 @@ int forward(lstk_model *M, int32_t seq, int T, int n_cells, float *d_logits, int
         if (blas) {
             const int rc = timed_span(M, 1, st, [&] {
                 // Q, K and V rows side by side in the output; one product when the weights are too
-                if (M->qkv_joined[l]) return blas_gemm(M, L.wq, hq + 2 * hk, h, M->hn16, T, M->q, M->ld_qkv, false, st);
-                int r = blas_gemm(M, L.wq, hq, h, M->hn16, T, M->q, M->ld_qkv, false, st);
-                if (r == LSTK_OK) r = blas_gemm(M, L.wk, hk, h, M->hn16, T, M->k, M->ld_qkv, false, st);
-                if (r == LSTK_OK) r = blas_gemm(M, L.wv, hk, h, M->hn16, T, M->v, M->ld_qkv, false, st);
+                if (M->qkv_joined[l]) return project(M, L.wq, hq + 2 * hk, h, M->hn16, T, M->q, M->ld_qkv, false, st);
+                int r = project(M, L.wq, hq, h, M->hn16, T, M->q, M->ld_qkv, false, st);
+                if (r == LSTK_OK) r = project(M, L.wk, hk, h, M->hn16, T, M->k, M->ld_qkv, false, st);
+                if (r == LSTK_OK) r = project(M, L.wv, hk, h, M->hn16, T, M->v, M->ld_qkv, false, st);
                 return r;
             });
             if (rc != LSTK_OK) return rc;
@@ -546,7 +556,7 @@ int forward(lstk_model *M, int32_t seq, int T, int n_cells, float *d_logits, int
         float *xr = M->x + (size_t) (T - rows) * h;
         lstk::NormParams fp{xr, nullptr, nullptr, nullptr, L.ffn_norm, M->hn, rows, h, hp.rms_eps};
         if (blas) {
-            const int rc = timed_span(M, 3, st, [&] { return blas_gemm(M, L.wo, h, hq, M->attn16, T, M->x, h, true, st); });
+            const int rc = timed_span(M, 3, st, [&] { return project(M, L.wo, h, hq, M->attn16, T, M->x, h, true, st); });
             if (rc != LSTK_OK) return rc;
         } else if ((e = timed(M, 3, [&](const lstk::LaunchTiming *tm) { return lstk::launch_gemv(op, st, tm); })) != hipSuccess) {
             return hip_fail(e, "o-proj launch");
