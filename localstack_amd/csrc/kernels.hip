@@ -43,7 +43,10 @@ typedef int xvec __attribute__((ext_vector_type(4))); // 16 bytes of int8 activa
 constexpr int kDecodeRouteT = 1;  // gate_up runs the top-k itself for a single token
 // Threads of a gate_up work-group: single-token (routing) launches use 512 (32 rows per matrix at
 // h = 2048; fewer, larger work-groups stream the 8 experts' rows faster on MI355X), batches 256.
-constexpr int kGuRouteBlock = 512;
+#ifndef LSTK_GU_ROUTE_THREADS
+#define LSTK_GU_ROUTE_THREADS 512
+#endif
+constexpr int kGuRouteBlock = LSTK_GU_ROUTE_THREADS;
 
 
 
@@ -306,7 +309,8 @@ __device__ __forceinline__ GroupLds group_lds(unsigned char *base, int T, int k,
 template <int EPL>
 __device__ __forceinline__ bool route_one(const GroupParams &P, GroupLds g) {
     const int tid = threadIdx.x, lane = tid % kWave, wave = tid / kWave;
-    const int E = P.E, Ep = EPL * kWave, nsplit = (int) blockDim.x / Ep, span = Ep / nsplit;
+    // nsplit groups of Ep threads each count over `span` keys (even, so the pairs stay 16-byte aligned)
+    const int E = P.E, Ep = EPL * kWave, nsplit = (int) blockDim.x / Ep, span = ((Ep + nsplit - 1) / nsplit + 1) & ~1;
     unsigned long long *s_key = reinterpret_cast<unsigned long long *>(g.scratch + kMaxK * 4); // [Ep]
     int *s_cnt = reinterpret_cast<int *>(s_key + Ep);                                          // [nsplit][Ep]
     float *s_l = reinterpret_cast<float *>(s_cnt + kGuRouteBlock);                             // [Ep]
@@ -318,11 +322,12 @@ __device__ __forceinline__ bool route_one(const GroupParams &P, GroupLds g) {
         s_l[e] = le;
     }
     __syncthreads();
-    {
+    if (part < nsplit) {
         const unsigned long long mine = s_key[e];
         const unsigned long long *row = s_key + part * span;
+        const int lim = max(0, min(span, Ep - part * span));
         int c = 0;
-        for (int i = 0; i < span; i += 2) {
+        for (int i = 0; i < lim; i += 2) {
             const ulonglong2 v = *reinterpret_cast<const ulonglong2 *>(row + i);
             c += (v.x > mine) + (v.y > mine);
         }
