@@ -167,6 +167,77 @@ __device__ __forceinline__ void rope_head(const RopeParams &P, int t, int j, flo
     }
 }
 
+// One token's rotations for the attention prologue at head size 128 (one NEOX pair (i, i + 64) per
+// lane), with the step's cos / sin table (R.cs): wavefront w rotates the query heads r = w, w + 4, ...
+// (r < grp) of KV head g into s_q (row r), and with `owner` set wavefront 0 also rotates KV head g's K
+// and wavefront 1 rounds its V, both as fp16 into s_kv (K at [0, 128), V at [128, 256)); the caller
+// stores them into the cache. Each value is rope_head's, computed by the same expressions. All loads
+// are unconditional and every head is computed branch-free (heads past grp from head grp - 1's row,
+// not stored; absent norm weights read the query row, not applied), so the prologue's loads are in
+// flight together and its first use waits for them only: after_loads() runs once they are issued,
+// and the caller's own loads queue behind them.
+constexpr int kRopeMaxQ = 4; // query heads per wavefront: grp <= 16
+template <typename F>
+__device__ __forceinline__ void rope_token_128(const RopeParams &R, int g, int grp, bool owner, float *s_q,
+                                               uint16_t *s_kv, F after_loads) {
+    constexpr int hd = 128, half = 64, K = kRopeMaxQ;
+    const int lane = threadIdx.x & (kWave - 1), w = threadIdx.x / kWave;
+    const bool do_k = owner && w == 0, do_v = owner && w == 1;
+    float x0[K + 1], x1[K + 1];
+#pragma unroll
+    for (int i = 0; i < K; i++) {
+        const float *src = R.q + (size_t) (g * grp + min(w + 4 * i, grp - 1)) * hd;
+        x0[i] = src[lane];
+        x1[i] = src[lane + half];
+    }
+    {
+        const float *src = do_k ? R.k + (size_t) g * hd : do_v ? R.v + (size_t) g * hd : R.q;
+        x0[K] = src[lane];
+        x1[K] = src[lane + half];
+    }
+    const bool qn = R.q_norm != nullptr, kn = R.k_norm != nullptr;
+    const float *qnw = qn ? R.q_norm : R.q, *knw = kn ? R.k_norm : R.q;
+    const float qn0 = qnw[lane], qn1 = qnw[lane + half], kn0 = knw[lane], kn1 = knw[lane + half];
+    const float2 csv = reinterpret_cast<const float2 *>(R.cs)[lane];
+    asm volatile("" ::: "memory");
+    after_loads();
+    const float c = csv.x, sn = csv.y;
+    float y0[K + 1], y1[K + 1];
+#pragma unroll
+    for (int i = 0; i <= K; i++) {
+        float a = x0[i], b = x1[i];
+        // QK-norm scale of the head from its lane pair, summed as rope_head sums it
+        double ss = 0.0;
+        ss += (double) (a * a);
+        ss += (double) (b * b);
+        ss = wave_sum_d(ss);
+        const float mean = (float) (ss / (double) hd);
+        const float scale = 1.0f / sqrtf(mean + R.eps);
+        const bool use = i < K ? qn : kn;
+        const float n0 = i < K ? qn0 : kn0, n1 = i < K ? qn1 : kn1;
+        const float an = (a * scale) * n0, bn = (b * scale) * n1;
+        a = use ? an : a;
+        b = use ? bn : b;
+        y0[i] = a * c - b * sn;
+        y1[i] = a * sn + b * c;
+    }
+#pragma unroll
+    for (int i = 0; i < K; i++) {
+        const int r = w + 4 * i;
+        if (r < grp) {
+            s_q[r * hd + lane] = y0[i];
+            s_q[r * hd + lane + half] = y1[i];
+        }
+    }
+    if (do_k) {
+        s_kv[lane] = f2h(y0[K]);
+        s_kv[lane + half] = f2h(y1[K]);
+    } else if (do_v) {
+        s_kv[hd + lane] = f2h(x0[K]);
+        s_kv[hd + lane + half] = f2h(x1[K]);
+    }
+}
+
 __global__ __launch_bounds__(kWave) void rope_kernel(RopeParams P) {
     rope_head(P, blockIdx.x, blockIdx.y, nullptr, blockIdx.y == 0);
 }
@@ -448,14 +519,19 @@ __device__ __forceinline__ half4v ld_half4(const uint16_t *p) {
     return __builtin_bit_cast(half4v, *reinterpret_cast<const uint2 *>(p));
 }
 
-template <int HD, int NRT>
+// R1: the single-token RoPE-in launch at head size 128 with the step's cos / sin table and grp <= 16
+// (rope_token_128's case), an instantiation of its own so that its prologue's loads and the first
+// pass's K / V loads are in flight together.
+template <int HD, int NRT, bool R1>
 __global__ __launch_bounds__(kAtBlock) void attn_kernel(AttnParams P) {
+    static_assert(!R1 || (NRT == 1 && HD == 128), "R1 is the single-token head-size-128 launch");
     constexpr int NK = HD / 16, DT = NK / 4, RB = 16 * NRT, PS = kFaCells + 8; // P row stride (halves)
     __shared__ float s_S[RB][kFaCells];
     __shared__ uint16_t s_Ph[RB][PS], s_Pl[RB][PS];
     __shared__ float s_M[RB], s_L[RB], s_f[RB];
     __shared__ int s_pos[RB];
     __shared__ float s_q[NRT == 1 ? 16 * HD : 1]; // rotated Q rows when this launch applies RoPE
+    __shared__ __align__(8) uint16_t s_kv[NRT == 1 && HD == 128 ? 2 * HD : 4]; // the new cell's K and V (fp16)
     const int tid = threadIdx.x, w = tid / kWave, l = tid & (kWave - 1), lr = l & 15, lq = l >> 4;
     const int grp = P.n_head / P.n_kv;
     const int g = blockIdx.x % P.n_kv, rest = blockIdx.x / P.n_kv;
@@ -468,17 +544,49 @@ __global__ __launch_bounds__(kAtBlock) void attn_kernel(AttnParams P) {
         s_L[tid] = 0.0f;
     }
     const int begin = c * P.chunk, end = min(begin + P.chunk, P.n_cells), last4 = P.kv_size - 4;
-    if (NRT == 1 && P.rope_in) {
-        // one token: every work-group rotates its own query rows (rope_kernel's work, bit for bit),
-        // and the work-group whose chunk holds the token's cell first stores that cell's K and V of
-        // KV head g and its cell-table entries, so its reads below see them
-        const int cell0 = P.rope.cells[0];
-        if (cell0 >= begin && cell0 < end) {
-            if (w == 0) rope_head(P.rope, 0, P.n_head + g, nullptr, true);
-            else if (w == 1) rope_head(P.rope, 0, P.n_head + P.n_kv + g, nullptr, false);
+    // fresh: this work-group's chunk holds the token's new cell, whose K / V it computes itself; its
+    // reads of that cell take them from LDS, and it stores them into the cache after its last barrier
+    const bool rope_in = R1 || (NRT == 1 && P.rope_in);
+    const int cell0 = rope_in ? P.rope.cells[0] : -1;
+    const bool owner = cell0 >= begin && cell0 < end;
+    const bool fresh = R1 && owner;
+    // The first pass's K / V fragments and cell-table entries are requested before the prologue
+    // (R1: right behind the prologue's own loads), except by a work-group that stores the new cell in
+    // its prologue and then reads it back (late).
+    const bool late = !R1 && rope_in && owner;
+    const uint16_t *kb = P.kc + (size_t) g * (HD / 4) * P.kv_size * 4;
+    half4v vf[4][DT]; // V fragments of a pass (B operand of O += P V): cells kc*16 + 4 lq .. +3, dim (w*DT + dt)*16 + lr
+    half4v kf[NK];    // K fragments of the wavefront's 16 cells
+    int cseq, cpos0;  // cell-table entries of the lane's cell
+    auto load_pass = [&](int c0) {
+#pragma unroll
+        for (int kc = 0; kc < 4; kc++) {
+            const int cg = min(c0 + kc * 16 + 4 * lq, last4);
+#pragma unroll
+            for (int dt = 0; dt < DT; dt++) vf[kc][dt] = ld_half4(P.vc + v_index(g, (w * DT + dt) * 16 + lr, cg, HD, P.kv_size));
         }
-        for (int r = w; r < grp; r += kAtBlock / kWave) rope_head(P.rope, 0, g * grp + r, s_q + r * HD, false);
+        const int cc = min(c0 + 16 * w + lr, P.kv_size - 1);
+#pragma unroll
+        for (int ks = 0; ks < NK; ks++) kf[ks] = ld_half4(kb + ((size_t) (ks * 4 + lq) * P.kv_size + cc) * 4);
+        cseq = P.cell_seq[cc];
+        cpos0 = P.cell_pos[cc];
+    };
+    // one token: every work-group rotates its own query rows (rope_kernel's work, bit for bit); the
+    // work-group whose chunk holds the token's cell also computes that cell's K and V of KV head g
+    // (kept in LDS with R1, else stored into the cache with its cell-table entries here)
+    if constexpr (R1) {
+        rope_token_128(P.rope, g, grp, owner, s_q, s_kv, [&] { load_pass(begin); });
         __syncthreads();
+    } else {
+        if (!late) load_pass(begin);
+        if (rope_in) {
+            if (owner) {
+                if (w == 0) rope_head(P.rope, 0, P.n_head + g, nullptr, true);
+                else if (w == 1) rope_head(P.rope, 0, P.n_head + P.n_kv + g, nullptr, false);
+            }
+            for (int r = w; r < grp; r += kAtBlock / kWave) rope_head(P.rope, 0, g * grp + r, s_q + r * HD, false);
+            __syncthreads();
+        }
     }
     // Q fragments (A operand): row rt*16 + lr, dims ks*16 + 4 lq .. +3
     half4v qa[NRT][NK];
@@ -486,7 +594,8 @@ __global__ __launch_bounds__(kAtBlock) void attn_kernel(AttnParams P) {
     for (int rt = 0; rt < NRT; rt++) {
         const int r = row0 + rt * 16 + lr;
         const bool on = r < rows;
-        const float *q = NRT == 1 && P.rope_in ? s_q + (on ? r % grp : 0) * HD
+        // (a RoPE-in launch is one token in one row block: its live rows r < grp are the heads themselves)
+        const float *q = rope_in ? s_q + (on ? r : 0) * HD
                                                : P.q + ((size_t) (on ? r / grp : 0) * P.n_head + g * grp + (on ? r % grp : 0)) * HD;
 #pragma unroll
         for (int ks = 0; ks < NK; ks++) {
@@ -501,24 +610,19 @@ __global__ __launch_bounds__(kAtBlock) void attn_kernel(AttnParams P) {
         for (int dt = 0; dt < DT; dt++) O[rt][dt] = f32x4v{0, 0, 0, 0};
     __syncthreads();
 
-    const uint16_t *kb = P.kc + (size_t) g * (HD / 4) * P.kv_size * 4;
     for (int c0 = begin; c0 < end; c0 += kFaCells) {
-        // V fragments of this pass (B operand of O += P V): cells kc*16 + 4 lq .. +3, dim (w*DT + dt)*16 + lr
-        half4v vf[4][DT];
-#pragma unroll
-        for (int kc = 0; kc < 4; kc++) {
-            const int cg = min(c0 + kc * 16 + 4 * lq, last4);
-#pragma unroll
-            for (int dt = 0; dt < DT; dt++) vf[kc][dt] = ld_half4(P.vc + v_index(g, (w * DT + dt) * 16 + lr, cg, HD, P.kv_size));
-        }
+        if (c0 != begin || late) load_pass(c0);
         // S = Q K^T for this wavefront's 16 cells
         const int cell = c0 + 16 * w + lr;
         const int cc = min(cell, P.kv_size - 1);
-        half4v kf[NK];
+        bool live = cell < end && cseq == P.seq;
+        int cpos = cpos0;
+        if (fresh && cc == cell0) {
 #pragma unroll
-        for (int ks = 0; ks < NK; ks++) kf[ks] = ld_half4(kb + ((size_t) (ks * 4 + lq) * P.kv_size + cc) * 4);
-        const bool live = cell < end && P.cell_seq[cc] == P.seq;
-        const int cpos = P.cell_pos[cc];
+            for (int ks = 0; ks < NK; ks++) kf[ks] = ld_half4(&s_kv[(ks * 4 + lq) * 4]);
+            live = true;
+            cpos = P.rope.pos[0];
+        }
 #pragma unroll
         for (int rt = 0; rt < NRT; rt++) {
             f32x4v sacc = f32x4v{0, 0, 0, 0};
@@ -532,8 +636,43 @@ __global__ __launch_bounds__(kAtBlock) void attn_kernel(AttnParams P) {
             }
         }
         __syncthreads();
-        // online softmax: 4 threads per row, 16 cells each
-        {
+        if (NRT == 1) {
+            // online softmax of one 16-row tile: 16 threads per row, 4 cells each
+            const int r = tid >> 4, part = tid & 15;
+            float sv[4];
+            float m = -INFINITY;
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                sv[i] = s_S[r][part * 4 + i];
+                m = fmaxf(m, sv[i]);
+            }
+            m = fmaxf(m, dpp_f<0xB1>(m)); // the 16 lanes of the row (DPP row): pairs, quads, octets, halves
+            m = fmaxf(m, dpp_f<0x4E>(m));
+            m = fmaxf(m, dpp_f<0x141>(m));
+            m = fmaxf(m, dpp_f<0x140>(m));
+            const float m_old = s_M[r], m_new = fmaxf(m_old, m);
+            float sum = 0.0f;
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const float p = sv[i] == -INFINITY ? 0.0f : expf(sv[i] - m_new);
+                const _Float16 hi = (_Float16) p;
+                const _Float16 lo = (_Float16) (p - (float) hi);
+                s_Ph[r][part * 4 + i] = __builtin_bit_cast(uint16_t, hi);
+                s_Pl[r][part * 4 + i] = __builtin_bit_cast(uint16_t, lo);
+                sum += p;
+            }
+            sum += dpp_f<0xB1>(sum);
+            sum += dpp_f<0x4E>(sum);
+            sum += dpp_f<0x141>(sum);
+            sum += dpp_f<0x140>(sum);
+            if (part == 0) {
+                const float f = m_old == -INFINITY ? 0.0f : expf(m_old - m_new);
+                s_f[r] = f;
+                s_L[r] = s_L[r] * f + sum;
+                s_M[r] = m_new;
+            }
+        } else {
+            // online softmax: 4 threads per row, 16 cells each
             const int r = tid >> 2, part = tid & 3;
             if (r < RB) {
                 float sv[16];
@@ -543,8 +682,8 @@ __global__ __launch_bounds__(kAtBlock) void attn_kernel(AttnParams P) {
                     sv[i] = s_S[r][part * 16 + i];
                     m = fmaxf(m, sv[i]);
                 }
-                m = fmaxf(m, __shfl_xor(m, 1));
-                m = fmaxf(m, __shfl_xor(m, 2));
+                m = fmaxf(m, dpp_f<0xB1>(m)); // lanes l ^ 1, then l ^ 2
+                m = fmaxf(m, dpp_f<0x4E>(m));
                 const float m_old = s_M[r], m_new = fmaxf(m_old, m);
                 float sum = 0.0f;
 #pragma unroll
@@ -556,8 +695,8 @@ __global__ __launch_bounds__(kAtBlock) void attn_kernel(AttnParams P) {
                     s_Pl[r][part * 16 + i] = __builtin_bit_cast(uint16_t, lo);
                     sum += p;
                 }
-                sum += __shfl_xor(sum, 1);
-                sum += __shfl_xor(sum, 2);
+                sum += dpp_f<0xB1>(sum);
+                sum += dpp_f<0x4E>(sum);
                 if (part == 0) {
                     const float f = m_old == -INFINITY ? 0.0f : expf(m_old - m_new);
                     s_f[r] = f;
@@ -567,6 +706,18 @@ __global__ __launch_bounds__(kAtBlock) void attn_kernel(AttnParams P) {
             }
         }
         __syncthreads();
+        if (fresh) {
+            // the new cell's V in the fragment that holds it
+#pragma unroll
+            for (int kc = 0; kc < 4; kc++) {
+                const int cg = c0 + kc * 16 + 4 * lq;
+                if (cg <= last4 && cell0 >= cg && cell0 < cg + 4) {
+#pragma unroll
+                    for (int dt = 0; dt < DT; dt++)
+                        vf[kc][dt][cell0 - cg] = __builtin_bit_cast(_Float16, s_kv[HD + (w * DT + dt) * 16 + lr]);
+                }
+            }
+        }
         // O = O * f + P V
 #pragma unroll
         for (int rt = 0; rt < NRT; rt++) {
@@ -589,14 +740,21 @@ __global__ __launch_bounds__(kAtBlock) void attn_kernel(AttnParams P) {
         }
         __syncthreads();
     }
-    // rows of this lane: rt*16 + 4 lq + v, dims (w*DT + dt)*16 + lr
+    // rows of this lane: rt*16 + 4 lq + v, dims (w*DT + dt)*16 + lr; row r is query head r % grp of
+    // token r / grp, stepped from the first row's quotient instead of divided per row
 #pragma unroll
     for (int rt = 0; rt < NRT; rt++) {
+        const int r0 = row0 + rt * 16 + 4 * lq;
+        int tq = r0 / grp, hq = r0 - tq * grp;
 #pragma unroll
         for (int v = 0; v < 4; v++) {
             const int rl = rt * 16 + 4 * lq + v, r = row0 + rl;
+            const int t = tq, h = g * grp + hq;
+            if (++hq == grp) {
+                hq = 0;
+                ++tq;
+            }
             if (r >= rows) continue;
-            const int t = r / grp, h = g * grp + r % grp;
             if (P.n_chunk == 1) {
                 const float inv_l = s_L[rl];
 #pragma unroll
@@ -617,26 +775,59 @@ __global__ __launch_bounds__(kAtBlock) void attn_kernel(AttnParams P) {
             }
         }
     }
+    if (fresh && w < 2) {
+        // the new cell into the cache (read by later launches only): K and the cell tables by
+        // wavefront 0, V by wavefront 1
+        const RopeParams &R = P.rope;
+        if (w == 0) {
+            if (l == 0) {
+                R.cell_seq[cell0] = R.seq;
+                R.cell_pos[cell0] = R.pos[0];
+            }
+            R.kc[k_index(g, l, cell0, HD, R.kv_size)] = s_kv[l];
+            R.kc[k_index(g, l + HD / 2, cell0, HD, R.kv_size)] = s_kv[l + HD / 2];
+        } else {
+            R.vc[v_index(g, l, cell0, HD, R.kv_size)] = s_kv[HD + l];
+            R.vc[v_index(g, l + HD / 2, cell0, HD, R.kv_size)] = s_kv[HD + l + HD / 2];
+        }
+    }
 }
 
 // Merges the chunks' partial rows of one (query head, token): out = sum_c o_c e^(m_c - M) / sum_c l_c e^(m_c - M).
-// Every thread takes chunks for the max and the factors; then hd / 4 threads per chunk read float4
-// slices of the partial outputs, 256 / (hd / 4) chunks at a time, four batches in flight.
+// Every load is issued before the first reduction: thread i takes chunk i's (m, l) (and chunks i + 256,
+// ... past 256 chunks), and hd / 4 threads per chunk hold the float4 slices of up to kCombRegs chunks
+// each in registers (chunks cl, cl + CL, ...; any further ones are read after the factors). Each
+// thread's slices are summed in ascending chunk order, then the CL thread sums in order.
+constexpr int kCombRegs = 16;
 __global__ __launch_bounds__(kBlock) void attn_combine_kernel(AttnParams P) {
     extern __shared__ float s_f[]; // [n_chunk] factors, then [kBlock / (hd / 4)][hd] sums
     __shared__ float s_red[kBlock / kWave];
     const int h = blockIdx.x, t = blockIdx.y, tid = threadIdx.x, lane = tid & (kWave - 1), wv = tid / kWave;
     const int hd = P.hd, n = P.n_chunk, stride = hd + 4;
     const float *pp = P.part + ((size_t) t * P.n_head + h) * n * stride;
-    float m = -INFINITY;
-    for (int c = tid; c < n; c += kBlock) m = fmaxf(m, pp[(size_t) c * stride]);
+    const int nq = hd / 4, CL = kBlock / nq, dq = tid % nq, cl = tid / nq;
+    float4 vr[kCombRegs];
+#pragma unroll
+    for (int j = 0; j < kCombRegs; j++) {
+        const int c = cl + j * CL;
+        vr[j] = c < n ? *reinterpret_cast<const float4 *>(pp + (size_t) c * stride + 4 + 4 * dq) : make_float4(0, 0, 0, 0);
+    }
+    const float m0 = tid < n ? pp[(size_t) tid * stride] : -INFINITY;
+    const float l0 = tid < n ? pp[(size_t) tid * stride + 1] : 0.0f;
+    float m = m0;
+    for (int c = tid + kBlock; c < n; c += kBlock) m = fmaxf(m, pp[(size_t) c * stride]);
     m = wave_max(m);
     if (lane == 0) s_red[wv] = m;
     __syncthreads();
     const float M = fmaxf(fmaxf(s_red[0], s_red[1]), fmaxf(s_red[2], s_red[3]));
     __syncthreads();
     float ls = 0.0f;
-    for (int c = tid; c < n; c += kBlock) {
+    if (tid < n) {
+        const float f = m0 == -INFINITY ? 0.0f : expf(m0 - M);
+        s_f[tid] = f;
+        ls += l0 * f;
+    }
+    for (int c = tid + kBlock; c < n; c += kBlock) {
         const float mc = pp[(size_t) c * stride];
         const float f = mc == -INFINITY ? 0.0f : expf(mc - M);
         s_f[c] = f;
@@ -646,25 +837,22 @@ __global__ __launch_bounds__(kBlock) void attn_combine_kernel(AttnParams P) {
     if (lane == 0) s_red[wv] = ls;
     __syncthreads();
     const float L = (s_red[0] + s_red[1]) + (s_red[2] + s_red[3]);
-    const int nq = hd / 4, CL = kBlock / nq, dq = tid % nq, cl = tid / nq;
     float4 acc = make_float4(0, 0, 0, 0);
-    for (int c0 = cl; c0 < n; c0 += 4 * CL) {
-        float4 v[4];
-        float f[4];
+    auto add = [&](const float4 &v, float f) {
+        acc.x += v.x * f;
+        acc.y += v.y * f;
+        acc.z += v.z * f;
+        acc.w += v.w * f;
+    };
 #pragma unroll
-        for (int i = 0; i < 4; i++) {
-            const int c = c0 + i * CL;
-            f[i] = c < n ? s_f[c] : 0.0f;
-            v[i] = c < n ? *reinterpret_cast<const float4 *>(pp + (size_t) c * stride + 4 + 4 * dq) : make_float4(0, 0, 0, 0);
-        }
-#pragma unroll
-        for (int i = 0; i < 4; i++) {
-            if (f[i] == 0.0f) continue;
-            acc.x += v[i].x * f[i];
-            acc.y += v[i].y * f[i];
-            acc.z += v[i].z * f[i];
-            acc.w += v[i].w * f[i];
-        }
+    for (int j = 0; j < kCombRegs; j++) {
+        const int c = cl + j * CL;
+        const float f = c < n ? s_f[c] : 0.0f;
+        if (f != 0.0f) add(vr[j], f);
+    }
+    for (int c = cl + kCombRegs * CL; c < n; c += CL) {
+        const float f = s_f[c];
+        if (f != 0.0f) add(*reinterpret_cast<const float4 *>(pp + (size_t) c * stride + 4 + 4 * dq), f);
     }
     float *s_o = s_f + ((n + 3) & ~3); // 16-byte aligned
     reinterpret_cast<float4 *>(s_o)[cl * nq + dq] = acc;
@@ -819,9 +1007,13 @@ hipError_t launch_rope(const RopeParams &P, hipStream_t st, const LaunchTiming *
 template <int HD>
 hipError_t launch_attn_hd(const AttnParams &P, hipStream_t st, const LaunchTiming *tm) {
     const dim3 grid(P.n_kv * P.n_chunk * P.n_rowblk), block(kAtBlock);
-    if (P.rb_rows == 16) return launch(attn_kernel<HD, 1>, grid, block, 0, st, tm, P);
-    if (P.rb_rows == 32) return launch(attn_kernel<HD, 2>, grid, block, 0, st, tm, P);
-    return launch(attn_kernel<HD, 4>, grid, block, 0, st, tm, P);
+    if constexpr (HD == 128) {
+        if (P.rb_rows == 16 && P.rope_in && P.n_head / P.n_kv <= 4 * kRopeMaxQ && P.rope.cs)
+            return launch(attn_kernel<HD, 1, true>, grid, block, 0, st, tm, P);
+    }
+    if (P.rb_rows == 16) return launch(attn_kernel<HD, 1, false>, grid, block, 0, st, tm, P);
+    if (P.rb_rows == 32) return launch(attn_kernel<HD, 2, false>, grid, block, 0, st, tm, P);
+    return launch(attn_kernel<HD, 4, false>, grid, block, 0, st, tm, P);
 }
 
 hipError_t launch_attn(const AttnParams &P, hipStream_t st, const LaunchTiming *tm) {
