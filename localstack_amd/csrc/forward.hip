@@ -318,17 +318,21 @@ __global__ __launch_bounds__(kGvWaves *kWave) void gemv_kernel(GemvParams P) {
 }
 
 // ------------------------------------------------------------------------------------------------
-// single-token F16 GEMV: every weight chunk of the wavefront's RW rows is requested before anything
-// waits (NJ = ceil(cols / 512) 16-byte chunks per lane per row), the activation row comes straight
-// from memory into registers (no LDS, no barrier), optionally gathered from the embedding and
-// RMS-normalised on the way (one wavefront-wide double sum per wavefront).
+// single-token F16 GEMV: every load of a wavefront (the activation row, the norm weights, NJ =
+// ceil(cols / 512) 16-byte chunks per lane of each of its RW rows, the residual values) is requested
+// before anything waits; the activation row comes straight from memory into registers (no LDS, no
+// barrier), optionally gathered from the embedding (EMB) and RMS-normalised on the way (NORM: one
+// wavefront-wide double sum per wavefront, while the weight rows stream in).
 // ------------------------------------------------------------------------------------------------
 
-template <int NJ, int RW>
+template <int NJ, int RW, bool NORM, bool EMB>
 __global__ __launch_bounds__(kGvWaves *kWave) void gemv1_kernel(GemvParams P) {
     const int tid = threadIdx.x, lane = tid & (kWave - 1), wv = tid / kWave;
     const int cols = P.cols, nc = cols / 8;
     const int row0 = (blockIdx.x * kGvWaves + wv) * RW;
+    // each row's matrix by comparison with the segment bounds (the parameters read at fixed indices,
+    // so no address waits on a memory read); rows past the end read row 0 and store nothing
+    const int b1 = P.seg[0].rows, b2 = b1 + (P.nseg > 1 ? P.seg[1].rows : 0);
     const uint4 *wr[RW];
     float *yr[RW];
     const float *ar[RW];
@@ -337,67 +341,71 @@ __global__ __launch_bounds__(kGvWaves *kWave) void gemv1_kernel(GemvParams P) {
     for (int rr = 0; rr < RW; rr++) {
         const int r = row0 + rr;
         on[rr] = r < P.rows_total;
-        int loc = on[rr] ? r : 0, s = 0;
-        while (s + 1 < P.nseg && loc >= P.seg[s].rows) {
-            loc -= P.seg[s].rows;
-            s++;
+        const int rc = on[rr] ? r : 0;
+        const int s = (P.nseg > 1 && rc >= b1) + (P.nseg > 2 && rc >= b2);
+        const int loc = rc - (s == 0 ? 0 : s == 1 ? b1 : b2);
+        const uint16_t *w = s == 0 ? P.seg[0].w : s == 1 ? P.seg[1].w : P.seg[2].w;
+        float *y = s == 0 ? P.seg[0].y : s == 1 ? P.seg[1].y : P.seg[2].y;
+        const float *a = s == 0 ? P.seg[0].add : s == 1 ? P.seg[1].add : P.seg[2].add;
+        wr[rr] = reinterpret_cast<const uint4 *>(w + (size_t) loc * cols);
+        yr[rr] = y + loc;
+        ar[rr] = a ? a + loc : nullptr;
+    }
+    // Every load is unconditional and issued up front, in the order of first use: the activation row
+    // (or the embedding row) and the norm weights, then the weight rows (streamed while the row is
+    // normalised), then the rows' residual values. Chunks past the row's end (c >= nc) load chunk
+    // nc - 1 and use zero activations, so they add nothing.
+    const uint16_t *e = EMB ? P.emb + (size_t) P.tokens[0] * cols : nullptr;
+    float xv[NJ][8], nw[NJ][8];
+#pragma unroll
+    for (int j = 0; j < NJ; j++) {
+        const int cc = min(lane + kWave * j, nc - 1);
+        if constexpr (EMB) {
+            const uint4 hv = reinterpret_cast<const uint4 *>(e)[cc];
+            const uint32_t hw[4] = {hv.x, hv.y, hv.z, hv.w};
+#pragma unroll
+            for (int q = 0; q < 4; q++) {
+                xv[j][2 * q] = h2f(hw[q]);
+                xv[j][2 * q + 1] = h2f(hw[q] >> 16);
+            }
+        } else {
+            const float4 a = reinterpret_cast<const float4 *>(P.x)[2 * cc];
+            const float4 b = reinterpret_cast<const float4 *>(P.x)[2 * cc + 1];
+            xv[j][0] = a.x, xv[j][1] = a.y, xv[j][2] = a.z, xv[j][3] = a.w;
+            xv[j][4] = b.x, xv[j][5] = b.y, xv[j][6] = b.z, xv[j][7] = b.w;
         }
-        wr[rr] = reinterpret_cast<const uint4 *>(P.seg[s].w + (size_t) loc * cols);
-        yr[rr] = P.seg[s].y + loc;
-        ar[rr] = P.seg[s].add ? P.seg[s].add + loc : nullptr;
+        if constexpr (NORM) {
+            const float4 a = reinterpret_cast<const float4 *>(P.norm_w)[2 * cc];
+            const float4 b = reinterpret_cast<const float4 *>(P.norm_w)[2 * cc + 1];
+            nw[j][0] = a.x, nw[j][1] = a.y, nw[j][2] = a.z, nw[j][3] = a.w;
+            nw[j][4] = b.x, nw[j][5] = b.y, nw[j][6] = b.z, nw[j][7] = b.w;
+        }
     }
     uint4 w[RW][NJ];
 #pragma unroll
     for (int j = 0; j < NJ; j++) {
-        const int c = lane + kWave * j;
+        const int cc = min(lane + kWave * j, nc - 1);
 #pragma unroll
-        for (int rr = 0; rr < RW; rr++) w[rr][j] = c < nc ? load_weights(wr[rr] + c) : make_uint4(0, 0, 0, 0);
+        for (int rr = 0; rr < RW; rr++) w[rr][j] = load_weights(wr[rr] + cc);
     }
-    float xv[NJ][8];
-    const uint16_t *e = P.emb ? P.emb + (size_t) P.tokens[0] * cols : nullptr;
+    float addv[RW];
+#pragma unroll
+    for (int rr = 0; rr < RW; rr++) addv[rr] = *(ar[rr] ? ar[rr] : yr[rr]);
 #pragma unroll
     for (int j = 0; j < NJ; j++) {
-        const int c = lane + kWave * j;
-        if (c < nc) {
-            if (e) {
-                const uint4 hv = reinterpret_cast<const uint4 *>(e)[c];
-                const uint32_t hw[4] = {hv.x, hv.y, hv.z, hv.w};
-#pragma unroll
-                for (int q = 0; q < 4; q++) {
-                    xv[j][2 * q] = h2f(hw[q]);
-                    xv[j][2 * q + 1] = h2f(hw[q] >> 16);
-                }
-            } else {
-                const float4 a = reinterpret_cast<const float4 *>(P.x)[2 * c];
-                const float4 b = reinterpret_cast<const float4 *>(P.x)[2 * c + 1];
-                xv[j][0] = a.x, xv[j][1] = a.y, xv[j][2] = a.z, xv[j][3] = a.w;
-                xv[j][4] = b.x, xv[j][5] = b.y, xv[j][6] = b.z, xv[j][7] = b.w;
-            }
-        } else {
+        if (lane + kWave * j >= nc) {
 #pragma unroll
             for (int q = 0; q < 8; q++) xv[j][q] = 0.0f;
         }
     }
-    if (e && blockIdx.x == 0 && wv == 0) {
+    float xraw[EMB ? NJ : 1][8];
+    if constexpr (EMB) {
 #pragma unroll
-        for (int j = 0; j < NJ; j++) {
-            const int c = lane + kWave * j;
-            if (c < nc) {
-                reinterpret_cast<float4 *>(P.x_out)[2 * c] = make_float4(xv[j][0], xv[j][1], xv[j][2], xv[j][3]);
-                reinterpret_cast<float4 *>(P.x_out)[2 * c + 1] = make_float4(xv[j][4], xv[j][5], xv[j][6], xv[j][7]);
-            }
-        }
+        for (int j = 0; j < NJ; j++)
+#pragma unroll
+            for (int q = 0; q < 8; q++) xraw[j][q] = xv[j][q];
     }
-    if (P.norm_w) {
-        float nw[NJ][8];
-#pragma unroll
-        for (int j = 0; j < NJ; j++) {
-            const int c = lane + kWave * j;
-            const float4 a = c < nc ? reinterpret_cast<const float4 *>(P.norm_w)[2 * c] : make_float4(0, 0, 0, 0);
-            const float4 b = c < nc ? reinterpret_cast<const float4 *>(P.norm_w)[2 * c + 1] : make_float4(0, 0, 0, 0);
-            nw[j][0] = a.x, nw[j][1] = a.y, nw[j][2] = a.z, nw[j][3] = a.w;
-            nw[j][4] = b.x, nw[j][5] = b.y, nw[j][6] = b.z, nw[j][7] = b.w;
-        }
+    if constexpr (NORM) {
         double s = 0.0;
 #pragma unroll
         for (int j = 0; j < NJ; j++)
@@ -424,7 +432,20 @@ __global__ __launch_bounds__(kGvWaves *kWave) void gemv1_kernel(GemvParams P) {
 #pragma unroll
     for (int rr = 0; rr < RW; rr++) {
         const float sum = wave_sum_tree(acc[rr]);
-        if (lane == 0 && on[rr]) yr[rr][0] = ar[rr] ? sum + ar[rr][0] : sum;
+        if (lane == 0 && on[rr]) yr[rr][0] = ar[rr] ? sum + addv[rr] : sum;
+    }
+    if constexpr (EMB) {
+        // the gathered embedding row is the layer's residual input (written once, by work-group 0)
+        if (blockIdx.x == 0 && wv == 0) {
+#pragma unroll
+            for (int j = 0; j < NJ; j++) {
+                const int c = lane + kWave * j;
+                if (c < nc) {
+                    reinterpret_cast<float4 *>(P.x_out)[2 * c] = make_float4(xraw[j][0], xraw[j][1], xraw[j][2], xraw[j][3]);
+                    reinterpret_cast<float4 *>(P.x_out)[2 * c + 1] = make_float4(xraw[j][4], xraw[j][5], xraw[j][6], xraw[j][7]);
+                }
+            }
+        }
     }
 }
 
@@ -968,7 +989,13 @@ hipError_t launch_gemm16(const Gemm16Params &P, hipStream_t st, const LaunchTimi
 template <int NJ, int RW>
 hipError_t launch_gemv1_t(const GemvParams &P, hipStream_t st, const LaunchTiming *tm) {
     const int per_wg = kGvWaves * RW;
-    return launch(gemv1_kernel<NJ, RW>, dim3((P.rows_total + per_wg - 1) / per_wg), dim3(kGvWaves * kWave), 0, st, tm, P);
+    const dim3 grid((P.rows_total + per_wg - 1) / per_wg), block(kGvWaves * kWave);
+    if (P.emb) {
+        if (P.norm_w) return launch(gemv1_kernel<NJ, RW, true, true>, grid, block, 0, st, tm, P);
+        return launch(gemv1_kernel<NJ, RW, false, true>, grid, block, 0, st, tm, P);
+    }
+    if (P.norm_w) return launch(gemv1_kernel<NJ, RW, true, false>, grid, block, 0, st, tm, P);
+    return launch(gemv1_kernel<NJ, RW, false, false>, grid, block, 0, st, tm, P);
 }
 
 hipError_t launch_gemv(const GemvParams &P, hipStream_t st, const LaunchTiming *tm) {
@@ -979,7 +1006,12 @@ hipError_t launch_gemv(const GemvParams &P, hipStream_t st, const LaunchTiming *
         const int nj = (P.cols / 8 + kWave - 1) / kWave;
         if (nj <= 1) return launch_gemv1_t<1, 4>(P, st, tm);
         if (nj <= 2) return launch_gemv1_t<2, 4>(P, st, tm);
-        if (nj <= 4) return launch_gemv1_t<4, 4>(P, st, tm);
+        if (nj <= 4) {
+            // five rows per wavefront when that fits the rows in one work-group per CU and four do not
+            // (Q/K/V of the 30B shape: 5120 rows in 256 work-groups instead of 320)
+            if ((P.rows_total + 19) / 20 <= 256 && (P.rows_total + 15) / 16 > 256) return launch_gemv1_t<4, 5>(P, st, tm);
+            return launch_gemv1_t<4, 4>(P, st, tm);
+        }
         if (nj <= 8) return launch_gemv1_t<8, 2>(P, st, tm);
         if (nj <= 16) return launch_gemv1_t<16, 1>(P, st, tm);
     }
