@@ -94,31 +94,40 @@ __device__ __forceinline__ void route_tile(const RouteParams &P, int b, float *x
     constexpr int h = NG * 256;
     constexpr int kPre = 32768 / 16 / kBlock; // float4 of one stage per thread (tt * h * 4 <= 32 KiB)
     const int wave = threadIdx.x / kWave, lane = threadIdx.x % kWave;
+    // every load unconditional and unrolled, so all of them are in flight before the first use; F16
+    // rows stay packed until the activation loads are issued too (converting them would wait for them)
+    uint2 wh[GT == kTypeF16 ? kRouteEPW : 1][NG];
     float w[kRouteEPW][NG][4];
-    // every load unconditional and unrolled, so all of them are in flight before the first use
 #pragma unroll
     for (int ee = 0; ee < kRouteEPW; ee++) {
         const int e = min(eg * kRouteEG + wave * kRouteEPW + ee, P.E - 1);
 #pragma unroll
         for (int g = 0; g < NG; g++) {
-            {
-                const size_t i = (size_t) e * h + 256 * g + 4 * lane;
-                if (GT == kTypeF16) {
-                    const uint2 raw = *reinterpret_cast<const uint2 *>(static_cast<const unsigned short *>(P.gate_inp) + i);
-                    w[ee][g][0] = h2f(raw.x);
-                    w[ee][g][1] = h2f(raw.x >> 16);
-                    w[ee][g][2] = h2f(raw.y);
-                    w[ee][g][3] = h2f(raw.y >> 16);
-                } else {
-                    const float4 raw = *reinterpret_cast<const float4 *>(static_cast<const float *>(P.gate_inp) + i);
-                    w[ee][g][0] = raw.x;
-                    w[ee][g][1] = raw.y;
-                    w[ee][g][2] = raw.z;
-                    w[ee][g][3] = raw.w;
-                }
+            const size_t i = (size_t) e * h + 256 * g + 4 * lane;
+            if constexpr (GT == kTypeF16) {
+                wh[ee][g] = *reinterpret_cast<const uint2 *>(static_cast<const unsigned short *>(P.gate_inp) + i);
+            } else {
+                const float4 raw = *reinterpret_cast<const float4 *>(static_cast<const float *>(P.gate_inp) + i);
+                w[ee][g][0] = raw.x;
+                w[ee][g][1] = raw.y;
+                w[ee][g][2] = raw.z;
+                w[ee][g][3] = raw.w;
             }
         }
     }
+    auto unpack = [&] {
+        if constexpr (GT == kTypeF16) {
+#pragma unroll
+            for (int ee = 0; ee < kRouteEPW; ee++)
+#pragma unroll
+                for (int g = 0; g < NG; g++) {
+                    w[ee][g][0] = h2f(wh[ee][g].x);
+                    w[ee][g][1] = h2f(wh[ee][g].x >> 16);
+                    w[ee][g][2] = h2f(wh[ee][g].y);
+                    w[ee][g][3] = h2f(wh[ee][g].y >> 16);
+                }
+        }
+    };
     // the work-group's ns stages of tt tokens: stage s + 1 is loaded into registers while the
     // tokens of stage s are multiplied from LDS
     if (P.x_raw) {
@@ -127,6 +136,7 @@ __device__ __forceinline__ void route_tile(const RouteParams &P, int b, float *x
         norm_row<NG>(P.x_raw, P.norm_w, h, P.eps, y, s_part);
 #pragma unroll
         for (int k = 0; k < NG; k++) xs[threadIdx.x + k * kBlock] = GT == kTypeF16 ? round_f16(y[k]) : y[k];
+        unpack();
         __syncthreads();
         float acc[kRouteEPW];
 #pragma unroll
@@ -150,6 +160,7 @@ __device__ __forceinline__ void route_tile(const RouteParams &P, int b, float *x
         }
         return;
     }
+    unpack();
     const int tbase = tile * tt * ns;
     float4 pre[kPre];
     auto load = [&](int s) {
@@ -221,16 +232,18 @@ __global__ __launch_bounds__(kBlock) void route_kernel(RouteParams P, int n_rout
     } else if (P.qtype != 0) {
         const int h = P.h;
         if (P.x_raw) {
-            // one token: this work-group normalises the row, stores it, and quantizes what it stored
+            // one token: this work-group normalises the row, quantizes it from LDS, and stores it
             float y[NG];
             norm_row<NG>(P.x_raw, P.norm_w, h, P.eps, y, s_part);
 #pragma unroll
-            for (int k = 0; k < NG; k++) P.hnorm_out[threadIdx.x + k * kBlock] = y[k];
+            for (int k = 0; k < NG; k++) lds[threadIdx.x + k * kBlock] = y[k];
             __syncthreads();
             if (P.qtype == kTypeQ8_0)
-                quantize_row<kTypeQ8_0>(P.hnorm_out, h, P.xq.qs, P.xq.d, P.xq.bs);
+                quantize_row<kTypeQ8_0>(lds, h, P.xq.qs, P.xq.d, P.xq.bs);
             else
-                quantize_row<kTypeQ4_K>(P.hnorm_out, h, P.xq.qs, P.xq.d, P.xq.bs);
+                quantize_row<kTypeQ4_K>(lds, h, P.xq.qs, P.xq.d, P.xq.bs);
+#pragma unroll
+            for (int k = 0; k < NG; k++) P.hnorm_out[threadIdx.x + k * kBlock] = y[k];
             return;
         }
         for (int t = b - n_route_wg; t < P.T; t += n_quant_wg) {
@@ -732,6 +745,7 @@ __global__ __launch_bounds__(kBlock) void down_combine_kernel(DownCombineParams 
     // unconditional loads (indexes clamped), so the weight loads follow without a branch
     int b = P.ids[min(j, k - 1)];
     const float wj = P.weights[min(tid, k - 1)];
+    const float resid = P.resid[blockIdx.x * rd + min(tid, rd - 1)]; // the residual of output row tid (tid < rd)
     // Q8_0 activations: NP whole 32-value blocks per thread (one amax and one pair of divisions per
     // block); Q8_K: NP passes of 8 values per thread (32 threads per 256-value block)
     constexpr int NV = QT == kTypeQ8_0 ? 32 : 8;
@@ -822,8 +836,7 @@ __global__ __launch_bounds__(kBlock) void down_combine_kernel(DownCombineParams 
             const float y = ds * s_w[jj];
             acc = jj == 0 ? y : acc + y;
         }
-        const int orow = blockIdx.x * rd + tid;
-        P.out[orow] = acc + P.resid[orow];
+        P.out[blockIdx.x * rd + tid] = acc + resid;
     }
 }
 
@@ -884,7 +897,8 @@ hipError_t launch_route_t(const RouteParams &P, hipStream_t st, const LaunchTimi
     }
     const int n_quant = P.qtype ? std::min(P.T, 256) : 0;
     const int grid = std::max(1, n_route + n_quant);
-    const size_t lds = P.do_route ? (size_t) tt * P.h * 4 : 16;
+    // (a single token's row is staged in LDS by the quantizing work-group too)
+    const size_t lds = std::max(P.do_route ? (size_t) tt * P.h * 4 : (size_t) 16, P.x_raw ? (size_t) P.h * 4 : (size_t) 16);
     if (epw == 1) return launch(route_kernel<GT, NG, 1>, dim3(grid), dim3(kBlock), lds, st, tm, P, n_route, n_quant, tt, ns);
     return launch(route_kernel<GT, NG, kRouteEPWMax>, dim3(grid), dim3(kBlock), lds, st, tm, P, n_route, n_quant, tt, ns);
 }
