@@ -828,13 +828,30 @@ __global__ __launch_bounds__(kBlock) void down_combine_kernel(DownCombineParams 
     }
     __syncthreads();
     if (tid < rd) {
+        // slots 8 at a time, super-blocks up to kDcSb at a time: every LDS read of a batch is issued
+        // before the sums, which keep their order (super-blocks left to right, then slots)
+        constexpr int kDcSb = 8;
         float acc = 0.0f;
-        for (int jj = 0; jj < k; jj++) {
-            const float *pp = part + (jj * rd + tid) * nsbf;
-            float ds = pp[0];
-            for (int s2 = 1; s2 < nsbf; s2++) ds += pp[s2];
-            const float y = ds * s_w[jj];
-            acc = jj == 0 ? y : acc + y;
+        for (int jj0 = 0; jj0 < k; jj0 += 8) {
+            float pv[8][kDcSb], wv[8];
+#pragma unroll
+            for (int u = 0; u < 8; u++) {
+                const int jj = min(jj0 + u, k - 1);
+                const float *pp = part + (jj * rd + tid) * nsbf;
+#pragma unroll
+                for (int s2 = 0; s2 < kDcSb; s2++) pv[u][s2] = pp[min(s2, nsbf - 1)];
+                wv[u] = s_w[jj];
+            }
+#pragma unroll
+            for (int u = 0; u < 8; u++) {
+                const int jj = jj0 + u;
+                float ds = pv[u][0];
+#pragma unroll
+                for (int s2 = 1; s2 < kDcSb; s2++) ds = s2 < nsbf ? ds + pv[u][s2] : ds;
+                for (int s2 = kDcSb; s2 < nsbf; s2++) ds += part[(min(jj, k - 1) * rd + tid) * nsbf + s2];
+                const float y = ds * wv[u];
+                acc = jj < k ? (jj == 0 ? y : acc + y) : acc;
+            }
         }
         P.out[blockIdx.x * rd + tid] = acc + resid;
     }
