@@ -319,11 +319,13 @@ __device__ __forceinline__ GroupLds group_lds(unsigned char *base, int T, int k,
 // takes the block's expert = the y-th expert of rank < k by ascending id, and its pair index
 // j = t * k + rank = rank. Work-group (0, 0) also runs the softmax and stores ids / weights.
 // Returns false when y >= k.
-template <int EPL>
+template <int EPL, int NT>
 __device__ __forceinline__ bool route_one(const GroupParams &P, GroupLds g) {
     const int tid = threadIdx.x, lane = tid % kWave, wave = tid / kWave;
-    // nsplit groups of Ep threads each count over `span` keys (even, so the pairs stay 16-byte aligned)
-    const int E = P.E, Ep = EPL * kWave, nsplit = (int) blockDim.x / Ep, span = ((Ep + nsplit - 1) / nsplit + 1) & ~1;
+    // nsplit groups of Ep threads each count over `span` keys (even, so the pairs stay 16-byte aligned);
+    // all compile-time, so each thread's LDS reads are issued together
+    const int E = P.E;
+    constexpr int Ep = EPL * kWave, nsplit = NT / Ep, span = ((Ep + nsplit - 1) / nsplit + 1) & ~1;
     unsigned long long *s_key = reinterpret_cast<unsigned long long *>(g.scratch + kMaxK * 4); // [Ep]
     int *s_cnt = reinterpret_cast<int *>(s_key + Ep);                                          // [nsplit][Ep]
     float *s_l = reinterpret_cast<float *>(s_cnt + kGuRouteBlock);                             // [Ep]
@@ -338,11 +340,12 @@ __device__ __forceinline__ bool route_one(const GroupParams &P, GroupLds g) {
     if (part < nsplit) {
         const unsigned long long mine = s_key[e];
         const unsigned long long *row = s_key + part * span;
-        const int lim = max(0, min(span, Ep - part * span));
+        const int lim = Ep - part * span; // keys of this group: span, or fewer in the last group
         int c = 0;
-        for (int i = 0; i < lim; i += 2) {
-            const ulonglong2 v = *reinterpret_cast<const ulonglong2 *>(row + i);
-            c += (v.x > mine) + (v.y > mine);
+#pragma unroll
+        for (int i = 0; i < span; i += 2) {
+            const ulonglong2 v = *reinterpret_cast<const ulonglong2 *>(row + min(i, max(lim - 2, 0)));
+            c += i < lim ? (v.x > mine) + (v.y > mine) : 0;
         }
         s_cnt[part * Ep + e] = c;
     }
@@ -390,7 +393,7 @@ __device__ __forceinline__ bool route_one(const GroupParams &P, GroupLds g) {
 // order (the order ggml's CPU mul_mat_id walks experts), work-group y takes the y-th active bin, and
 // its pairs (t, j) in token-major order. Bins out of range are clamped and flagged in *err.
 // Returns false when this work-group has no bin (y >= number of active bins).
-template <bool ROUTE>
+template <bool ROUTE, int NT = kBlock>
 __device__ __forceinline__ bool group_pairs(const GroupParams &P, GroupLds g) {
     const int tid = threadIdx.x, bd = blockDim.x;
     const int lane = tid % kWave, wave = tid / kWave;
@@ -401,9 +404,9 @@ __device__ __forceinline__ bool group_pairs(const GroupParams &P, GroupLds g) {
         // work-group (0, 0) runs the softmax and stores ids / weights for the caller and down
         const int epl = (P.E + kWave - 1) / kWave;
         bool ok;
-        if (epl == 1) ok = route_one<1>(P, g);
-        else if (epl == 2) ok = route_one<2>(P, g);
-        else ok = route_one<4>(P, g);
+        if (epl == 1) ok = route_one<1, NT>(P, g);
+        else if (epl == 2) ok = route_one<2, NT>(P, g);
+        else ok = route_one<4, NT>(P, g);
         return ok;
     } else {
         for (int p = tid; p < np; p += bd) {
@@ -482,7 +485,7 @@ __global__ __launch_bounds__(NT) void gate_up_kernel(GateUpParams P) {
     GroupLds gl = group_lds(smem, P.gp.T, k, P.gp.n_bins, ROUTE);
     // offset from the LDS base (no integer round trip, so the accesses stay ds_read / ds_write)
     unsigned char *work = smem + ((group_lds_bytes(P.gp.T, k, P.gp.n_bins, ROUTE) + 15) & ~size_t(15));
-    if (!group_pairs<ROUTE>(P.gp, gl)) return;
+    if (!group_pairs<ROUTE, NT>(P.gp, gl)) return;
     const int e = gl.misc[0], cnt = gl.misc[1];
     const uint8_t *base = m ? P.w_up + (size_t) e * P.stride_up : P.w_gate + (size_t) e * P.stride_gate;
     const int h32 = h / 32, h16 = h / 16;
