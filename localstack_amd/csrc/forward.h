@@ -39,7 +39,7 @@ struct RopeParams {
     int32_t *cell_seq, *cell_pos; // [kv_size], written for the step's cells
     int T, n_head, n_kv, hd, kv_size;
     float theta_scale; // freq_base^(-2 / hd)
-    float *q_out;      // [T][n_head][hd]
+    uint16_t *q_out;   // [T][n_head][hd] rotated Q rounded to fp16 (attention's Q operand)
     uint16_t *kc, *vc; // this layer's caches
     const float *cs;   // [T][hd / 2][2]: cos and sin of each pair's angle (launch_rope_table), or null
     int ld;            // row stride of q, k and v (floats)
@@ -79,7 +79,7 @@ struct GemvParams {
 // [c * chunk, (c + 1) * chunk), reading each K/V fragment once for all of them. With n_chunk == 1 it
 // writes `out` directly, otherwise partial (max, sum, unnormalised output) rows into `part`.
 struct AttnParams {
-    const float *q; // [T][n_head][hd]
+    const uint16_t *q; // [T][n_head][hd] rotated Q as fp16
     const uint16_t *kc, *vc;
     const int32_t *cell_seq, *cell_pos, *pos;
     int32_t seq;

@@ -156,10 +156,13 @@ __device__ __forceinline__ void rope_head(const RopeParams &P, int t, int j, flo
         }
         const float y0 = x0 * c - x1 * sn;
         const float y1 = x0 * sn + x1 * c;
-        if (is_q) {
-            float *dst = q_dst ? q_dst : P.q_out + ((size_t) t * P.n_head + head) * hd;
-            dst[i] = y0;
-            dst[i + half] = y1;
+        if (is_q && q_dst) {
+            q_dst[i] = y0;
+            q_dst[i + half] = y1;
+        } else if (is_q) {
+            uint16_t *dst = P.q_out + ((size_t) t * P.n_head + head) * hd;
+            dst[i] = f2h(y0);
+            dst[i + half] = f2h(y1);
         } else {
             P.kc[k_index(head, i, cell, hd, P.kv_size)] = f2h(y0);
             P.kc[k_index(head, i + half, cell, hd, P.kv_size)] = f2h(y1);
@@ -615,13 +618,24 @@ __global__ __launch_bounds__(kAtBlock) void attn_kernel(AttnParams P) {
     for (int rt = 0; rt < NRT; rt++) {
         const int r = row0 + rt * 16 + lr;
         const bool on = r < rows;
+        const int rc = on ? r : rows - 1; // rows past the end load the last row (unconditional loads) and use zeros
         // (a RoPE-in launch is one token in one row block: its live rows r < grp are the heads themselves)
-        const float *q = rope_in ? s_q + (on ? r : 0) * HD
-                                               : P.q + ((size_t) (on ? r / grp : 0) * P.n_head + g * grp + (on ? r % grp : 0)) * HD;
+        if (rope_in) {
+            const float *q = s_q + rc * HD;
 #pragma unroll
-        for (int ks = 0; ks < NK; ks++) {
-            const float4 v = on ? *reinterpret_cast<const float4 *>(q + ks * 16 + 4 * lq) : make_float4(0, 0, 0, 0);
-            qa[rt][ks] = half4v{(_Float16) v.x, (_Float16) v.y, (_Float16) v.z, (_Float16) v.w};
+            for (int ks = 0; ks < NK; ks++) {
+                float4 v = *reinterpret_cast<const float4 *>(q + ks * 16 + 4 * lq);
+                v = on ? v : make_float4(0, 0, 0, 0);
+                qa[rt][ks] = half4v{(_Float16) v.x, (_Float16) v.y, (_Float16) v.z, (_Float16) v.w};
+            }
+        } else {
+            // fp16 rows straight into the operand registers (the rotation kernel rounded them)
+            const uint16_t *q = P.q + ((size_t) (rc / grp) * P.n_head + g * grp + rc % grp) * HD;
+#pragma unroll
+            for (int ks = 0; ks < NK; ks++) {
+                const half4v v = ld_half4(q + ks * 16 + 4 * lq);
+                qa[rt][ks] = on ? v : half4v{0, 0, 0, 0};
+            }
         }
     }
     f32x4v O[NRT][DT];
@@ -820,13 +834,15 @@ __global__ __launch_bounds__(kAtBlock) void attn_kernel(AttnParams P) {
 // each in registers (chunks cl, cl + CL, ...; any further ones are read after the factors). Each
 // thread's slices are summed in ascending chunk order, then the CL thread sums in order.
 constexpr int kCombRegs = 16;
+template <int HD>
 __global__ __launch_bounds__(kBlock) void attn_combine_kernel(AttnParams P) {
     extern __shared__ float s_f[]; // [n_chunk] factors, then [kBlock / (hd / 4)][hd] sums
     __shared__ float s_red[kBlock / kWave];
     const int h = blockIdx.x, t = blockIdx.y, tid = threadIdx.x, lane = tid & (kWave - 1), wv = tid / kWave;
-    const int hd = P.hd, n = P.n_chunk, stride = hd + 4;
+    constexpr int hd = HD, stride = hd + 4, nq = hd / 4, CL = kBlock / nq;
+    const int n = P.n_chunk;
     const float *pp = P.part + ((size_t) t * P.n_head + h) * n * stride;
-    const int nq = hd / 4, CL = kBlock / nq, dq = tid % nq, cl = tid / nq;
+    const int dq = tid % nq, cl = tid / nq;
     float4 vr[kCombRegs];
 #pragma unroll
     for (int j = 0; j < kCombRegs; j++) {
@@ -880,6 +896,7 @@ __global__ __launch_bounds__(kBlock) void attn_combine_kernel(AttnParams P) {
     __syncthreads();
     if (tid < hd) {
         float o = 0.0f;
+#pragma unroll
         for (int i = 0; i < CL; i++) o += s_o[i * hd + tid];
         const size_t oi = ((size_t) t * P.n_head + h) * hd + tid;
         P.out[oi] = o / L;
@@ -1064,7 +1081,13 @@ hipError_t launch_attn(const AttnParams &P, hipStream_t st, const LaunchTiming *
 hipError_t launch_attn_combine(const AttnParams &P, hipStream_t st, const LaunchTiming *tm) {
     if (P.T == 0 || P.n_chunk == 1) return hipSuccess;
     const size_t lds = ((size_t) ((P.n_chunk + 3) & ~3) + (size_t) kBlock / (P.hd / 4) * P.hd) * sizeof(float);
-    return launch(attn_combine_kernel, dim3(P.n_head, P.T), dim3(kBlock), lds, st, tm, P);
+    const dim3 grid(P.n_head, P.T), block(kBlock);
+    switch (P.hd) {
+    case 64: return launch(attn_combine_kernel<64>, grid, block, lds, st, tm, P);
+    case 128: return launch(attn_combine_kernel<128>, grid, block, lds, st, tm, P);
+    case 256: return launch(attn_combine_kernel<256>, grid, block, lds, st, tm, P);
+    default: return hipErrorInvalidValue;
+    }
 }
 
 hipError_t launch_fill_kv(const FillKvParams &P, hipStream_t st, const LaunchTiming *tm) {

@@ -171,7 +171,8 @@ struct lstk_model {
     uint16_t *kcache = nullptr, *vcache = nullptr;
     size_t layer_elems = 0; // fp16 values of one layer's K (or V) cache
     int32_t *cell_seq = nullptr, *cell_pos = nullptr;
-    float *x = nullptr, *hn = nullptr, *q = nullptr, *k = nullptr, *v = nullptr, *qr = nullptr, *attn = nullptr,
+    uint16_t *qr = nullptr; // [n_batch][n_head][head_dim] rotated Q, fp16 (the attention's Q operand)
+    float *x = nullptr, *hn = nullptr, *q = nullptr, *k = nullptr, *v = nullptr, *attn = nullptr,
           *part = nullptr, *weights = nullptr;
     int32_t *ids = nullptr, *slots = nullptr, *in = nullptr; // in = tokens | cells | positions
     uint16_t *hn16 = nullptr, *attn16 = nullptr;             // fp16 inputs of the multi-token products
@@ -283,7 +284,7 @@ int create(const lstk_qwen3_hparams *hpp, const lstk_qwen3_weights *w, lstk_pool
         {(void **) &M->x, nb * h * 4},
         {(void **) &M->hn, nb * h * 4},
         {(void **) &M->q, nb * (hq + 2 * hk) * 4},
-        {(void **) &M->qr, nb * hq * 4},
+        {(void **) &M->qr, nb * hq * 2},
         {(void **) &M->attn, nb * hq * 4},
         {(void **) &M->part, part_rows * (hp.head_dim + 4) * 4},
         {(void **) &M->weights, nb * k * 4},
