@@ -17,10 +17,10 @@ bool pool_streaming(const lstk_pool *pool);
 bool pool_dry(const lstk_pool *pool);
 // Whether the pool's bookkeeping lives on the device (LSTK_POOL_DEVICE_LRU).
 bool pool_device_lru(const lstk_pool *pool);
-// lstk_moe_block for one token of a resident pool whose hnorm row the router launch computes itself as
-// rms_norm(x) * norm_w (bit-identical to the RMSNorm kernel's row; also stored to d_hnorm).
+// lstk_moe_block for T tokens of a resident pool whose hnorm rows the router launch computes itself as
+// rms_norm(x) * norm_w (bit-identical to the RMSNorm kernel's rows; also stored to d_hnorm).
 int moe_block_normed(lstk_pool *pool, int layer, const float *d_x, const float *d_norm_w, float eps, float *d_hnorm,
                      const void *d_gate_inp, int gate_type, const float *d_resid, float *d_out, int32_t *d_ids,
-                     float *d_weights, hipStream_t st);
+                     float *d_weights, int T, hipStream_t st);
 
 }  // namespace lstk

@@ -130,7 +130,7 @@ __device__ __forceinline__ void route_tile(const RouteParams &P, int b, float *x
     };
     // the work-group's ns stages of tt tokens: stage s + 1 is loaded into registers while the
     // tokens of stage s are multiplied from LDS
-    if (P.x_raw) {
+    if (P.x_raw && P.T == 1) {
         // one token, normalised here from the raw row while the router rows stream in
         float y[NG];
         norm_row<NG>(P.x_raw, P.norm_w, h, P.eps, y, s_part);
@@ -162,9 +162,29 @@ __device__ __forceinline__ void route_tile(const RouteParams &P, int b, float *x
     }
     unpack();
     const int tbase = tile * tt * ns;
+    // x_raw: the rows are normalised here (ffn_norm), each in the RMSNorm kernel's order (thread i holds
+    // x[i + 256 k], sums (double) (x * x) over k, then the wavefront tree and (w0 + w1) + (w2 + w3)),
+    // so the staged values equal the RMSNorm kernel's output bit for bit
+    constexpr int kR = 32 / NG < 8 ? 32 / NG : 8; // rows of a stage held in registers (tt <= kR)
+    __shared__ double s_rows[kR][kBlock / kWave];
+    float raw[kR][NG], nwv[NG];
     float4 pre[kPre];
+    const bool normed = P.x_raw != nullptr;
+    if (normed) {
+#pragma unroll
+        for (int k = 0; k < NG; k++) nwv[k] = P.norm_w[threadIdx.x + k * kBlock];
+    }
     auto load = [&](int s) {
         const int t0 = tbase + s * tt, nt = max(0, min(tt, P.T - t0));
+        if (normed) {
+#pragma unroll
+            for (int r = 0; r < kR; r++) {
+                const float *src = P.x_raw + (size_t) min(t0 + r, P.T - 1) * h;
+#pragma unroll
+                for (int k = 0; k < NG; k++) raw[r][k] = src[threadIdx.x + k * kBlock];
+            }
+            return;
+        }
         const float4 *src = reinterpret_cast<const float4 *>(P.hnorm + (size_t) t0 * h);
 #pragma unroll
         for (int u = 0; u < kPre; u++) {
@@ -177,20 +197,46 @@ __device__ __forceinline__ void route_tile(const RouteParams &P, int b, float *x
         const int t0 = tbase + s * tt;
         const int nt = min(tt, P.T - t0);
         if (nt <= 0) break;
-        __syncthreads();
-        float4 *dst = reinterpret_cast<float4 *>(xs);
+        if (normed) {
 #pragma unroll
-        for (int u = 0; u < kPre; u++) {
-            const int i = threadIdx.x + u * kBlock;
-            if (i < nt * h / 4) {
-                float4 v = pre[u];
-                if (GT == kTypeF16) {
-                    v.x = round_f16(v.x);
-                    v.y = round_f16(v.y);
-                    v.z = round_f16(v.z);
-                    v.w = round_f16(v.w);
+            for (int r = 0; r < kR; r++) {
+                double sm = 0.0;
+#pragma unroll
+                for (int k = 0; k < NG; k++) sm += (double) (raw[r][k] * raw[r][k]);
+                sm = wave_sum_d(sm);
+                if (lane == 0) s_rows[r][wave] = sm;
+            }
+        }
+        __syncthreads();
+        if (normed) {
+#pragma unroll
+            for (int r = 0; r < kR; r++) {
+                if (r < nt) {
+                    const double tot = (s_rows[r][0] + s_rows[r][1]) + (s_rows[r][2] + s_rows[r][3]);
+                    const float mean = (float) (tot / (double) h);
+                    const float scale = 1.0f / sqrtf(mean + P.eps);
+#pragma unroll
+                    for (int k = 0; k < NG; k++) {
+                        const float y = (raw[r][k] * scale) * nwv[k];
+                        xs[(size_t) r * h + threadIdx.x + k * kBlock] = GT == kTypeF16 ? round_f16(y) : y;
+                    }
                 }
-                dst[i] = v;
+            }
+        } else {
+            float4 *dst = reinterpret_cast<float4 *>(xs);
+#pragma unroll
+            for (int u = 0; u < kPre; u++) {
+                const int i = threadIdx.x + u * kBlock;
+                if (i < nt * h / 4) {
+                    float4 v = pre[u];
+                    if (GT == kTypeF16) {
+                        v.x = round_f16(v.x);
+                        v.y = round_f16(v.y);
+                        v.z = round_f16(v.z);
+                        v.w = round_f16(v.w);
+                    }
+                    dst[i] = v;
+                }
             }
         }
         __syncthreads();
@@ -232,18 +278,23 @@ __global__ __launch_bounds__(kBlock) void route_kernel(RouteParams P, int n_rout
     } else if (P.qtype != 0) {
         const int h = P.h;
         if (P.x_raw) {
-            // one token: this work-group normalises the row, quantizes it from LDS, and stores it
-            float y[NG];
-            norm_row<NG>(P.x_raw, P.norm_w, h, P.eps, y, s_part);
+            // this work-group's tokens: each row normalised, quantized from LDS, and stored
+            for (int t = b - n_route_wg; t < P.T; t += n_quant_wg) {
+                float y[NG];
+                norm_row<NG>(P.x_raw + (size_t) t * h, P.norm_w, h, P.eps, y, s_part);
 #pragma unroll
-            for (int k = 0; k < NG; k++) lds[threadIdx.x + k * kBlock] = y[k];
-            __syncthreads();
-            if (P.qtype == kTypeQ8_0)
-                quantize_row<kTypeQ8_0>(lds, h, P.xq.qs, P.xq.d, P.xq.bs);
-            else
-                quantize_row<kTypeQ4_K>(lds, h, P.xq.qs, P.xq.d, P.xq.bs);
+                for (int k = 0; k < NG; k++) lds[threadIdx.x + k * kBlock] = y[k];
+                __syncthreads();
+                if (P.qtype == kTypeQ8_0)
+                    quantize_row<kTypeQ8_0>(lds, h, P.xq.qs + (size_t) t * h, P.xq.d + (size_t) t * (h / 32),
+                                            P.xq.bs + (size_t) t * (h / 32));
+                else
+                    quantize_row<kTypeQ4_K>(lds, h, P.xq.qs + (size_t) t * h, P.xq.d + (size_t) t * (h / 32),
+                                            P.xq.bs + (size_t) t * (h / 32));
 #pragma unroll
-            for (int k = 0; k < NG; k++) P.hnorm_out[threadIdx.x + k * kBlock] = y[k];
+                for (int k = 0; k < NG; k++) P.hnorm_out[(size_t) t * h + threadIdx.x + k * kBlock] = y[k];
+                __syncthreads(); // the row's LDS and s_part are reused by the next token
+            }
             return;
         }
         for (int t = b - n_route_wg; t < P.T; t += n_quant_wg) {
@@ -905,8 +956,8 @@ size_t align16(size_t x) { return (x + 15) / 16 * 16; }
 
 template <int GT, int NG>
 hipError_t launch_route_t(const RouteParams &P, hipStream_t st, const LaunchTiming *tm) {
-    // the in-launch normalisation serves one token and needs the quantizing work-group to store the row
-    if (P.x_raw && (P.T != 1 || !P.norm_w || !P.hnorm_out || !P.qtype)) return hipErrorInvalidValue;
+    // the in-launch normalisation needs the quantizing work-groups to store the rows
+    if (P.x_raw && (!P.norm_w || !P.hnorm_out || !P.qtype)) return hipErrorInvalidValue;
     int n_route = 0, tt = 1, ns = 1;
     const int epw = P.T == 1 ? 1 : kRouteEPWMax;
     if (P.do_route) {
