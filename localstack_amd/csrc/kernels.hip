@@ -365,10 +365,10 @@ __device__ __forceinline__ GroupLds group_lds(unsigned char *base, int T, int k,
 // Single-token routing inside an expert work-group (route mode). Every expert e < E gets a unique
 // 64-bit key (select_key(logit) << 8 | 255 - e: larger logit first, ties to the lower id) in LDS;
 // the work-group's threads count, in parallel, how many keys exceed each expert's key (expert
-// t % Ep against a 1 / (256 / Ep) share of the row, Ep = E rounded up to 64), so rank = that count
-// is the position in the descending selection order of rank_token / the oracle. Wavefront 0 then
+// t % Ep against a 1 / (NT / Ep) share of the row, Ep = E rounded up to 64), so rank = that count
+// is the position in the descending selection order of rank_token / the oracle. Every wavefront then
 // takes the block's expert = the y-th expert of rank < k by ascending id, and its pair index
-// j = t * k + rank = rank. Work-group (0, 0) also runs the softmax and stores ids / weights.
+// j = t * k + rank = rank. Wavefront 0 of work-group (0, 0) also runs the softmax and stores ids / weights.
 // Returns false when y >= k.
 template <int EPL, int NT>
 __device__ __forceinline__ bool route_one(const GroupParams &P, GroupLds g) {
@@ -401,7 +401,9 @@ __device__ __forceinline__ bool route_one(const GroupParams &P, GroupLds g) {
         s_cnt[part * Ep + e] = c;
     }
     __syncthreads();
-    if (wave == 0) {
+    // every wavefront makes the (identical) selection itself and keeps it in LDS for its own reads, so no
+    // barrier follows
+    {
         float l[EPL];
         bool valid[EPL];
         int rank[EPL];
@@ -414,7 +416,7 @@ __device__ __forceinline__ bool route_one(const GroupParams &P, GroupLds g) {
             for (int q = 0; q < nsplit; q++) r += s_cnt[q * Ep + ee];
             rank[i] = valid[i] ? r : INT_MAX;
         }
-        if (blockIdx.x == 0 && blockIdx.y == 0)
+        if (wave == 0 && blockIdx.x == 0 && blockIdx.y == 0)
             weights_token<EPL>(P.k, l, valid, rank, s_p, nullptr, nullptr, nullptr, P.ids_out, P.weights_out);
         const int y = blockIdx.y;
         int ex = -1, j = 0, cum = 0;
@@ -435,9 +437,8 @@ __device__ __forceinline__ bool route_one(const GroupParams &P, GroupLds g) {
             g.misc[1] = ex >= 0 ? 1 : 0;
             g.list[0] = j;
         }
+        return ex >= 0;
     }
-    __syncthreads();
-    return g.misc[0] >= 0;
 }
 
 // Every work-group derives the same grouping from the same routing: the active bins in ascending
