@@ -86,7 +86,9 @@ __device__ __forceinline__ void norm_row(const float *x, const float *wn, int n,
 // logits agree bit for bit and so does the top-k. F16 weights see fp16-rounded activations, as
 // ggml's CPU mul_mat converts src1 to the F16 vec_dot_type (src/qwen3.cpp:178).
 // The wavefront's kRouteEPW weight rows are loaded before the activations are staged.
-template <int GT, int NG, int kRouteEPW>
+// NR: the staged rows are normalised here from P.x_raw (an instantiation of its own: the extra state
+// would cost the plain one registers)
+template <int GT, int NG, int kRouteEPW, bool NR>
 __device__ __forceinline__ void route_tile(const RouteParams &P, int b, float *xs, int tt, int ns, double *s_part) {
     constexpr int kRouteEG = 4 * kRouteEPW;
     const int n_eg = (P.E + kRouteEG - 1) / kRouteEG;
@@ -165,31 +167,31 @@ __device__ __forceinline__ void route_tile(const RouteParams &P, int b, float *x
     // x_raw: the rows are normalised here (ffn_norm), each in the RMSNorm kernel's order (thread i holds
     // x[i + 256 k], sums (double) (x * x) over k, then the wavefront tree and (w0 + w1) + (w2 + w3)),
     // so the staged values equal the RMSNorm kernel's output bit for bit
-    constexpr int kR = 32 / NG < 8 ? 32 / NG : 8; // rows of a stage held in registers (tt <= kR)
+    constexpr int kR = NR ? (32 / NG < 8 ? 32 / NG : 8) : 1; // rows of a stage held in registers (tt <= kR)
     __shared__ double s_rows[kR][kBlock / kWave];
-    float raw[kR][NG], nwv[NG];
-    float4 pre[kPre];
-    const bool normed = P.x_raw != nullptr;
-    if (normed) {
+    float raw[kR][NR ? NG : 1], nwv[NR ? NG : 1];
+    float4 pre[NR ? 1 : kPre];
+    constexpr bool normed = NR;
+    if constexpr (normed) {
 #pragma unroll
         for (int k = 0; k < NG; k++) nwv[k] = P.norm_w[threadIdx.x + k * kBlock];
     }
     auto load = [&](int s) {
         const int t0 = tbase + s * tt, nt = max(0, min(tt, P.T - t0));
-        if (normed) {
+        if constexpr (normed) {
 #pragma unroll
             for (int r = 0; r < kR; r++) {
                 const float *src = P.x_raw + (size_t) min(t0 + r, P.T - 1) * h;
 #pragma unroll
                 for (int k = 0; k < NG; k++) raw[r][k] = src[threadIdx.x + k * kBlock];
             }
-            return;
-        }
-        const float4 *src = reinterpret_cast<const float4 *>(P.hnorm + (size_t) t0 * h);
+        } else {
+            const float4 *src = reinterpret_cast<const float4 *>(P.hnorm + (size_t) t0 * h);
 #pragma unroll
-        for (int u = 0; u < kPre; u++) {
-            const int i = threadIdx.x + u * kBlock;
-            if (i < nt * h / 4) pre[u] = src[i];
+            for (int u = 0; u < kPre; u++) {
+                const int i = threadIdx.x + u * kBlock;
+                if (i < nt * h / 4) pre[u] = src[i];
+            }
         }
     };
     load(0);
@@ -197,7 +199,7 @@ __device__ __forceinline__ void route_tile(const RouteParams &P, int b, float *x
         const int t0 = tbase + s * tt;
         const int nt = min(tt, P.T - t0);
         if (nt <= 0) break;
-        if (normed) {
+        if constexpr (normed) {
 #pragma unroll
             for (int r = 0; r < kR; r++) {
                 double sm = 0.0;
@@ -208,7 +210,7 @@ __device__ __forceinline__ void route_tile(const RouteParams &P, int b, float *x
             }
         }
         __syncthreads();
-        if (normed) {
+        if constexpr (normed) {
 #pragma unroll
             for (int r = 0; r < kR; r++) {
                 if (r < nt) {
@@ -241,40 +243,51 @@ __device__ __forceinline__ void route_tile(const RouteParams &P, int b, float *x
         }
         __syncthreads();
         if (s + 1 < ns) load(s + 1);
-        for (int t = 0; t < nt; t++) {
-            float acc[kRouteEPW];
+        // two tokens per iteration (the second one's row clamped to the first when nt is odd and its
+        // logits not stored): twice the independent chains, each (token, expert) sum in the same order
+        for (int t = 0; t < nt; t += 2) {
+            const int t2 = min(t + 1, nt - 1);
+            float acc[2][kRouteEPW];
 #pragma unroll
-            for (int ee = 0; ee < kRouteEPW; ee++) acc[ee] = 0.0f;
+            for (int u = 0; u < 2; u++)
+#pragma unroll
+                for (int ee = 0; ee < kRouteEPW; ee++) acc[u][ee] = 0.0f;
 #pragma unroll
             for (int g = 0; g < NG; g++) {
-                {
-                    const float4 x = *reinterpret_cast<const float4 *>(xs + (size_t) t * h + 256 * g + 4 * lane);
+                const float4 xa = *reinterpret_cast<const float4 *>(xs + (size_t) t * h + 256 * g + 4 * lane);
+                const float4 xb = *reinterpret_cast<const float4 *>(xs + (size_t) t2 * h + 256 * g + 4 * lane);
 #pragma unroll
-                    for (int ee = 0; ee < kRouteEPW; ee++) {
-                        acc[ee] = fmaf(x.x, w[ee][g][0], acc[ee]);
-                        acc[ee] = fmaf(x.y, w[ee][g][1], acc[ee]);
-                        acc[ee] = fmaf(x.z, w[ee][g][2], acc[ee]);
-                        acc[ee] = fmaf(x.w, w[ee][g][3], acc[ee]);
-                    }
+                for (int ee = 0; ee < kRouteEPW; ee++) {
+                    acc[0][ee] = fmaf(xa.x, w[ee][g][0], acc[0][ee]);
+                    acc[1][ee] = fmaf(xb.x, w[ee][g][0], acc[1][ee]);
+                    acc[0][ee] = fmaf(xa.y, w[ee][g][1], acc[0][ee]);
+                    acc[1][ee] = fmaf(xb.y, w[ee][g][1], acc[1][ee]);
+                    acc[0][ee] = fmaf(xa.z, w[ee][g][2], acc[0][ee]);
+                    acc[1][ee] = fmaf(xb.z, w[ee][g][2], acc[1][ee]);
+                    acc[0][ee] = fmaf(xa.w, w[ee][g][3], acc[0][ee]);
+                    acc[1][ee] = fmaf(xb.w, w[ee][g][3], acc[1][ee]);
                 }
             }
 #pragma unroll
-            for (int ee = 0; ee < kRouteEPW; ee++) {
-                const int e = eg * kRouteEG + wave * kRouteEPW + ee;
-                const float sum = wave_sum_tree(acc[ee]);
-                if (lane == 0 && e < P.E) P.logits[(size_t) (t0 + t) * P.E + e] = sum;
+            for (int u = 0; u < 2; u++) {
+#pragma unroll
+                for (int ee = 0; ee < kRouteEPW; ee++) {
+                    const int e = eg * kRouteEG + wave * kRouteEPW + ee;
+                    const float sum = wave_sum_tree(acc[u][ee]);
+                    if (lane == 0 && e < P.E && t + u < nt) P.logits[(size_t) (t0 + t + u) * P.E + e] = sum;
+                }
             }
         }
     }
 }
 
-template <int GT, int NG, int EPW>
+template <int GT, int NG, int EPW, bool NR>
 __global__ __launch_bounds__(kBlock) void route_kernel(RouteParams P, int n_route_wg, int n_quant_wg, int route_tt, int route_ns) {
     extern __shared__ __align__(16) float lds[];
     __shared__ double s_part[kBlock / kWave];
     const int b = blockIdx.x;
     if (b < n_route_wg) {
-        route_tile<GT, NG, EPW>(P, b, lds, route_tt, route_ns, s_part);
+        route_tile<GT, NG, EPW, NR>(P, b, lds, route_tt, route_ns, s_part);
     } else if (P.qtype != 0) {
         const int h = P.h;
         if (P.x_raw) {
@@ -971,8 +984,10 @@ hipError_t launch_route_t(const RouteParams &P, hipStream_t st, const LaunchTimi
     const int grid = std::max(1, n_route + n_quant);
     // (a single token's row is staged in LDS by the quantizing work-group too)
     const size_t lds = std::max(P.do_route ? (size_t) tt * P.h * 4 : (size_t) 16, P.x_raw ? (size_t) P.h * 4 : (size_t) 16);
-    if (epw == 1) return launch(route_kernel<GT, NG, 1>, dim3(grid), dim3(kBlock), lds, st, tm, P, n_route, n_quant, tt, ns);
-    return launch(route_kernel<GT, NG, kRouteEPWMax>, dim3(grid), dim3(kBlock), lds, st, tm, P, n_route, n_quant, tt, ns);
+    if (epw == 1) return launch(route_kernel<GT, NG, 1, false>, dim3(grid), dim3(kBlock), lds, st, tm, P, n_route, n_quant, tt, ns);
+    if (P.x_raw)
+        return launch(route_kernel<GT, NG, kRouteEPWMax, true>, dim3(grid), dim3(kBlock), lds, st, tm, P, n_route, n_quant, tt, ns);
+    return launch(route_kernel<GT, NG, kRouteEPWMax, false>, dim3(grid), dim3(kBlock), lds, st, tm, P, n_route, n_quant, tt, ns);
 }
 
 template <int GT>
