@@ -243,39 +243,28 @@ __device__ __forceinline__ void route_tile(const RouteParams &P, int b, float *x
         }
         __syncthreads();
         if (s + 1 < ns) load(s + 1);
-        // two tokens per iteration (the second one's row clamped to the first when nt is odd and its
-        // logits not stored): twice the independent chains, each (token, expert) sum in the same order
-        for (int t = 0; t < nt; t += 2) {
-            const int t2 = min(t + 1, nt - 1);
-            float acc[2][kRouteEPW];
+        for (int t = 0; t < nt; t++) {
+            float acc[kRouteEPW];
 #pragma unroll
-            for (int u = 0; u < 2; u++)
-#pragma unroll
-                for (int ee = 0; ee < kRouteEPW; ee++) acc[u][ee] = 0.0f;
+            for (int ee = 0; ee < kRouteEPW; ee++) acc[ee] = 0.0f;
 #pragma unroll
             for (int g = 0; g < NG; g++) {
-                const float4 xa = *reinterpret_cast<const float4 *>(xs + (size_t) t * h + 256 * g + 4 * lane);
-                const float4 xb = *reinterpret_cast<const float4 *>(xs + (size_t) t2 * h + 256 * g + 4 * lane);
+                {
+                    const float4 x = *reinterpret_cast<const float4 *>(xs + (size_t) t * h + 256 * g + 4 * lane);
 #pragma unroll
-                for (int ee = 0; ee < kRouteEPW; ee++) {
-                    acc[0][ee] = fmaf(xa.x, w[ee][g][0], acc[0][ee]);
-                    acc[1][ee] = fmaf(xb.x, w[ee][g][0], acc[1][ee]);
-                    acc[0][ee] = fmaf(xa.y, w[ee][g][1], acc[0][ee]);
-                    acc[1][ee] = fmaf(xb.y, w[ee][g][1], acc[1][ee]);
-                    acc[0][ee] = fmaf(xa.z, w[ee][g][2], acc[0][ee]);
-                    acc[1][ee] = fmaf(xb.z, w[ee][g][2], acc[1][ee]);
-                    acc[0][ee] = fmaf(xa.w, w[ee][g][3], acc[0][ee]);
-                    acc[1][ee] = fmaf(xb.w, w[ee][g][3], acc[1][ee]);
+                    for (int ee = 0; ee < kRouteEPW; ee++) {
+                        acc[ee] = fmaf(x.x, w[ee][g][0], acc[ee]);
+                        acc[ee] = fmaf(x.y, w[ee][g][1], acc[ee]);
+                        acc[ee] = fmaf(x.z, w[ee][g][2], acc[ee]);
+                        acc[ee] = fmaf(x.w, w[ee][g][3], acc[ee]);
+                    }
                 }
             }
 #pragma unroll
-            for (int u = 0; u < 2; u++) {
-#pragma unroll
-                for (int ee = 0; ee < kRouteEPW; ee++) {
-                    const int e = eg * kRouteEG + wave * kRouteEPW + ee;
-                    const float sum = wave_sum_tree(acc[u][ee]);
-                    if (lane == 0 && e < P.E && t + u < nt) P.logits[(size_t) (t0 + t + u) * P.E + e] = sum;
-                }
+            for (int ee = 0; ee < kRouteEPW; ee++) {
+                const int e = eg * kRouteEG + wave * kRouteEPW + ee;
+                const float sum = wave_sum_tree(acc[ee]);
+                if (lane == 0 && e < P.E) P.logits[(size_t) (t0 + t) * P.E + e] = sum;
             }
         }
     }
