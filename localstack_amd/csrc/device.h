@@ -53,20 +53,23 @@ __device__ __forceinline__ float h2f(unsigned h) { return __half2float(__ushort_
 __device__ __forceinline__ float round_f16(float x) { return __half2float(__float2half_rn(x)); }
 
 // ------------------------------------------------------------------------------------------------
-// wavefront reductions without LDS: DPP within 16-lane rows, readlane across rows
+// wavefront reductions without LDS: DPP within 16-lane rows, then DPP row broadcasts across rows
 // ------------------------------------------------------------------------------------------------
 
-template <int CTRL>
+// DPP move of v by control CTRL into the rows set in ROWS (the other rows get 0)
+template <int CTRL, int ROWS = 0xF>
 __device__ __forceinline__ float dpp_f(float v) {
-    return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xF, 0xF, false));
+    return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, ROWS, 0xF, false));
 }
-template <int CTRL>
+template <int CTRL, int ROWS = 0xF>
 __device__ __forceinline__ double dpp_d(double v) {
     const unsigned long long u = __builtin_bit_cast(unsigned long long, v);
-    const int lo = __builtin_amdgcn_update_dpp(0, (int) (u & 0xffffffffu), CTRL, 0xF, 0xF, false);
-    const int hi = __builtin_amdgcn_update_dpp(0, (int) (u >> 32), CTRL, 0xF, 0xF, false);
+    const int lo = __builtin_amdgcn_update_dpp(0, (int) (u & 0xffffffffu), CTRL, ROWS, 0xF, false);
+    const int hi = __builtin_amdgcn_update_dpp(0, (int) (u >> 32), CTRL, ROWS, 0xF, false);
     return __builtin_bit_cast(double, ((unsigned long long) (unsigned) hi << 32) | (unsigned) lo);
 }
+constexpr int kDppRowBcast15 = 0x142; // each row receives lane 15 of the row before it
+constexpr int kDppRowBcast31 = 0x143; // rows 2 and 3 receive lane 31
 __device__ __forceinline__ float readlane_f(float v, int l) {
     return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), l));
 }
@@ -78,14 +81,18 @@ __device__ __forceinline__ double readlane_d(double v, int l) {
 }
 
 // Sum over the 64 lanes as a pairwise tree: lanes l and l^1, then quads, octets, halves of rows,
-// rows (0+1, 2+3) and the two row pairs. IEEE addition is commutative, so every lane of a level
-// holds the same partial; the oracle evaluates the same tree. Result uniform.
+// rows (0+1, 2+3) and the two row pairs, i.e. (r0 + r1) + (r2 + r3) of the four row sums. IEEE addition
+// is commutative, so every lane of a level holds the same partial; the oracle evaluates the same tree.
+// The rows meet by broadcasts: row 1 adds row 0 and row 3 adds row 2 (row_bcast:15), then row 3 adds
+// row 1 (row_bcast:31), so lane 63 holds (r3 + r2) + (r1 + r0), the same value. Result uniform.
 __device__ __forceinline__ float wave_sum_tree(float v) {
     v = v + dpp_f<0xB1>(v);   // quad_perm [1,0,3,2]
     v = v + dpp_f<0x4E>(v);   // quad_perm [2,3,0,1]
     v = v + dpp_f<0x141>(v);  // row_half_mirror: the other quad of the octet
     v = v + dpp_f<0x140>(v);  // row_mirror: the other octet of the row
-    return (readlane_f(v, 0) + readlane_f(v, 16)) + (readlane_f(v, 32) + readlane_f(v, 48));
+    v = v + dpp_f<kDppRowBcast15, 0xA>(v);
+    v = v + dpp_f<kDppRowBcast31, 0x8>(v);
+    return readlane_f(v, 63);
 }
 
 __device__ __forceinline__ double wave_sum_d(double v) {
@@ -93,7 +100,9 @@ __device__ __forceinline__ double wave_sum_d(double v) {
     v = v + dpp_d<0x4E>(v);
     v = v + dpp_d<0x141>(v);
     v = v + dpp_d<0x140>(v);
-    return (readlane_d(v, 0) + readlane_d(v, 16)) + (readlane_d(v, 32) + readlane_d(v, 48));
+    v = v + dpp_d<kDppRowBcast15, 0xA>(v);
+    v = v + dpp_d<kDppRowBcast31, 0x8>(v);
+    return readlane_d(v, 63);
 }
 
 __device__ __forceinline__ float wave_max(float v) {
@@ -101,7 +110,9 @@ __device__ __forceinline__ float wave_max(float v) {
     v = fmaxf(v, dpp_f<0x4E>(v));
     v = fmaxf(v, dpp_f<0x141>(v));
     v = fmaxf(v, dpp_f<0x140>(v));
-    return fmaxf(fmaxf(readlane_f(v, 0), readlane_f(v, 16)), fmaxf(readlane_f(v, 32), readlane_f(v, 48)));
+    v = fmaxf(v, dpp_f<kDppRowBcast15, 0xA>(v));
+    v = fmaxf(v, dpp_f<kDppRowBcast31, 0x8>(v));
+    return readlane_f(v, 63);
 }
 
 // ------------------------------------------------------------------------------------------------
