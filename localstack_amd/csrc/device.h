@@ -124,9 +124,18 @@ __device__ __forceinline__ float wave_max(float v) {
 // Q8_K (QT 12): max = the signed value of the first largest |x| of the 256, iscale = -127/max,
 // q = min(127, rne(iscale x)), d = 1/iscale; groups of 32 threads; bs = sums of 32-value groups.
 // Every thread runs the shuffles; threads past the end contribute zeros and write nothing.
-// One pass of the quantizer: this thread's 8 values v at i0 (on = i0 < n).
+// A group sum s (|s| <= 4096) as two fp16 values, both exact: 64 floor(s / 64) in the low half and
+// s mod 64 in the high half, which add up to s. Products of either with integers below 64, and sums
+// of a few dozen such products, are integers below 2^24, so f32 holds them exactly.
+__device__ __forceinline__ unsigned split_sum_f16(int s) {
+    return __builtin_bit_cast(unsigned, __builtin_amdgcn_cvt_pkrtz((float) (s & ~63), (float) (s & 63)));
+}
+
+// One pass of the quantizer: this thread's 8 values v at i0 (on = i0 < n). bh, when non-null, also
+// receives the group sums as split_sum_f16.
 template <int QT>
-__device__ __forceinline__ void quantize8(const float (&v)[8], int i0, bool on, int8_t *qs, float *d, int32_t *bs) {
+__device__ __forceinline__ void quantize8(const float (&v)[8], int i0, bool on, int8_t *qs, float *d, int32_t *bs,
+                                          uint32_t *bh = nullptr) {
     int q[8];
     float dd;
     if (QT == kTypeQ8_0) {
@@ -200,12 +209,14 @@ __device__ __forceinline__ void quantize8(const float (&v)[8], int i0, bool on, 
         if ((threadIdx.x & 3) == 0) {
             d[i0 / 32] = dd;
             bs[i0 / 32] = s;
+            if (bh) bh[i0 / 32] = split_sum_f16(s);
         }
     }
 }
 
 template <int QT>
-__device__ __forceinline__ void quantize_row(const float *__restrict__ x, int n, int8_t *qs, float *d, int32_t *bs) {
+__device__ __forceinline__ void quantize_row(const float *__restrict__ x, int n, int8_t *qs, float *d, int32_t *bs,
+                                             uint32_t *bh = nullptr) {
     for (int base = 0; base < n; base += blockDim.x * 8) {
         const int i0 = base + threadIdx.x * 8;
         const bool on = i0 < n;
@@ -219,7 +230,7 @@ __device__ __forceinline__ void quantize_row(const float *__restrict__ x, int n,
 #pragma unroll
             for (int j = 0; j < 8; j++) v[j] = 0.0f;
         }
-        quantize8<QT>(v, i0, on, qs, d, bs);
+        quantize8<QT>(v, i0, on, qs, d, bs, bh);
     }
 }
 

@@ -12,10 +12,12 @@
 // Integer semantics of ggml's vec_dot_q4_K_q8_K on the matrix cores. Per super-block of 256 values
 // ggml computes d_x (d_w isum - dmin_w imin) with isum = sum_j sc_j sum_i q_ji x_ji (q in [0, 15],
 // sc_j and m_j 6-bit) and imin = sum_j m_j sum_i x_ji. sc_j q does not fit int8, so sc_j is split as
-// 8 sh_j + sl_j (both <= 7) and three int8 weight planes go through the MFMA with the same int8
-// activations: sh_j q, sl_j q (both <= 105) and m_j. Then isum = 8 accH + accL and imin = accM,
-// exactly as in ggml's integer arithmetic; only the f32 accumulation over super-blocks is ordered
-// differently.
+// 8 sh_j + sl_j (both <= 7) and two int8 weight planes go through v_mfma_i32_32x32x32_i8 with the
+// int8 activations: sh_j q and sl_j q (both <= 105); isum = 8 accH + accL. imin is one
+// v_mfma_f32_32x32x16_f16 per super-block over the activations' group sums s_j, each given as the
+// fp16 pair (64 floor(s_j / 64), s_j mod 64) (the quantizer writes them), against (m_j, m_j): every
+// product and partial sum is an integer below 2^24, so the f32 result is imin exactly. Both match
+// ggml's integer arithmetic; only the f32 accumulation over super-blocks is ordered differently.
 #include "device.h"
 #include "formats.h"
 #include "kernels.h"
@@ -27,6 +29,9 @@ namespace {
 
 typedef int i32x4 __attribute__((ext_vector_type(4)));
 typedef int i32x16 __attribute__((ext_vector_type(16)));
+typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef unsigned short u16x2 __attribute__((ext_vector_type(2)));
 
 constexpr int kGThreads = 256;        // 4 wavefronts per grouped work-group
@@ -36,6 +41,10 @@ constexpr int kPermMaxPairs = 8192;
 
 __device__ __forceinline__ i32x16 mfma_i8(i32x4 a, i32x4 b, i32x16 c) {
     return __builtin_amdgcn_mfma_i32_32x32x32_i8(a, b, c, 0, 0, 0);
+}
+__device__ __forceinline__ f32x16 mfma_f16(u32x4 a, u32x4 b) {
+    const f32x16 z = {};
+    return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, a), __builtin_bit_cast(f16x8, b), z, 0, 0, 0);
 }
 
 // Byte-wise product of four values <= 15 with s <= 7 (s2 = s | s << 16): the products stay below
@@ -183,8 +192,9 @@ __global__ __launch_bounds__(kPermThreads) void permute_kernel(PermuteParams P) 
 //       16 t + (p ^ (t & 15)), so 16 consecutive rows reading one piece hit 16 different bank groups;
 //   DX  [kGroupedChunk] f32: the rows' Q8_K scales;
 //   W   [4 wavefronts][9 chunks][32 rows][16 B]: each wavefront's Q4_K rows.
-// Everything arrives by global_load_lds (lane i of an instruction lands at ldsptr + size * i), so the
-// staging holds no registers. Per stage, wavefront 0 issues kLoads0 loads and the others kLoads1.
+// The activation rows, their scales and the weight rows arrive by global_load_lds (lane i of an
+// instruction lands at ldsptr + size * i); each lane also loads its 16 bytes of the rows' split group
+// sums into registers. Per stage, wavefront 0 issues kLoads0 loads and the others kLoads1.
 #ifndef LSTK_GROUPED_STAGES
 #define LSTK_GROUPED_STAGES 2
 #endif
@@ -195,7 +205,7 @@ constexpr int kABytes = kGroupedChunk * 256;
 constexpr int kDXBytes = kGroupedChunk * 4;
 constexpr int kWWaveBytes = 9 * 32 * 16;
 constexpr int kStageBytes = kABytes + kDXBytes + 4 * kWWaveBytes;
-constexpr int kLoads1 = kAInstr + 5, kLoads0 = kLoads1 + 1;
+constexpr int kLoads1 = kAInstr + 5 + kMT, kLoads0 = kLoads1 + 1;
 constexpr size_t kGLdsBytes = (size_t) kNS * kStageBytes + 2 * kGroupedChunk * 4;
 
 typedef __attribute__((address_space(3))) void lds_void;
@@ -226,9 +236,10 @@ __device__ __forceinline__ GLds g_lds(unsigned char *base) {
 }
 
 // Per-lane byte offsets of a work item's loads (fixed over the super-blocks, so the loop only moves
-// the wave-uniform bases): kAInstr activation pieces, the row scale, 5 weight chunk pairs.
+// the wave-uniform bases): kAInstr activation pieces, the row scale, 5 weight chunk pairs, and per
+// M-tile the split group sums 4 (lane / 32) .. + 3 of row 32 mt + lane % 32.
 struct DmaOffs {
-    unsigned a[kAInstr], dx, w[5];
+    unsigned a[kAInstr], dx, w[5], bh[kMT];
     unsigned live; // bit i: activation piece i is a real row of the chunk (t < n); bit 31: the lane's scale is
 };
 
@@ -250,13 +261,16 @@ __device__ __forceinline__ DmaOffs dma_offsets(const GroupedParams &P, const GLd
         const int c = min(2 * i + (lane >> 5), 8);
         o.w[i] = (unsigned) chunk_offset(kChunksQ4_K, P.rows, 0, c, row0 + (lane & 31));
     }
+#pragma unroll
+    for (int mt = 0; mt < kMT; mt++)
+        o.bh[mt] = ((unsigned) g.src[min(32 * mt + (lane & 31), n - 1)] * (unsigned) (P.K / 32) + 4 * (lane >> 5)) * 4;
     return o;
 }
 
 // Issues the loads of super-block sb (activation rows of the chunk, the wavefront's 32 weight rows
-// of matrix w) into ring stage `slot`.
+// of matrix w) into ring stage `slot`, and the lane's split group sums into bq.
 __device__ __forceinline__ void issue_stage(const GroupedParams &P, const GLds &g, const DmaOffs &o, const uint8_t *w,
-                                            int sb, int slot) {
+                                            int sb, int slot, u32x4 (&bq)[kMT]) {
     const int wave = threadIdx.x / kWave, lane = threadIdx.x % kWave;
     unsigned char *st = g.ring + (size_t) slot * kStageBytes;
     const uint8_t *xa = reinterpret_cast<const uint8_t *>(P.xqs) + sb * 256;
@@ -271,16 +285,22 @@ __device__ __forceinline__ void issue_stage(const GroupedParams &P, const GLds &
 #pragma unroll
     for (int i = 0; i < 4; i++) dma16(wb + o.w[i], wl + i * 1024);
     if (lane < 32) dma16(wb + o.w[4], wl + 4 * 1024);
+    const uint8_t *xb = reinterpret_cast<const uint8_t *>(P.xbh) + sb * 32;
+#pragma unroll
+    for (int mt = 0; mt < kMT; mt++) bq[mt] = *reinterpret_cast<const u32x4 *>(xb + o.bh[mt]);
 }
 
 // Multiplies one staged super-block: the wavefront's 32 weight rows (lane % 32) with the chunk's
 // rows (M-tile mt = rows 32 mt .. 32 mt + 31), adding d_x (d_w isum - dmin_w imin) to acc[mt][r] for
-// chunk row 32 mt + 8 (r / 4) + 4 (lane / 32) + r % 4.
+// chunk row 32 mt + 8 (r / 4) + 4 (lane / 32) + r % 4. bq[mt]: the lane's split group sums
+// (sub-blocks 4 (lane / 32) .. + 3 of chunk row 32 mt + lane % 32).
 //
 // Lane half h = lane / 32 takes qs bytes [32 c + 16 h, + 16) of each 64-value chunk c of its row:
 // low nibbles are values 64 c + 16 h + [0, 16) of sub-block 2 c, high nibbles values
 // 64 c + 32 + 16 h + [0, 16) of sub-block 2 c + 1, exactly the K slice the MFMA takes from the lane.
-__device__ __forceinline__ void q4k_superblock(const unsigned char *st, int n, float (&acc)[kMT][16]) {
+// In the imin product, lane half h gives K entries 8 h .. 8 h + 7, the pairs of sub-blocks 4 h .. + 3.
+__device__ __forceinline__ void q4k_superblock(const unsigned char *st, int n, const u32x4 (&bq)[kMT],
+                                               float (&acc)[kMT][16]) {
     const int wave = threadIdx.x / kWave, lane = threadIdx.x % kWave, h = lane / 32, r32 = lane % 32;
     const unsigned char *wl = st + kABytes + kDXBytes + wave * kWWaveBytes;
     const uint4 hdr = *reinterpret_cast<const uint4 *>(wl + r32 * 16);
@@ -289,29 +309,25 @@ __device__ __forceinline__ void q4k_superblock(const unsigned char *st, int n, f
     for (int c = 0; c < 4; c++) qv[c] = *reinterpret_cast<const uint4 *>(wl + (1 + 2 * c + h) * 512 + r32 * 16);
     const float dw = h2f(hdr.x), dmin = h2f(hdr.x >> 16);
     const unsigned s0 = hdr.y, s1 = hdr.z, s2 = hdr.w;
-    i32x16 aH[kMT], aL[kMT], aM[kMT];
+    // the 6-bit scales of get_scale_min_k4, one per byte (sub-blocks 0-3 and 4-7), split as 8 sh + sl
+    const unsigned sc_lo = s0 & 0x3f3f3f3fu, sc_hi = (s2 & 0x0f0f0f0fu) | ((s0 >> 2) & 0x30303030u);
+    const unsigned sh4[2] = {(sc_lo >> 3) & 0x07070707u, (sc_hi >> 3) & 0x07070707u};
+    const unsigned sl4[2] = {sc_lo & 0x07070707u, sc_hi & 0x07070707u};
+    i32x16 aH[kMT], aL[kMT];
 #pragma unroll
     for (int c = 0; c < 4; c++) {
 #pragma unroll
         for (int nib = 0; nib < 2; nib++) {
-            int sc, m;
-            if (c == 0 && nib == 0) scale_min_k4<0>(s0, s1, s2, sc, m);
-            else if (c == 0) scale_min_k4<1>(s0, s1, s2, sc, m);
-            else if (c == 1 && nib == 0) scale_min_k4<2>(s0, s1, s2, sc, m);
-            else if (c == 1) scale_min_k4<3>(s0, s1, s2, sc, m);
-            else if (c == 2 && nib == 0) scale_min_k4<4>(s0, s1, s2, sc, m);
-            else if (c == 2) scale_min_k4<5>(s0, s1, s2, sc, m);
-            else if (nib == 0) scale_min_k4<6>(s0, s1, s2, sc, m);
-            else scale_min_k4<7>(s0, s1, s2, sc, m);
-            const unsigned sh = (unsigned) (sc >> 3) * 0x10001u, sl = (unsigned) (sc & 7) * 0x10001u;
-            const int mp = (int) __builtin_amdgcn_perm(0u, (unsigned) m, 0u); // m in all 4 bytes
+            // byte j % 4 of the packed scales into both 16-bit halves (v_perm_b32 selector 0x0c is a zero byte)
+            const int j = 2 * c + nib;
+            const unsigned sel = 0x0c000c00u | (unsigned) (j & 3) * 0x10001u;
+            const unsigned sh = __builtin_amdgcn_perm(0u, sh4[j >> 2], sel), sl = __builtin_amdgcn_perm(0u, sl4[j >> 2], sel);
             const uint4 q = qv[c];
             const unsigned k4 = 0x0f0f0f0fu;
             const unsigned n0 = nib ? (q.x >> 4) & k4 : q.x & k4, n1 = nib ? (q.y >> 4) & k4 : q.y & k4;
             const unsigned n2 = nib ? (q.z >> 4) & k4 : q.z & k4, n3 = nib ? (q.w >> 4) & k4 : q.w & k4;
             const i32x4 bh = {mul_bytes(n0, sh), mul_bytes(n1, sh), mul_bytes(n2, sh), mul_bytes(n3, sh)};
             const i32x4 bl = {mul_bytes(n0, sl), mul_bytes(n1, sl), mul_bytes(n2, sl), mul_bytes(n3, sl)};
-            const i32x4 bm = {mp, mp, mp, mp};
             const int part = 4 * c + 2 * nib + h;
 #pragma unroll
             for (int mt = 0; mt < kMT; mt++) {
@@ -322,19 +338,26 @@ __device__ __forceinline__ void q4k_superblock(const unsigned char *st, int n, f
                     const i32x16 z = {};
                     aH[mt] = mfma_i8(a, bh, z);
                     aL[mt] = mfma_i8(a, bl, z);
-                    aM[mt] = mfma_i8(a, bm, z);
                 } else {
                     aH[mt] = mfma_i8(a, bh, aH[mt]);
                     aL[mt] = mfma_i8(a, bl, aL[mt]);
-                    aM[mt] = mfma_i8(a, bm, aM[mt]);
                 }
             }
         }
+    }
+    // the 6-bit mins of sub-blocks 4 h .. 4 h + 3 (get_scale_min_k4), one per byte, then each as an fp16 pair
+    const unsigned mins = h ? ((s2 >> 4) & 0x0f0f0f0fu) | ((s1 >> 2) & 0x30303030u) : s1 & 0x3f3f3f3fu;
+    u32x4 bm;
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        const float mf = (float) ((mins >> (8 * i)) & 0xffu);
+        bm[i] = __builtin_bit_cast(unsigned, __builtin_amdgcn_cvt_pkrtz(mf, mf));
     }
     const float *dxs = reinterpret_cast<const float *>(st + kABytes);
 #pragma unroll
     for (int mt = 0; mt < kMT; mt++) {
         if (mt > 0 && n <= 32 * mt) continue;
+        const f32x16 aM = mfma_f16(bq[mt], bm);
 #pragma unroll
         for (int a4 = 0; a4 < 4; a4++) {
             const float4 d4 = *reinterpret_cast<const float4 *>(dxs + mt * 32 + 8 * a4 + 4 * h);
@@ -343,7 +366,7 @@ __device__ __forceinline__ void q4k_superblock(const unsigned char *st, int n, f
             for (int b = 0; b < 4; b++) {
                 const int r = 4 * a4 + b;
                 const float isum = (float) (8 * aH[mt][r] + aL[mt][r]);
-                acc[mt][r] = fmaf(dv[b], fmaf(dw, isum, -(dmin * (float) aM[mt][r])), acc[mt][r]);
+                acc[mt][r] = fmaf(dv[b], fmaf(dw, isum, -(dmin * aM[r])), acc[mt][r]);
             }
         }
     }
@@ -351,7 +374,7 @@ __device__ __forceinline__ void q4k_superblock(const unsigned char *st, int n, f
 
 // The whole K of the wavefront's 32 rows (row0 + lane % 32 of matrix w) against the chunk's n
 // activation rows; called uniformly by the 4 wavefronts. Stage sb + kNS - 1 is in flight while
-// stage sb is multiplied.
+// stage sb is multiplied (its split group sums in bq[kNS - 2]).
 __device__ __forceinline__ void q4k_rows(const GroupedParams &P, const GLds &g, int n, const uint8_t *w, int row0,
                                          float (&acc)[kMT][16]) {
     const int nsb = P.K / 256;
@@ -361,17 +384,27 @@ __device__ __forceinline__ void q4k_rows(const GroupedParams &P, const GLds &g, 
 #pragma unroll
         for (int r = 0; r < 16; r++) acc[mt][r] = 0.0f;
     const DmaOffs o = dma_offsets(P, g, n, row0);
-    for (int s = 0; s < kNS - 1 && s < nsb; s++) issue_stage(P, g, o, w, s, s);
+    u32x4 bq[kNS - 1][kMT];
+#pragma unroll
+    for (int s = 0; s < kNS - 1; s++)
+        if (s < nsb) issue_stage(P, g, o, w, s, s, bq[s]);
     for (int sb = 0; sb < nsb; sb++) {
+        u32x4 cur[kMT];
+#pragma unroll
+        for (int mt = 0; mt < kMT; mt++) cur[mt] = bq[0][mt];
+#pragma unroll
+        for (int s = 0; s + 1 < kNS - 1; s++)
+#pragma unroll
+            for (int mt = 0; mt < kMT; mt++) bq[s][mt] = bq[s + 1][mt];
         if (sb + kNS - 1 < nsb) {
-            issue_stage(P, g, o, w, sb + kNS - 1, (sb + kNS - 1) % kNS);
+            issue_stage(P, g, o, w, sb + kNS - 1, (sb + kNS - 1) % kNS, bq[kNS - 2]);
             if (w0) wait_vm<kLoads0 * (kNS - 1)>();
             else wait_vm<kLoads1 * (kNS - 1)>();
         } else {
             wait_vm<0>();
         }
         __syncthreads();
-        q4k_superblock(g.ring + (size_t) (sb % kNS) * kStageBytes, n, acc);
+        q4k_superblock(g.ring + (size_t) (sb % kNS) * kStageBytes, n, cur, acc);
         __syncthreads();
     }
 }
@@ -464,9 +497,10 @@ __global__ __launch_bounds__(kGThreads) void down_grouped_kernel(GroupedParams P
     }
 }
 
-__global__ __launch_bounds__(128) void act_quant_kernel(const float *act, int f, int8_t *qs, float *d, int32_t *bs) {
+__global__ __launch_bounds__(128) void act_quant_kernel(const float *act, int f, int8_t *qs, float *d, int32_t *bs,
+                                                        uint32_t *bh) {
     const size_t p = blockIdx.x;
-    quantize_row<kTypeQ4_K>(act + p * f, f, qs + p * f, d + p * (f / 32), bs + p * (f / 32));
+    quantize_row<kTypeQ4_K>(act + p * f, f, qs + p * f, d + p * (f / 32), bs + p * (f / 32), bh + p * (f / 32));
 }
 
 }  // namespace
@@ -499,6 +533,7 @@ hipError_t allow_lds() {
 
 hipError_t launch_gate_up_grouped(const GroupedParams &P, int max_items, hipStream_t st, const LaunchTiming *tm) {
     if (max_items <= 0) return hipSuccess;
+    if (!P.xbh) return hipErrorInvalidValue;
     if (const hipError_t e = allow_lds(); e != hipSuccess) return e;
     const int per = (max_items + kXcds - 1) / kXcds;
     return launch(gate_up_grouped_kernel, dim3(kXcds * per * (P.rows / 64)), dim3(kGThreads), kGLdsBytes, st, tm, P);
@@ -506,6 +541,7 @@ hipError_t launch_gate_up_grouped(const GroupedParams &P, int max_items, hipStre
 
 hipError_t launch_down_grouped(const GroupedParams &P, int max_items, hipStream_t st, const LaunchTiming *tm) {
     if (max_items <= 0) return hipSuccess;
+    if (!P.xbh) return hipErrorInvalidValue;
     if (const hipError_t e = allow_lds(); e != hipSuccess) return e;
     const int per = (max_items + kXcds - 1) / kXcds;
     return launch(down_grouped_kernel, dim3(kXcds * per * (P.rows / 128)), dim3(kGThreads), kGLdsBytes, st, tm, P);
@@ -513,7 +549,8 @@ hipError_t launch_down_grouped(const GroupedParams &P, int max_items, hipStream_
 
 hipError_t launch_act_quant(const float *act, int f, int np, const ActBuf &aq, hipStream_t st, const LaunchTiming *tm) {
     if (np <= 0) return hipSuccess;
-    return launch(act_quant_kernel, dim3(np), dim3(128), 0, st, tm, act, f, aq.qs, aq.d, aq.bs);
+    if (!aq.bh) return hipErrorInvalidValue;
+    return launch(act_quant_kernel, dim3(np), dim3(128), 0, st, tm, act, f, aq.qs, aq.d, aq.bs, aq.bh);
 }
 
 }  // namespace lstk

@@ -9,11 +9,14 @@
 namespace lstk {
 
 // Quantized activations: qs [rows][K] int8, d [rows][K/32] f32 (the scale of each 32-value group;
-// Q8_K's per-256 scale is repeated 8 times), bs [rows][K/32] int32 (group sums, Q8_K only).
+// Q8_K's per-256 scale is repeated 8 times), bs [rows][K/32] int32 (group sums, Q8_K only), and when
+// non-null bh [rows][K/32]: the same sums as two exact fp16 values (split_sum_f16, Q8_K only), the
+// operand the grouped MFMA kernels take them in.
 struct ActBuf {
     int8_t *qs;
     float *d;
     int32_t *bs;
+    uint32_t *bh;
 };
 
 // When non-null, a launch records its own start/stop timestamps into these events
@@ -138,6 +141,7 @@ struct GroupedParams {
     int rows, K;             // weight matrix rows x K (= cols)
     const int8_t *xqs;       // activation rows [*][K] int8
     const float *xd;         // [*][K / 32], the Q8_K scale of each super-block repeated 8 times
+    const uint32_t *xbh;     // [*][K / 32], the 32-value group sums as split_sum_f16 pairs
     int row_div;             // activation row = pair / row_div
     const float *weights;    // down: router weight of each pair
     float *out;

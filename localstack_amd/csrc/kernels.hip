@@ -292,7 +292,7 @@ __global__ __launch_bounds__(kBlock) void route_kernel(RouteParams P, int n_rout
                                             P.xq.bs + (size_t) t * (h / 32));
                 else
                     quantize_row<kTypeQ4_K>(lds, h, P.xq.qs + (size_t) t * h, P.xq.d + (size_t) t * (h / 32),
-                                            P.xq.bs + (size_t) t * (h / 32));
+                                            P.xq.bs + (size_t) t * (h / 32), P.xq.bh ? P.xq.bh + (size_t) t * (h / 32) : nullptr);
 #pragma unroll
                 for (int k = 0; k < NG; k++) P.hnorm_out[(size_t) t * h + threadIdx.x + k * kBlock] = y[k];
                 __syncthreads(); // the row's LDS and s_part are reused by the next token
@@ -305,7 +305,7 @@ __global__ __launch_bounds__(kBlock) void route_kernel(RouteParams P, int n_rout
                                         P.xq.bs + (size_t) t * (h / 32));
             else
                 quantize_row<kTypeQ4_K>(P.hnorm + (size_t) t * h, h, P.xq.qs + (size_t) t * h, P.xq.d + (size_t) t * (h / 32),
-                                        P.xq.bs + (size_t) t * (h / 32));
+                                        P.xq.bs + (size_t) t * (h / 32), P.xq.bh ? P.xq.bh + (size_t) t * (h / 32) : nullptr);
         }
     }
 }
