@@ -57,6 +57,9 @@ __device__ __forceinline__ int mul_bytes(unsigned v, unsigned s2) {
 // permutation
 // ------------------------------------------------------------------------------------------------
 
+// The wavefront's index within the work-group, as a wave-uniform (scalar) value.
+__device__ __forceinline__ int wave_id() { return __builtin_amdgcn_readfirstlane((int) threadIdx.x / kWave); }
+
 __device__ __forceinline__ void lds_fence() { asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory"); }
 
 // Inclusive prefix sum over the wavefront.
@@ -195,10 +198,17 @@ __global__ __launch_bounds__(kPermThreads) void permute_kernel(PermuteParams P) 
 // The activation rows, their scales and the weight rows arrive by global_load_lds (lane i of an
 // instruction lands at ldsptr + size * i); each lane also loads its 16 bytes of the rows' split group
 // sums into registers. Per stage, wavefront 0 issues kLoads0 loads and the others kLoads1.
+// One stage by default: at 26.8 KB of LDS and under 128 VGPRs, four work-groups share a CU (four
+// wavefronts per SIMD); a two-stage ring holds the CU to three, and the compiler waits for the
+// next stage's loads at every barrier anyway, so the second stage overlaps nothing.
 #ifndef LSTK_GROUPED_STAGES
-#define LSTK_GROUPED_STAGES 2
+#define LSTK_GROUPED_STAGES 1
 #endif
 constexpr int kNS = LSTK_GROUPED_STAGES;
+// Minimum wavefronts per SIMD the grouped kernels are compiled for (0: the compiler's choice).
+#ifndef LSTK_GROUPED_MIN_WAVES
+#define LSTK_GROUPED_MIN_WAVES 0
+#endif
 constexpr int kMT = kGroupedChunk / 32;              // 32-row M-tiles per wavefront
 constexpr int kAInstr = kGroupedChunk * 16 / kWave / 4; // activation loads per wavefront
 constexpr int kABytes = kGroupedChunk * 256;
@@ -244,7 +254,7 @@ struct DmaOffs {
 };
 
 __device__ __forceinline__ DmaOffs dma_offsets(const GroupedParams &P, const GLds &g, int n, int row0) {
-    const int wave = threadIdx.x / kWave, lane = threadIdx.x % kWave;
+    const int wave = wave_id(), lane = threadIdx.x % kWave;
     DmaOffs o;
 #pragma unroll
     for (int i = 0; i < kAInstr; i++) {
@@ -271,23 +281,31 @@ __device__ __forceinline__ DmaOffs dma_offsets(const GroupedParams &P, const GLd
 // of matrix w) into ring stage `slot`, and the lane's split group sums into bq.
 __device__ __forceinline__ void issue_stage(const GroupedParams &P, const GLds &g, const DmaOffs &o, const uint8_t *w,
                                             int sb, int slot, u32x4 (&bq)[kMT]) {
-    const int wave = threadIdx.x / kWave, lane = threadIdx.x % kWave;
+    const int wave = wave_id(), lane = threadIdx.x % kWave;
+    // Each 32-bit offset passes through an empty asm here, so it is extended to 64 bits next to its
+    // load: the load then takes the form (scalar base + 32-bit vector offset) instead of a 64-bit
+    // vector address kept live across the loop.
+    auto off = [](unsigned v) {
+        asm volatile("" : "+v"(v));
+        return v;
+    };
     unsigned char *st = g.ring + (size_t) slot * kStageBytes;
     const uint8_t *xa = reinterpret_cast<const uint8_t *>(P.xqs) + sb * 256;
 #pragma unroll
     // rows past the chunk's n pairs are not loaded: their LDS rows hold stale bytes, and the products of
     // those rows are never stored
     for (int i = 0; i < kAInstr; i++)
-        if (o.live & (1u << i)) dma16(xa + o.a[i], st + (wave * kAInstr + i) * 1024);
-    if (wave == 0 && lane < kGroupedChunk && (o.live >> 31)) dma4(reinterpret_cast<const uint8_t *>(P.xd) + sb * 32 + o.dx, st + kABytes);
+        if (o.live & (1u << i)) dma16(xa + off(o.a[i]), st + (wave * kAInstr + i) * 1024);
+    if (wave == 0 && lane < kGroupedChunk && (o.live >> 31))
+        dma4(reinterpret_cast<const uint8_t *>(P.xd) + sb * 32 + off(o.dx), st + kABytes);
     const uint8_t *wb = w + (size_t) sb * kChunksQ4_K * P.rows * 16;
     unsigned char *wl = st + kABytes + kDXBytes + wave * kWWaveBytes;
 #pragma unroll
-    for (int i = 0; i < 4; i++) dma16(wb + o.w[i], wl + i * 1024);
-    if (lane < 32) dma16(wb + o.w[4], wl + 4 * 1024);
+    for (int i = 0; i < 4; i++) dma16(wb + off(o.w[i]), wl + i * 1024);
+    if (lane < 32) dma16(wb + off(o.w[4]), wl + 4 * 1024);
     const uint8_t *xb = reinterpret_cast<const uint8_t *>(P.xbh) + sb * 32;
 #pragma unroll
-    for (int mt = 0; mt < kMT; mt++) bq[mt] = *reinterpret_cast<const u32x4 *>(xb + o.bh[mt]);
+    for (int mt = 0; mt < kMT; mt++) bq[mt] = *reinterpret_cast<const u32x4 *>(xb + off(o.bh[mt]));
 }
 
 // Multiplies one staged super-block: the wavefront's 32 weight rows (lane % 32) with the chunk's
@@ -301,7 +319,7 @@ __device__ __forceinline__ void issue_stage(const GroupedParams &P, const GLds &
 // In the imin product, lane half h gives K entries 8 h .. 8 h + 7, the pairs of sub-blocks 4 h .. + 3.
 __device__ __forceinline__ void q4k_superblock(const unsigned char *st, int n, const u32x4 (&bq)[kMT],
                                                float (&acc)[kMT][16]) {
-    const int wave = threadIdx.x / kWave, lane = threadIdx.x % kWave, h = lane / 32, r32 = lane % 32;
+    const int wave = wave_id(), lane = threadIdx.x % kWave, h = lane / 32, r32 = lane % 32;
     const unsigned char *wl = st + kABytes + kDXBytes + wave * kWWaveBytes;
     const uint4 hdr = *reinterpret_cast<const uint4 *>(wl + r32 * 16);
     uint4 qv[4];
@@ -373,39 +391,51 @@ __device__ __forceinline__ void q4k_superblock(const unsigned char *st, int n, c
 }
 
 // The whole K of the wavefront's 32 rows (row0 + lane % 32 of matrix w) against the chunk's n
-// activation rows; called uniformly by the 4 wavefronts. Stage sb + kNS - 1 is in flight while
-// stage sb is multiplied (its split group sums in bq[kNS - 2]).
+// activation rows; called uniformly by the 4 wavefronts. With kNS > 1 stages, stage sb + kNS - 1 is
+// in flight while stage sb is multiplied (its split group sums in bq[kNS - 2]); with one stage, each
+// super-block is loaded, waited for and multiplied in turn.
 __device__ __forceinline__ void q4k_rows(const GroupedParams &P, const GLds &g, int n, const uint8_t *w, int row0,
                                          float (&acc)[kMT][16]) {
     const int nsb = P.K / 256;
-    const bool w0 = threadIdx.x < kWave;
 #pragma unroll
     for (int mt = 0; mt < kMT; mt++)
 #pragma unroll
         for (int r = 0; r < 16; r++) acc[mt][r] = 0.0f;
     const DmaOffs o = dma_offsets(P, g, n, row0);
-    u32x4 bq[kNS - 1][kMT];
-#pragma unroll
-    for (int s = 0; s < kNS - 1; s++)
-        if (s < nsb) issue_stage(P, g, o, w, s, s, bq[s]);
-    for (int sb = 0; sb < nsb; sb++) {
-        u32x4 cur[kMT];
-#pragma unroll
-        for (int mt = 0; mt < kMT; mt++) cur[mt] = bq[0][mt];
-#pragma unroll
-        for (int s = 0; s + 1 < kNS - 1; s++)
-#pragma unroll
-            for (int mt = 0; mt < kMT; mt++) bq[s][mt] = bq[s + 1][mt];
-        if (sb + kNS - 1 < nsb) {
-            issue_stage(P, g, o, w, sb + kNS - 1, (sb + kNS - 1) % kNS, bq[kNS - 2]);
-            if (w0) wait_vm<kLoads0 * (kNS - 1)>();
-            else wait_vm<kLoads1 * (kNS - 1)>();
-        } else {
+    if constexpr (kNS == 1) {
+        for (int sb = 0; sb < nsb; sb++) {
+            u32x4 cur[kMT];
+            issue_stage(P, g, o, w, sb, 0, cur);
             wait_vm<0>();
+            __syncthreads();
+            q4k_superblock(g.ring, n, cur, acc);
+            __syncthreads();
         }
-        __syncthreads();
-        q4k_superblock(g.ring + (size_t) (sb % kNS) * kStageBytes, n, cur, acc);
-        __syncthreads();
+    } else {
+        const bool w0 = threadIdx.x < kWave;
+        u32x4 bq[kNS > 1 ? kNS - 1 : 1][kMT]; // (sized 1 where the one-stage branch is the live one)
+#pragma unroll
+        for (int s = 0; s < kNS - 1; s++)
+            if (s < nsb) issue_stage(P, g, o, w, s, s, bq[s]);
+        for (int sb = 0; sb < nsb; sb++) {
+            u32x4 cur[kMT];
+#pragma unroll
+            for (int mt = 0; mt < kMT; mt++) cur[mt] = bq[0][mt];
+#pragma unroll
+            for (int s = 0; s + 1 < kNS - 1; s++)
+#pragma unroll
+                for (int mt = 0; mt < kMT; mt++) bq[s][mt] = bq[s + 1][mt];
+            if (sb + kNS - 1 < nsb) {
+                issue_stage(P, g, o, w, sb + kNS - 1, (sb + kNS - 1) % kNS, bq[kNS > 1 ? kNS - 2 : 0]);
+                if (w0) wait_vm<kLoads0 * (kNS - 1)>();
+                else wait_vm<kLoads1 * (kNS - 1)>();
+            } else {
+                wait_vm<0>();
+            }
+            __syncthreads();
+            q4k_superblock(g.ring + (size_t) (sb % kNS) * kStageBytes, n, cur, acc);
+            __syncthreads();
+        }
     }
 }
 
@@ -433,7 +463,7 @@ __device__ __forceinline__ bool g_item(const GroupedParams &P, int n_rb, const G
 
 // gate_up: wavefront w computes rows rb * 64 + 32 (w / 2) .. + 31 of gate (w even) or up (w odd);
 // the up wavefronts hand their sums to the gate wavefronts through LDS for the SwiGLU.
-__global__ __launch_bounds__(kGThreads) void gate_up_grouped_kernel(GroupedParams P) {
+__global__ __launch_bounds__(kGThreads, LSTK_GROUPED_MIN_WAVES) void gate_up_grouped_kernel(GroupedParams P) {
     extern __shared__ __align__(16) unsigned char smem[];
     const GLds g = g_lds(smem);
     const int n_rb = P.rows / 64;
@@ -472,7 +502,7 @@ __global__ __launch_bounds__(kGThreads) void gate_up_grouped_kernel(GroupedParam
 }
 
 // down: wavefront w computes rows rb * 128 + 32 w .. + 31, times the pair's router weight.
-__global__ __launch_bounds__(kGThreads) void down_grouped_kernel(GroupedParams P) {
+__global__ __launch_bounds__(kGThreads, LSTK_GROUPED_MIN_WAVES) void down_grouped_kernel(GroupedParams P) {
     extern __shared__ __align__(16) unsigned char smem[];
     const GLds g = g_lds(smem);
     const int n_rb = P.rows / 128;
