@@ -89,10 +89,8 @@ __device__ __forceinline__ void norm_row(const float *x, const float *wn, int n,
 // NR: the staged rows are normalised here from P.x_raw (an instantiation of its own: the extra state
 // would cost the plain one registers)
 template <int GT, int NG, int kRouteEPW, bool NR>
-__device__ __forceinline__ void route_tile(const RouteParams &P, int b, float *xs, int tt, int ns, double *s_part) {
+__device__ __forceinline__ void route_tile(const RouteParams &P, int tile, int eg, float *xs, int tt, int ns, double *s_part) {
     constexpr int kRouteEG = 4 * kRouteEPW;
-    const int n_eg = (P.E + kRouteEG - 1) / kRouteEG;
-    const int tile = b / n_eg, eg = b - tile * n_eg;
     constexpr int h = NG * 256;
     constexpr int kPre = 32768 / 16 / kBlock; // float4 of one stage per thread (tt * h * 4 <= 32 KiB)
     const int wave = threadIdx.x / kWave, lane = threadIdx.x % kWave;
@@ -271,12 +269,26 @@ __device__ __forceinline__ void route_tile(const RouteParams &P, int b, float *x
 }
 
 template <int GT, int NG, int EPW, bool NR>
-__global__ __launch_bounds__(kBlock) void route_kernel(RouteParams P, int n_route_wg, int n_quant_wg, int route_tt, int route_ns) {
+// Route work-group b -> (token tile, expert group). xcd_per > 0: XCD-aware, as the dispatcher deals
+// work-groups to the 8 XCDs in turn (b goes to XCD b % 8), XCD x takes the tiles [x xcd_per,
+// (x + 1) xcd_per), all expert groups of a tile, so a tile's token rows are fetched into one L2 and
+// read there by its expert groups (n_route_wg is then 8 xcd_per n_eg; work-groups past the last
+// tile have none). xcd_per = 0: tile-major.
+__global__ __launch_bounds__(kBlock) void route_kernel(RouteParams P, int n_route_wg, int n_quant_wg, int route_tt, int route_ns,
+                                                       int xcd_per) {
     extern __shared__ __align__(16) float lds[];
     __shared__ double s_part[kBlock / kWave];
     const int b = blockIdx.x;
     if (b < n_route_wg) {
-        route_tile<GT, NG, EPW, NR>(P, b, lds, route_tt, route_ns, s_part);
+        const int n_eg = (P.E + 4 * EPW - 1) / (4 * EPW);
+        int tile = b / n_eg, eg = b - tile * n_eg;
+        if (xcd_per > 0) {
+            const int local = b / 8;
+            tile = (b % 8) * xcd_per + local / n_eg;
+            eg = local % n_eg;
+            if (local / n_eg >= xcd_per || tile * route_tt * route_ns >= P.T) return;
+        }
+        route_tile<GT, NG, EPW, NR>(P, tile, eg, lds, route_tt, route_ns, s_part);
     } else if (P.qtype != 0) {
         const int h = P.h;
         if (P.x_raw) {
@@ -961,22 +973,28 @@ template <int GT, int NG>
 hipError_t launch_route_t(const RouteParams &P, hipStream_t st, const LaunchTiming *tm) {
     // the in-launch normalisation needs the quantizing work-groups to store the rows
     if (P.x_raw && (!P.norm_w || !P.hnorm_out || !P.qtype)) return hipErrorInvalidValue;
-    int n_route = 0, tt = 1, ns = 1;
+    int n_route = 0, tt = 1, ns = 1, xcd_per = 0;
     const int epw = P.T == 1 ? 1 : kRouteEPWMax;
     if (P.do_route) {
         tt = route_tile_tokens(P.h);
         // many tokens: each work-group keeps its router rows in registers over 4 stages of tokens
         ns = P.T > 8 * tt ? 4 : 1;
-        n_route = ((P.T + tt * ns - 1) / (tt * ns)) * ((P.E + 4 * epw - 1) / (4 * epw));
+        const int n_tile = (P.T + tt * ns - 1) / (tt * ns), n_eg = (P.E + 4 * epw - 1) / (4 * epw);
+        n_route = n_tile * n_eg;
+        // at least a tile per XCD: each tile's expert groups on the XCD whose L2 holds its rows
+        if (n_tile >= 8) {
+            xcd_per = (n_tile + 7) / 8;
+            n_route = 8 * xcd_per * n_eg;
+        }
     }
     const int n_quant = P.qtype ? std::min(P.T, 256) : 0;
     const int grid = std::max(1, n_route + n_quant);
     // (a single token's row is staged in LDS by the quantizing work-group too)
     const size_t lds = std::max(P.do_route ? (size_t) tt * P.h * 4 : (size_t) 16, P.x_raw ? (size_t) P.h * 4 : (size_t) 16);
-    if (epw == 1) return launch(route_kernel<GT, NG, 1, false>, dim3(grid), dim3(kBlock), lds, st, tm, P, n_route, n_quant, tt, ns);
+    if (epw == 1) return launch(route_kernel<GT, NG, 1, false>, dim3(grid), dim3(kBlock), lds, st, tm, P, n_route, n_quant, tt, ns, xcd_per);
     if (P.x_raw)
-        return launch(route_kernel<GT, NG, kRouteEPWMax, true>, dim3(grid), dim3(kBlock), lds, st, tm, P, n_route, n_quant, tt, ns);
-    return launch(route_kernel<GT, NG, kRouteEPWMax, false>, dim3(grid), dim3(kBlock), lds, st, tm, P, n_route, n_quant, tt, ns);
+        return launch(route_kernel<GT, NG, kRouteEPWMax, true>, dim3(grid), dim3(kBlock), lds, st, tm, P, n_route, n_quant, tt, ns, xcd_per);
+    return launch(route_kernel<GT, NG, kRouteEPWMax, false>, dim3(grid), dim3(kBlock), lds, st, tm, P, n_route, n_quant, tt, ns, xcd_per);
 }
 
 template <int GT>
