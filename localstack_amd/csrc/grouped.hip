@@ -62,14 +62,16 @@ __device__ __forceinline__ int wave_id() { return __builtin_amdgcn_readfirstlane
 
 __device__ __forceinline__ void lds_fence() { asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory"); }
 
-// Inclusive prefix sum over the wavefront.
+// Inclusive prefix sum over the wavefront by DPP: within each row of 16 lanes (row_shr 1, 2, 4, 8,
+// lanes without a source adding 0), then the totals of rows 0 and 2 into rows 1 and 3 (row_bcast:15)
+// and the total of rows 0-1 into rows 2 and 3 (row_bcast:31).
 __device__ __forceinline__ int wave_incl_scan(int v) {
-    const int lane = threadIdx.x % kWave;
-#pragma unroll
-    for (int o = 1; o < kWave; o <<= 1) {
-        const int y = __shfl_up(v, o, kWave);
-        if (lane >= o) v += y;
-    }
+    v += __builtin_amdgcn_update_dpp(0, v, 0x111, 0xF, 0xF, false);
+    v += __builtin_amdgcn_update_dpp(0, v, 0x112, 0xF, 0xF, false);
+    v += __builtin_amdgcn_update_dpp(0, v, 0x114, 0xF, 0xF, false);
+    v += __builtin_amdgcn_update_dpp(0, v, 0x118, 0xF, 0xF, false);
+    v += __builtin_amdgcn_update_dpp(0, v, kDppRowBcast15, 0xA, 0xF, false);
+    v += __builtin_amdgcn_update_dpp(0, v, kDppRowBcast31, 0xC, 0xF, false);
     return v;
 }
 
@@ -87,7 +89,8 @@ __global__ __launch_bounds__(kPermThreads) void permute_kernel(PermuteParams P) 
     __shared__ int wsum[2][kPermSeg];
     const int tid = threadIdx.x, lane = tid % kWave, w = tid / kWave;
     const int np = P.np, nb = P.n_bins;
-    for (int i = tid; i < kPermSeg * (kGroupedMaxBins / 2); i += kPermThreads) (&seg[0][0])[i] = 0u;
+    const int wpr = (nb + 1) / 2; // count words in use per segment
+    for (int i = tid; i < kPermSeg * wpr; i += kPermThreads) seg[i / wpr][i % wpr] = 0u;
     __syncthreads();
     const int L = ((np + kPermSeg - 1) / kPermSeg + kWave - 1) / kWave * kWave;
     const int s0 = min(np, w * L), s1 = min(np, s0 + L);
@@ -158,14 +161,14 @@ __global__ __launch_bounds__(kPermThreads) void permute_kernel(PermuteParams P) 
         if (P.n_items) *P.n_items = tot1;
     }
     __syncthreads();
+    const int key_bits = 32 - __builtin_clz((unsigned) nb);
     for (int base = s0; base < s1; base += kWave) {
         const int p = base + lane;
         const bool on = p < s1;
-        const int b = on ? (int) bl[p] : kGroupedMaxBins; // a key no real bin has (bit 10)
-        // lanes with the same bin: the AND over the key's 11 bits of the matching ballots
+        const int b = on ? (int) bl[p] : nb; // a key no real bin has
+        // lanes with the same bin: the AND over the key's bits (keys 0 .. nb) of the matching ballots
         unsigned long long mask = ~0ull;
-#pragma unroll
-        for (int bit = 0; bit < 11; bit++) {
+        for (int bit = 0; bit < key_bits; bit++) {
             const bool set = (b >> bit) & 1;
             const unsigned long long bb = __ballot(set);
             mask &= set ? bb : ~bb;
