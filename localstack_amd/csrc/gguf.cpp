@@ -1,7 +1,7 @@
 // gguf.cpp - memory-mapped GGUF reader (include/lstk_gguf.h).
 //
-// The reference reads GGUF through ggml's gguf library (src/gguf_model.cpp:14-103), which is not part of
-// this build; this is a reader written from the published GGUF layout (versions 2 and 3):
+// The reference reads GGUF through ggml's gguf library (src/gguf_model.cpp:14-103), which this library
+// does not link; this is a reader written from the published GGUF layout (versions 2 and 3):
 //   "GGUF" | u32 version | u64 n_tensors | u64 n_kv
 //   n_kv x   { string key | u32 value type | value }
 //   n_tensors x { string name | u32 n_dims | u64 ne[n_dims] | u32 ggml type | u64 offset }
