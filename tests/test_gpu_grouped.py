@@ -26,6 +26,9 @@ def model(name):
         "30b_q4": dict(h=2048, f=768, E=128, k=8, types=(Q4_K,) * 3, n_batch=512),
         # small Q4_K layer: 16 experts, top-4, 256 x 512
         "small_q4": dict(h=256, f=512, E=16, k=4, types=(Q4_K,) * 3, n_batch=256),
+        # Qwen3-235B-A22B expert shape (h 4096, f 1536, top-8; 16 experts): gate/up over 16 super-blocks,
+        # down over 6, 24 and 32 row blocks per item
+        "235b_q4": dict(h=4096, f=1536, E=16, k=8, types=(Q4_K,) * 3, n_batch=128),
         # top-64 of 64 experts: the largest k the kernels take
         "k64": dict(h=256, f=256, E=64, k=64, types=(Q8_0,) * 3, n_batch=64),
     }[name]
@@ -107,7 +110,8 @@ def ffn_err(got, ref, resid):
     return np.abs(got - ref).max() / max(np.abs(ref - resid).max(), 1e-12)
 
 
-@pytest.mark.parametrize("name,T", [("30b_q4", 64), ("30b_q4", 100), ("30b_q4", 512), ("small_q4", 256), ("small_q4", 65)])
+@pytest.mark.parametrize("name,T", [("30b_q4", 64), ("30b_q4", 100), ("30b_q4", 512), ("small_q4", 256), ("small_q4", 65),
+                                    ("235b_q4", 64), ("235b_q4", 128)])
 def test_grouped_ffn_matches_oracle(orc, lstk, dev, name, T):
     import torch
     cfg, lb, router, store = model(name)
