@@ -535,6 +535,8 @@ __global__ __launch_bounds__(KS *kWave) void gemm16_kernel(Gemm16Params P) {
 
 typedef _Float16 half4v __attribute__((ext_vector_type(4)));
 constexpr int kFaCells = 64;
+constexpr int kAttnSkipMinT = 64;    // steps of at least this many tokens skip passes with no cell of the sequence
+constexpr int kAttnMaxPasses = 2048; // passes per chunk the skip map covers (131072 cells)
 
 __device__ __forceinline__ f32x4v mfma16(half4v a, half4v b, f32x4v c) {
     return __builtin_amdgcn_mfma_f32_16x16x16f16(a, b, c, 0, 0, 0);
@@ -546,9 +548,10 @@ __device__ __forceinline__ half4v ld_half4(const uint16_t *p) {
 // R1: the single-token RoPE-in launch at head size 128 with the step's cos / sin table and grp <= 16
 // (rope_token_128's case), an instantiation of its own so that its prologue's loads and the first
 // pass's K / V loads are in flight together.
-template <int HD, int NRT, bool R1>
+template <int HD, int NRT, bool R1, bool SKIP = false>
 __global__ __launch_bounds__(kAtBlock) void attn_kernel(AttnParams P) {
     static_assert(!R1 || (NRT == 1 && HD == 128), "R1 is the single-token head-size-128 launch");
+    static_assert(!(R1 && SKIP), "the single-token launch keeps every pass");
     constexpr int NK = HD / 16, DT = NK / 4, RB = 16 * NRT, PS = kFaCells + 8; // P row stride (halves)
     __shared__ float s_S[RB][kFaCells];
     __shared__ uint16_t s_Ph[RB][PS], s_Pl[RB][PS];
@@ -643,9 +646,33 @@ __global__ __launch_bounds__(kAtBlock) void attn_kernel(AttnParams P) {
     for (int rt = 0; rt < NRT; rt++)
 #pragma unroll
         for (int dt = 0; dt < DT; dt++) O[rt][dt] = f32x4v{0, 0, 0, 0};
+    // A step of many tokens skips the chunk's passes that hold no cell of the sequence (cells of other
+    // or removed sequences, e.g. when the sequence's blocks sit high in the cache): such a pass would
+    // leave the running max, sum and output exactly as they are (every score -inf: sum 0, factor 1, or
+    // 0 while nothing is live and the output is still zero). The cell table is current here: the step's
+    // RoPE launch wrote the new cells' entries. A wavefront's 64 lanes read one pass's 64 entries, eight
+    // passes per wavefront in flight.
+    const int n_pass = (end - begin + kFaCells - 1) / kFaCells;
+    const bool skip = SKIP && !rope_in && n_pass <= kAttnMaxPasses;
+    __shared__ uint8_t s_live[SKIP ? kAttnMaxPasses : 1];
+    if (skip) {
+        for (int p0 = 0; p0 < n_pass; p0 += 8 * (kAtBlock / kWave)) {
+            int cs[8];
+#pragma unroll
+            for (int u = 0; u < 8; u++) cs[u] = P.cell_seq[min(begin + (p0 + u * (kAtBlock / kWave) + w) * kFaCells + l, P.kv_size - 1)];
+#pragma unroll
+            for (int u = 0; u < 8; u++) {
+                const int pass = p0 + u * (kAtBlock / kWave) + w;
+                const bool mine = cs[u] == P.seq && begin + pass * kFaCells + l < end;
+                const bool any = __ballot(mine) != 0ull;
+                if (l == 0 && pass < n_pass) s_live[pass] = any ? 1 : 0;
+            }
+        }
+    }
     __syncthreads();
 
     for (int c0 = begin; c0 < end; c0 += kFaCells) {
+        if (skip && !s_live[(c0 - begin) / kFaCells]) continue; // uniform: the whole work-group reads one byte
         if (c0 != begin || late) load_pass(c0);
         // S = Q K^T for this wavefront's 16 cells
         const int cell = c0 + 16 * w + lr;
@@ -1059,6 +1086,12 @@ hipError_t launch_attn_hd(const AttnParams &P, hipStream_t st, const LaunchTimin
     if constexpr (HD == 128) {
         if (P.rb_rows == 16 && P.rope_in && P.n_head / P.n_kv <= 4 * kRopeMaxQ && P.rope.cs)
             return launch(attn_kernel<HD, 1, true>, grid, block, 0, st, tm, P);
+    }
+    // steps of many tokens (prompts): the instantiation that skips passes with no cell of the sequence
+    if (P.T >= kAttnSkipMinT && !P.rope_in) {
+        if (P.rb_rows == 16) return launch(attn_kernel<HD, 1, false, true>, grid, block, 0, st, tm, P);
+        if (P.rb_rows == 32) return launch(attn_kernel<HD, 2, false, true>, grid, block, 0, st, tm, P);
+        return launch(attn_kernel<HD, 4, false, true>, grid, block, 0, st, tm, P);
     }
     if (P.rb_rows == 16) return launch(attn_kernel<HD, 1, false>, grid, block, 0, st, tm, P);
     if (P.rb_rows == 32) return launch(attn_kernel<HD, 2, false>, grid, block, 0, st, tm, P);
