@@ -84,6 +84,7 @@ struct AttnParams {
     const int32_t *cell_seq, *cell_pos, *pos;
     int32_t seq;
     int T, n_head, n_kv, hd, kv_size, n_cells, chunk, n_chunk, n_rowblk, rb_rows;
+    int cell_begin; // cells [cell_begin, n_cells) are attended: no cell of seq lies below (a multiple of 64)
     float scale;
     float *part; // [T][n_head][n_chunk][hd + 4]: max, sum, 2 unused, unnormalised output
     float *out;  // [T][n_head * hd]

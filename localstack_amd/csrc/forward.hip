@@ -570,7 +570,7 @@ __global__ __launch_bounds__(kAtBlock) void attn_kernel(AttnParams P) {
         s_M[tid] = -INFINITY;
         s_L[tid] = 0.0f;
     }
-    const int begin = c * P.chunk, end = min(begin + P.chunk, P.n_cells), last4 = P.kv_size - 4;
+    const int begin = P.cell_begin + c * P.chunk, end = min(begin + P.chunk, P.n_cells), last4 = P.kv_size - 4;
     // fresh: this work-group's chunk holds the token's new cell, whose K / V it computes itself; its
     // reads of that cell take them from LDS, and it stores them into the cache after its last barrier
     const bool rope_in = R1 || (NRT == 1 && P.rope_in);
@@ -983,7 +983,7 @@ void attn_plan(AttnParams &P) {
     const int rows = P.T * (P.n_head / P.n_kv);
     P.rb_rows = rows <= 16 ? 16 : rows <= 32 ? 32 : 64;
     P.n_rowblk = (rows + P.rb_rows - 1) / P.rb_rows;
-    const int passes = (P.n_cells + kFaCells - 1) / kFaCells;
+    const int passes = (P.n_cells - P.cell_begin + kFaCells - 1) / kFaCells;
     if (P.rope_in) {
         if ((long) P.n_head * passes <= 32768) {
             P.chunk = kFaCells;
@@ -995,7 +995,7 @@ void attn_plan(AttnParams &P) {
     int want = (kAttnTarget + P.n_kv * P.n_rowblk - 1) / (P.n_kv * P.n_rowblk);
     want = want < 1 ? 1 : (want > passes ? passes : want);
     P.chunk = (passes + want - 1) / want * kFaCells;
-    P.n_chunk = (P.n_cells + P.chunk - 1) / P.chunk;
+    P.n_chunk = (P.n_cells - P.cell_begin + P.chunk - 1) / P.chunk;
 }
 
 size_t attn_part_rows(int n_batch, int n_head) { return 32768 + (size_t) n_batch * n_head; }

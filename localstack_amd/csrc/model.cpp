@@ -141,6 +141,13 @@ struct KvBook {
     }
     // Engine::n_kv_for (src/engine.cpp:193-196): the cells up to the last occupied one, rounded up to a
     // multiple of 256 (at least 256), capped at the cache size.
+    // The first cell of the sequence's lowest block (0 for an unknown sequence): no cell of the sequence
+    // lies below it, so the attention need not look there.
+    int first_cell(int32_t seq) const {
+        const auto it = seqs.find(seq);
+        if (it == seqs.end() || it->second.blocks.empty()) return 0;
+        return (int) (*std::min_element(it->second.blocks.begin(), it->second.blocks.end()) * kCellBlock);
+    }
     int n_kv() const {
         uint32_t end = 0;
         for (uint32_t b = 0; b < (uint32_t) fill.size(); b++)
@@ -531,6 +538,7 @@ int forward(lstk_model *M, int32_t seq, int T, int n_cells, float *d_logits, int
         ap.hd = hd;
         ap.kv_size = (int) M->kv.size;
         ap.n_cells = n_cells;
+        ap.cell_begin = std::min(M->kv.first_cell(seq), std::max(0, n_cells - 1)) / 64 * 64;
         ap.scale = 1.0f / sqrtf((float) hd);
         ap.part = M->part;
         ap.out = M->attn;
