@@ -17,12 +17,13 @@ BLOCK = 256         # kBlock (attn_combine_kernel)
 LDS_MAX = 65536
 
 
-def plan(T, n_head, n_kv, n_cells, target=512, rope_in=False):
-    """attn_plan (forward.hip): rows per work-group, row blocks, chunk (cells), chunks; rope_in kept or not."""
+def plan(T, n_head, n_kv, n_cells, target=512, rope_in=False, cell_begin=0):
+    """attn_plan (forward.hip): rows per work-group, row blocks, chunk (cells), chunks; rope_in kept or not.
+    The attended cells are [cell_begin, n_cells)."""
     rows = T * (n_head // n_kv)
     rb_rows = 16 if rows <= 16 else 32 if rows <= 32 else 64
     n_rowblk = (rows + rb_rows - 1) // rb_rows
-    passes = (n_cells + FA_CELLS - 1) // FA_CELLS
+    passes = (n_cells - cell_begin + FA_CELLS - 1) // FA_CELLS
     if rope_in:
         if n_head * passes <= 32768:
             return rb_rows, n_rowblk, FA_CELLS, passes, True
@@ -30,7 +31,7 @@ def plan(T, n_head, n_kv, n_cells, target=512, rope_in=False):
     want = (target + n_kv * n_rowblk - 1) // (n_kv * n_rowblk)
     want = max(1, min(want, passes))
     chunk = (passes + want - 1) // want * FA_CELLS
-    n_chunk = (n_cells + chunk - 1) // chunk
+    n_chunk = (n_cells - cell_begin + chunk - 1) // chunk
     return rb_rows, n_rowblk, chunk, n_chunk, rope_in
 
 
@@ -38,11 +39,12 @@ def part_rows(n_batch, n_head):
     return 32768 + n_batch * n_head  # attn_part_rows
 
 
-def check_launch(T, n_head, n_kv, hd, kv_size, n_cells, n_batch, target, rope_in):
+def check_launch(T, n_head, n_kv, hd, kv_size, n_cells, n_batch, target, rope_in, cell_begin=0):
     """Every access of one attention launch (and its combine) against the buffers' sizes."""
     assert 1 <= T <= n_batch and 1 <= n_cells <= kv_size and kv_size % 256 == 0
+    assert 0 <= cell_begin < n_cells and cell_begin % 64 == 0
     grp = n_head // n_kv
-    rb_rows, n_rowblk, chunk, n_chunk, rope_in = plan(T, n_head, n_kv, n_cells, target, rope_in)
+    rb_rows, n_rowblk, chunk, n_chunk, rope_in = plan(T, n_head, n_kv, n_cells, target, rope_in, cell_begin)
     NRT = rb_rows // 16
     RB, NK = 16 * NRT, hd // 16
     DT = NK // 4
@@ -54,9 +56,10 @@ def check_launch(T, n_head, n_kv, hd, kv_size, n_cells, n_batch, target, rope_in
     g, rest = wg % n_kv, wg // n_kv
     c, rb = rest % n_chunk, rest // n_chunk
     assert c.max() < n_chunk and rb.max() < n_rowblk and g.max() < n_kv
-    begin = c * chunk
+    begin = cell_begin + c * chunk
     end = np.minimum(begin + chunk, n_cells)
     assert (begin < end).all(), "a chunk without cells"
+    assert end.max() == n_cells and begin.min() == cell_begin, "the chunks cover the attended cells"
     row0 = rb * rb_rows
     # s_pos / Q rows: r < rows reads pos[r / grp] and q[(r / grp) * n_head + g * grp + r % grp]
     r = row0[:, None] + np.arange(RB)[None, :]
@@ -119,6 +122,11 @@ def test_every_attention_index_in_bounds(target, shape):
                 rope = T == 1 and grp <= 16
                 check_launch(T, n_head, n_kv, hd, kv_size, n_cells, n_batch, target, rope)
                 plans += 1
+                if n_cells > 256:
+                    # the sequence's lowest block high in the cache: the range starts there
+                    check_launch(T, n_head, n_kv, hd, kv_size, n_cells, n_batch, target, rope,
+                                 cell_begin=(n_cells - 256) // 64 * 64)
+                    plans += 1
     assert plans > 100
 
 
