@@ -537,6 +537,7 @@ typedef _Float16 half4v __attribute__((ext_vector_type(4)));
 constexpr int kFaCells = 64;
 constexpr int kAttnSkipMinT = 64;    // steps of at least this many tokens skip passes with no cell of the sequence
 constexpr int kAttnMaxPasses = 2048; // passes per chunk the skip map covers (131072 cells)
+constexpr int kAttnOneChunkWgs = 256; // row-block work-groups from which a many-token step keeps one chunk
 
 __device__ __forceinline__ f32x4v mfma16(half4v a, half4v b, f32x4v c) {
     return __builtin_amdgcn_mfma_f32_16x16x16f16(a, b, c, 0, 0, 0);
@@ -993,6 +994,9 @@ void attn_plan(AttnParams &P) {
         P.rope_in = 0;
     }
     int want = (kAttnTarget + P.n_kv * P.n_rowblk - 1) / (P.n_kv * P.n_rowblk);
+    // a step of many tokens whose row blocks alone fill the device takes one chunk per row block, so
+    // the launch writes the output itself and no combine follows
+    if (P.T >= kAttnSkipMinT && P.n_kv * P.n_rowblk >= kAttnOneChunkWgs) want = 1;
     want = want < 1 ? 1 : (want > passes ? passes : want);
     P.chunk = (passes + want - 1) / want * kFaCells;
     P.n_chunk = (P.n_cells - P.cell_begin + P.chunk - 1) / P.chunk;

@@ -29,6 +29,8 @@ def plan(T, n_head, n_kv, n_cells, target=512, rope_in=False, cell_begin=0):
             return rb_rows, n_rowblk, FA_CELLS, passes, True
         rope_in = False
     want = (target + n_kv * n_rowblk - 1) // (n_kv * n_rowblk)
+    if T >= 64 and n_kv * n_rowblk >= 256:  # kAttnSkipMinT, kAttnOneChunkWgs: one chunk per row block
+        want = 1
     want = max(1, min(want, passes))
     chunk = (passes + want - 1) // want * FA_CELLS
     n_chunk = (n_cells - cell_begin + chunk - 1) // chunk
@@ -138,7 +140,8 @@ def test_rope_in_keeps_single_pass_chunks():
     assert not rope and chunk > 64
     # the committed plan without RoPE: several passes per chunk once the target is reached
     assert plan(32, 32, 4, 4352)[2] == 3 * 64
-    assert plan(512, 32, 4, 512)[2:4] == (4 * 64, 2)  # a 512-token prompt: 64 row blocks x 4 KV heads x 2
+    assert plan(512, 32, 4, 512)[2:4] == (8 * 64, 1)  # a 512-token prompt: 64 row blocks x 4 KV heads, one chunk
+    assert plan(64, 32, 4, 4352)[2:4] == (5 * 64, 14)  # 64 tokens: 8 row blocks x 4 KV heads, several chunks
 
 
 def softmax_passes(s, T_rows, pass_cells=FA_CELLS):
