@@ -119,6 +119,29 @@ def test_chunked_prefill_matches_one_step(lstk, dev):
     assert np.max(np.abs(a2 - b2)) <= 1e-4
 
 
+def test_prompt_high_in_cache_matches_fresh(lstk, dev):
+    """A 64-token prompt (the attention's many-token launch) placed high in the cache agrees with the same
+    prompt on a fresh cache. A 700-token sequence and then a 200-token one are decoded, the first is
+    removed: the prompt's blocks come from the top of the freed ones (cells 640-703), the attended range
+    starts at its lowest block and runs past the other sequence's cells (704-927) to the padded end, so
+    the launch skips the passes that hold none of the prompt's cells. Only f32 summation orders differ."""
+    hp, w = weights("tiny")
+    toks = prompt(11, 64, hp["n_vocab"])
+    _, fresh = build(lstk, dev, hp, w)
+    a, _ = run(fresh, 0, toks, hp, dev)
+    _, used = build(lstk, dev, hp, w)
+    first, second = prompt(12, 700, hp["n_vocab"]), prompt(13, 200, hp["n_vocab"])
+    for i in range(0, len(first), 64):
+        run(used, 5, first[i:i + 64], hp, dev)
+    for i in range(0, len(second), 64):
+        run(used, 6, second[i:i + 64], hp, dev)
+    used.remove_seq(5)
+    b, _ = run(used, 0, toks, hp, dev)
+    assert used.seq_len(0) == 64 and used.seq_len(6) == 200
+    assert np.max(np.abs(a - b)) <= 1e-4
+    assert np.argmax(a) == np.argmax(b)
+
+
 def test_sequences_are_isolated_and_removable(lstk, dev):
     hp, w = weights("tiny")
     A, B, C = prompt(1, 10, 1024), prompt(2, 7, 1024), prompt(3, 9, 1024)
