@@ -98,7 +98,9 @@ int lstk_model_decode(lstk_model *model, int32_t seq, const int32_t *tokens, int
  * forward: the step's kernels over those inputs, writing the last token's logits (and the trace, as
  *   lstk_model_decode). With a resident pool it makes no host synchronisation and no allocation, so it
  *   may be captured; a captured forward replays correctly after each prepare of the same seq,
- *   n_tokens and n_cells (n_cells changes only when the sequence crosses a multiple of 256 cells).
+ *   n_tokens and n_cells (n_cells changes only when the sequence crosses a multiple of 256 cells),
+ *   wherever the new cells lie: while the stream is capturing, attention covers cells [0, n_cells)
+ *   (an eager forward starts at the sequence's lowest cache block instead).
  *   With a streaming pool it synchronises the stream once per layer (the router's ids go to the host),
  *   unless the pool was created with LSTK_POOL_DEVICE_LRU: then the experts are acquired on the device
  *   (lstk_pool_acquire_device), nothing waits on the host and the forward may be captured too. */
@@ -123,6 +125,22 @@ int lstk_model_fill_context(lstk_model *model, int32_t seq, int n_cells, uint64_
  * a reference fed the same layer inputs; NULL turns it off. After the last layer only the output row has
  * been through the MoE block. */
 int lstk_model_debug_capture(lstk_model *model, float *d_states);
+
+/* Test hook (no counterpart in the reference): options of the model's later forwards. Bit 0 set: a
+ * single-token step runs RoPE and the new cell's K / V store in a launch of their own before the
+ * attention, whose chunks then take several 64-cell passes, instead of inside the attention launch with
+ * one-pass chunks (the plan steps of more tokens and contexts past 65536 cells always take), so a test can
+ * compare the two plans on the same cache. 0 restores the default. */
+int lstk_model_debug_options(lstk_model *model, int flags);
+
+/* Test hook (no counterpart in the reference): the attention launch plan a step of n_tokens takes (host
+ * arithmetic only, no device call), for n_head query / n_kv KV heads of head_dim over cells
+ * [cell_begin, n_cells) of a kv_size-cell cache; rope_in asks for RoPE inside the launch (one token).
+ * out[0..5] = query rows per work-group, row blocks, cells per chunk, chunks, RoPE kept inside the launch
+ * (0 / 1), work-groups of the attention launch. Fails with LSTK_E_INVALID on arguments a model would
+ * never pass. */
+int lstk_debug_attn_plan(int n_tokens, int n_head, int n_kv, int head_dim, int kv_size, int n_cells, int cell_begin,
+                         int rope_in, int32_t out[6]);
 
 /* Engine::set_routing_trace (src/engine.cpp:179-186): with a path, creates the file and writes the
  * trace header ("LSTKRTE1", n_layer, n_expert, n_expert_used as little-endian int32); every later step

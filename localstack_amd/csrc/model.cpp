@@ -195,6 +195,8 @@ struct lstk_model {
     std::vector<TimedLaunch> launched[kStages];
     // test hook: the residual stream after every layer, [n_layer][T][n_embd] (lstk_model_debug_capture)
     float *capture = nullptr;
+    // test hook (lstk_model_debug_options bit 0): RoPE of a single-token step in its own launch
+    bool rope_apart = false;
     // routing trace
     FILE *trace = nullptr;
     int32_t *trace_dev = nullptr; // [n_layer][n_batch][k] when the caller passes no trace buffer
@@ -467,6 +469,14 @@ int forward(lstk_model *M, int32_t seq, int T, int n_cells, float *d_logits, int
     hipError_t e;
     const int32_t *d_tok = M->in, *d_cells = M->in + nb, *d_pos = M->in + 2 * nb;
     const bool blas = T >= kBlasMinTokens;
+    // The attended range starts at the sequence's lowest block when the step runs now. A captured forward
+    // is replayed after later prepares whose new blocks may lie below that block (freed blocks come back
+    // in the order they were released), so a capture attends from cell 0: cells of other sequences and
+    // free cells are masked, and the cell that holds each new token is always inside the range.
+    hipStreamCaptureStatus capturing = hipStreamCaptureStatusNone;
+    if ((e = hipStreamIsCapturing(st, &capturing)) != hipSuccess) return hip_fail(e, "hipStreamIsCapturing");
+    const int range_begin =
+        capturing == hipStreamCaptureStatusNone ? std::min(M->kv.first_cell(seq), std::max(0, n_cells - 1)) / 64 * 64 : 0;
     {
         // the step's RoPE angles, shared by every layer
         lstk::RopeParams tp{};
@@ -510,7 +520,7 @@ int forward(lstk_model *M, int32_t seq, int T, int n_cells, float *d_logits, int
                             M->ld_qkv};
         // one token (its query rows in one 16-row tile): QK-norm, RoPE and the K / V store run inside
         // the attention launch
-        const bool rope_in_attn = T == 1 && hp.n_head / hp.n_head_kv <= 16;
+        const bool rope_in_attn = T == 1 && hp.n_head / hp.n_head_kv <= 16 && !M->rope_apart;
         if (blas) {
             const int rc = timed_span(M, 1, st, [&] {
                 // Q, K and V rows side by side in the output; one product when the weights are too
@@ -538,7 +548,7 @@ int forward(lstk_model *M, int32_t seq, int T, int n_cells, float *d_logits, int
         ap.hd = hd;
         ap.kv_size = (int) M->kv.size;
         ap.n_cells = n_cells;
-        ap.cell_begin = std::min(M->kv.first_cell(seq), std::max(0, n_cells - 1)) / 64 * 64;
+        ap.cell_begin = range_begin;
         ap.scale = 1.0f / sqrtf((float) hd);
         ap.part = M->part;
         ap.out = M->attn;
@@ -763,6 +773,38 @@ int lstk_model_truncate_seq(lstk_model *model, int32_t seq, int32_t keep) {
 int32_t lstk_model_seq_len(const lstk_model *model, int32_t seq) {
     if (!model) return 0;
     return model->kv.length(seq);
+}
+
+int lstk_model_debug_options(lstk_model *model, int flags) {
+    if (!model) return set_error(LSTK_E_INVALID, "null model");
+    if (flags & ~1) return set_error(LSTK_E_INVALID, "unknown debug option bits");
+    model->rope_apart = (flags & 1) != 0;
+    return LSTK_OK;
+}
+
+int lstk_debug_attn_plan(int n_tokens, int n_head, int n_kv, int head_dim, int kv_size, int n_cells, int cell_begin,
+                         int rope_in, int32_t out[6]) {
+    if (!out || n_tokens < 1 || n_head < 1 || n_kv < 1 || n_head % n_kv || !lstk::attn_supported(head_dim) ||
+        kv_size < 32 || kv_size % 32 || n_cells < 1 || n_cells > kv_size || cell_begin < 0 || cell_begin >= n_cells ||
+        cell_begin % 64)
+        return set_error(LSTK_E_INVALID, "lstk_debug_attn_plan: bad arguments");
+    lstk::AttnParams ap{};
+    ap.T = n_tokens;
+    ap.n_head = n_head;
+    ap.n_kv = n_kv;
+    ap.hd = head_dim;
+    ap.kv_size = kv_size;
+    ap.n_cells = n_cells;
+    ap.cell_begin = cell_begin;
+    ap.rope_in = rope_in ? 1 : 0;
+    lstk::attn_plan(ap);
+    out[0] = ap.rb_rows;
+    out[1] = ap.n_rowblk;
+    out[2] = ap.chunk;
+    out[3] = ap.n_chunk;
+    out[4] = ap.rope_in;
+    out[5] = n_kv * ap.n_chunk * ap.n_rowblk;
+    return LSTK_OK;
 }
 
 int lstk_model_set_timing(lstk_model *model, int enable) {

@@ -331,6 +331,76 @@ def test_graph_replay_matches_eager(lstk, dev):
     assert gm.seq_len(0) == eager.seq_len(0) == 22
 
 
+def test_graph_replay_high_in_cache_takes_lower_blocks(lstk, dev):
+    """A single-token forward captured while the sequence sits high in the cache, replayed as it grows into
+    blocks below the ones it held at capture. Layout as in test_prompt_high_in_cache_matches_fresh: the
+    64-token prompt holds cells 640-703 and every later block comes from further down (608, 576, 544, ...),
+    while another sequence's cells (704-927) keep the attended cells at 1024. The replays cross four block
+    boundaries. Each replay and each eager step in the same layout is held to the oracle's bar (logits,
+    RMS, top-1, and the replay's captured router ids bit-exact); replay and eager differ only by the
+    combine's f32 summation order (the eager range starts at the lowest block, the captured one at cell 0),
+    reported. A replay that attended only the range of the capture would miss the new cells (their K / V
+    and cell-table entries are written by the work-group whose chunk holds them): logits off by 0.1 or more."""
+    import torch
+    hp, w = weights("tiny")
+    models = []
+    for _ in range(2):
+        _, m = build(lstk, dev, hp, w)
+        first, second = prompt(12, 700, hp["n_vocab"]), prompt(13, 200, hp["n_vocab"])
+        for i in range(0, len(first), 64):
+            run(m, 5, first[i:i + 64], hp, dev)
+        for i in range(0, len(second), 64):
+            run(m, 6, second[i:i + 64], hp, dev)
+        m.remove_seq(5)
+        models.append(m)
+    eager, gm = models
+    ref = oracle.Qwen3(hp, w, 256)
+    toks = prompt(11, 64, hp["n_vocab"])
+    rl = ref.decode(toks)
+    a, _ = run(eager, 0, toks, hp, dev)
+    b, _ = run(gm, 0, toks, hp, dev)
+    np.testing.assert_array_equal(a, b)
+    feed = np.array([np.argmax(rl)], np.int32)
+    stream = torch.cuda.Stream()
+    logits = torch.zeros(hp["n_vocab"], dtype=torch.float32, device=dev)
+    tr = torch.full((hp["n_layer"], 1, hp["n_expert_used"]), -7, dtype=torch.int32, device=dev)
+    graph, worst_ge, worst_go, worst_eo, flips = None, 0.0, 0.0, 0.0, 0
+    for step in range(140):
+        rl, rt = ref.decode(feed, want_trace=True)
+        ea, et = run(eager, 0, feed, hp, dev)
+        with torch.cuda.stream(stream):
+            n = gm.prepare(0, feed, stream=stream)
+            assert n == 1024
+            if graph is None:
+                graph = torch.cuda.CUDAGraph()
+                with torch.cuda.graph(graph, stream=stream):
+                    gm.forward(0, 1, n, trace=tr, logits=logits, stream=stream)
+            graph.replay()
+        torch.cuda.synchronize()
+        got = logits.cpu().numpy()
+        d_ge = float(np.max(np.abs(got - ea)))
+        e_g, rms_g, ra, ga = oracle.diff_logits(rl, got)
+        e_e, rms_e, _, gae = oracle.diff_logits(rl, ea)
+        worst_ge, worst_go, worst_eo = max(worst_ge, d_ge), max(worst_go, e_g), max(worst_eo, e_e)
+        if d_ge > 1e-4:
+            print(f"[graph replay high in cache step {step} pos {64 + step}] replay vs eager {d_ge:.2e}, "
+                  f"vs oracle: replay {e_g:.2e} eager {e_e:.2e}", flush=True)
+        assert e_g <= LOGITS_TOL and rms_g <= RMS_TOL and ga == ra, ("replay", step, e_g, rms_g)
+        assert e_e <= LOGITS_TOL and rms_e <= RMS_TOL and gae == ra, ("eager", step, e_e, rms_e)
+        for name, ids in (("replay", tr.cpu().numpy()), ("eager", et)):
+            for l in np.flatnonzero(np.any(ids != rt, axis=(1, 2))):
+                print(f"[graph replay high in cache step {step}] {name} layer {l} router ids {ids[l].tolist()} vs "
+                      f"{rt[l].tolist()}", flush=True)
+                flips += 1
+        feed = np.array([ra], np.int32)
+    # the router's inputs differ from the oracle's by f32 summation order upstream (attention), so a near-tie
+    # at the top-k boundary may pick the other expert; at most 1% of the 2 x 140 rows per path
+    assert flips <= 2 * 280 // 100, flips
+    assert gm.seq_len(0) == eager.seq_len(0) == len(ref) == 64 + 140
+    print(f"[graph replay high in cache] 140 replays from position 64: max|dlogit| replay vs eager {worst_ge:.2e}, "
+          f"vs oracle: replay {worst_go:.2e}, eager {worst_eo:.2e}", flush=True)
+
+
 def test_separate_qkv_weights_match_joined(lstk, dev):
     """Q/K/V weights in three separate buffers (three library products per multi-token step) decode like
     the joined upload (one product): the same tokens, logits within 1e-4 (f32 summation order only)."""
