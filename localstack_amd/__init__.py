@@ -129,6 +129,8 @@ SIGNATURES = {
     "lstk_gguf_qwen3_experts": (_I, [_P, ctypes.POINTER(Qwen3HParams), _P]),
     "lstk_dequant_f16": (_I, [_I, _P, ctypes.c_size_t, _P]),
     "lstk_model_set_timing": (_I, [_P, _I]),
+    "lstk_debug_attn_plan": (_I, [_I, _I, _I, _I, _I, _I, _I, _I, _P]),
+    "lstk_model_debug_options": (_I, [_P, _I]),
     "lstk_model_timing": (_I, [_P, ctypes.POINTER(ctypes.c_double), ctypes.POINTER(ctypes.c_int64)]),
 }
 
@@ -199,6 +201,15 @@ def default_pool_bytes(table_bytes, weight_bytes, kv_bytes, device_total, device
     free - 3 GiB), at least 16 KiB."""
     return lib().lstk_pool_default_bytes(int(table_bytes), int(weight_bytes), int(kv_bytes), int(device_total),
                                          int(device_free))
+
+
+def attn_plan(n_tokens, n_head, n_kv, head_dim, kv_size, n_cells, cell_begin=0, rope_in=False):
+    """The attention launch plan the library takes for a step (host arithmetic, no device call):
+    (rows per work-group, row blocks, cells per chunk, chunks, RoPE inside the launch, work-groups)."""
+    out = (ctypes.c_int32 * 6)()
+    _check(lib().lstk_debug_attn_plan(int(n_tokens), int(n_head), int(n_kv), int(head_dim), int(kv_size), int(n_cells),
+                                      int(cell_begin), 1 if rope_in else 0, ctypes.cast(out, ctypes.c_void_p)))
+    return out[0], out[1], out[2], out[3], bool(out[4]), out[5]
 
 
 def repack_matrix(type_, rows, cols, gguf):
@@ -441,6 +452,11 @@ class Qwen3Model:
         states ([n_layer][T][n_embd] f32, T the step's tokens); None turns it off."""
         self._capture = states
         _check(lib().lstk_model_debug_capture(self._h, None if states is None else _ptr(states)))
+
+    def debug_options(self, rope_apart=False):
+        """Test hook: rope_apart runs a single-token step's RoPE in its own launch (multi-pass attention
+        chunks) instead of inside the attention launch (one-pass chunks)."""
+        _check(lib().lstk_model_debug_options(self._h, 1 if rope_apart else 0))
 
     def set_trace(self, path):
         """Routing trace to `path` (LSTKRTE1, read by localstack_amd.trace); None closes it."""

@@ -81,6 +81,7 @@ def lib():
             "or_qwen3_run_layer": (i32, [P, i32, P, i32, P]),
             "or_qwen3_head": (None, [P, P, P]),
             "or_qwen3_advance": (None, [P, i32]),
+            "or_qwen3_set_kv": (i32, [P, i32, i32, i32, P, P]),
         }
         for name, (res, args) in sig.items():
             fn = getattr(L, name)
@@ -430,6 +431,12 @@ class Qwen3:
 
     def advance(self, T):
         lib().or_qwen3_advance(self._h, int(T))
+
+    def set_kv(self, l, pos, K, V):
+        """Sets the fp16 K / V rows [n][n_head_kv * head_dim] of positions pos .. pos + n - 1 of layer l."""
+        K, V = _c(K, np.float16), _c(V, np.float16)
+        if lib().or_qwen3_set_kv(self._h, int(l), int(pos), K.shape[0], _p(K), _p(V)) != 0:
+            raise ValueError("positions outside the context")
 
     def __len__(self):
         return lib().or_qwen3_len(self._h)

@@ -181,6 +181,8 @@ int or_qwen3_decode(or_qwen3 *m, const int32_t *tokens, int T, float *logits, in
 int or_qwen3_run_layer(or_qwen3 *m, int l, float *x, int T, int32_t *ids);
 void or_qwen3_head(const or_qwen3 *m, const float *x, float *logits);
 void or_qwen3_advance(or_qwen3 *m, int T);
+/* Test input: fp16 K / V rows of positions pos .. pos + n - 1 of layer l set directly. */
+int or_qwen3_set_kv(or_qwen3 *m, int l, int pos, int n, const uint16_t *k, const uint16_t *v);
 int or_qwen3_len(const or_qwen3 *m);
 void or_qwen3_truncate(or_qwen3 *m, int keep);
 

@@ -736,7 +736,7 @@ int or_pool_acquire(or_pool *P, int layer, const int32_t *experts, int n, int32_
         }
         const int32_t s = lru_pop_head(p);
         if (s < 0) {
-            snprintf(err, err_len, "expert pool exhausted: layer %d needs more than %u slots at once", layer, p->n_slots);
+            snprintf(err, err_len, "layer %d: every one of the %u slots is pinned (pool exhausted)", layer, p->n_slots);
             return -1;
         }
         if (p->owner_layer[s] >= 0) P->slot_of[(size_t) p->owner_layer[s] * P->n_expert + p->owner_expert[s]] = -1;
@@ -1027,6 +1027,18 @@ void or_qwen3_head(const or_qwen3 *m, const float *x, float *logits) {
 }
 
 void or_qwen3_advance(or_qwen3 *m, int T) { m->len += T; }
+
+/* Writes the fp16 K and V rows [n][n_head_kv * head_dim] of positions pos .. pos + n - 1 of layer l (a
+ * cache given by the test instead of computed from tokens, e.g. a synthetic context). Returns 0, or -1
+ * when the positions fall outside the context. */
+int or_qwen3_set_kv(or_qwen3 *m, int l, int pos, int n, const uint16_t *k, const uint16_t *v) {
+    const or_qwen3_hparams *hp = &m->hp;
+    if (l < 0 || l >= hp->n_layer || pos < 0 || n < 0 || pos + n > m->max_ctx) return -1;
+    const size_t hk = (size_t) hp->n_head_kv * hp->head_dim, base = ((size_t) l * m->max_ctx + (size_t) pos) * hk;
+    memcpy(m->K + base, k, sizeof(uint16_t) * hk * (size_t) n);
+    memcpy(m->V + base, v, sizeof(uint16_t) * hk * (size_t) n);
+    return 0;
+}
 
 /* One step of the forward pass (src/qwen3.cpp:223-259) over T tokens: embedding, every layer (the last on
  * the last row only), logits [n_vocab] of the last token. trace (optional) [n_layer][T][k] receives the

@@ -2,7 +2,9 @@
 (localstack_amd/csrc/forward.hip: attn_plan, attn_kernel, attn_combine_kernel; buffers sized as
 model.cpp allocates them), for work-group targets of 512 (the build's), 256 and 128, over the shapes the
 tests and the benchmark run and past them: every global index stays inside its buffer, every LDS index
-inside its array, and the partial rows inside attn_part_rows. No GPU.
+inside its array, and the partial rows inside attn_part_rows. No GPU. The replayed plan is held equal to
+the library's own (lstk_debug_attn_plan, host code) at the build's target, so the replay cannot drift
+from the C++ it checks.
 
 Also a restatement of the kernel's online softmax over 64-cell passes (running max, sum and rescale per
 row, P split into fp16 hi + lo parts, passes in which a row sees no cell) against a direct softmax, and of
@@ -13,6 +15,7 @@ import pytest
 
 FA_CELLS = 64       # kFaCells
 AT_BLOCK = 256      # kAtBlock: 4 wavefronts
+MAX_PASSES = 2048   # kAttnMaxPasses: passes per chunk the skip map of many-token steps covers
 BLOCK = 256         # kBlock (attn_combine_kernel)
 LDS_MAX = 65536
 
@@ -43,7 +46,7 @@ def part_rows(n_batch, n_head):
 
 def check_launch(T, n_head, n_kv, hd, kv_size, n_cells, n_batch, target, rope_in, cell_begin=0):
     """Every access of one attention launch (and its combine) against the buffers' sizes."""
-    assert 1 <= T <= n_batch and 1 <= n_cells <= kv_size and kv_size % 256 == 0
+    assert 1 <= T <= n_batch and 1 <= n_cells <= kv_size and kv_size % 32 == 0
     assert 0 <= cell_begin < n_cells and cell_begin % 64 == 0
     grp = n_head // n_kv
     rb_rows, n_rowblk, chunk, n_chunk, rope_in = plan(T, n_head, n_kv, n_cells, target, rope_in, cell_begin)
@@ -88,9 +91,14 @@ def check_launch(T, n_head, n_kv, hd, kv_size, n_cells, n_batch, target, rope_in
         ki_max = ((gg * (hd // 4) + (hd // 4 - 1)) * kv_size + cc.max()) * 4 + 3
         assert cc.max() < kv_size and ki_max < kv_elems
     # LDS of attn_kernel: s_S [RB][64] f32, s_Ph / s_Pl [RB][72] u16, s_M / s_L / s_f [RB], s_pos [RB],
-    # s_q [16 hd] (NRT = 1) f32
-    lds = RB * FA_CELLS * 4 + 2 * RB * (FA_CELLS + 8) * 2 + 3 * RB * 4 + RB * 4 + (16 * hd if NRT == 1 else 1) * 4
+    # s_q [16 hd] (NRT = 1) f32, s_kv [2 hd] u16 (NRT = 1 and hd = 128: the new cell's K and V), s_live
+    # [MAX_PASSES] u8 (the pass-skipping instantiation of steps of >= 64 tokens)
+    skip = T >= 64 and not rope_in
+    lds = (RB * FA_CELLS * 4 + 2 * RB * (FA_CELLS + 8) * 2 + 3 * RB * 4 + RB * 4 + (16 * hd if NRT == 1 else 1) * 4 +
+           (2 * hd if NRT == 1 and hd == 128 else 4) * 2 + (MAX_PASSES if skip else 1))
     assert lds <= LDS_MAX
+    if skip:  # the skip map holds one byte per pass of the chunk
+        assert (chunk + FA_CELLS - 1) // FA_CELLS <= MAX_PASSES
     # outputs: n_chunk == 1 writes out[(t * n_head + h) * hd + d]; else part rows
     if n_chunk > 1:
         t = r // grp
@@ -105,8 +113,31 @@ def check_launch(T, n_head, n_kv, hd, kv_size, n_cells, n_batch, target, rope_in
     return rb_rows, n_rowblk, chunk, n_chunk, rope_in
 
 
+def test_replayed_plan_is_the_library_plan(lstk):
+    """plan() against lstk_debug_attn_plan over the shapes, token counts, cache sizes (multiples of 32 and
+    of 256), attended cells and range starts the model can pass."""
+    cases = 0
+    for n_head, n_kv, hd in SHAPES.values():
+        grp = n_head // n_kv
+        for kv_size in (96, 288, 1000 // 32 * 32, 1024, 4608, 4352 + 32, 65536, 65600, 131072):
+            for n_cells in sorted({min(kv_size, c) for c in (1, 64, 256, 300, 4352, 8192, 65536, 65600, 131072)}):
+                for cell_begin in sorted({0, (n_cells - 1) // 2 // 64 * 64, (n_cells - 1) // 64 * 64}):
+                    for T in (1, 2, 8, 32, 64, 256, 512):
+                        for rope in ((False, True) if T == 1 and grp <= 16 else (False,)):
+                            want = plan(T, n_head, n_kv, n_cells, 512, rope, cell_begin)
+                            got = lstk.attn_plan(T, n_head, n_kv, hd, kv_size, n_cells, cell_begin, rope)
+                            assert got[:5] == want, (n_head, kv_size, n_cells, cell_begin, T, rope)
+                            assert got[5] == n_kv * want[1] * want[3]
+                            cases += 1
+    assert cases > 1000
+    with pytest.raises(lstk.LstkError):
+        lstk.attn_plan(1, 32, 4, 128, 1000, 256)  # kv_size not a multiple of 32
+    with pytest.raises(lstk.LstkError):
+        lstk.attn_plan(1, 32, 4, 128, 1024, 256, cell_begin=32)  # range start not a multiple of 64
+
+
 SHAPES = {"tiny": (4, 2, 64), "30b": (32, 4, 128), "235b": (64, 4, 128)}
-CELLS = [256, 512, 4352, 8192, 8256, 16384, 32768, 65536, 131072]
+CELLS = [256, 300, 512, 4352, 8192, 8256, 16384, 32768, 65536, 65600, 131072]
 
 
 @pytest.mark.parametrize("target", [512, 256, 128])
@@ -116,20 +147,29 @@ def test_every_attention_index_in_bounds(target, shape):
     grp = n_head // n_kv
     plans = 0
     for n_cells in CELLS:
-        kv_size = (n_cells + 255) // 256 * 256
-        for T in (1, 2, 8, 32, 64, 256, 512):
-            for n_batch in sorted({T, 64, 512}):
-                if T > n_batch:
-                    continue
-                rope = T == 1 and grp <= 16
-                check_launch(T, n_head, n_kv, hd, kv_size, n_cells, n_batch, target, rope)
-                plans += 1
-                if n_cells > 256:
-                    # the sequence's lowest block high in the cache: the range starts there
-                    check_launch(T, n_head, n_kv, hd, kv_size, n_cells, n_batch, target, rope,
-                                 cell_begin=(n_cells - 256) // 64 * 64)
-                    plans += 1
+        # the cache sizes a model may be made with: multiples of 32 (the cells then end short of a 256 step)
+        for kv_size in sorted({(n_cells + 255) // 256 * 256, (n_cells + 31) // 32 * 32}):
+            plans += check_cells(n_head, n_kv, hd, grp, n_cells, kv_size, target)
     assert plans > 100
+
+
+def check_cells(n_head, n_kv, hd, grp, n_cells, kv_size, target):
+    """check_launch for every step size and n_batch over n_cells of a kv_size-cell cache, with the range
+    from cell 0 and from high in the cache; returns the number of launches checked."""
+    plans = 0
+    for T in (1, 2, 8, 32, 64, 256, 512):
+        for n_batch in sorted({T, 64, 512}):
+            if T > n_batch:
+                continue
+            rope = T == 1 and grp <= 16
+            check_launch(T, n_head, n_kv, hd, kv_size, n_cells, n_batch, target, rope)
+            plans += 1
+            if n_cells > 256:
+                # the sequence's lowest block high in the cache: the range starts there
+                check_launch(T, n_head, n_kv, hd, kv_size, n_cells, n_batch, target, rope,
+                             cell_begin=(n_cells - 256) // 64 * 64)
+                plans += 1
+    return plans
 
 
 def test_rope_in_keeps_single_pass_chunks():
