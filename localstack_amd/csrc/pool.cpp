@@ -696,8 +696,9 @@ int acquire(lstk_pool *P, int layer, const int32_t *experts, int n, int32_t *slo
         }
         const int32_t s = p.idle.take_oldest();
         if (s < 0) {
-            rc = fail(LSTK_E_EXHAUSTED, "expert pool exhausted: layer " + std::to_string(layer) + " needs more than " +
-                                            std::to_string(p.n_slots) + " slots at once; raise the pool size or lower n_batch");
+            rc = fail(LSTK_E_EXHAUSTED, "no idle slot for layer " + std::to_string(layer) + ": this call pins all " +
+                                            std::to_string(p.n_slots) + " slots of its shard (pool exhausted); create the "
+                                            "pool with more bytes or pass fewer tokens per call");
             break;
         }
         if (p.owner_layer[s] >= 0) P->slot_of[(size_t) p.owner_layer[s] * d.n_expert + p.owner_expert[s]] = -1;
