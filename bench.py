@@ -50,6 +50,7 @@ Q8_0 = 8
 Q4_K = 12
 HBM_PEAK_GBS = 8000.0
 INT8_PEAK_TOPS = 5000.0  # dense MFMA int8, MI355X
+FP16_PEAK_TFLOPS = 2500.0  # dense MFMA fp16, MI355X
 
 
 def parse():
@@ -429,9 +430,10 @@ def model30b_leg(torch, L, n_layer, ctx, steps, warmup, t_list=(1, 8, 32)):
     log(f"[bench] 30B model: {n_layer} layers built in {time.time() - t0:.1f}s, experts {store.total_bytes() / 1e9:.1f} GB, "
         f"KV cache {kv} cells")
     hq, hk = 32 * 128, 4 * 128
-    attn_w = (hq * H * 2 + hk * H * 2 * 2)  # q, o, k, v (bytes, fp16)
+    attn_w = 2 * hq * H * 2 + 2 * hk * H * 2  # q and o (hq x H each), k and v (hk x H each), fp16 bytes
     kv_b = ctx * hk * 2 * 2
-    moe_b = E * H * 2 + K * 3 * (F * (H // 256) * 144)
+    expert_mat_b = F * (H // 256) * 144  # one Q4_K expert matrix (884,736 B)
+    moe_b = E * H * 2 + K * 3 * expert_mat_b
     head_b = hp["n_vocab"] * H * 2
     per_tok = n_layer * (attn_w + kv_b + moe_b) + head_b
     res = {"n_layer": n_layer, "context": ctx, "bytes_per_token_T1": per_tok,
@@ -452,9 +454,11 @@ def model30b_leg(torch, L, n_layer, ctx, steps, warmup, t_list=(1, 8, 32)):
         model.truncate_seq(seq, ctx)
         model.set_timing(True)
         store.set_timing(True)
+        tr = torch.full((n_layer, T, K), -1, dtype=torch.int32, device=dev)
         for i in range(2):
-            model.decode(seq, toks[i], logits=logits)
+            model.decode(seq, toks[i], logits=logits, trace=tr)
         torch.cuda.synchronize()
+        distinct = distinct_experts(tr.cpu().numpy())
         mms, mn = model.timing()
         pms, pn = store.timing()
         model.set_timing(False)
@@ -485,13 +489,18 @@ def model30b_leg(torch, L, n_layer, ctx, steps, warmup, t_list=(1, 8, 32)):
         r = {"tok_s": T * 1000.0 / ms, "ms_per_step": ms, "steps": steps,
              "eager_stage_ms_per_step": stage, "moe_ms_per_step": moe_ms,
              "launches_per_step": (sum(mn) + sum(pn)) // 2, "seq_len_end": model.seq_len(seq)}
-        if T == 1:
-            r["gbs"] = per_tok / (ms * 1e-3) / 1e9
-            r["frac_hbm"] = r["gbs"] / HBM_PEAK_GBS
-            r["roofline"] = {"bound": "hbm", "achieved": r["gbs"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                             "frac": r["frac_hbm"],
-                             "what": "48 x (attention weights + K/V of the context + router + 8 Q4_K experts) + head"}
-            r["moe_gbs_eager"] = n_layer * moe_b / (moe_ms * 1e-3) / 1e9
+        # algorithmic HBM bytes of the step: every layer's attention weights, the K/V of the attended cells (read
+        # once for all T tokens), the router and the distinct experts the step routed to; the head on one row
+        ctx_now = ctx + T * (3 + warmup + steps // 2)
+        step_b = n_layer * (attn_w + ctx_now * hk * 2 * 2 + E * H * 2 + distinct * 3 * expert_mat_b) + head_b
+        r["bytes_per_step"] = step_b
+        r["distinct_experts_per_layer"] = distinct
+        r["gbs"] = step_b / (ms * 1e-3) / 1e9
+        r["frac_hbm"] = r["gbs"] / HBM_PEAK_GBS
+        r["roofline"] = {"bound": "hbm", "achieved": r["gbs"], "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": r["frac_hbm"],
+                         "what": f"48 x (attention weights + K/V of ~{ctx_now} cells + router + "
+                                 f"{distinct:.1f} distinct Q4_K experts) + head, per step of {T} tokens"}
+        r["moe_gbs_eager"] = n_layer * (E * H * 2 + distinct * 3 * expert_mat_b) / (moe_ms * 1e-3) / 1e9
         res[f"T{T}"] = r
         log(f"[bench] 30B model T={T}: {json.dumps(r)}")
         del graph
@@ -499,19 +508,43 @@ def model30b_leg(torch, L, n_layer, ctx, steps, warmup, t_list=(1, 8, 32)):
     # prompt processing: one 512-token step into an empty cache (eager: the step's host work included)
     prompt = rng.integers(0, hp["n_vocab"], n_prefill).astype(np.int32)
     times = []
+    tr = torch.full((n_layer, n_prefill, K), -1, dtype=torch.int32, device=dev)
     for rep in range(3):
         torch.cuda.synchronize()
         t0 = time.time()
-        model.decode(1000 + rep, prompt, logits=logits)
+        model.decode(1000 + rep, prompt, logits=logits, trace=tr if rep == 0 else None)
         torch.cuda.synchronize()
         times.append(time.time() - t0)
         model.remove_seq(1000 + rep)
     ms = 1e3 * min(times[1:])
-    res["prefill512"] = {"tok_s": n_prefill * 1000.0 / ms, "ms": ms}
+    active = distinct_experts(tr.cpu().numpy())
+    # algorithmic work of the step: the MoE products on the int8 matrix cores; Q/K/V, o-proj, the causal
+    # attention and the router in fp16 / f32; the head on the last row. Its roofline time is each part at
+    # its own dense peak, and the effective peak is the step's flops over that time.
+    T = n_prefill
+    f_moe = n_layer * 2.0 * T * K * 3 * H * F
+    f_dense = n_layer * (2.0 * T * (hq + 2 * hk) * H + 2.0 * T * hq * H + 4.0 * 32 * 128 * T * (T + 1) / 2 +
+                         2.0 * T * H * E) + 2.0 * H * hp["n_vocab"]
+    t_min = f_moe / (INT8_PEAK_TOPS * 1e12) + f_dense / (FP16_PEAK_TFLOPS * 1e12)
+    tflops = (f_moe + f_dense) / (ms * 1e-3) / 1e12
+    peak = (f_moe + f_dense) / t_min / 1e12
+    pb = n_layer * (attn_w + T * hk * 2 * 2 + E * H * 2 + active * 3 * expert_mat_b) + head_b
+    res["prefill512"] = {"tok_s": n_prefill * 1000.0 / ms, "ms": ms, "active_experts_per_layer": active,
+                         "tflop_per_step": (f_moe + f_dense) / 1e12, "moe_share_of_flops": f_moe / (f_moe + f_dense),
+                         "hbm_gbs": pb / (ms * 1e-3) / 1e9, "frac_hbm": pb / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS,
+                         "roofline": {"bound": "mfma", "achieved": tflops, "peak": peak, "unit": "TFLOP/s",
+                                      "frac": tflops / peak,
+                                      "what": "the step's algorithmic flops; peak = those flops over their time at the "
+                                              "dense MFMA peaks (MoE int8 5.0 POP/s, the rest fp16 2.5 PFLOP/s)"}}
     log(f"[bench] 30B model prefill {n_prefill}: {json.dumps(res['prefill512'])}")
     model.close()
     store.close()
     return res
+
+
+def distinct_experts(trace):
+    """Mean over layers of the distinct expert ids in a step's router trace [n_layer][T][k] (-1 = no row)."""
+    return float(np.mean([len(np.unique(t[t >= 0])) for t in trace]))
 
 
 def cpu_model():
@@ -549,6 +582,19 @@ def cpu_baseline(T, seconds):
         if el >= seconds or n >= 100000:
             break
     per_layer = el / n
+    # the same layer at T = 8 (config 2's second batch size), for a quarter of the time
+    x8 = [synth.activations(rng, 8, H) for _ in range(16)]
+    r8 = synth.activations(rng, 8, H)
+    cpu_ggml.moe_block(x8[0], gate_inp, up, gate, down, Q8_0, r8, E, F, K, n_threads=cores)
+    n8 = 0
+    t0 = time.time()
+    while True:
+        cpu_ggml.moe_block(x8[n8 % len(x8)], gate_inp, up, gate, down, Q8_0, r8, E, F, K, n_threads=cores)
+        n8 += 1
+        el8 = time.time() - t0
+        if el8 >= seconds / 4 or n8 >= 100000:
+            break
+    per_layer8 = el8 / n8
     del up, gate, down
     # prefill: 512 tokens, Q4_K experts, Zipf(1.1)-biased router (the GPU prefill leg's workload)
     up4, gate4, down4 = (synth.experts(rng, Q4_K, E, F, H), synth.experts(rng, Q4_K, E, F, H),
@@ -570,6 +616,8 @@ def cpu_baseline(T, seconds):
                 sample=f"{n} passes of one Qwen3-30B-A3B MoE layer (router + Q8_0 experts, T={T}, new hnorm rows "
                        f"each pass) by oracle/cpu_ggml.c on {cores} threads, scaled to 48 layers; "
                        f"{per_layer * 1e3:.3f} ms per layer",
+                t8={"value": 8 / (per_layer8 * N_LAYER), "unit": "tok/s", "ms_per_layer": per_layer8 * 1e3,
+                    "passes": n8, "what": "the same layer at T=8 (new hnorm rows each pass), scaled to 48 layers"},
                 prefill={"layer_tok_s": 512 / pre_layer, "ms_per_layer": pre_layer * 1e3, "passes": m,
                          "what": "512-token Q4_K Zipf(1.1) prefill through one MoE layer"})
 
