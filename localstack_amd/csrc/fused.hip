@@ -1,9 +1,12 @@
 // fused.hip - the MoE block of a single token (decode at batch 1) in one launch on gfx950.
 //
-// On MI355X every kernel boundary inside a replayed graph costs about 3.5 us (the cross-XCD cache
-// release / acquire between dependent kernels), which is most of a 5 us decode layer. So router,
-// gate/up + SwiGLU, down + router weight, k-way combine and residual (src/qwen3.cpp:175-214, :250)
-// run as one grid whose stages hand over inside the kernel:
+// An opt-in alternative to the three-launch single-token path (route, gate_up, down_combine). Each kernel
+// boundary there costs about 1.1-1.3 us inside a replayed graph, plus 0.4-1 us for the first read of the
+// previous kernel's output. Here router, gate/up + SwiGLU, down + router weight, k-way combine and residual
+// (src/qwen3.cpp:175-214, :250) run as one grid whose stages hand over inside the kernel. Measured on
+// MI355X it is slower: the 48-layer Qwen3-30B-A3B Q8_0 stack at T = 1 runs at 705 tok/s against 1181 tok/s
+// for the three launches (two A/B pairs, one box), because each hand-over waits for device-coherent stores
+// to complete and for flag polls across the XCDs' L2s. The stages:
 //   stage A  work-groups [0, nA): one router logit per wavefront, stored device-coherent, then flag_a.
 //   stage B  work-groups [0, nB): wait for flag_a, top-k in the work-group, then one gate/up unit
 //            (pair j, block of RW rows of gate and up) exactly as the multi-kernel gate_up kernel
