@@ -173,6 +173,42 @@ def test_block_repeatable_and_in_place(orc, lstk, dev):
     assert torch.equal(r2.cpu(), outs[0])
 
 
+def test_failed_copy_on_device_recovers(orc, lstk, dev):
+    """A host-tier copy that fails (injected where its hipMemcpyAsync would be issued) reports LSTK_E_IO,
+    and the slot it was meant for holds no expert afterwards: after release_all the next acquire of the
+    same ids copies that expert in again, and the experts run on the streamed slots give exactly the
+    resident pool's output (src/expert_store.cpp:268-285 unmaps a slot whose read failed)."""
+    import torch
+    import localstack_amd as L
+    cfg, layers, routers, res_store = model("tiny")
+    T, k, h = 4, cfg["k"], cfg["h"]
+    rng = np.random.default_rng(410)
+    x, resid = synth.activations(rng, T, h), synth.activations(rng, T, h)
+    rids, rw, _, _ = orc.router(x, routers[0], 1, k)
+    ref = torch.zeros((T, h), dtype=torch.float32, device=dev)
+    res_store.ffn(0, to_dev(x, dev), to_dev(rids, dev), to_dev(rw, dev), to_dev(resid, dev), ref)
+    types = [(cfg["types"],) + lb for lb in layers]
+    st = L.ExpertStore(2, h, cfg["f"], cfg["E"], k, T, types, pool_bytes=1, min_slots=2 * k + 2, streaming=True)
+    st.debug_fail_copies(1)
+    with pytest.raises(L.LstkError) as ei:
+        st.acquire(0, rids)
+    assert ei.value.code == L.E_IO and "copy failed" in str(ei.value)
+    st.release_all()
+    before = st.stats()
+    slots = st.acquire(0, rids)
+    after = st.stats()
+    n_distinct = len(set(rids.ravel().tolist()))
+    # the expert whose copy failed is a miss again; the others were copied in by the failed call
+    assert after["misses"] - before["misses"] >= 1 and after["hits"] + after["misses"] - before["hits"] - \
+        before["misses"] == rids.size
+    out = torch.zeros((T, h), dtype=torch.float32, device=dev)
+    st.ffn(0, to_dev(x, dev), to_dev(slots, dev), to_dev(rw, dev), to_dev(resid, dev), out)
+    st.release_all()
+    st.check()
+    print(f"[failed copy] {n_distinct} distinct experts, stats before {before} after {after}", flush=True)
+    np.testing.assert_array_equal(out.cpu().numpy(), ref.cpu().numpy())
+
+
 def test_streaming_pool_is_bit_identical_to_resident(orc, lstk, dev):
     # tools/test_streaming.sh: a pool that evicts constantly, one where everything fits, and a
     # chunked prefill must all give exactly the resident result
