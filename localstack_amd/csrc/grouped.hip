@@ -311,30 +311,37 @@ __device__ __forceinline__ void issue_stage(const GroupedParams &P, const GLds &
     for (int mt = 0; mt < kMT; mt++) bq[mt] = *reinterpret_cast<const u32x4 *>(xb + off(o.bh[mt]));
 }
 
-// Multiplies one staged super-block: the wavefront's 32 weight rows (lane % 32) with the chunk's
-// rows (M-tile mt = rows 32 mt .. 32 mt + 31), adding d_x (d_w isum - dmin_w imin) to acc[mt][r] for
-// chunk row 32 mt + 8 (r / 4) + 4 (lane / 32) + r % 4. bq[mt]: the lane's split group sums
-// (sub-blocks 4 (lane / 32) .. + 3 of chunk row 32 mt + lane % 32).
+// One staged super-block in two phases. Phase 1 (q4k_products) reads everything it needs from the stage -
+// the weight header and chunks of the wavefront's 32 rows (lane % 32), the chunk's activation fragments and
+// their rows' Q8_K scales - builds the weight planes and runs the int8 products of M-tile mt = chunk rows
+// 32 mt .. 32 mt + 31 into S. Phase 2 (q4k_accumulate) runs from registers only: the min-term product and
+// acc[mt][r] += d_x (d_w isum - dmin_w imin) for chunk row 32 mt + 8 (r / 4) + 4 (lane / 32) + r % 4. So
+// the next stage's loads can be issued between the two and land while phase 2 runs. bq[mt]: the lane's
+// split group sums (sub-blocks 4 (lane / 32) .. + 3 of chunk row 32 mt + lane % 32).
 //
 // Lane half h = lane / 32 takes qs bytes [32 c + 16 h, + 16) of each 64-value chunk c of its row:
 // low nibbles are values 64 c + 16 h + [0, 16) of sub-block 2 c, high nibbles values
 // 64 c + 32 + 16 h + [0, 16) of sub-block 2 c + 1, exactly the K slice the MFMA takes from the lane.
 // In the imin product, lane half h gives K entries 8 h .. 8 h + 7, the pairs of sub-blocks 4 h .. + 3.
-__device__ __forceinline__ void q4k_superblock(const unsigned char *st, int n, const u32x4 (&bq)[kMT],
-                                               float (&acc)[kMT][16]) {
+struct SbProducts {
+    i32x16 aH[kMT], aL[kMT];
+    float dx[kMT][16]; // the Q8_K scale of each output's chunk row
+    unsigned dd;       // the rows' d and dmin (fp16 pair)
+    unsigned mins;     // the 6-bit mins of sub-blocks 4 h .. 4 h + 3, one per byte
+};
+
+__device__ __forceinline__ void q4k_products(const unsigned char *st, int n, SbProducts &S) {
     const int wave = wave_id(), lane = threadIdx.x % kWave, h = lane / 32, r32 = lane % 32;
     const unsigned char *wl = st + kABytes + kDXBytes + wave * kWWaveBytes;
     const uint4 hdr = *reinterpret_cast<const uint4 *>(wl + r32 * 16);
     uint4 qv[4];
 #pragma unroll
     for (int c = 0; c < 4; c++) qv[c] = *reinterpret_cast<const uint4 *>(wl + (1 + 2 * c + h) * 512 + r32 * 16);
-    const float dw = h2f(hdr.x), dmin = h2f(hdr.x >> 16);
     const unsigned s0 = hdr.y, s1 = hdr.z, s2 = hdr.w;
     // the 6-bit scales of get_scale_min_k4, one per byte (sub-blocks 0-3 and 4-7), split as 8 sh + sl
     const unsigned sc_lo = s0 & 0x3f3f3f3fu, sc_hi = (s2 & 0x0f0f0f0fu) | ((s0 >> 2) & 0x30303030u);
     const unsigned sh4[2] = {(sc_lo >> 3) & 0x07070707u, (sc_hi >> 3) & 0x07070707u};
     const unsigned sl4[2] = {sc_lo & 0x07070707u, sc_hi & 0x07070707u};
-    i32x16 aH[kMT], aL[kMT];
 #pragma unroll
     for (int c = 0; c < 4; c++) {
 #pragma unroll
@@ -357,38 +364,47 @@ __device__ __forceinline__ void q4k_superblock(const unsigned char *st, int n, c
                 const i32x4 a = *reinterpret_cast<const i32x4 *>(st + (t * 16 + (part ^ (t & 15))) * 16);
                 if (c == 0 && nib == 0) {
                     const i32x16 z = {};
-                    aH[mt] = mfma_i8(a, bh, z);
-                    aL[mt] = mfma_i8(a, bl, z);
+                    S.aH[mt] = mfma_i8(a, bh, z);
+                    S.aL[mt] = mfma_i8(a, bl, z);
                 } else {
-                    aH[mt] = mfma_i8(a, bh, aH[mt]);
-                    aL[mt] = mfma_i8(a, bl, aL[mt]);
+                    S.aH[mt] = mfma_i8(a, bh, S.aH[mt]);
+                    S.aL[mt] = mfma_i8(a, bl, S.aL[mt]);
                 }
             }
         }
     }
-    // the 6-bit mins of sub-blocks 4 h .. 4 h + 3 (get_scale_min_k4), one per byte, then each as an fp16 pair
-    const unsigned mins = h ? ((s2 >> 4) & 0x0f0f0f0fu) | ((s1 >> 2) & 0x30303030u) : s1 & 0x3f3f3f3fu;
+    S.dd = hdr.x;
+    S.mins = h ? ((s2 >> 4) & 0x0f0f0f0fu) | ((s1 >> 2) & 0x30303030u) : s1 & 0x3f3f3f3fu;
+    const float *dxs = reinterpret_cast<const float *>(st + kABytes);
+#pragma unroll
+    for (int mt = 0; mt < kMT; mt++)
+#pragma unroll
+        for (int a4 = 0; a4 < 4; a4++) {
+            const float4 d4 = *reinterpret_cast<const float4 *>(dxs + mt * 32 + 8 * a4 + 4 * h);
+            S.dx[mt][4 * a4] = d4.x;
+            S.dx[mt][4 * a4 + 1] = d4.y;
+            S.dx[mt][4 * a4 + 2] = d4.z;
+            S.dx[mt][4 * a4 + 3] = d4.w;
+        }
+}
+
+__device__ __forceinline__ void q4k_accumulate(const SbProducts &S, int n, const u32x4 (&bq)[kMT], float (&acc)[kMT][16]) {
+    const float dw = h2f(S.dd), dmin = h2f(S.dd >> 16);
+    // each min as an fp16 pair
     u32x4 bm;
 #pragma unroll
     for (int i = 0; i < 4; i++) {
-        const float mf = (float) ((mins >> (8 * i)) & 0xffu);
+        const float mf = (float) ((S.mins >> (8 * i)) & 0xffu);
         bm[i] = __builtin_bit_cast(unsigned, __builtin_amdgcn_cvt_pkrtz(mf, mf));
     }
-    const float *dxs = reinterpret_cast<const float *>(st + kABytes);
 #pragma unroll
     for (int mt = 0; mt < kMT; mt++) {
         if (mt > 0 && n <= 32 * mt) continue;
         const f32x16 aM = mfma_f16(bq[mt], bm);
 #pragma unroll
-        for (int a4 = 0; a4 < 4; a4++) {
-            const float4 d4 = *reinterpret_cast<const float4 *>(dxs + mt * 32 + 8 * a4 + 4 * h);
-            const float dv[4] = {d4.x, d4.y, d4.z, d4.w};
-#pragma unroll
-            for (int b = 0; b < 4; b++) {
-                const int r = 4 * a4 + b;
-                const float isum = (float) (8 * aH[mt][r] + aL[mt][r]);
-                acc[mt][r] = fmaf(dv[b], fmaf(dw, isum, -(dmin * aM[r])), acc[mt][r]);
-            }
+        for (int r = 0; r < 16; r++) {
+            const float isum = (float) (8 * S.aH[mt][r] + S.aL[mt][r]);
+            acc[mt][r] = fmaf(S.dx[mt][r], fmaf(dw, isum, -(dmin * aM[r])), acc[mt][r]);
         }
     }
 }
@@ -406,13 +422,21 @@ __device__ __forceinline__ void q4k_rows(const GroupedParams &P, const GLds &g, 
         for (int r = 0; r < 16; r++) acc[mt][r] = 0.0f;
     const DmaOffs o = dma_offsets(P, g, n, row0);
     if constexpr (kNS == 1) {
+        // the next super-block's loads are issued as soon as every wavefront has read the stage, so they
+        // are in flight while the float epilogue of this one runs from registers
+        u32x4 cur[kMT];
+        issue_stage(P, g, o, w, 0, 0, cur);
         for (int sb = 0; sb < nsb; sb++) {
-            u32x4 cur[kMT];
-            issue_stage(P, g, o, w, sb, 0, cur);
             wait_vm<0>();
             __syncthreads();
-            q4k_superblock(g.ring, n, cur, acc);
+            SbProducts S;
+            q4k_products(g.ring, n, S);
             __syncthreads();
+            u32x4 nxt[kMT];
+            if (sb + 1 < nsb) issue_stage(P, g, o, w, sb + 1, 0, nxt);
+            q4k_accumulate(S, n, cur, acc);
+#pragma unroll
+            for (int mt = 0; mt < kMT; mt++) cur[mt] = nxt[mt];
         }
     } else {
         const bool w0 = threadIdx.x < kWave;
@@ -436,7 +460,9 @@ __device__ __forceinline__ void q4k_rows(const GroupedParams &P, const GLds &g, 
                 wait_vm<0>();
             }
             __syncthreads();
-            q4k_superblock(g.ring + (size_t) (sb % kNS) * kStageBytes, n, cur, acc);
+            SbProducts S;
+            q4k_products(g.ring + (size_t) (sb % kNS) * kStageBytes, n, S);
+            q4k_accumulate(S, n, cur, acc);
             __syncthreads();
         }
     }
