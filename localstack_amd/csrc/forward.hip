@@ -546,20 +546,15 @@ __device__ __forceinline__ half4v ld_half4(const uint16_t *p) {
     return __builtin_bit_cast(half4v, *reinterpret_cast<const uint2 *>(p));
 }
 
-// R1: the single-token RoPE-in launch at head size 128 with the step's cos / sin table and grp <= 16
-// (rope_token_128's case), an instantiation of its own so that its prologue's loads and the first
-// pass's K / V loads are in flight together.
-template <int HD, int NRT, bool R1, bool SKIP = false>
+// (The single-token launch at head size 128 with grp <= 16 is attn1_kernel below.)
+template <int HD, int NRT, bool SKIP = false>
 __global__ __launch_bounds__(kAtBlock) void attn_kernel(AttnParams P) {
-    static_assert(!R1 || (NRT == 1 && HD == 128), "R1 is the single-token head-size-128 launch");
-    static_assert(!(R1 && SKIP), "the single-token launch keeps every pass");
     constexpr int NK = HD / 16, DT = NK / 4, RB = 16 * NRT, PS = kFaCells + 8; // P row stride (halves)
     __shared__ float s_S[RB][kFaCells];
     __shared__ uint16_t s_Ph[RB][PS], s_Pl[RB][PS];
     __shared__ float s_M[RB], s_L[RB], s_f[RB];
     __shared__ int s_pos[RB];
     __shared__ float s_q[NRT == 1 ? 16 * HD : 1]; // rotated Q rows when this launch applies RoPE
-    __shared__ __align__(8) uint16_t s_kv[NRT == 1 && HD == 128 ? 2 * HD : 4]; // the new cell's K and V (fp16)
     const int tid = threadIdx.x, w = tid / kWave, l = tid & (kWave - 1), lr = l & 15, lq = l >> 4;
     const int grp = P.n_head / P.n_kv;
     const int g = blockIdx.x % P.n_kv, rest = blockIdx.x / P.n_kv;
@@ -572,16 +567,12 @@ __global__ __launch_bounds__(kAtBlock) void attn_kernel(AttnParams P) {
         s_L[tid] = 0.0f;
     }
     const int begin = P.cell_begin + c * P.chunk, end = min(begin + P.chunk, P.n_cells), last4 = P.kv_size - 4;
-    // fresh: this work-group's chunk holds the token's new cell, whose K / V it computes itself; its
-    // reads of that cell take them from LDS, and it stores them into the cache after its last barrier
-    const bool rope_in = R1 || (NRT == 1 && P.rope_in);
+    const bool rope_in = NRT == 1 && P.rope_in;
     const int cell0 = rope_in ? P.rope.cells[0] : -1;
     const bool owner = cell0 >= begin && cell0 < end;
-    const bool fresh = R1 && owner;
-    // The first pass's K / V fragments and cell-table entries are requested before the prologue
-    // (R1: right behind the prologue's own loads), except by a work-group that stores the new cell in
-    // its prologue and then reads it back (late).
-    const bool late = !R1 && rope_in && owner;
+    // The first pass's K / V fragments and cell-table entries are requested before the prologue, except
+    // by a work-group that stores the new cell in its prologue and then reads it back (late).
+    const bool late = rope_in && owner;
     const uint16_t *kb = P.kc + (size_t) g * (HD / 4) * P.kv_size * 4;
     half4v vf[4][DT]; // V fragments of a pass (B operand of O += P V): cells kc*16 + 4 lq .. +3, dim (w*DT + dt)*16 + lr
     half4v kf[NK];    // K fragments of the wavefront's 16 cells
@@ -600,21 +591,16 @@ __global__ __launch_bounds__(kAtBlock) void attn_kernel(AttnParams P) {
         cpos0 = P.cell_pos[cc];
     };
     // one token: every work-group rotates its own query rows (rope_kernel's work, bit for bit); the
-    // work-group whose chunk holds the token's cell also computes that cell's K and V of KV head g
-    // (kept in LDS with R1, else stored into the cache with its cell-table entries here)
-    if constexpr (R1) {
-        rope_token_128(P.rope, g, grp, owner, s_q, s_kv, [&] { load_pass(begin); });
-        __syncthreads();
-    } else {
-        if (!late) load_pass(begin);
-        if (rope_in) {
-            if (owner) {
-                if (w == 0) rope_head(P.rope, 0, P.n_head + g, nullptr, true);
-                else if (w == 1) rope_head(P.rope, 0, P.n_head + P.n_kv + g, nullptr, false);
-            }
-            for (int r = w; r < grp; r += kAtBlock / kWave) rope_head(P.rope, 0, g * grp + r, s_q + r * HD, false);
-            __syncthreads();
+    // work-group whose chunk holds the token's cell also computes that cell's K and V of KV head g and
+    // stores them into the cache with its cell-table entries
+    if (!late) load_pass(begin);
+    if (rope_in) {
+        if (owner) {
+            if (w == 0) rope_head(P.rope, 0, P.n_head + g, nullptr, true);
+            else if (w == 1) rope_head(P.rope, 0, P.n_head + P.n_kv + g, nullptr, false);
         }
+        for (int r = w; r < grp; r += kAtBlock / kWave) rope_head(P.rope, 0, g * grp + r, s_q + r * HD, false);
+        __syncthreads();
     }
     // Q fragments (A operand): row rt*16 + lr, dims ks*16 + 4 lq .. +3
     half4v qa[NRT][NK];
@@ -678,14 +664,8 @@ __global__ __launch_bounds__(kAtBlock) void attn_kernel(AttnParams P) {
         // S = Q K^T for this wavefront's 16 cells
         const int cell = c0 + 16 * w + lr;
         const int cc = min(cell, P.kv_size - 1);
-        bool live = cell < end && cseq == P.seq;
-        int cpos = cpos0;
-        if (fresh && cc == cell0) {
-#pragma unroll
-            for (int ks = 0; ks < NK; ks++) kf[ks] = ld_half4(&s_kv[(ks * 4 + lq) * 4]);
-            live = true;
-            cpos = P.rope.pos[0];
-        }
+        const bool live = cell < end && cseq == P.seq;
+        const int cpos = cpos0;
 #pragma unroll
         for (int rt = 0; rt < NRT; rt++) {
             f32x4v sacc = f32x4v{0, 0, 0, 0};
@@ -769,18 +749,6 @@ __global__ __launch_bounds__(kAtBlock) void attn_kernel(AttnParams P) {
             }
         }
         __syncthreads();
-        if (fresh) {
-            // the new cell's V in the fragment that holds it
-#pragma unroll
-            for (int kc = 0; kc < 4; kc++) {
-                const int cg = c0 + kc * 16 + 4 * lq;
-                if (cg <= last4 && cell0 >= cg && cell0 < cg + 4) {
-#pragma unroll
-                    for (int dt = 0; dt < DT; dt++)
-                        vf[kc][dt][cell0 - cg] = __builtin_bit_cast(_Float16, s_kv[HD + (w * DT + dt) * 16 + lr]);
-                }
-            }
-        }
         // O = O * f + P V
 #pragma unroll
         for (int rt = 0; rt < NRT; rt++) {
@@ -838,14 +806,153 @@ __global__ __launch_bounds__(kAtBlock) void attn_kernel(AttnParams P) {
             }
         }
     }
-    if (fresh && w < 2) {
+}
+
+// ------------------------------------------------------------------------------------------------
+// Single-token attention at head size 128 with RoPE inside (grp <= 16 query heads per KV head): each
+// wavefront runs its own 16 cells of the work-group's 64-cell chunk from registers to registers, so
+// the pass has no barrier and no LDS round trip. With the K fragments as the A operand and the query
+// rows as the B operand the product comes out transposed, S^T [cell][row]: lane (row j, quad q) holds
+// cells 4q .. 4q + 3 of row j, which is exactly the B operand of O^T = V^T P^T (and the V fragments
+// of the cache are the A operand as they stand). A row's softmax state and output stay in the lanes
+// of that row; the row's max over its 16 cells takes two lane exchanges (quads 0-3). At the end the
+// four wavefronts' (max, sum, output) rows are merged through LDS, and the merged row is the chunk's
+// partial (or, with one chunk, the output). Probabilities enter the product as fp16 hi + lo parts
+// (p = hi + lo to 2^-22), Q and K as fp16, all accumulation in f32, as in attn_kernel.
+// ------------------------------------------------------------------------------------------------
+constexpr int kA1Cells = 16; // cells per wavefront
+static_assert(kA1Cells * (kAtBlock / kWave) == kFaCells, "a work-group covers one 64-cell chunk");
+__device__ __forceinline__ float xor_lanes(float v, int m) { return __shfl_xor(v, m, kWave); }
+
+__global__ __launch_bounds__(kAtBlock) void attn1_kernel(AttnParams P) {
+    constexpr int HD = 128, NK = HD / 16, NW = kAtBlock / kWave, RS = HD + 4;
+    __shared__ float s_q[16 * HD];
+    __shared__ __align__(8) uint16_t s_kv[2 * HD];
+    __shared__ __align__(16) float s_o[NW][16][RS];
+    __shared__ float s_m[NW][16], s_l[NW][16];
+    const int tid = threadIdx.x, w = tid / kWave, l = tid & (kWave - 1), lr = l & 15, lq = l >> 4;
+    const int grp = P.n_head / P.n_kv;
+    const int g = blockIdx.x % P.n_kv, c = blockIdx.x / P.n_kv;
+    const int begin = P.cell_begin + c * P.chunk, end = min(begin + P.chunk, P.n_cells);
+    const int cell0 = P.rope.cells[0], pos = P.rope.pos[0];
+    const bool owner = cell0 >= begin && cell0 < end;
+    const int wb = begin + w * kA1Cells; // this wavefront's cells [wb, wb + 16)
+    const uint16_t *kb = P.kc + (size_t) g * (HD / 4) * P.kv_size * 4;
+    half4v kf[NK]; // A operand of S^T: cell wb + lr, dims ks*16 + 4 lq .. +3
+    half4v vf[NK]; // A operand of O^T: dim dt*16 + lr, cells wb + 4 lq .. +3
+    int4 cseq, cpos; // cell-table entries of cells wb + 4 lq .. +3
+    auto loads = [&] {
+        const int ck = min(wb + lr, P.kv_size - 1), cv = min(wb + 4 * lq, P.kv_size - 4);
+#pragma unroll
+        for (int ks = 0; ks < NK; ks++) kf[ks] = ld_half4(kb + ((size_t) (ks * 4 + lq) * P.kv_size + ck) * 4);
+#pragma unroll
+        for (int dt = 0; dt < NK; dt++) vf[dt] = ld_half4(P.vc + v_index(g, dt * 16 + lr, cv, HD, P.kv_size));
+        cseq = *reinterpret_cast<const int4 *>(P.cell_seq + cv);
+        cpos = *reinterpret_cast<const int4 *>(P.cell_pos + cv);
+    };
+    rope_token_128(P.rope, g, grp, owner, s_q, s_kv, loads);
+    __syncthreads();
+    // B operand of S^T: query row lr (zero past grp), dims ks*16 + 4 lq .. +3
+    half4v qb[NK];
+#pragma unroll
+    for (int ks = 0; ks < NK; ks++) {
+        const float4 v = *reinterpret_cast<const float4 *>(s_q + min(lr, grp - 1) * HD + ks * 16 + 4 * lq);
+        qb[ks] = lr < grp ? half4v{(_Float16) v.x, (_Float16) v.y, (_Float16) v.z, (_Float16) v.w} : half4v{0, 0, 0, 0};
+    }
+    // the token's own cell: K and V from LDS (the cache gets them at the end), visible to the token
+    if (owner) {
+        if (wb + lr == cell0) {
+#pragma unroll
+            for (int ks = 0; ks < NK; ks++) kf[ks] = ld_half4(&s_kv[(ks * 4 + lq) * 4]);
+        }
+        const int d = cell0 - (wb + 4 * lq);
+        if (d >= 0 && d < 4) {
+#pragma unroll
+            for (int dt = 0; dt < NK; dt++) vf[dt][d] = __builtin_bit_cast(_Float16, s_kv[HD + dt * 16 + lr]);
+        }
+    }
+    f32x4v s = f32x4v{0, 0, 0, 0};
+#pragma unroll
+    for (int ks = 0; ks < NK; ks++) s = mfma16(kf[ks], qb[ks], s);
+    const int cs[4] = {cseq.x, cseq.y, cseq.z, cseq.w}, cp[4] = {cpos.x, cpos.y, cpos.z, cpos.w};
+    float sv[4];
+    float m = -INFINITY;
+#pragma unroll
+    for (int v = 0; v < 4; v++) {
+        const int cell = wb + 4 * lq + v;
+        const bool vis = cell < end && ((cs[v] == P.seq && cp[v] <= pos) || (owner && cell == cell0));
+        sv[v] = vis ? s[v] * P.scale : -INFINITY;
+        m = fmaxf(m, sv[v]);
+    }
+    m = fmaxf(m, xor_lanes(m, 16));
+    m = fmaxf(m, xor_lanes(m, 32));
+    float lsum = 0.0f;
+    half4v ph, pl;
+#pragma unroll
+    for (int v = 0; v < 4; v++) {
+        const float p = sv[v] == -INFINITY ? 0.0f : expf(sv[v] - m);
+        ph[v] = (_Float16) p;
+        pl[v] = (_Float16) (p - (float) ph[v]);
+        lsum += p;
+    }
+    lsum += xor_lanes(lsum, 16);
+    lsum += xor_lanes(lsum, 32);
+    f32x4v o[NK];
+#pragma unroll
+    for (int dt = 0; dt < NK; dt++) {
+        o[dt] = mfma16(vf[dt], ph, f32x4v{0, 0, 0, 0});
+        o[dt] = mfma16(vf[dt], pl, o[dt]);
+    }
+    // lane (row lr, quad lq) holds dims dt*16 + 4 lq .. +3 of row lr
+    if (lq == 0) {
+        s_m[w][lr] = m;
+        s_l[w][lr] = lsum;
+    }
+#pragma unroll
+    for (int dt = 0; dt < NK; dt++) *reinterpret_cast<f32x4v *>(&s_o[w][lr][dt * 16 + 4 * lq]) = o[dt];
+    __syncthreads();
+    // merge the wavefronts: thread (row r, dims 4 dq .. +3)
+    for (int i = tid; i < grp * (HD / 4); i += kAtBlock) {
+        const int r = i / (HD / 4), dq = i % (HD / 4), h = g * grp + r;
+        float M = s_m[0][r];
+#pragma unroll
+        for (int u = 1; u < NW; u++) M = fmaxf(M, s_m[u][r]);
+        float L = 0.0f;
+        float4 acc = make_float4(0, 0, 0, 0);
+#pragma unroll
+        for (int u = 0; u < NW; u++) {
+            const float f = s_m[u][r] == -INFINITY ? 0.0f : expf(s_m[u][r] - M);
+            const float4 ov = *reinterpret_cast<const float4 *>(&s_o[u][r][4 * dq]);
+            L += s_l[u][r] * f;
+            acc.x += ov.x * f;
+            acc.y += ov.y * f;
+            acc.z += ov.z * f;
+            acc.w += ov.w * f;
+        }
+        if (P.n_chunk == 1) {
+            const float4 y = make_float4(acc.x / L, acc.y / L, acc.z / L, acc.w / L);
+            *reinterpret_cast<float4 *>(P.out + (size_t) h * HD + 4 * dq) = y;
+            if (P.out16) {
+                uint16_t *o16 = P.out16 + (size_t) h * HD + 4 * dq;
+                *reinterpret_cast<uint2 *>(o16) = make_uint2(pack2(y.x, y.y), pack2(y.z, y.w));
+            }
+        } else {
+            float *pp = P.part + ((size_t) h * P.n_chunk + c) * RS;
+            *reinterpret_cast<float4 *>(pp + 4 + 4 * dq) = acc;
+            if (dq == 0) {
+                pp[0] = M;
+                pp[1] = L;
+            }
+        }
+    }
+    if (owner && w < 2) {
         // the new cell into the cache (read by later launches only): K and the cell tables by
         // wavefront 0, V by wavefront 1
         const RopeParams &R = P.rope;
         if (w == 0) {
             if (l == 0) {
                 R.cell_seq[cell0] = R.seq;
-                R.cell_pos[cell0] = R.pos[0];
+                R.cell_pos[cell0] = pos;
             }
             R.kc[k_index(g, l, cell0, HD, R.kv_size)] = s_kv[l];
             R.kc[k_index(g, l + HD / 2, cell0, HD, R.kv_size)] = s_kv[l + HD / 2];
@@ -1088,18 +1195,18 @@ template <int HD>
 hipError_t launch_attn_hd(const AttnParams &P, hipStream_t st, const LaunchTiming *tm) {
     const dim3 grid(P.n_kv * P.n_chunk * P.n_rowblk), block(kAtBlock);
     if constexpr (HD == 128) {
-        if (P.rb_rows == 16 && P.rope_in && P.n_head / P.n_kv <= 4 * kRopeMaxQ && P.rope.cs)
-            return launch(attn_kernel<HD, 1, true>, grid, block, 0, st, tm, P);
+        if (P.rb_rows == 16 && P.rope_in && P.n_head / P.n_kv <= 4 * kRopeMaxQ && P.rope.cs && P.chunk == kFaCells)
+            return launch(attn1_kernel, grid, block, 0, st, tm, P);
     }
     // steps of many tokens (prompts): the instantiation that skips passes with no cell of the sequence
     if (P.T >= kAttnSkipMinT && !P.rope_in) {
-        if (P.rb_rows == 16) return launch(attn_kernel<HD, 1, false, true>, grid, block, 0, st, tm, P);
-        if (P.rb_rows == 32) return launch(attn_kernel<HD, 2, false, true>, grid, block, 0, st, tm, P);
-        return launch(attn_kernel<HD, 4, false, true>, grid, block, 0, st, tm, P);
+        if (P.rb_rows == 16) return launch(attn_kernel<HD, 1, true>, grid, block, 0, st, tm, P);
+        if (P.rb_rows == 32) return launch(attn_kernel<HD, 2, true>, grid, block, 0, st, tm, P);
+        return launch(attn_kernel<HD, 4, true>, grid, block, 0, st, tm, P);
     }
-    if (P.rb_rows == 16) return launch(attn_kernel<HD, 1, false>, grid, block, 0, st, tm, P);
-    if (P.rb_rows == 32) return launch(attn_kernel<HD, 2, false>, grid, block, 0, st, tm, P);
-    return launch(attn_kernel<HD, 4, false>, grid, block, 0, st, tm, P);
+    if (P.rb_rows == 16) return launch(attn_kernel<HD, 1>, grid, block, 0, st, tm, P);
+    if (P.rb_rows == 32) return launch(attn_kernel<HD, 2>, grid, block, 0, st, tm, P);
+    return launch(attn_kernel<HD, 4>, grid, block, 0, st, tm, P);
 }
 
 hipError_t launch_attn(const AttnParams &P, hipStream_t st, const LaunchTiming *tm) {
