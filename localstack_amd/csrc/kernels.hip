@@ -562,7 +562,8 @@ __global__ __launch_bounds__(NT) void gate_up_kernel(GateUpParams P) {
     // registers before the weight loads are issued (a single token of up to 8192 values), so the
     // LDS staging below waits for them only; the rest of a chunk is staged from global memory.
     constexpr int kXr = 2;
-    const int nt0 = min(kTC, cnt);
+    const int TC = min(kTC, P.gp.T); // staging slots (a pair per token at most, so a step of T < kTC tokens needs T)
+    const int nt0 = min(TC, cnt);
     const int n16 = nt0 * h16, n32 = nt0 * h32;
     const int bd = blockDim.x;
     xvec xr[kXr];
@@ -588,9 +589,9 @@ __global__ __launch_bounds__(NT) void gate_up_kernel(GateUpParams P) {
         for (int c = 0; c < C; c++) w[s][c] = load_weights(reinterpret_cast<const uint4 *>(base + chunk_offset(C, f, sb, c, row)));
     }
     int8_t *xs = reinterpret_cast<int8_t *>(work);
-    float *xd = reinterpret_cast<float *>(work + (size_t) kTC * h);
-    int *xb = reinterpret_cast<int *>(xd + kTC * h32);
-    float *red = reinterpret_cast<float *>(xb + kTC * h32);
+    float *xd = reinterpret_cast<float *>(work + (size_t) TC * h);
+    int *xb = reinterpret_cast<int *>(xd + TC * h32);
+    float *red = reinterpret_cast<float *>(xb + TC * h32);
 #pragma unroll
     for (int u = 0; u < kXr; u++) {
         const int idx = tid + u * bd;
@@ -607,8 +608,33 @@ __global__ __launch_bounds__(NT) void gate_up_kernel(GateUpParams P) {
         xd[idx] = P.xq.d[o];
         if (WT == kTypeQ4_K) xb[idx] = P.xq.bs[o];
     }
-    for (int c0 = 0; c0 < cnt; c0 += kTC) {
-        const int nt = min(kTC, cnt - c0);
+    if constexpr (ROUTE) {
+        // one token (cnt == 1): straight-line code, the super-blocks one after the other (in the
+        // chunk loop below the compiler unpacks every super-block's nibbles ahead of the loop,
+        // which at two super-blocks per thread holds the work-group to two wavefronts per SIMD)
+        __syncthreads();
+        float acc = 0.0f;
+#pragma unroll
+        for (int s = 0; s < S; s++) {
+            const int sb = g + s * G;
+            acc = dot_sb<WT>(w[s], xs + sb * 256, xd + sb * 8, xb + sb * 8, acc);
+            __builtin_amdgcn_sched_barrier(0);
+        }
+        red[(g * 2 + m) * RW + r] = acc;
+        __syncthreads();
+        if (tid < RW) {
+            float gs = red[r], us = red[RW + r];
+            for (int gg = 1; gg < G; gg++) {
+                gs += red[(gg * 2) * RW + r];
+                us += red[(gg * 2 + 1) * RW + r];
+            }
+            const float a = (gs / (1.0f + expf(-gs))) * us;
+            P.act[(size_t) gl.list[0] * f + blockIdx.x * RW + r] = a;
+        }
+        return;
+    }
+    for (int c0 = 0; c0 < cnt; c0 += TC) {
+        const int nt = min(TC, cnt - c0);
         if (c0 > 0) { // later chunks (more than 8 tokens on one expert) are staged here
             for (int tc = 0; tc < nt; tc++) {
                 const int t = gl.list[c0 + tc] / k;
@@ -799,8 +825,8 @@ __device__ __forceinline__ void q8k_block_lanes(const float (&v)[VPT], int lanes
 // SEG > 0 (Q8_K activations with k * nsbf * rd0 threads exactly): the rd0 threads of pair j and
 // super-block sb quantize that 256-value Q8_K block together, SEG = 256 / rd0 values each, in one
 // pass (q8k_block_lanes); otherwise every thread takes NP passes of 8 values (quantize_row).
-template <int WT, int NP, int R, int SEG>
-__global__ __launch_bounds__(kBlock) void down_combine_kernel(DownCombineParams P, int rd0) {
+template <int WT, int NP, int R, int SEG, int NT = kBlock>
+__global__ __launch_bounds__(NT) void down_combine_kernel(DownCombineParams P, int rd0) {
     constexpr int C = chunks_of(WT);
     constexpr int QT = WT == kTypeQ8_0 ? kTypeQ8_0 : kTypeQ4_K; // Q8_K activations for every k-quant
     extern __shared__ __align__(16) unsigned char smem[];
@@ -1012,10 +1038,12 @@ hipError_t launch_route_g(const RouteParams &P, hipStream_t st, const LaunchTimi
     }
 }
 
-// Dynamic LDS of a gate_up launch: grouping, kTC staged tokens and the partial sums of RW rows.
+// Dynamic LDS of a gate_up launch: grouping, min(kTC, T) staged tokens and the partial sums of RW rows.
+// (A single token's launch at h 4096 then takes 12 KB instead of 55 KB, so its 768 work-groups are
+// resident at once instead of in two rounds.)
 size_t gate_up_lds(int T, int k, int n_bins, int route, int h, int G, int RW) {
-    return align16(group_lds_bytes(T, k, n_bins, route)) + 16 + (size_t) kTC * h + (size_t) 2 * kTC * (h / 32) * 4 +
-           (size_t) kTC * G * 2 * RW * 4;
+    const size_t tc = (size_t) std::min(kTC, T);
+    return align16(group_lds_bytes(T, k, n_bins, route)) + 16 + tc * h + 2 * tc * (h / 32) * 4 + tc * G * 2 * RW * 4;
 }
 
 template <int WT, int S>
@@ -1050,11 +1078,15 @@ hipError_t launch_down_t(const DownParams &P, int G, hipStream_t st, const Launc
 }
 
 // Row stride of a down_combine work-group: the largest power of two rd0 with k * nsbf * rd0 <= 256
-// threads.
-int down_combine_rows(int f, int k) {
+// threads, then doubled up to kDcMaxThreads threads while the grid keeps 256 work-groups at one row
+// per thread (the 235B shape: 8 x 6 x 8 = 384 threads with 2 rows each instead of 192 with 4, so the
+// work-group's quantization and dot products spread over twice the wavefronts).
+constexpr int kDcMaxThreads = 512;
+int down_combine_rows(int h, int f, int k) {
     const int per = k * (f / 256);
     int rd = 1;
     while (rd * 2 * per <= kBlock) rd *= 2;
+    while (rd * 2 * per <= kDcMaxThreads && h % (rd * 2) == 0 && h / (rd * 2) >= 256) rd *= 2;
     return rd;
 }
 
@@ -1071,6 +1103,15 @@ template <int WT, int R>
 hipError_t launch_down_combine_r(const DownCombineParams &P, int rd0, int np, size_t lds, int threads, hipStream_t st,
                                  const LaunchTiming *tm) {
     const dim3 grid(P.h / (rd0 * R)), block(threads);
+    if (threads > kBlock) {
+        // past 256 threads only the one-block-per-(pair, super-block) quantization (k-quants)
+        if (WT == kTypeQ8_0 || threads != P.k * (P.f / 256) * rd0) return hipErrorInvalidValue;
+        switch (rd0) {
+            case 8: return launch(down_combine_kernel<WT, 1, R, 32, kDcMaxThreads>, grid, block, lds, st, tm, P, rd0);
+            case 16: return launch(down_combine_kernel<WT, 1, R, 16, kDcMaxThreads>, grid, block, lds, st, tm, P, rd0);
+            default: return hipErrorInvalidValue;
+        }
+    }
     if (WT != kTypeQ8_0 && threads == P.k * (P.f / 256) * rd0) {
         // one Q8_K block per (pair, super-block), quantized by that combination's rd0 threads
         switch (rd0) {
@@ -1089,7 +1130,7 @@ hipError_t launch_down_combine_r(const DownCombineParams &P, int rd0, int np, si
 
 template <int WT>
 hipError_t launch_down_combine_t(const DownCombineParams &P, hipStream_t st, const LaunchTiming *tm) {
-    const int rd0 = down_combine_rows(P.f, P.k), nsbf = P.f / 256, nact = P.k * P.f;
+    const int rd0 = down_combine_rows(P.h, P.f, P.k), nsbf = P.f / 256, nact = P.k * P.f;
     const int R = down_combine_rows_per_thread(WT, P.h, rd0);
     const int threads = (P.k * nsbf * rd0 + kWave - 1) / kWave * kWave;
     const size_t lds = (size_t) nact + (size_t) nact / 32 * 8 + (size_t) P.k * nsbf * rd0 * R * 4 + (size_t) P.k * 4;
@@ -1106,7 +1147,7 @@ hipError_t launch_down_combine_t(const DownCombineParams &P, hipStream_t st, con
 bool down_combine_supported(int h, int f, int k) {
     if (k < 1 || k > kMaxK || f % 256 != 0 || h % 256 != 0 || (long) k * f > kDcMaxAct) return false;
     if (k * (f / 256) > kBlock) return false;
-    const int rd = down_combine_rows(f, k);
+    const int rd = down_combine_rows(h, f, k);
     const int threads = (k * (f / 256) * rd + kWave - 1) / kWave * kWave;
     return h % rd == 0 && (long) k * f <= 8L * threads * 8; // at most 8 passes (or blocks) per thread
 }
