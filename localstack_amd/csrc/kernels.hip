@@ -925,30 +925,34 @@ __global__ __launch_bounds__(NT) void down_combine_kernel(DownCombineParams P, i
             part[(j * rd + ir * rd0 + rr) * nsbf + sb] = dot_sb<WT>(w[ir], qs + o, qd + o / 32, qb + o / 32, 0.0f);
     }
     __syncthreads();
-    if (tid < rd) {
-        // slots 8 at a time, super-blocks up to kDcSb at a time: every LDS read of a batch is issued
-        // before the sums, which keep their order (super-blocks left to right, then slots)
+    // slot j's output of row r: its super-blocks summed left to right, times the router weight
+    // (item j * rd + r)
+    float *ys = s_w + k;
+    for (int i = tid; i < k * rd; i += blockDim.x) {
+        const int jj = i / rd, r2 = i - jj * rd;
+        const float *pp = part + (jj * rd + r2) * nsbf;
         constexpr int kDcSb = 8;
+        float pv[kDcSb];
+#pragma unroll
+        for (int s2 = 0; s2 < kDcSb; s2++) pv[s2] = pp[min(s2, nsbf - 1)];
+        float ds = pv[0];
+#pragma unroll
+        for (int s2 = 1; s2 < kDcSb; s2++) ds = s2 < nsbf ? ds + pv[s2] : ds;
+        for (int s2 = kDcSb; s2 < nsbf; s2++) ds += pp[s2];
+        ys[i] = ds * s_w[jj];
+    }
+    __syncthreads();
+    if (tid < rd) {
+        // the k-way sum in slot order, every LDS read of a batch of 8 slots issued before the sums
         float acc = 0.0f;
         for (int jj0 = 0; jj0 < k; jj0 += 8) {
-            float pv[8][kDcSb], wv[8];
+            float yv[8];
 #pragma unroll
-            for (int u = 0; u < 8; u++) {
-                const int jj = min(jj0 + u, k - 1);
-                const float *pp = part + (jj * rd + tid) * nsbf;
-#pragma unroll
-                for (int s2 = 0; s2 < kDcSb; s2++) pv[u][s2] = pp[min(s2, nsbf - 1)];
-                wv[u] = s_w[jj];
-            }
+            for (int u = 0; u < 8; u++) yv[u] = ys[min(jj0 + u, k - 1) * rd + tid];
 #pragma unroll
             for (int u = 0; u < 8; u++) {
                 const int jj = jj0 + u;
-                float ds = pv[u][0];
-#pragma unroll
-                for (int s2 = 1; s2 < kDcSb; s2++) ds = s2 < nsbf ? ds + pv[u][s2] : ds;
-                for (int s2 = kDcSb; s2 < nsbf; s2++) ds += part[(min(jj, k - 1) * rd + tid) * nsbf + s2];
-                const float y = ds * wv[u];
-                acc = jj < k ? (jj == 0 ? y : acc + y) : acc;
+                acc = jj < k ? (jj == 0 ? yv[u] : acc + yv[u]) : acc;
             }
         }
         P.out[blockIdx.x * rd + tid] = acc + resid;
@@ -1133,7 +1137,8 @@ hipError_t launch_down_combine_t(const DownCombineParams &P, hipStream_t st, con
     const int rd0 = down_combine_rows(P.h, P.f, P.k), nsbf = P.f / 256, nact = P.k * P.f;
     const int R = down_combine_rows_per_thread(WT, P.h, rd0);
     const int threads = (P.k * nsbf * rd0 + kWave - 1) / kWave * kWave;
-    const size_t lds = (size_t) nact + (size_t) nact / 32 * 8 + (size_t) P.k * nsbf * rd0 * R * 4 + (size_t) P.k * 4;
+    const size_t lds = (size_t) nact + (size_t) nact / 32 * 8 + (size_t) P.k * nsbf * rd0 * R * 4 + (size_t) P.k * 4 +
+                       (size_t) P.k * rd0 * R * 4;
     // Q8_0: whole 32-value blocks per thread; Q8_K: passes of 8 values per thread
     const int per = WT != kTypeQ8_0 ? threads * 8 : threads * 32;
     const int np = (nact + per - 1) / per;
