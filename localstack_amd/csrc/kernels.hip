@@ -1082,15 +1082,23 @@ hipError_t launch_down_t(const DownParams &P, int G, hipStream_t st, const Launc
 }
 
 // Row stride of a down_combine work-group: the largest power of two rd0 with k * nsbf * rd0 <= 256
-// threads, then doubled up to kDcMaxThreads threads while the grid keeps 256 work-groups at one row
-// per thread (the 235B shape: 8 x 6 x 8 = 384 threads with 2 rows each instead of 192 with 4, so the
-// work-group's quantization and dot products spread over twice the wavefronts).
-constexpr int kDcMaxThreads = 512;
-int down_combine_rows(int h, int f, int k) {
+// threads.
+int down_combine_rows(int f, int k) {
     const int per = k * (f / 256);
     int rd = 1;
     while (rd * 2 * per <= kBlock) rd *= 2;
-    while (rd * 2 * per <= kDcMaxThreads && h % (rd * 2) == 0 && h / (rd * 2) >= 256) rd *= 2;
+    return rd;
+}
+
+// k-quant experts (one Q8_K block per (pair, super-block) and rd0 threads): the row stride doubled,
+// up to 16 rows and kDcMaxThreads threads, while the grid keeps 256 work-groups at one row per
+// thread. At the 235B shape that is 8 x 6 x 16 = 768 threads of one row each instead of 192 of four,
+// so the work-group's quantization and dot products spread over four times the wavefronts.
+constexpr int kDcMaxThreads = 1024;
+int down_combine_rows_wide(int h, int f, int k) {
+    const int per = k * (f / 256);
+    int rd = down_combine_rows(f, k);
+    while (rd < 16 && rd * 2 * per <= kDcMaxThreads && h % (rd * 2) == 0 && h / (rd * 2) >= 256) rd *= 2;
     return rd;
 }
 
@@ -1108,13 +1116,14 @@ hipError_t launch_down_combine_r(const DownCombineParams &P, int rd0, int np, si
                                  const LaunchTiming *tm) {
     const dim3 grid(P.h / (rd0 * R)), block(threads);
     if (threads > kBlock) {
-        // past 256 threads only the one-block-per-(pair, super-block) quantization (k-quants)
-        if (WT == kTypeQ8_0 || threads != P.k * (P.f / 256) * rd0) return hipErrorInvalidValue;
-        switch (rd0) {
-            case 8: return launch(down_combine_kernel<WT, 1, R, 32, kDcMaxThreads>, grid, block, lds, st, tm, P, rd0);
-            case 16: return launch(down_combine_kernel<WT, 1, R, 16, kDcMaxThreads>, grid, block, lds, st, tm, P, rd0);
-            default: return hipErrorInvalidValue;
+        // past 256 threads: k-quants, one row per thread, rd0 threads per (pair, super-block) block
+        if constexpr (WT != kTypeQ8_0 && R == 1) {
+            if (threads == P.k * (P.f / 256) * rd0) {
+                if (rd0 == 8) return launch(down_combine_kernel<WT, 1, 1, 32, kDcMaxThreads>, grid, block, lds, st, tm, P, rd0);
+                if (rd0 == 16) return launch(down_combine_kernel<WT, 1, 1, 16, kDcMaxThreads>, grid, block, lds, st, tm, P, rd0);
+            }
         }
+        return hipErrorInvalidValue;
     }
     if (WT != kTypeQ8_0 && threads == P.k * (P.f / 256) * rd0) {
         // one Q8_K block per (pair, super-block), quantized by that combination's rd0 threads
@@ -1134,8 +1143,15 @@ hipError_t launch_down_combine_r(const DownCombineParams &P, int rd0, int np, si
 
 template <int WT>
 hipError_t launch_down_combine_t(const DownCombineParams &P, hipStream_t st, const LaunchTiming *tm) {
-    const int rd0 = down_combine_rows(P.h, P.f, P.k), nsbf = P.f / 256, nact = P.k * P.f;
-    const int R = down_combine_rows_per_thread(WT, P.h, rd0);
+    int rd0 = down_combine_rows(P.f, P.k), R = down_combine_rows_per_thread(WT, P.h, rd0);
+    if (WT != kTypeQ8_0) {
+        const int wide = down_combine_rows_wide(P.h, P.f, P.k);
+        if (wide > rd0 && down_combine_rows_per_thread(WT, P.h, wide) == 1) {
+            rd0 = wide;
+            R = 1;
+        }
+    }
+    const int nsbf = P.f / 256, nact = P.k * P.f;
     const int threads = (P.k * nsbf * rd0 + kWave - 1) / kWave * kWave;
     const size_t lds = (size_t) nact + (size_t) nact / 32 * 8 + (size_t) P.k * nsbf * rd0 * R * 4 + (size_t) P.k * 4 +
                        (size_t) P.k * rd0 * R * 4;
@@ -1152,7 +1168,7 @@ hipError_t launch_down_combine_t(const DownCombineParams &P, hipStream_t st, con
 bool down_combine_supported(int h, int f, int k) {
     if (k < 1 || k > kMaxK || f % 256 != 0 || h % 256 != 0 || (long) k * f > kDcMaxAct) return false;
     if (k * (f / 256) > kBlock) return false;
-    const int rd = down_combine_rows(h, f, k);
+    const int rd = down_combine_rows(f, k);
     const int threads = (k * (f / 256) * rd + kWave - 1) / kWave * kWave;
     return h % rd == 0 && (long) k * f <= 8L * threads * 8; // at most 8 passes (or blocks) per thread
 }

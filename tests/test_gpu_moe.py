@@ -40,6 +40,8 @@ def model(name):
         "mixed": dict(h=256, f=768, E=16, k=4, types=(Q4_K, Q4_K, Q8_0), n_layer=1, n_batch=64),
         # Qwen3-235B-A22B MoE layer shape (h 4096, f 1536, top-8, Q4_K) over 16 experts
         "235b_q4": dict(h=4096, f=1536, E=16, k=8, types=(Q4_K,) * 3, n_layer=1, n_batch=64),
+        # the same shape with Q8_0 experts (whole 32-value blocks per thread in the single-token down)
+        "235b_q8": dict(h=4096, f=1536, E=16, k=8, types=(Q8_0,) * 3, n_layer=1, n_batch=64),
         # the other k-quants (stored unpacked, KQ8) at the 30B shape over 32 experts, in the mixes real
         # files use: Q4_K_M (Q4_K gate/up, Q6_K down), Q5_K_M, and the 3- and 2-bit classes
         "q4km": dict(h=2048, f=768, E=32, k=8, types=(Q4_K, Q4_K, Q6_K), n_layer=1, n_batch=64),
@@ -111,7 +113,7 @@ def test_route_f32_weights_and_zipf(orc, lstk, dev):
                                     ("30b_q4", 1), ("30b_q4", 8), ("30b_q4", 64), ("mixed", 5), ("235b_q4", 1),
                                     ("235b_q4", 8), ("235b_q4", 64), ("q4km", 1), ("q4km", 8), ("q4km", 64),
                                     ("q5km", 1), ("q5km", 16), ("q3", 1), ("q3", 8), ("q2", 1), ("q2", 8),
-                                    ("235b_q6", 1), ("235b_q6", 8)])
+                                    ("235b_q6", 1), ("235b_q6", 8), ("235b_q8", 1), ("235b_q8", 8)])
 def test_ffn_matches_oracle(orc, lstk, dev, name, T):
     import torch
     cfg, layers, routers, store = model(name)
@@ -131,7 +133,8 @@ def test_ffn_matches_oracle(orc, lstk, dev, name, T):
 
 
 @pytest.mark.parametrize("name,T", [("tiny", 16), ("30b_q8", 1), ("30b_q8", 8), ("30b_q4", 16), ("235b_q4", 1),
-                                    ("q4km", 1), ("q5km", 1), ("q3", 1), ("q2", 1), ("235b_q6", 1), ("q4km", 64)])
+                                    ("q4km", 1), ("q5km", 1), ("q3", 1), ("q2", 1), ("235b_q6", 1), ("q4km", 64),
+                                    ("235b_q8", 1)])
 def test_block_matches_oracle(orc, lstk, dev, name, T):
     import torch
     cfg, layers, routers, store = model(name)
@@ -366,7 +369,7 @@ def test_stage_timing_counts_launches(orc, lstk, dev):
     assert n == [3 + 2, 4, 4, 1] and all(m > 0 for m in ms)
 
 
-@pytest.mark.parametrize("name", ["tiny", "30b_q8", "30b_q4", "mixed", "235b_q4", "q4km", "q2", "235b_q6"])
+@pytest.mark.parametrize("name", ["tiny", "30b_q8", "30b_q4", "mixed", "235b_q4", "q4km", "q2", "235b_q6", "235b_q8"])
 def test_single_token_equals_batched_row(orc, lstk, dev, name):
     """A single token (gate_up ranking its experts, down + combine in one launch) gives the bits of
     the same token inside a batch (separate top-k, down and combine launches)."""
