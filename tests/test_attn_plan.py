@@ -90,13 +90,25 @@ def check_launch(T, n_head, n_kv, hd, kv_size, n_cells, n_batch, target, rope_in
         cc = np.minimum(cell, kv_size - 1)
         ki_max = ((gg * (hd // 4) + (hd // 4 - 1)) * kv_size + cc.max()) * 4 + 3
         assert cc.max() < kv_size and ki_max < kv_elems
-    # LDS of attn_kernel: s_S [RB][64] f32, s_Ph / s_Pl [RB][72] u16, s_M / s_L / s_f [RB], s_pos [RB],
-    # s_q [16 hd] (NRT = 1) f32, s_kv [2 hd] u16 (NRT = 1 and hd = 128: the new cell's K and V), s_live
-    # [MAX_PASSES] u8 (the pass-skipping instantiation of steps of >= 64 tokens)
     skip = T >= 64 and not rope_in
-    lds = (RB * FA_CELLS * 4 + 2 * RB * (FA_CELLS + 8) * 2 + 3 * RB * 4 + RB * 4 + (16 * hd if NRT == 1 else 1) * 4 +
-           (2 * hd if NRT == 1 and hd == 128 else 4) * 2 + (MAX_PASSES if skip else 1))
-    assert lds <= LDS_MAX
+    if rope_in and hd == 128:
+        # attn1_kernel (launch_attn_hd's single-token case): wavefront w of a work-group runs cells
+        # wb = begin + 16 w .. + 15; its cell-table entries are one int4 load at cv = min(wb + 4 lq,
+        # kv_size - 4), 16-byte aligned; LDS: s_q [16][128] f32, s_kv [256] u16, s_o [4][16][132] f32,
+        # s_m / s_l [4][16] f32
+        assert chunk == FA_CELLS and grp <= 16
+        wb = begin[:, None] + 16 * np.arange(4)[None, :]
+        cv = np.minimum(wb[:, :, None] + 4 * np.arange(4)[None, None, :], kv_size - 4)
+        assert (cv % 4 == 0).all() and cv.min() >= 0 and cv.max() + 3 < kv_size
+        lds = 16 * 128 * 4 + 2 * 128 * 2 + 4 * 16 * 132 * 4 + 2 * 4 * 16 * 4
+        assert lds == 43008 and lds <= LDS_MAX
+    else:
+        # LDS of attn_kernel: s_S [RB][64] f32, s_Ph / s_Pl [RB][72] u16, s_M / s_L / s_f [RB], s_pos [RB],
+        # s_q [16 hd] (NRT = 1) f32, s_live [MAX_PASSES] u8 (the pass-skipping instantiation of steps of
+        # >= 64 tokens)
+        lds = (RB * FA_CELLS * 4 + 2 * RB * (FA_CELLS + 8) * 2 + 3 * RB * 4 + RB * 4 + (16 * hd if NRT == 1 else 1) * 4 +
+               (MAX_PASSES if skip else 1))
+        assert lds <= LDS_MAX
     if skip:  # the skip map holds one byte per pass of the chunk
         assert (chunk + FA_CELLS - 1) // FA_CELLS <= MAX_PASSES
     # outputs: n_chunk == 1 writes out[(t * n_head + h) * hd + d]; else part rows
@@ -233,3 +245,51 @@ def test_online_softmax_over_passes_and_chunks_matches_direct():
     Ls = sum(p[1] * f for p, f in zip(parts, fs))
     Os = np.concatenate([p[2] * f[:, None] for p, f in zip(parts, fs)], axis=1)
     assert np.max(np.abs(Os / Ls[:, None] - direct)) < 2e-6
+
+
+def softmax_wavefronts(s, wave_cells=16, waves=4):
+    """attn1_kernel's arithmetic on one 64-cell chunk per row block of cells: each wavefront takes the
+    max over its 16 cells, p = e^(s - m_w) in f32, split into fp16 hi + lo (the operand of O^T += V^T P^T),
+    and sums p; the four wavefronts' (m_w, l_w, O_w) then merge with factors e^(m_w - M). Returns the
+    chunk's (M, L, O) as the partial row the combine reads."""
+    rows, n = s.shape
+    assert n == wave_cells * waves
+    ms, ls, os_ = [], [], []
+    for w in range(waves):
+        sw = s[:, w * wave_cells:(w + 1) * wave_cells].astype(np.float32)
+        m = np.max(sw, axis=1)
+        p = np.where(sw == -np.inf, np.float32(0), np.exp(sw - np.where(m == -np.inf, 0, m)[:, None])).astype(np.float32)
+        hi = p.astype(np.float16)
+        lo = (p - hi.astype(np.float32)).astype(np.float16)
+        o = np.zeros((rows, n), np.float64)
+        o[:, w * wave_cells:(w + 1) * wave_cells] = hi.astype(np.float64) + lo.astype(np.float64)
+        ms.append(m), ls.append(p.sum(axis=1, dtype=np.float32)), os_.append(o)
+    M = np.max(ms, axis=0)
+    with np.errstate(invalid="ignore"):  # m = M = -inf (no visible cell in the chunk) gives factor 0
+        fs = [np.where(m == -np.inf, np.float32(0), np.exp(m - M)) for m in ms]
+    return M, sum(l * f for l, f in zip(ls, fs)), sum(o * f[:, None] for o, f in zip(os_, fs))
+
+
+def test_wavefront_softmax_of_single_token_attention_matches_direct():
+    """The single-token kernel's per-wavefront softmax and LDS merge, then the chunk combine, against a
+    direct softmax: rows with masked cells, a wavefront with no visible cell, a row that sees one cell."""
+    rng = np.random.default_rng(9)
+    rows, n = 16, 64 * 12
+    s = (rng.standard_normal((rows, n)) * 4).astype(np.float32)
+    for r in range(rows):
+        s[r, (r * 53) % 400:(r * 53) % 400 + 40] = -np.inf   # whole wavefronts and chunks masked
+        s[r, 700 + r:] = -np.inf
+    s[3, :] = -np.inf
+    s[3, 130] = 0.25
+    direct = np.exp(s.astype(np.float64) - np.max(s, axis=1, keepdims=True))
+    direct /= direct.sum(axis=1, keepdims=True)
+    parts = [softmax_wavefronts(s[:, c0:c0 + 64]) for c0 in range(0, n, 64)]
+    M = np.max([p[0] for p in parts], axis=0)
+    fs = [np.where(p[0] == -np.inf, 0.0, np.exp(p[0] - M)) for p in parts]
+    L = sum(p[1] * f for p, f in zip(parts, fs))
+    O = np.concatenate([p[2] * f[:, None] for p, f in zip(parts, fs)], axis=1)
+    assert np.max(np.abs(O / L[:, None] - direct)) < 2e-6
+    assert O[3, 130] / L[3] == 1.0
+    # the restatement catches a combine that leaves out the chunks' factors
+    unscaled = np.concatenate([p[2] for p in parts], axis=1)
+    assert np.max(np.abs(unscaled / unscaled.sum(axis=1, keepdims=True) - direct)) > 1e-2
