@@ -963,6 +963,163 @@ __global__ __launch_bounds__(kAtBlock) void attn1_kernel(AttnParams P) {
     }
 }
 
+// ------------------------------------------------------------------------------------------------
+// Attention of 64-row blocks (steps of many tokens): wavefront w owns query rows row0 + 16 w .. + 15
+// over the whole chunk and runs them from registers to registers as attn1_kernel does (S^T = K Q^T puts
+// a row's scores in that row's lanes, the online softmax stays there, O^T += V^T P^T with P as fp16
+// hi + lo). The K and V fragments of each 64-cell block (and its cell-table entries) are loaded once
+// per work-group, wavefront w fetching those of cells 16 w .. 16 w + 15, into LDS, where all four
+// wavefronts read them; the next live block's loads are in flight while a block is multiplied. Two
+// barriers per 64-cell block; no score or probability goes through LDS.
+// ------------------------------------------------------------------------------------------------
+template <int HD, bool SKIP>
+__global__ __launch_bounds__(kAtBlock) void attn_rows_kernel(AttnParams P) {
+    constexpr int NK = HD / 16;
+    __shared__ __align__(16) half4v s_k[4][NK][kWave];
+    __shared__ __align__(16) half4v s_v[4][NK][kWave];
+    __shared__ __align__(16) int s_cs[kFaCells], s_cp[kFaCells];
+    __shared__ uint8_t s_live[SKIP ? kAttnMaxPasses : 1];
+    const int tid = threadIdx.x, w = tid / kWave, l = tid & (kWave - 1), lr = l & 15, lq = l >> 4;
+    const int grp = P.n_head / P.n_kv;
+    const int g = blockIdx.x % P.n_kv, rest = blockIdx.x / P.n_kv;
+    const int c = rest % P.n_chunk, rb = rest / P.n_chunk;
+    const int rows = P.T * grp;
+    const int begin = P.cell_begin + c * P.chunk, end = min(begin + P.chunk, P.n_cells);
+    const int n_pass = (end - begin + kFaCells - 1) / kFaCells;
+    const uint16_t *kb = P.kc + (size_t) g * (HD / 4) * P.kv_size * 4;
+    // the lane's query row: row lr of the wavefront's tile (B operand of S^T); rows past the end read
+    // the last row, see no cell and store nothing
+    const int r = rb * 64 + 16 * w + lr;
+    const bool on = r < rows;
+    const int rc = on ? r : rows - 1;
+    const int t = rc / grp, h = g * grp + rc % grp;
+    const int pos = on ? P.pos[t] : -1;
+    half4v kr[NK], vr[NK]; // this wavefront's share of a block: K of cell 16 w + lr, V of cells 16 w + 4 lq ..
+    int ctr;               // lanes 0-15: cell_seq of cell 16 w + lane, 16-31: cell_pos of cell 16 w + lane - 16
+    auto load_block = [&](int b0) {
+        const int ck = min(b0 + 16 * w + lr, P.kv_size - 1), cv = min(b0 + 16 * w + 4 * lq, P.kv_size - 4);
+#pragma unroll
+        for (int ks = 0; ks < NK; ks++) kr[ks] = ld_half4(kb + ((size_t) (ks * 4 + lq) * P.kv_size + ck) * 4);
+#pragma unroll
+        for (int dt = 0; dt < NK; dt++) vr[dt] = ld_half4(P.vc + v_index(g, dt * 16 + lr, cv, HD, P.kv_size));
+        const int ct = min(b0 + 16 * w + (l & 15), P.kv_size - 1);
+        ctr = l < 16 ? P.cell_seq[ct] : P.cell_pos[ct];
+    };
+    // A step of many tokens skips the chunk's passes that hold no cell of the sequence (attn_kernel's map)
+    const bool skip = SKIP && n_pass <= kAttnMaxPasses;
+    if (skip) {
+        for (int p0 = 0; p0 < n_pass; p0 += 8 * (kAtBlock / kWave)) {
+            int cs[8];
+#pragma unroll
+            for (int u = 0; u < 8; u++) cs[u] = P.cell_seq[min(begin + (p0 + u * (kAtBlock / kWave) + w) * kFaCells + l, P.kv_size - 1)];
+#pragma unroll
+            for (int u = 0; u < 8; u++) {
+                const int pass = p0 + u * (kAtBlock / kWave) + w;
+                const bool mine = cs[u] == P.seq && begin + pass * kFaCells + l < end;
+                const bool any = __ballot(mine) != 0ull;
+                if (l == 0 && pass < n_pass) s_live[pass] = any ? 1 : 0;
+            }
+        }
+    }
+    half4v qb[NK];
+    const uint16_t *q = P.q + ((size_t) t * P.n_head + h) * HD;
+#pragma unroll
+    for (int ks = 0; ks < NK; ks++) {
+        const half4v v = ld_half4(q + ks * 16 + 4 * lq);
+        qb[ks] = on ? v : half4v{0, 0, 0, 0};
+    }
+    __syncthreads(); // the skip map
+    auto next_live = [&](int p) {
+        if (skip)
+            while (p < n_pass && !s_live[p]) p++;
+        return p;
+    };
+    int p = next_live(0);
+    load_block(begin + min(p, n_pass - 1) * kFaCells);
+    float m_run = -INFINITY, l_run = 0.0f;
+    f32x4v o[NK];
+#pragma unroll
+    for (int dt = 0; dt < NK; dt++) o[dt] = f32x4v{0, 0, 0, 0};
+    while (p < n_pass) {
+        const int b0 = begin + p * kFaCells;
+        __syncthreads(); // every wavefront is done with the previous block's fragments
+#pragma unroll
+        for (int ks = 0; ks < NK; ks++) s_k[w][ks][l] = kr[ks];
+#pragma unroll
+        for (int dt = 0; dt < NK; dt++) s_v[w][dt][l] = vr[dt];
+        if (l < 16) s_cs[16 * w + l] = ctr;
+        else if (l < 32) s_cp[16 * w + l - 16] = ctr;
+        __syncthreads();
+        const int pn = next_live(p + 1);
+        load_block(begin + min(pn, n_pass - 1) * kFaCells); // unconditional: the last block again past the end
+#pragma unroll
+        for (int kc = 0; kc < 4; kc++) {
+            half4v kf[NK];
+#pragma unroll
+            for (int ks = 0; ks < NK; ks++) kf[ks] = s_k[kc][ks][l];
+            f32x4v sc = f32x4v{0, 0, 0, 0};
+#pragma unroll
+            for (int ks = 0; ks < NK; ks++) sc = mfma16(kf[ks], qb[ks], sc);
+            const int4 cs = *reinterpret_cast<const int4 *>(&s_cs[16 * kc + 4 * lq]);
+            const int4 cp = *reinterpret_cast<const int4 *>(&s_cp[16 * kc + 4 * lq]);
+            const int csv[4] = {cs.x, cs.y, cs.z, cs.w}, cpv[4] = {cp.x, cp.y, cp.z, cp.w};
+            float sv[4];
+            float mt = -INFINITY;
+#pragma unroll
+            for (int v = 0; v < 4; v++) {
+                const bool vis = b0 + 16 * kc + 4 * lq + v < end && csv[v] == P.seq && cpv[v] <= pos;
+                sv[v] = vis ? sc[v] * P.scale : -INFINITY;
+                mt = fmaxf(mt, sv[v]);
+            }
+            mt = fmaxf(mt, xor_lanes(mt, 16));
+            mt = fmaxf(mt, xor_lanes(mt, 32));
+            const float m_new = fmaxf(m_run, mt);
+            const float f = m_run == -INFINITY ? 0.0f : expf(m_run - m_new);
+            float ps = 0.0f;
+            half4v ph, pl;
+#pragma unroll
+            for (int v = 0; v < 4; v++) {
+                const float pv = sv[v] == -INFINITY ? 0.0f : expf(sv[v] - m_new);
+                ph[v] = (_Float16) pv;
+                pl[v] = (_Float16) (pv - (float) ph[v]);
+                ps += pv;
+            }
+            l_run = l_run * f + ps;
+            m_run = m_new;
+#pragma unroll
+            for (int dt = 0; dt < NK; dt++) {
+                const half4v vf = s_v[kc][dt][l];
+                o[dt] *= f;
+                o[dt] = mfma16(vf, ph, o[dt]);
+                o[dt] = mfma16(vf, pl, o[dt]);
+            }
+        }
+        p = pn;
+    }
+    l_run += xor_lanes(l_run, 16);
+    l_run += xor_lanes(l_run, 32);
+    if (!on) return;
+    // lane (row lr, quad lq) holds dims dt*16 + 4 lq .. +3 of its row
+    if (P.n_chunk == 1) {
+#pragma unroll
+        for (int dt = 0; dt < NK; dt++) {
+            const size_t oi = ((size_t) t * P.n_head + h) * HD + dt * 16 + 4 * lq;
+            const float4 y = make_float4(o[dt][0] / l_run, o[dt][1] / l_run, o[dt][2] / l_run, o[dt][3] / l_run);
+            *reinterpret_cast<float4 *>(P.out + oi) = y;
+            if (P.out16) *reinterpret_cast<uint2 *>(P.out16 + oi) = make_uint2(pack2(y.x, y.y), pack2(y.z, y.w));
+        }
+    } else {
+        float *pp = P.part + (((size_t) t * P.n_head + h) * P.n_chunk + c) * (HD + 4);
+#pragma unroll
+        for (int dt = 0; dt < NK; dt++)
+            *reinterpret_cast<float4 *>(pp + 4 + dt * 16 + 4 * lq) = make_float4(o[dt][0], o[dt][1], o[dt][2], o[dt][3]);
+        if (lq == 0) {
+            pp[0] = m_run;
+            pp[1] = l_run;
+        }
+    }
+}
+
 // Merges the chunks' partial rows of one (query head, token): out = sum_c o_c e^(m_c - M) / sum_c l_c e^(m_c - M).
 // Every load is issued before the first reduction: thread i takes chunk i's (m, l) (and chunks i + 256,
 // ... past 256 chunks), and hd / 4 threads per chunk hold the float4 slices of up to kCombRegs chunks
@@ -1197,6 +1354,14 @@ hipError_t launch_attn_hd(const AttnParams &P, hipStream_t st, const LaunchTimin
     if constexpr (HD == 128) {
         if (P.rb_rows == 16 && P.rope_in && P.n_head / P.n_kv <= 4 * kRopeMaxQ && P.rope.cs && P.chunk == kFaCells)
             return launch(attn1_kernel, grid, block, 0, st, tm, P);
+    }
+    // 64-row blocks: each wavefront on its own 16 rows (head sizes 64 and 128; 256 would need 128 KB of
+    // fragments per block)
+    if constexpr (HD <= 128) {
+        if (P.rb_rows == 64 && !P.rope_in) {
+            if (P.T >= kAttnSkipMinT) return launch(attn_rows_kernel<HD, true>, grid, block, 0, st, tm, P);
+            return launch(attn_rows_kernel<HD, false>, grid, block, 0, st, tm, P);
+        }
     }
     // steps of many tokens (prompts): the instantiation that skips passes with no cell of the sequence
     if (P.T >= kAttnSkipMinT && !P.rope_in) {
