@@ -1,5 +1,5 @@
 """CPU replay of the attention launch plan and of every index the attention kernels compute
-(localstack_amd/csrc/forward.hip: attn_plan, attn_kernel, attn_combine_kernel; buffers sized as
+(localstack_amd/csrc/forward.hip: attn_plan, attn_kernel, attn1_kernel, attn_rows_kernel, attn_combine_kernel; buffers sized as
 model.cpp allocates them), for work-group targets of 512 (the build's), 256 and 128, over the shapes the
 tests and the benchmark run and past them: every global index stays inside its buffer, every LDS index
 inside its array, and the partial rows inside attn_part_rows. No GPU. The replayed plan is held equal to
@@ -102,6 +102,24 @@ def check_launch(T, n_head, n_kv, hd, kv_size, n_cells, n_batch, target, rope_in
         assert (cv % 4 == 0).all() and cv.min() >= 0 and cv.max() + 3 < kv_size
         lds = 16 * 128 * 4 + 2 * 128 * 2 + 4 * 16 * 132 * 4 + 2 * 4 * 16 * 4
         assert lds == 43008 and lds <= LDS_MAX
+    elif rb_rows == 64 and hd <= 128:
+        # attn_rows_kernel: wavefront w fetches K of cell b0 + 16 w + lr, V of cells b0 + 16 w + 4 lq ..
+        # + 3 and the cell tables of cell b0 + 16 w + (lane & 15), clamped to the cache; partial rows and
+        # outputs are float4 stores at dims 16 dt + 4 lq; LDS: s_k / s_v [4][hd / 16][64] half4, s_cs / s_cp
+        # [64] int, s_live [MAX_PASSES] u8 (skip map)
+        for b0, e0 in zip(begin, end):
+            blocks = np.arange(b0, e0, FA_CELLS)
+            assert (blocks % 4 == 0).all()
+            wl = 16 * np.arange(4)[:, None] + np.arange(16)[None, :]      # 16 w + lr (or lane & 15)
+            ck = np.minimum(blocks[:, None, None] + wl[None], kv_size - 1)
+            cv = np.minimum(blocks[:, None, None] + 16 * np.arange(4)[None, :, None] + 4 * np.arange(4)[None, None, :],
+                            kv_size - 4)
+            assert ck.min() >= 0 and ck.max() < kv_size and (cv % 4 == 0).all() and cv.max() + 3 < kv_size
+        assert hd % 4 == 0  # partial rows (hd + 4 floats) and output rows stay 16-byte aligned for the float4 stores
+        lds = 2 * 4 * (hd // 16) * 64 * 8 + 2 * 64 * 4 + (MAX_PASSES if skip else 1)
+        assert lds <= LDS_MAX
+        if hd == 128 and skip:
+            assert lds == 35328  # the compiler's figure for attn_rows_kernel<128, true>
     else:
         # LDS of attn_kernel: s_S [RB][64] f32, s_Ph / s_Pl [RB][72] u16, s_M / s_L / s_f [RB], s_pos [RB],
         # s_q [16 hd] (NRT = 1) f32, s_live [MAX_PASSES] u8 (the pass-skipping instantiation of steps of
