@@ -1052,46 +1052,60 @@ __global__ __launch_bounds__(kAtBlock) void attn_rows_kernel(AttnParams P) {
         __syncthreads();
         const int pn = next_live(p + 1);
         load_block(begin + min(pn, n_pass - 1) * kFaCells); // unconditional: the last block again past the end
+        // the block's four 16-cell groups together: S^T of each (four independent product chains), one
+        // softmax step over the 64 cells, then O^T += V^T P^T over the groups (eight chains, one per dim tile)
+        f32x4v sc[4];
 #pragma unroll
         for (int kc = 0; kc < 4; kc++) {
-            half4v kf[NK];
+            sc[kc] = f32x4v{0, 0, 0, 0};
 #pragma unroll
-            for (int ks = 0; ks < NK; ks++) kf[ks] = s_k[kc][ks][l];
-            f32x4v sc = f32x4v{0, 0, 0, 0};
+            for (int ks = 0; ks < NK; ks++) sc[kc] = mfma16(s_k[kc][ks][l], qb[ks], sc[kc]);
+        }
+        float sv[4][4];
+        float mt = -INFINITY;
 #pragma unroll
-            for (int ks = 0; ks < NK; ks++) sc = mfma16(kf[ks], qb[ks], sc);
+        for (int kc = 0; kc < 4; kc++) {
             const int4 cs = *reinterpret_cast<const int4 *>(&s_cs[16 * kc + 4 * lq]);
             const int4 cp = *reinterpret_cast<const int4 *>(&s_cp[16 * kc + 4 * lq]);
             const int csv[4] = {cs.x, cs.y, cs.z, cs.w}, cpv[4] = {cp.x, cp.y, cp.z, cp.w};
-            float sv[4];
-            float mt = -INFINITY;
 #pragma unroll
             for (int v = 0; v < 4; v++) {
                 const bool vis = b0 + 16 * kc + 4 * lq + v < end && csv[v] == P.seq && cpv[v] <= pos;
-                sv[v] = vis ? sc[v] * P.scale : -INFINITY;
-                mt = fmaxf(mt, sv[v]);
+                sv[kc][v] = vis ? sc[kc][v] * P.scale : -INFINITY;
+                mt = fmaxf(mt, sv[kc][v]);
             }
-            mt = fmaxf(mt, xor_lanes(mt, 16));
-            mt = fmaxf(mt, xor_lanes(mt, 32));
-            const float m_new = fmaxf(m_run, mt);
+        }
+        mt = fmaxf(mt, xor_lanes(mt, 16));
+        mt = fmaxf(mt, xor_lanes(mt, 32));
+        const float m_new = fmaxf(m_run, mt);
+        // the rescale by e^(m_run - m_new) only when some row's max moved (otherwise every factor is 1)
+        if (__ballot(m_new != m_run) != 0ull) { // wavefront-uniform
             const float f = m_run == -INFINITY ? 0.0f : expf(m_run - m_new);
-            float ps = 0.0f;
-            half4v ph, pl;
+            l_run *= f;
+#pragma unroll
+            for (int dt = 0; dt < NK; dt++) o[dt] *= f;
+        }
+        m_run = m_new;
+        float ps = 0.0f;
+        half4v ph[4], pl[4];
+#pragma unroll
+        for (int kc = 0; kc < 4; kc++) {
 #pragma unroll
             for (int v = 0; v < 4; v++) {
-                const float pv = sv[v] == -INFINITY ? 0.0f : expf(sv[v] - m_new);
-                ph[v] = (_Float16) pv;
-                pl[v] = (_Float16) (pv - (float) ph[v]);
+                const float pv = sv[kc][v] == -INFINITY ? 0.0f : expf(sv[kc][v] - m_new);
+                ph[kc][v] = (_Float16) pv;
+                pl[kc][v] = (_Float16) (pv - (float) ph[kc][v]);
                 ps += pv;
             }
-            l_run = l_run * f + ps;
-            m_run = m_new;
+        }
+        l_run += ps;
 #pragma unroll
-            for (int dt = 0; dt < NK; dt++) {
+        for (int dt = 0; dt < NK; dt++) {
+#pragma unroll
+            for (int kc = 0; kc < 4; kc++) {
                 const half4v vf = s_v[kc][dt][l];
-                o[dt] *= f;
-                o[dt] = mfma16(vf, ph, o[dt]);
-                o[dt] = mfma16(vf, pl, o[dt]);
+                o[dt] = mfma16(vf, ph[kc], o[dt]);
+                o[dt] = mfma16(vf, pl[kc], o[dt]);
             }
         }
         p = pn;
