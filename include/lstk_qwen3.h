@@ -126,6 +126,12 @@ int lstk_model_fill_context(lstk_model *model, int32_t seq, int n_cells, uint64_
  * been through the MoE block. */
 int lstk_model_debug_capture(lstk_model *model, float *d_states);
 
+/* Test hook (no counterpart in the reference): with d_moe_in set, every forward also copies the residual
+ * stream entering layer l's MoE block (after attention, o-proj and residual; the input of ffn_norm and the
+ * router), [T][n_embd] f32, to d_moe_in + l * T * n_embd, so a test can run a reference router on exactly
+ * the device's router input; NULL turns it off. */
+int lstk_model_debug_capture_moe_in(lstk_model *model, float *d_moe_in);
+
 /* Test hook (no counterpart in the reference): options of the model's later forwards. Bit 0 set: a
  * single-token step runs RoPE and the new cell's K / V store in a launch of their own before the
  * attention, whose chunks then take several 64-cell passes, instead of inside the attention launch with

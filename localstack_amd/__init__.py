@@ -110,6 +110,7 @@ SIGNATURES = {
     "lstk_model_fill_context": (_I, [_P, ctypes.c_int32, _I, ctypes.c_uint64, _P]),
     "lstk_model_set_trace": (_I, [_P, ctypes.c_char_p]),
     "lstk_model_debug_capture": (_I, [_P, _P]),
+    "lstk_model_debug_capture_moe_in": (_I, [_P, _P]),
     "lstk_model_remove_seq": (_I, [_P, ctypes.c_int32]),
     "lstk_model_truncate_seq": (_I, [_P, ctypes.c_int32, ctypes.c_int32]),
     "lstk_model_seq_len": (ctypes.c_int32, [_P, ctypes.c_int32]),
@@ -452,6 +453,12 @@ class Qwen3Model:
         states ([n_layer][T][n_embd] f32, T the step's tokens); None turns it off."""
         self._capture = states
         _check(lib().lstk_model_debug_capture(self._h, None if states is None else _ptr(states)))
+
+    def debug_capture_moe_in(self, states):
+        """Test hook: every forward copies the residual stream entering each layer's MoE block (the router's
+        input before ffn_norm) into the device tensor states ([n_layer][T][n_embd] f32); None turns it off."""
+        self._capture_moe = states
+        _check(lib().lstk_model_debug_capture_moe_in(self._h, None if states is None else _ptr(states)))
 
     def debug_options(self, rope_apart=False):
         """Test hook: rope_apart runs a single-token step's RoPE in its own launch (multi-pass attention

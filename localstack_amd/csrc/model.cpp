@@ -195,6 +195,8 @@ struct lstk_model {
     std::vector<TimedLaunch> launched[kStages];
     // test hook: the residual stream after every layer, [n_layer][T][n_embd] (lstk_model_debug_capture)
     float *capture = nullptr;
+    // test hook: the residual stream entering every layer's MoE block (lstk_model_debug_capture_moe_in)
+    float *capture_moe = nullptr;
     // test hook (lstk_model_debug_options bit 0): RoPE of a single-token step in its own launch
     bool rope_apart = false;
     // routing trace
@@ -580,6 +582,9 @@ int forward(lstk_model *M, int32_t seq, int T, int n_cells, float *d_logits, int
         } else if ((e = timed(M, 3, [&](const lstk::LaunchTiming *tm) { return lstk::launch_gemv(op, st, tm); })) != hipSuccess) {
             return hip_fail(e, "o-proj launch");
         }
+        if (M->capture_moe && (e = hipMemcpyAsync(M->capture_moe + (size_t) l * T * h, M->x, (size_t) T * h * sizeof(float),
+                                                  hipMemcpyDeviceToDevice, st)) != hipSuccess)
+            return hip_fail(e, "capture copy");
         // ffn_norm inside the router launch (resident pools) up to 63 rows: a 512-token prompt measured 1.6%
         // slower that way (each row normalised by every expert group's work-group) than with its own launch
         const bool norm_in_router = !M->streaming && rows < 64;
@@ -731,6 +736,12 @@ int lstk_model_fill_context(lstk_model *model, int32_t seq, int n_cells, uint64_
 int lstk_model_debug_capture(lstk_model *model, float *d_states) {
     if (!model) return set_error(LSTK_E_INVALID, "null model");
     model->capture = d_states;
+    return LSTK_OK;
+}
+
+int lstk_model_debug_capture_moe_in(lstk_model *model, float *d_moe_in) {
+    if (!model) return set_error(LSTK_E_INVALID, "null model");
+    model->capture_moe = d_moe_in;
     return LSTK_OK;
 }
 

@@ -14,8 +14,10 @@ the host generation to seconds.
    output within LAYER_TOL, router ids equal but for near-ties at the top-k boundary (FLIP_FRAC; -1 for
    the rows the last layer skips), and the oracle's final norm + head on the device's last hidden row
    within LOGITS_TOL / RMS_TOL (diff_logits, src/main.cpp:195-207) with the same top-1. (With identical
-   router inputs - the MoE block tests - the ids are bit-exact; here the attention before the router is
-   summed in another f32 order on each side.)
+   router inputs the ids are bit-exact: every layer's router is also run by the oracle on the device's own
+   MoE input (the residual entering the block, lstk_model_debug_capture_moe_in) and must give the device's
+   ids at every row of every step; against the oracle's own layer the attention before the router is summed
+   in another f32 order on each side, hence FLIP_FRAC.)
    Free-running logits are not compared at this depth: 48 random layers are chaotic. The oracle's own
    logits move by 1.3e-1 to 6.6e-1 max-abs, with different router ids from layer 0-2 on and a different
    top-1, when only its F16 dot products are summed in double instead of ggml's f32 order (2 layers:
@@ -92,7 +94,9 @@ def test_full_30b_model_matches_oracle_layer_by_layer(lstk, dev, model30b_weight
     T_MAX = 32
     model = lstk.Qwen3Model(HP, w, store30b, 512, T_MAX, device=dev)
     states = torch.zeros((HP["n_layer"], T_MAX, HP["n_embd"]), dtype=torch.float32, device=dev)
+    moe_in = torch.zeros((HP["n_layer"], T_MAX, HP["n_embd"]), dtype=torch.float32, device=dev)
     model.debug_capture(states)
+    model.debug_capture_moe_in(moe_in)
     ref = oracle.Qwen3(HP, w, 128)
     rng = np.random.default_rng(31)
     feed = rng.integers(0, HP["n_vocab"], 8).astype(np.int32)
@@ -105,8 +109,14 @@ def test_full_30b_model_matches_oracle_layer_by_layer(lstk, dev, model30b_weight
         T = len(feed)
         gl, gt = _run(model, 0, feed, dev)
         st = states.view(-1)[:HP["n_layer"] * T * HP["n_embd"]].view(HP["n_layer"], T, HP["n_embd"]).cpu().numpy()
+        mi = moe_in.view(-1)[:HP["n_layer"] * T * HP["n_embd"]].view(HP["n_layer"], T, HP["n_embd"]).cpu().numpy()
         x = w["tok_embd"][feed].astype(np.float32)  # layer 0's input: the embedding rows
         for l in range(HP["n_layer"]):
+            # the router on exactly the device's MoE input (ffn_norm, F16 router, top-8): bit-exact ids
+            r0 = T - 1 if l == HP["n_layer"] - 1 else 0  # the last layer routes its output row only
+            hn = np.stack([oracle.rms_norm(mi[l][r], w["layers"][l]["ffn_norm"], HP["rms_eps"]) for r in range(r0, T)])
+            own_ids = oracle.router(hn, w["layers"][l]["gate_inp"], oracle.TYPE_F16, HP["n_expert_used"])[0]
+            assert np.array_equal(gt[l][r0:], own_ids), (step, l, "router ids on the device's own MoE input")
             xr, ids = ref.run_layer(l, x)
             same = np.all(gt[l] == ids, axis=1)
             for r in np.flatnonzero(~same):
@@ -132,6 +142,7 @@ def test_full_30b_model_matches_oracle_layer_by_layer(lstk, dev, model30b_weight
     assert flips <= FLIP_FRAC * rows, (flips, rows)
     assert model.seq_len(0) == len(ref) == 8 + 3 + 32 + 1
     model.debug_capture(None)
+    model.debug_capture_moe_in(None)
     model.close()
 
 
