@@ -122,13 +122,25 @@ def test_chunked_prefill_matches_one_step(lstk, dev):
 def test_prompt_high_in_cache_matches_fresh(lstk, dev):
     """A 64-token prompt (the attention's many-token launch) placed high in the cache agrees with the same
     prompt on a fresh cache. A 700-token sequence and then a 200-token one are decoded, the first is
-    removed: the prompt's blocks come from the top of the freed ones (cells 640-703), the attended range
-    starts at its lowest block and runs past the other sequence's cells (704-927) to the padded end, so
-    the launch skips the passes that hold none of the prompt's cells. Only f32 summation orders differ."""
+    removed: the prompt's blocks come from the top of the freed ones (cells 640-703, block order not the
+    positions' order), the attended range starts at its lowest block and runs past the other sequence's
+    cells (704-927) to the padded end, so the launch skips the passes that hold none of the prompt's cells.
+    Only f32 summation orders differ: layer 0's attention output (the residual entering its MoE block, both
+    runs on the same embedding rows) agrees to 1e-5 of its size; the logits agree to 1e-4 when both runs
+    route alike, and a router near-tie that the summation order tips (a swapped pair, at most 1% of the
+    rows) leaves them within the oracle bar."""
+    import torch
     hp, w = weights("tiny")
     toks = prompt(11, 64, hp["n_vocab"])
+
+    def capture(model):
+        mid = torch.zeros((hp["n_layer"], 64, hp["n_embd"]), dtype=torch.float32, device=dev)
+        model.debug_capture_moe_in(mid)
+        return mid
+
     _, fresh = build(lstk, dev, hp, w)
-    a, _ = run(fresh, 0, toks, hp, dev)
+    mid_a = capture(fresh)
+    a, ta = run(fresh, 0, toks, hp, dev)
     _, used = build(lstk, dev, hp, w)
     first, second = prompt(12, 700, hp["n_vocab"]), prompt(13, 200, hp["n_vocab"])
     for i in range(0, len(first), 64):
@@ -136,10 +148,25 @@ def test_prompt_high_in_cache_matches_fresh(lstk, dev):
     for i in range(0, len(second), 64):
         run(used, 6, second[i:i + 64], hp, dev)
     used.remove_seq(5)
-    b, _ = run(used, 0, toks, hp, dev)
+    mid_b = capture(used)
+    b, tb = run(used, 0, toks, hp, dev)
     assert used.seq_len(0) == 64 and used.seq_len(6) == 200
-    assert np.max(np.abs(a - b)) <= 1e-4
+    m0a, m0b = mid_a[0].cpu().numpy(), mid_b[0].cpu().numpy()
+    rel0 = float(np.max(np.abs(m0a - m0b)) / np.max(np.abs(m0a)))
+    same = np.all(ta == tb, axis=2)
+    print(f"[prompt high in cache] layer 0 attention rel diff {rel0:.2e}; rows routed differently "
+          f"{int((~same).sum())}/{same.size}; max|dlogit| {float(np.max(np.abs(a - b))):.2e}", flush=True)
+    assert rel0 <= 1e-5
+    if same.all():
+        assert np.max(np.abs(a - b)) <= 1e-4
+    else:
+        for l, r in zip(*np.nonzero(~same)):
+            assert len(set(ta[l][r].tolist()) ^ set(tb[l][r].tolist())) <= 2, (l, r)
+        assert (~same).sum() <= 0.01 * same.size + 1
+        assert np.max(np.abs(a - b)) <= LOGITS_TOL
     assert np.argmax(a) == np.argmax(b)
+    for m in (fresh, used):
+        m.debug_capture_moe_in(None)
 
 
 def test_sequences_are_isolated_and_removable(lstk, dev):
