@@ -222,12 +222,13 @@ int lstk_pool_set_timing(lstk_pool *pool, int enable);
 int lstk_pool_timing(lstk_pool *pool, double ms[4], int64_t launches[4]);
 
 /* Host-side repacking between GGUF expert bytes and the pool's HBM layout (one expert matrix of
- * `rows` x `cols`). The pool layout is [cols/256][C][rows][16 B]: each 256-value super-block row is
- * split into C 16-byte chunks (Q8_0: 8 fp16 scales + 16 chunks of int8; Q4_K: {d, dmin, scales}
- * + 8 chunks of 4-bit pairs; Q2_K, Q3_K, Q5_K and Q6_K unpacked to integers: {f32 d, f32 dmin},
- * 16 int8 scales, 16 mins and 16 chunks of int8 quants, one per 16 values) and the chunks of
- * neighbouring rows are adjacent, so a wavefront reading one chunk of 64 rows issues one coalesced
- * 1 KiB load. lstk_matrix_bytes is the pool size (the GGUF size for Q8_0 and Q4_K, 304 B per
+ * `rows` x `cols`). The pool layout is [rows/16][cols/256][C][16 rows][16 B], the last row block
+ * holding the rows left over: each 256-value super-block row is split into C 16-byte chunks (Q8_0:
+ * 8 fp16 scales + 16 chunks of int8; Q4_K: {d, dmin, scales} + 8 chunks of 4-bit pairs; Q2_K, Q3_K,
+ * Q5_K and Q6_K unpacked to integers: {f32 d, f32 dmin}, 16 int8 scales, 16 mins and 16 chunks of
+ * int8 quants, one per 16 values), chunk c of a row block's 16 rows is one 256-byte piece, and a row
+ * block's super-blocks and chunks are contiguous, so a work-group that takes whole row blocks reads
+ * one contiguous span. lstk_matrix_bytes is the pool size (the GGUF size for Q8_0 and Q4_K, 304 B per
  * super-block row for the other k-quants); lstk_unpack_matrix inverts Q8_0 and Q4_K only. */
 size_t lstk_matrix_bytes(int type, int rows, int cols);
 int lstk_repack_matrix(int type, int rows, int cols, const void *gguf, void *packed);

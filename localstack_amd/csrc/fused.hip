@@ -216,7 +216,7 @@ __global__ __launch_bounds__(kBlock) void fused_kernel(FusedParams P) {
         for (int s = 0; s < S; s++) {
             const int sb = g + s * G;
 #pragma unroll
-            for (int c = 0; c < CG; c++) wv[s][c] = *reinterpret_cast<const uint4 *>(base + chunk_offset(CG, f, sb, c, row));
+            for (int c = 0; c < CG; c++) wv[s][c] = *reinterpret_cast<const uint4 *>(base + chunk_offset(CG, f, h / 256, sb, c, row));
         }
         float acc = 0.0f;
 #pragma unroll
@@ -250,7 +250,7 @@ __global__ __launch_bounds__(kBlock) void fused_kernel(FusedParams P) {
             const uint8_t *base = P.w_down + (size_t) L.ids[jj] * P.s_down;
 #pragma unroll
             for (int cc = 0; cc < CD; cc++)
-                wv[cc] = *reinterpret_cast<const uint4 *>(base + chunk_offset(CD, h, on ? sb : 0, cc, on ? row : c * rd));
+                wv[cc] = *reinterpret_cast<const uint4 *>(base + chunk_offset(CD, h, f / 256, on ? sb : 0, cc, on ? row : c * rd));
         }
         wait_flags(P.flag_b, P.nB, n, P.spin_max, P.err);
         quantize_row_dev<QD, kFusedMaxAct / (8 * kBlock)>(P.act, k * f, L.u.c.qs, L.u.c.qd, L.u.c.qb);

@@ -272,7 +272,7 @@ __device__ __forceinline__ DmaOffs dma_offsets(const GroupedParams &P, const GLd
 #pragma unroll
     for (int i = 0; i < 5; i++) {
         const int c = min(2 * i + (lane >> 5), 8);
-        o.w[i] = (unsigned) chunk_offset(kChunksQ4_K, P.rows, 0, c, row0 + (lane & 31));
+        o.w[i] = (unsigned) chunk_offset(kChunksQ4_K, P.rows, P.K / 256, 0, c, row0 + (lane & 31));
     }
 #pragma unroll
     for (int mt = 0; mt < kMT; mt++)
@@ -301,7 +301,7 @@ __device__ __forceinline__ void issue_stage(const GroupedParams &P, const GLds &
         if (o.live & (1u << i)) dma16(xa + off(o.a[i]), st + (wave * kAInstr + i) * 1024);
     if (wave == 0 && lane < kGroupedChunk && (o.live >> 31))
         dma4(reinterpret_cast<const uint8_t *>(P.xd) + sb * 32 + off(o.dx), st + kABytes);
-    const uint8_t *wb = w + (size_t) sb * kChunksQ4_K * P.rows * 16;
+    const uint8_t *wb = w + (size_t) sb * kChunksQ4_K * kPoolRB * 16; // rows % kPoolRB == 0
     unsigned char *wl = st + kABytes + kDXBytes + wave * kWWaveBytes;
 #pragma unroll
     for (int i = 0; i < 4; i++) dma16(wb + off(o.w[i]), wl + i * 1024);

@@ -586,7 +586,7 @@ __global__ __launch_bounds__(NT) void gate_up_kernel(GateUpParams P) {
     for (int s = 0; s < S; s++) {
         const int sb = g + s * G;
 #pragma unroll
-        for (int c = 0; c < C; c++) w[s][c] = load_weights(reinterpret_cast<const uint4 *>(base + chunk_offset(C, f, sb, c, row)));
+        for (int c = 0; c < C; c++) w[s][c] = load_weights(reinterpret_cast<const uint4 *>(base + chunk_offset(C, f, h / 256, sb, c, row)));
     }
     int8_t *xs = reinterpret_cast<int8_t *>(work);
     float *xd = reinterpret_cast<float *>(work + (size_t) TC * h);
@@ -704,7 +704,7 @@ __global__ __launch_bounds__(kDnRows * kMaxG) void down_kernel(DownParams P) {
     for (int s = 0; s < S; s++) {
         const int sb = g + s * G;
 #pragma unroll
-        for (int c = 0; c < C; c++) w[s][c] = load_weights(reinterpret_cast<const uint4 *>(base + chunk_offset(C, h, sb, c, row)));
+        for (int c = 0; c < C; c++) w[s][c] = load_weights(reinterpret_cast<const uint4 *>(base + chunk_offset(C, h, f / 256, sb, c, row)));
     }
     const int f32 = f / 32;
     int8_t *xs = reinterpret_cast<int8_t *>(work);
@@ -885,7 +885,7 @@ __global__ __launch_bounds__(NT) void down_combine_kernel(DownCombineParams P, i
     for (int ir = 0; ir < R; ir++) {
         const int row = blockIdx.x * rd + ir * rd0 + rr;
 #pragma unroll
-        for (int c = 0; c < C; c++) w[ir][c] = load_weights(reinterpret_cast<const uint4 *>(base + chunk_offset(C, P.h, on ? sb : 0, c, row)));
+        for (int c = 0; c < C; c++) w[ir][c] = load_weights(reinterpret_cast<const uint4 *>(base + chunk_offset(C, P.h, f / 256, on ? sb : 0, c, row)));
     }
     if constexpr (SEG > 0) {
         q8k_block_lanes<SEG>(vs, rd0, rr, qs + (size_t) q * 256, qd + (size_t) q * 8, qb + (size_t) q * 8);

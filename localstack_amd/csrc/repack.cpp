@@ -3,7 +3,7 @@
 // The reference keeps GGUF bytes verbatim in its slots because Metal reads them zero-copy
 // (src/expert_store.cpp:156-187, docs/decisions.md:13). On MI355X the slot format is internal, so
 // each expert matrix is transposed once, when it enters the pool or the host tier, into
-// [cols/256][C][rows][16 B] chunks (formats.h). Q8_0's 34-byte blocks are regrouped in eights so
+// [rows/16][cols/256][C][16 rows][16 B] chunks (formats.h). Q8_0's 34-byte blocks are regrouped in eights so
 // every load is an aligned 16-byte chunk; Q2_K, Q3_K, Q5_K and Q6_K blocks are unpacked to KQ8.
 #include <algorithm>
 #include <cstring>
@@ -158,7 +158,7 @@ static int convert_matrix(int type, int rows, int cols, uint8_t *gguf, uint8_t *
         uint8_t *chunk[kMaxChunks];
         for (int r = r0; r < r1; r++) {
             for (int sb = 0; sb < nsb; sb++) {
-                for (int c = 0; c < C; c++) chunk[c] = packed + chunk_offset(C, rows, sb, c, r);
+                for (int c = 0; c < C; c++) chunk[c] = packed + chunk_offset(C, rows, nsb, sb, c, r);
                 convert_row_block(type, gguf + (size_t) r * row_bytes + (size_t) sb * sb_bytes, chunk, to_pool);
             }
         }

@@ -32,7 +32,8 @@ def test_exports_every_declared_symbol(lstk):
     assert lstk.lib().lstk_abi_version() == 1
 
 
-@pytest.mark.parametrize("wtype,rows,cols", [(8, 768, 2048), (8, 2048, 768), (12, 768, 2048), (12, 256, 512), (8, 3, 256)])
+@pytest.mark.parametrize("wtype,rows,cols", [(8, 768, 2048), (8, 2048, 768), (12, 768, 2048), (12, 256, 512), (8, 3, 256),
+                                             (12, 40, 512)])
 def test_repack_roundtrip_and_layout(lstk, wtype, rows, cols):
     rng = np.random.default_rng(rows + cols + wtype)
     g = synth.experts(rng, wtype, 1, rows, cols)
@@ -40,21 +41,25 @@ def test_repack_roundtrip_and_layout(lstk, wtype, rows, cols):
     p = lstk.repack_matrix(wtype, rows, cols, g)
     assert np.array_equal(lstk.unpack_matrix(wtype, rows, cols, p), g)
     assert not np.array_equal(p, g) or rows == 1
-    # chunk (sb, c, r) of the pool layout sits at ((sb * C + c) * rows + r) * 16
+    # chunk (sb, c) of row r sits in row block r // 16 (16 rows, or the rows left over in the last one):
+    # at ((r // 16) * 16 * nsb * C + (sb * C + c) * block_rows + r % 16) * 16
     C = 17 if wtype == 8 else 9
-    sbb = C * 16
-    r, sb = rows - 1, cols // 256 - 1
-    row = g[r * (cols // 256) * sbb:(r + 1) * (cols // 256) * sbb]
-    blk = row[sb * sbb:(sb + 1) * sbb]
-    at = lambda c: p[((sb * C + c) * rows + r) * 16:((sb * C + c) * rows + r) * 16 + 16]
-    if wtype == 12:
-        for c in range(9):
-            assert np.array_equal(at(c), blk[16 * c:16 * c + 16])
-    else:
-        b = blk.reshape(8, 34)
-        assert np.array_equal(at(0), b[:, 0:2].reshape(-1))
-        for i in range(8):
-            assert np.array_equal(at(1 + 2 * i), b[i, 2:18]) and np.array_equal(at(2 + 2 * i), b[i, 18:34])
+    sbb, nsb = C * 16, cols // 256
+    for r in sorted({0, 15 % rows, rows // 2, rows - 1}):
+        for sb in sorted({0, nsb - 1}):
+            row = g[r * nsb * sbb:(r + 1) * nsb * sbb]
+            blk = row[sb * sbb:(sb + 1) * sbb]
+            rb, rr = r // 16, r % 16
+            block_rows = min(16, rows - 16 * rb)
+            at = lambda c: p[(rb * 16 * nsb * C + (sb * C + c) * block_rows + rr) * 16:][:16]
+            if wtype == 12:
+                for c in range(9):
+                    assert np.array_equal(at(c), blk[16 * c:16 * c + 16])
+            else:
+                b = blk.reshape(8, 34)
+                assert np.array_equal(at(0), b[:, 0:2].reshape(-1))
+                for i in range(8):
+                    assert np.array_equal(at(1 + 2 * i), b[i, 2:18]) and np.array_equal(at(2 + 2 * i), b[i, 18:34])
 
 
 @pytest.mark.parametrize("wtype", [10, 11, 13, 14])
@@ -70,7 +75,8 @@ def test_repack_k_quants_to_kq8(lstk, wtype):
     assert lstk.matrix_bytes(wtype, rows, cols) == rows * (cols // 256) * 19 * 16
     p = lstk.repack_matrix(wtype, rows, cols, g)
     C, nsb = 19, cols // 256
-    chunks = p.reshape(nsb, C, rows, 16)  # [sb][c][row][16 B]
+    # [row block][sb][c][16 rows][16 B] (96 rows: six full blocks) -> [sb][c][row][16 B]
+    chunks = p.reshape(rows // 16, nsb, C, 16, 16).transpose(1, 2, 0, 3, 4).reshape(nsb, C, rows, 16)
     d = chunks[:, 0, :, 0:4].copy().view(np.float32)[..., 0]    # [sb][row]
     dmin = chunks[:, 0, :, 4:8].copy().view(np.float32)[..., 0]
     sc = chunks[:, 1].view(np.int8).astype(np.float32)           # [sb][row][16]
