@@ -301,7 +301,10 @@ __device__ __forceinline__ void issue_stage(const GroupedParams &P, const GLds &
         if (o.live & (1u << i)) dma16(xa + off(o.a[i]), st + (wave * kAInstr + i) * 1024);
     if (wave == 0 && lane < kGroupedChunk && (o.live >> 31))
         dma4(reinterpret_cast<const uint8_t *>(P.xd) + sb * 32 + off(o.dx), st + kABytes);
-    const uint8_t *wb = w + (size_t) sb * kChunksQ4_K * kPoolRB * 16; // rows % kPoolRB == 0
+    // every row block of the matrix is full (rows % 64 == 0, grouped_supported), so super-block sb of a
+    // lane's rows lies sb * C * kPoolRB chunks past its super-block 0
+    static_assert(64 % kPoolRB == 0, "the grouped kernels need row blocks that divide 64 rows");
+    const uint8_t *wb = w + (size_t) sb * kChunksQ4_K * kPoolRB * 16;
     unsigned char *wl = st + kABytes + kDXBytes + wave * kWWaveBytes;
 #pragma unroll
     for (int i = 0; i < 4; i++) dma16(wb + off(o.w[i]), wl + i * 1024);
