@@ -1253,7 +1253,7 @@ bool gemv_supported(int cols) { return cols > 0 && cols % 8 == 0 && cols <= 8192
 bool attn_supported(int hd) { return hd == 64 || hd == 128 || hd == 256; }
 
 // Rows of a work-group: 16, 32 or 64 (one, two or four 16-row tiles). Chunks are whole 64-cell passes,
-// as many as bring the launch to about kAttnTarget work-groups. Then T * n_head * n_chunk <= 32768 +
+// as many as bring the launch to about kAttnTarget work-groups (half that for a step of a few tokens). Then T * n_head * n_chunk <= 32768 +
 // T * n_head. With rope_in (one token) every chunk is one pass while n_head * passes <= 32768 (65536
 // cells at 32 query heads, 32768 at 64): the RoPE prologue has only been run with single-pass chunks on
 // the device. Past that, rope_in is cleared (the caller runs rope_kernel) and chunks take several passes.
@@ -1271,7 +1271,10 @@ void attn_plan(AttnParams &P) {
         }
         P.rope_in = 0;
     }
-    int want = (kAttnTarget + P.n_kv * P.n_rowblk - 1) / (P.n_kv * P.n_rowblk);
+    // a few tokens in one row block: half the target, so chunks of two passes (T = 8 at 4352 cells: 136
+    // work-groups writing half the partial rows of 272; measured 1715 -> 1732 tok/s for the whole model)
+    const int target = P.T > 1 && P.n_rowblk == 1 ? kAttnTarget / 2 : kAttnTarget;
+    int want = (target + P.n_kv * P.n_rowblk - 1) / (P.n_kv * P.n_rowblk);
     // a step of many tokens whose row blocks alone fill the device takes one chunk per row block, so
     // the launch writes the output itself and no combine follows
     if (P.T >= kAttnSkipMinT && P.n_kv * P.n_rowblk >= kAttnOneChunkWgs) want = 1;

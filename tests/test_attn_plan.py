@@ -31,6 +31,8 @@ def plan(T, n_head, n_kv, n_cells, target=512, rope_in=False, cell_begin=0):
         if n_head * passes <= 32768:
             return rb_rows, n_rowblk, FA_CELLS, passes, True
         rope_in = False
+    if T > 1 and n_rowblk == 1:  # a few tokens in one row block: half the target
+        target //= 2
     want = (target + n_kv * n_rowblk - 1) // (n_kv * n_rowblk)
     if T >= 64 and n_kv * n_rowblk >= 256:  # kAttnSkipMinT, kAttnOneChunkWgs: one chunk per row block
         want = 1
