@@ -108,54 +108,85 @@ __global__ __launch_bounds__(kWave) void rope_table_kernel(RopeParams P, float *
 
 // Head j (Q heads, then K heads, then V heads) of token t by one wavefront (lanes = threadIdx.x % 64).
 // A Q head's rotated row goes to q_dst (hd floats) or, when that is null, to its row of P.q_out;
-// with cells set, the wavefront also records the token's cell in the cell tables.
+// with cells set, the wavefront also records the token's cell in the cell tables. Every load (the
+// token's cell and position, the head's row, the norm weights, the step's cos / sin) is issued before
+// the first use and every store comes after the last load, so the wavefront waits on one round trip.
+constexpr int kRopeMaxPer = 4; // head dims per lane: hd <= 256
 __device__ __forceinline__ void rope_head(const RopeParams &P, int t, int j, float *q_dst, bool cells) {
     const int lane = threadIdx.x & (kWave - 1);
     const int hd = P.hd, half = hd / 2;
-    auto ld = [](const float *a) { return *a; };
-    const int cell = P.cells[t];
-    if (cells && lane == 0) {
-        P.cell_seq[cell] = P.seq;
-        P.cell_pos[cell] = P.pos[t];
-    }
+    const int cell = P.cells[t], pos = P.pos[t];
     if (j >= P.n_head + P.n_kv) {
         const int head = j - P.n_head - P.n_kv;
         const float *src = P.v + (size_t) t * P.ld + head * hd;
-        for (int d = lane; d < hd; d += kWave) P.vc[v_index(head, d, cell, hd, P.kv_size)] = f2h(ld(src + d));
+        float v[kRopeMaxPer];
+#pragma unroll
+        for (int k = 0; k < kRopeMaxPer; k++) v[k] = lane + kWave * k < hd ? src[lane + kWave * k] : 0.0f;
+        if (cells && lane == 0) {
+            P.cell_seq[cell] = P.seq;
+            P.cell_pos[cell] = pos;
+        }
+#pragma unroll
+        for (int k = 0; k < kRopeMaxPer; k++) {
+            const int d = lane + kWave * k;
+            if (d < hd) P.vc[v_index(head, d, cell, hd, P.kv_size)] = f2h(v[k]);
+        }
         return;
     }
     const bool is_q = j < P.n_head;
     const int head = is_q ? j : j - P.n_head;
     const float *src = (is_q ? P.q : P.k) + (size_t) t * P.ld + head * hd;
     const float *nw = is_q ? P.q_norm : P.k_norm;
+    // the pairs (i, i + half) of the lane, i = lane + 64 m < half, with their norm weights and cos / sin
+    constexpr int M = kRopeMaxPer / 2;
+    float x0[M], x1[M], n0[M], n1[M], c[M], sn[M];
+#pragma unroll
+    for (int m = 0; m < M; m++) {
+        const int i = min(lane + kWave * m, half - 1);
+        x0[m] = src[i];
+        x1[m] = src[i + half];
+        n0[m] = nw ? nw[i] : 1.0f;
+        n1[m] = nw ? nw[i + half] : 1.0f;
+        c[m] = 1.0f;
+        sn[m] = 0.0f;
+        if (P.cs) {
+            const float2 v = reinterpret_cast<const float2 *>(P.cs)[(size_t) t * half + i];
+            c[m] = v.x;
+            sn[m] = v.y;
+        }
+    }
+    // the squares in the order d = lane, lane + 64, ... (d < hd)
+    float v[kRopeMaxPer];
+#pragma unroll
+    for (int k = 0; k < kRopeMaxPer; k++) v[k] = lane + kWave * k < hd ? src[lane + kWave * k] : 0.0f;
     float scale = 1.0f;
     if (nw) {
         double s = 0.0;
-        for (int d = lane; d < hd; d += kWave) {
-            const float v = ld(src + d);
-            s += (double) (v * v);
-        }
+#pragma unroll
+        for (int k = 0; k < kRopeMaxPer; k++)
+            if (lane + kWave * k < hd) s += (double) (v[k] * v[k]);
         s = wave_sum_d(s);
         const float mean = (float) (s / (double) hd);
         scale = 1.0f / sqrtf(mean + P.eps);
     }
-    const float p = (float) P.pos[t];
-    for (int i = lane; i < half; i += kWave) {
-        float x0 = ld(src + i), x1 = ld(src + i + half);
+    if (cells && lane == 0) {
+        P.cell_seq[cell] = P.seq;
+        P.cell_pos[cell] = pos;
+    }
+    const float p = (float) pos;
+#pragma unroll
+    for (int m = 0; m < M; m++) {
+        const int i = lane + kWave * m;
+        if (i >= half) break;
+        float a = x0[m], b = x1[m];
         if (nw) {
-            x0 = (x0 * scale) * nw[i];
-            x1 = (x1 * scale) * nw[i + half];
+            a = (a * scale) * n0[m];
+            b = (b * scale) * n1[m];
         }
-        float c, sn;
-        if (P.cs) {
-            const float2 v = reinterpret_cast<const float2 *>(P.cs)[(size_t) t * half + i];
-            c = v.x;
-            sn = v.y;
-        } else {
-            rope_angle(p, P.theta_scale, i, c, sn);
-        }
-        const float y0 = x0 * c - x1 * sn;
-        const float y1 = x0 * sn + x1 * c;
+        float cc = c[m], ss = sn[m];
+        if (!P.cs) rope_angle(p, P.theta_scale, i, cc, ss);
+        const float y0 = a * cc - b * ss;
+        const float y1 = a * ss + b * cc;
         if (is_q && q_dst) {
             q_dst[i] = y0;
             q_dst[i + half] = y1;
