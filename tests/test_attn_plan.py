@@ -1,6 +1,7 @@
 """CPU replay of the attention launch plan and of every index the attention kernels compute
 (localstack_amd/csrc/forward.hip: attn_plan, attn_kernel, attn1_kernel, attn_rows_kernel, attn_combine_kernel; buffers sized as
-model.cpp allocates them), for work-group targets of 512 (the build's), 256 and 128, over the shapes the
+model.cpp allocates them), for work-group targets of 512 (the build's; halved for steps of a few tokens in
+one row block), 256 and 128, over the shapes the
 tests and the benchmark run and past them: every global index stays inside its buffer, every LDS index
 inside its array, and the partial rows inside attn_part_rows. No GPU. The replayed plan is held equal to
 the library's own (lstk_debug_attn_plan, host code) at the build's target, so the replay cannot drift
