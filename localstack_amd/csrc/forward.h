@@ -23,6 +23,10 @@ struct NormParams {
     int rows, n;
     float eps;
     uint16_t *y16; // when set, also y rounded to fp16 (the input of an F16 matrix product)
+    // when set, row r is first x_r + the k rows Y[r][0 .. k) of the previous MoE block (their sum in slot
+    // order, then the residual, as combine_kernel adds them), stored to x_out, then normalised
+    const float *Y = nullptr;
+    int k = 0;
 };
 
 // Per-head RMSNorm (optional), NEOX RoPE and the KV-cache store of one step.

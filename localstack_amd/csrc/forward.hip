@@ -37,8 +37,9 @@ __device__ __forceinline__ float dot8(const uint4 &a, const uint4 &b, float c) {
 // RMSNorm (ggml_rms_norm + ggml_mul), optionally gathering the row from the embedding table first
 // ------------------------------------------------------------------------------------------------
 
-// NPT values per thread, all loaded before any is used (one memory round trip per row).
-template <int NPT>
+// NPT values per thread, all loaded before any is used (one memory round trip per row). COMB: the row
+// is first the previous MoE block's combine (P.Y), formed here in combine_kernel's order.
+template <int NPT, bool COMB>
 __global__ __launch_bounds__(kNormBlock) void rmsnorm_kernel(NormParams P) {
     __shared__ double s_part[kNormBlock / kWave];
     const int r = blockIdx.x, tid = threadIdx.x;
@@ -53,6 +54,33 @@ __global__ __launch_bounds__(kNormBlock) void rmsnorm_kernel(NormParams P) {
         v[k] = !on ? 0.0f : e ? h2f(e[i]) : x[i];
         w[k] = on ? P.w[i] : 0.0f;
     }
+    if constexpr (COMB) {
+        // out = ((Y_0 + Y_1) + ... + Y_{k-1}) + x, the slots' loads in batches of 8 issued together
+        const float *yb = P.Y + (size_t) r * P.k * P.n;
+        float acc[NPT];
+#pragma unroll
+        for (int k = 0; k < NPT; k++) {
+            const int i = tid + k * kNormBlock;
+            acc[k] = i < P.n ? yb[i] : 0.0f;
+        }
+        for (int j0 = 1; j0 < P.k; j0 += 8) {
+            float t[8][NPT];
+#pragma unroll
+            for (int u = 0; u < 8; u++)
+#pragma unroll
+                for (int k = 0; k < NPT; k++) {
+                    const int i = tid + k * kNormBlock;
+                    t[u][k] = i < P.n ? yb[(size_t) min(j0 + u, P.k - 1) * P.n + i] : 0.0f;
+                }
+#pragma unroll
+            for (int u = 0; u < 8; u++)
+                if (j0 + u < P.k)
+#pragma unroll
+                    for (int k = 0; k < NPT; k++) acc[k] = acc[k] + t[u][k];
+        }
+#pragma unroll
+        for (int k = 0; k < NPT; k++) v[k] = acc[k] + v[k];
+    }
     double s = 0.0;
 #pragma unroll
     for (int k = 0; k < NPT; k++) s += (double) (v[k] * v[k]);
@@ -66,7 +94,7 @@ __global__ __launch_bounds__(kNormBlock) void rmsnorm_kernel(NormParams P) {
     for (int k = 0; k < NPT; k++) {
         const int i = tid + k * kNormBlock;
         if (i < P.n) {
-            if (e) P.x_out[off + i] = v[k];
+            if (e || COMB) P.x_out[off + i] = v[k];
             const float y = (v[k] * scale) * w[k];
             P.y[off + i] = y;
             if (P.y16) P.y16[off + i] = f2h(y);
@@ -1322,12 +1350,19 @@ hipError_t launch_rmsnorm(const NormParams &P, hipStream_t st, const LaunchTimin
     if (P.rows == 0) return hipSuccess;
     const dim3 g(P.rows), b(kNormBlock);
     const int npt = (P.n + kNormBlock - 1) / kNormBlock;
-    if (npt <= 1) return launch(rmsnorm_kernel<1>, g, b, 0, st, tm, P);
-    if (npt <= 2) return launch(rmsnorm_kernel<2>, g, b, 0, st, tm, P);
-    if (npt <= 4) return launch(rmsnorm_kernel<4>, g, b, 0, st, tm, P);
-    if (npt <= 8) return launch(rmsnorm_kernel<8>, g, b, 0, st, tm, P);
-    if (npt <= 16) return launch(rmsnorm_kernel<16>, g, b, 0, st, tm, P);
-    return launch(rmsnorm_kernel<32>, g, b, 0, st, tm, P);
+    if (P.Y) {
+        if (P.emb || !P.x_out || P.k < 1) return hipErrorInvalidValue;
+        if (npt <= 4) return launch(rmsnorm_kernel<4, true>, g, b, 0, st, tm, P);
+        if (npt <= 8) return launch(rmsnorm_kernel<8, true>, g, b, 0, st, tm, P);
+        if (npt <= 16) return launch(rmsnorm_kernel<16, true>, g, b, 0, st, tm, P);
+        return launch(rmsnorm_kernel<32, true>, g, b, 0, st, tm, P);
+    }
+    if (npt <= 1) return launch(rmsnorm_kernel<1, false>, g, b, 0, st, tm, P);
+    if (npt <= 2) return launch(rmsnorm_kernel<2, false>, g, b, 0, st, tm, P);
+    if (npt <= 4) return launch(rmsnorm_kernel<4, false>, g, b, 0, st, tm, P);
+    if (npt <= 8) return launch(rmsnorm_kernel<8, false>, g, b, 0, st, tm, P);
+    if (npt <= 16) return launch(rmsnorm_kernel<16, false>, g, b, 0, st, tm, P);
+    return launch(rmsnorm_kernel<32, false>, g, b, 0, st, tm, P);
 }
 
 bool gemm16_supported(int rows, int cols, int T) {

@@ -17,6 +17,11 @@ bool pool_streaming(const lstk_pool *pool);
 bool pool_dry(const lstk_pool *pool);
 // Whether the pool's bookkeeping lives on the device (LSTK_POOL_DEVICE_LRU).
 bool pool_device_lru(const lstk_pool *pool);
+// With `on`, blocks of several tokens stop before their combine: the k weighted expert rows of each
+// token are left in pool_moe_rows() ([T][k][n_embd] f32) for the caller to add into the residual (the
+// forward pass does it in the next layer's RMSNorm launch). Single-token blocks combine as always.
+void pool_defer_combine(lstk_pool *pool, bool on);
+const float *pool_moe_rows(const lstk_pool *pool);
 // lstk_moe_block for T tokens of a resident pool whose hnorm rows the router launch computes itself as
 // rms_norm(x) * norm_w (bit-identical to the RMSNorm kernel's rows; also stored to d_hnorm).
 int moe_block_normed(lstk_pool *pool, int layer, const float *d_x, const float *d_norm_w, float eps, float *d_hnorm,

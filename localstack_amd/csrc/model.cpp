@@ -13,7 +13,9 @@
 //     ffn_norm on the rows the FFN needs                (rmsnorm_kernel; at T = 1 with a resident pool
 //                                                        the router launch normalises the row itself)
 //     MoE block: lstk_moe_block (resident pool) or route -> acquire -> lstk_moe_ffn (streaming pool;
-//     the acquire runs on the device for an LSTK_POOL_DEVICE_LRU pool)
+//     the acquire runs on the device for an LSTK_POOL_DEVICE_LRU pool); with several tokens and a
+//     resident pool the block's combine + residual is left to the next layer's attn_norm launch,
+//     which forms the same sums before it normalises them
 //     the last layer runs its FFN on the output row only (src/qwen3.cpp:233-237)
 //   output_norm + head on the last row                  (rmsnorm_kernel, gemv_kernel)
 // With several tokens per step the projections are plain F16 matrix products: the normalised rows and
@@ -489,6 +491,12 @@ int forward(lstk_model *M, int32_t seq, int T, int n_cells, float *d_logits, int
         if ((e = lstk::launch_rope_table(tp, M->rope_cs, st)) != hipSuccess) return hip_fail(e, "rope table launch");
     }
 
+    // A step of several tokens leaves each layer's MoE combine (but the last's) to the next layer's
+    // attn_norm launch, which adds the expert rows into the residual and normalises the sum in one
+    // launch (the same values as the combine and RMSNorm launches; not when a debug capture wants the
+    // residual after each block, nor with a streaming pool).
+    const bool defer = T > 1 && !M->streaming && !M->capture && !M->capture_moe;
+    bool pending = false; // the previous layer's expert rows wait in the pool's rows
     for (int l = 0; l < hp.n_layer; l++) {
         const lstk_qwen3_layer &L = M->layers[l];
         lstk::GemvParams gp{};
@@ -512,6 +520,11 @@ int forward(lstk_model *M, int32_t seq, int T, int n_cells, float *d_logits, int
         } else {
             lstk::NormParams np{M->x, l == 0 ? M->tok_embd : nullptr, d_tok, M->x, L.attn_norm, M->hn, T, h, hp.rms_eps,
                                 blas ? M->hn16 : nullptr};
+            if (pending) {
+                np.Y = lstk::pool_moe_rows(M->pool);
+                np.k = k;
+                pending = false;
+            }
             if ((e = timed(M, 0, [&](const lstk::LaunchTiming *tm) { return lstk::launch_rmsnorm(np, st, tm); })) != hipSuccess)
                 return hip_fail(e, "attn_norm launch");
             gp.x = M->hn;
@@ -596,8 +609,12 @@ int forward(lstk_model *M, int32_t seq, int T, int n_cells, float *d_logits, int
             lstk::FillParams fl{d_trace + (size_t) l * T * k, (T - 1) * k, -1};
             if ((e = lstk::launch_fill(fl, st, nullptr)) != hipSuccess) return hip_fail(e, "trace fill launch");
         }
+        const bool defer_here = defer && !last;
+        if (defer_here) lstk::pool_defer_combine(M->pool, true);
         const int rc = moe(M, l, rows, xr, ids, st, norm_in_router ? L.ffn_norm : nullptr);
+        if (defer_here) lstk::pool_defer_combine(M->pool, false);
         if (rc != LSTK_OK) return rc;
+        pending = defer_here;
         if (M->capture && (e = hipMemcpyAsync(M->capture + (size_t) l * T * h, M->x, (size_t) T * h * sizeof(float),
                                               hipMemcpyDeviceToDevice, st)) != hipSuccess)
             return hip_fail(e, "capture copy");

@@ -181,6 +181,9 @@ struct lstk_pool {
     void *scratch_mem = nullptr;
     lstk::ActBuf xq{};
     float *logits = nullptr, *act = nullptr, *Y = nullptr;
+    // set by the forward pass around a block of several tokens: the combine is left to the next
+    // layer's RMSNorm launch, which sums the rows of Y into the residual itself (pool_defer_combine)
+    bool defer_combine = false;
     // this device's address of the library's fixed scratch array (lstk_moe_block_noalloc)
     uint8_t *noalloc = nullptr;
     int32_t *err = nullptr;
@@ -887,6 +890,7 @@ int run_grouped(lstk_pool *P, const Shard &s, const int32_t *bins, const float *
     dn.out = P->Y;
     e = timed(P, 2, [&](const lstk::LaunchTiming *tm) { return lstk::launch_down_grouped(dn, max_items, st, tm); });
     if (e != hipSuccess) return hip_fail(e, "down launch");
+    if (P->defer_combine) return LSTK_OK;
     lstk::CombineParams cp{P->Y, d_resid, d_out, T, k, h};
     e = timed(P, 3, [&](const lstk::LaunchTiming *tm) { return lstk::launch_combine(cp, st, tm); });
     if (e != hipSuccess) return hip_fail(e, "combine launch");
@@ -1093,6 +1097,7 @@ int run_block(lstk_pool *P, int layer, int mode, const float *d_hnorm, const voi
     dn.Y = sc.Y;
     e = timed(P, 2, [&](const lstk::LaunchTiming *tm) { return lstk::launch_down(dn, st, tm); });
     if (e != hipSuccess) return hip_fail(e, "down launch");
+    if (P->defer_combine && !fixed && T > 1) return LSTK_OK;
     lstk::CombineParams cp{sc.Y, d_resid, d_out, T, k, d.n_embd};
     e = timed(P, 3, [&](const lstk::LaunchTiming *tm) { return lstk::launch_combine(cp, st, tm); });
     if (e != hipSuccess) return hip_fail(e, "combine launch");
@@ -1120,6 +1125,8 @@ const lstk_moe_dims &pool_dims(const lstk_pool *pool) { return pool->dims; }
 bool pool_streaming(const lstk_pool *pool) { return pool->streaming; }
 bool pool_dry(const lstk_pool *pool) { return pool->dry; }
 bool pool_device_lru(const lstk_pool *pool) { return pool->device_lru; }
+void pool_defer_combine(lstk_pool *pool, bool on) { pool->defer_combine = on; }
+const float *pool_moe_rows(const lstk_pool *pool) { return pool->Y; }
 
 int moe_block_normed(lstk_pool *pool, int layer, const float *d_x, const float *d_norm_w, float eps, float *d_hnorm,
                      const void *d_gate_inp, int gate_type, const float *d_resid, float *d_out, int32_t *d_ids,

@@ -206,3 +206,32 @@ def test_single_token_long_context(lstk, dev, mid):
             chk.ref.truncate(done)
         chk.model.debug_options(rope_apart=False)
     chk.close()
+
+
+def test_deferred_moe_combine_is_bit_identical(lstk, dev, mid):
+    """Steps of several tokens leave each MoE block's combine (but the last layer's) to the next layer's
+    attn_norm launch. A debug capture of the residual stream turns that off, so the same steps with and
+    without one must give the same logits bit for bit: a 100-token prompt (grouped kernels), then 8, 32,
+    1 and 64 tokens."""
+    import torch
+    hp, w = mid
+    layers = [(L["types"], L["up"], L["gate"], L["down"]) for L in w["layers"]]
+    out = []
+    for capture in (False, True):
+        store = lstk.ExpertStore(hp["n_layer"], hp["n_embd"], hp["n_ff_exp"], hp["n_expert"], hp["n_expert_used"], 128,
+                                 layers)
+        model = lstk.Qwen3Model(hp, w, store, 1024, 128, device=dev)
+        states = torch.zeros((hp["n_layer"], 128, hp["n_embd"]), dtype=torch.float32, device=dev)
+        if capture:
+            model.debug_capture(states)
+        rng = np.random.default_rng(7)
+        lg = []
+        for T in (100, 8, 32, 1, 64):
+            lg.append(model.decode(1, rng.integers(0, hp["n_vocab"], T).astype(np.int32)).cpu().numpy().copy())
+        torch.cuda.synchronize()
+        model.debug_capture(None)
+        model.close()
+        store.close()
+        out.append(np.stack(lg))
+    print(f"[deferred combine] max |dlogit| {float(np.max(np.abs(out[0] - out[1]))):.1e}", flush=True)
+    assert np.array_equal(out[0].view(np.uint32), out[1].view(np.uint32))
