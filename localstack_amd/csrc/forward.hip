@@ -55,7 +55,9 @@ __global__ __launch_bounds__(kNormBlock) void rmsnorm_kernel(NormParams P) {
         w[k] = on ? P.w[i] : 0.0f;
     }
     if constexpr (COMB) {
-        // out = ((Y_0 + Y_1) + ... + Y_{k-1}) + x, the slots' loads in batches of 8 issued together
+        // out = ((Y_0 + Y_1) + ... + Y_{k-1}) + x, the slots' loads in batches of B issued together
+        // (B * NPT <= 64 values in flight per thread)
+        constexpr int B = NPT >= 32 ? 2 : NPT >= 16 ? 4 : 8;
         const float *yb = P.Y + (size_t) r * P.k * P.n;
         float acc[NPT];
 #pragma unroll
@@ -63,17 +65,17 @@ __global__ __launch_bounds__(kNormBlock) void rmsnorm_kernel(NormParams P) {
             const int i = tid + k * kNormBlock;
             acc[k] = i < P.n ? yb[i] : 0.0f;
         }
-        for (int j0 = 1; j0 < P.k; j0 += 8) {
-            float t[8][NPT];
+        for (int j0 = 1; j0 < P.k; j0 += B) {
+            float t[B][NPT];
 #pragma unroll
-            for (int u = 0; u < 8; u++)
+            for (int u = 0; u < B; u++)
 #pragma unroll
                 for (int k = 0; k < NPT; k++) {
                     const int i = tid + k * kNormBlock;
                     t[u][k] = i < P.n ? yb[(size_t) min(j0 + u, P.k - 1) * P.n + i] : 0.0f;
                 }
 #pragma unroll
-            for (int u = 0; u < 8; u++)
+            for (int u = 0; u < B; u++)
                 if (j0 + u < P.k)
 #pragma unroll
                     for (int k = 0; k < NPT; k++) acc[k] = acc[k] + t[u][k];
