@@ -126,6 +126,7 @@ struct Gemm16Params {
     const uint16_t *w, *x;
     float *y;
     int rows, cols, T, ldy, accumulate;
+    int rw = 16; // rows per work-group (set by launch_gemm16)
 };
 // rows a multiple of 16, cols 2048 or 4096, 1 <= T <= 16
 bool gemm16_supported(int rows, int cols, int T);

@@ -514,34 +514,45 @@ __global__ __launch_bounds__(kGvWaves *kWave) void gemv1_kernel(GemvParams P) {
 }
 
 // ------------------------------------------------------------------------------------------------
-// F16 projection of a few tokens on the matrix cores (v_mfma_f32_16x16x32_f16). Work-group = 16 weight
-// rows x all T tokens (16-token tiles); its KS wavefronts split K in interleaved 64-value steps, SPW
-// steps each, and every wavefront requests all of its weight and activation chunks before its first
-// product. Per step, lane (r = l % 16, q = l / 16) loads the 32 contiguous bytes [16 q, 16 q + 16) (in
-// halves) of weight row r and of token row r, and product i takes halves [8 i, 8 i + 8) of them: A and
-// B pair the same K index in every slot, and each row's 128-byte line is read whole by its four lanes.
-// The KS partial 16 x 16 tiles are summed in LDS in wavefront order.
+// F16 projection of a few tokens on the matrix cores (v_mfma_f32_16x16x32_f16). Work-group = rw weight
+// rows (NRT 16-row tiles, the last one padded with rows that are neither loaded nor stored) x all T
+// tokens (16-token tiles); rw is the matrix's rows over the work-groups of one wave of the device, so
+// every CU streams the same bytes. Its KS wavefronts split K in interleaved 64-value steps, SPW steps
+// each, and every wavefront requests all of its weight and activation chunks before its first product.
+// Per step, lane (r = l % 16, q = l / 16) loads the 32 contiguous bytes [16 q, 16 q + 16) (in halves) of
+// weight row r and of token row r, and product i takes halves [8 i, 8 i + 8) of them: A and B pair the
+// same K index in every slot, and each row's 128-byte line is read whole by its four lanes. The KS
+// partial 16 x 16 tiles are summed in LDS in wavefront order.
 // ------------------------------------------------------------------------------------------------
 
 typedef _Float16 half8v __attribute__((ext_vector_type(8)));
 typedef float f32x4v __attribute__((ext_vector_type(4)));
 
-template <int KS, int SPW, int NTILE>
+template <int KS, int SPW, int NTILE, int NRT>
 __global__ __launch_bounds__(KS *kWave) void gemm16_kernel(Gemm16Params P) {
     __shared__ f32x4v s_red[KS][kWave];
     const int lane = threadIdx.x & (kWave - 1), w = threadIdx.x / kWave, r = lane & 15, q = lane >> 4;
-    const int n0 = blockIdx.x * 16;
-    const uint4 *wrow = reinterpret_cast<const uint4 *>(P.w + (size_t) (n0 + r) * P.cols) + 2 * q;
+    const int n0 = blockIdx.x * P.rw;
+    const uint4 *wrow[NRT];
+    bool won[NRT];
+#pragma unroll
+    for (int rt = 0; rt < NRT; rt++) {
+        won[rt] = rt * 16 + r < P.rw;
+        wrow[rt] = reinterpret_cast<const uint4 *>(P.w + (size_t) (n0 + min(rt * 16 + r, P.rw - 1)) * P.cols) + 2 * q;
+    }
     const uint4 *xrow[NTILE];
 #pragma unroll
     for (int nt = 0; nt < NTILE; nt++)
         xrow[nt] = reinterpret_cast<const uint4 *>(P.x + (size_t) min(nt * 16 + r, P.T - 1) * P.cols) + 2 * q;
     // a 64-value step is 8 uint4 of a row; this lane's 2 of step s are uint4 8 s + 2 q, + 1
-    uint4 wv[SPW][2], xv[NTILE][SPW][2];
+    uint4 wv[NRT][SPW][2], xv[NTILE][SPW][2];
 #pragma unroll
-    for (int j = 0; j < SPW; j++)
+    for (int rt = 0; rt < NRT; rt++)
 #pragma unroll
-        for (int i = 0; i < 2; i++) wv[j][i] = load_weights(wrow + 8 * (w + KS * j) + i);
+        for (int j = 0; j < SPW; j++)
+#pragma unroll
+            for (int i = 0; i < 2; i++)
+                wv[rt][j][i] = won[rt] ? load_weights(wrow[rt] + 8 * (w + KS * j) + i) : make_uint4(0, 0, 0, 0);
 #pragma unroll
     for (int nt = 0; nt < NTILE; nt++)
 #pragma unroll
@@ -549,36 +560,43 @@ __global__ __launch_bounds__(KS *kWave) void gemm16_kernel(Gemm16Params P) {
 #pragma unroll
             for (int i = 0; i < 2; i++) xv[nt][j][i] = xrow[nt][8 * (w + KS * j) + i];
     __builtin_amdgcn_sched_barrier(0); // every load above is issued before the first product waits
-    f32x4v acc[NTILE];
+    f32x4v acc[NRT][NTILE];
 #pragma unroll
-    for (int nt = 0; nt < NTILE; nt++) acc[nt] = f32x4v{0, 0, 0, 0};
+    for (int rt = 0; rt < NRT; rt++)
+#pragma unroll
+        for (int nt = 0; nt < NTILE; nt++) acc[rt][nt] = f32x4v{0, 0, 0, 0};
 #pragma unroll
     for (int j = 0; j < SPW; j++)
 #pragma unroll
-        for (int i = 0; i < 2; i++) {
-            const half8v a = __builtin_bit_cast(half8v, wv[j][i]);
+        for (int i = 0; i < 2; i++)
 #pragma unroll
-            for (int nt = 0; nt < NTILE; nt++)
-                acc[nt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, __builtin_bit_cast(half8v, xv[nt][j][i]), acc[nt], 0, 0, 0);
-        }
-    // element e of lane l: weight row n0 + 4 (l / 16) + e, token nt * 16 + l % 16
+            for (int rt = 0; rt < NRT; rt++) {
+                const half8v a = __builtin_bit_cast(half8v, wv[rt][j][i]);
 #pragma unroll
-    for (int nt = 0; nt < NTILE; nt++) {
-        s_red[w][lane] = acc[nt];
-        __syncthreads();
-        for (int idx = threadIdx.x; idx < 4 * kWave; idx += KS * kWave) {
-            const int e = idx / kWave, l = idx % kWave;
-            float v = s_red[0][l][e];
-#pragma unroll
-            for (int ww = 1; ww < KS; ww++) v += s_red[ww][l][e];
-            const int t = nt * 16 + (l & 15), n = n0 + 4 * (l >> 4) + e;
-            if (t < P.T) {
-                float *y = P.y + (size_t) t * P.ldy + n;
-                *y = P.accumulate ? v + *y : v;
+                for (int nt = 0; nt < NTILE; nt++)
+                    acc[rt][nt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, __builtin_bit_cast(half8v, xv[nt][j][i]), acc[rt][nt], 0,
+                                                                         0, 0);
             }
+    // element e of lane l: weight row n0 + 16 rt + 4 (l / 16) + e, token nt * 16 + l % 16
+#pragma unroll
+    for (int rt = 0; rt < NRT; rt++)
+#pragma unroll
+        for (int nt = 0; nt < NTILE; nt++) {
+            s_red[w][lane] = acc[rt][nt];
+            __syncthreads();
+            for (int idx = threadIdx.x; idx < 4 * kWave; idx += KS * kWave) {
+                const int e = idx / kWave, l = idx % kWave;
+                float v = s_red[0][l][e];
+#pragma unroll
+                for (int ww = 1; ww < KS; ww++) v += s_red[ww][l][e];
+                const int t = nt * 16 + (l & 15), rr = rt * 16 + 4 * (l >> 4) + e;
+                if (t < P.T && rr < P.rw) {
+                    float *y = P.y + (size_t) t * P.ldy + n0 + rr;
+                    *y = P.accumulate ? v + *y : v;
+                }
+            }
+            __syncthreads();
         }
-        __syncthreads();
-    }
 }
 
 // ------------------------------------------------------------------------------------------------
@@ -724,7 +742,6 @@ __global__ __launch_bounds__(kAtBlock) void attn_kernel(AttnParams P) {
         if (c0 != begin || late) load_pass(c0);
         // S = Q K^T for this wavefront's 16 cells
         const int cell = c0 + 16 * w + lr;
-        const int cc = min(cell, P.kv_size - 1);
         const bool live = cell < end && cseq == P.seq;
         const int cpos = cpos0;
 #pragma unroll
@@ -1371,16 +1388,39 @@ bool gemm16_supported(int rows, int cols, int T) {
     return rows > 0 && rows % 16 == 0 && (cols == 2048 || cols == 4096) && T >= 1 && T <= 16;
 }
 
-// 8 wavefronts, 4 steps of 64 values each at 2048 columns, 8 at 4096; one 16-token tile. Measured on
-// MI355X at the 30B shape, T = 8: Q/K/V (21.0 MB) 9.46 us and o-proj (16.8 MB) 9.81 us, against about
-// 12 us each for rocblas_gemm_ex; with a second 16-token tile (T = 32) 14.4 and 15.1 us, slower than
-// rocBLAS, which keeps T > 16. 2, 4 or 16 wavefronts per work-group instead of 8 change nothing measurable
-// (the whole-model T = 8 step within 1%).
-hipError_t launch_gemm16(const Gemm16Params &P, hipStream_t st, const LaunchTiming *tm) {
-    if (!gemm16_supported(P.rows, P.cols, P.T)) return hipErrorInvalidValue;
-    const dim3 grid(P.rows / 16), block(8 * kWave);
-    return P.cols == 2048 ? launch(gemm16_kernel<8, 4, 1>, grid, block, 0, st, tm, P)
-                          : launch(gemm16_kernel<8, 8, 1>, grid, block, 0, st, tm, P);
+// Rows per work-group: the smallest rw dividing `rows` with rows / rw <= 256 (one work-group per CU on
+// MI355X's 256 CUs), so that no CU streams twice the bytes of another (320 work-groups of 16 rows for
+// the 5120 Q/K/V rows of the 30B shape left 64 CUs with two).
+// Rows per work-group at 2048 columns: up to 64 (four tiles); at 4096 columns up to 16 (one tile, whose
+// weights and activations already take 128 VGPRs).
+static int gemm16_rows_per_wg(int rows, int cols) {
+    const int cap = cols == 2048 ? 64 : 16;
+    for (int rw = (rows + 255) / 256; rw <= cap; rw++)
+        if (rows % rw == 0) return rw;
+    return 16;
+}
+
+// 8 wavefronts, 4 steps of 64 values each at 2048 columns, 8 at 4096; one 16-token tile. With 16 rows per
+// work-group, measured on MI355X at the 30B shape, T = 8: Q/K/V (21.0 MB) 9.46 us and o-proj (16.8 MB)
+// 9.81 us, against about 12 us each for rocblas_gemm_ex; with a second 16-token tile (T = 32) 14.4 and
+// 15.1 us, slower than rocBLAS, which keeps T > 16. 2, 4 or 16 wavefronts per work-group instead of 8
+// change nothing measurable (the whole-model T = 8 step within 1%). Rows per work-group from the rows
+// (20 for Q/K/V and 8 for o-proj: 256 work-groups each) take the eager per-layer Q/K/V + rope stage from
+// 16.3 to 14.7 us and o-proj from 12.2 to 11.4 us at T = 8 (whole model T = 8 1777 -> 1826 tok/s,
+// T = 16 2825 -> 2918), with the same sums in the same order per output.
+hipError_t launch_gemm16(const Gemm16Params &Pin, hipStream_t st, const LaunchTiming *tm) {
+    if (!gemm16_supported(Pin.rows, Pin.cols, Pin.T)) return hipErrorInvalidValue;
+    Gemm16Params P = Pin;
+    P.rw = gemm16_rows_per_wg(P.rows, P.cols);
+    const int nrt = (P.rw + 15) / 16;
+    const dim3 grid(P.rows / P.rw), block(8 * kWave);
+    if (P.cols == 2048) {
+        if (nrt == 1) return launch(gemm16_kernel<8, 4, 1, 1>, grid, block, 0, st, tm, P);
+        if (nrt == 2) return launch(gemm16_kernel<8, 4, 1, 2>, grid, block, 0, st, tm, P);
+        if (nrt == 3) return launch(gemm16_kernel<8, 4, 1, 3>, grid, block, 0, st, tm, P);
+        return launch(gemm16_kernel<8, 4, 1, 4>, grid, block, 0, st, tm, P);
+    }
+    return launch(gemm16_kernel<8, 8, 1, 1>, grid, block, 0, st, tm, P);
 }
 
 template <int NJ, int RW>
