@@ -711,10 +711,35 @@ __global__ __launch_bounds__(kDnRows * kMaxG) void down_kernel(DownParams P) {
     float *xd = reinterpret_cast<float *>(work + (size_t) kTC * f);
     int *xb = reinterpret_cast<int *>(xd + kTC * f32);
     float *red = reinterpret_cast<float *>(xb + kTC * f32);
+    // A chunk's nt SwiGLU rows are quantized as one array of nt * f values (f a multiple of 256, so each
+    // 256-value block lies in one row, as quantizing row by row takes it), NG passes of 8 values per
+    // thread at a time with every load of the NG passes issued before the first is quantized: one memory
+    // round trip per NG passes instead of one per pair. blockDim = 64 G threads, G = f / 256 / S, take
+    // 2 f / S values per pass, so kTC rows take NP = 4 S passes.
+    constexpr int NP = kTC / 2 * S, NG = 2;
+    const int bd = blockDim.x;
     for (int c0 = 0; c0 < cnt; c0 += kTC) {
-        const int nt = min(kTC, cnt - c0);
-        for (int tc = 0; tc < nt; tc++)
-            quantize_row<QT>(P.act + (size_t) gl.list[c0 + tc] * f, f, xs + (size_t) tc * f, xd + tc * f32, xb + tc * f32);
+        const int nt = min(kTC, cnt - c0), n = nt * f;
+#pragma unroll 1
+        for (int p0 = 0; p0 < NP; p0 += NG) {
+            if (p0 * bd * 8 >= n) break; // the same for every thread
+            float v[NG][8];
+#pragma unroll
+            for (int p = 0; p < NG; p++) {
+                const int i0 = ((p0 + p) * bd + tid) * 8, ia = min(i0, n - 8);
+                const float *x = P.act + (size_t) gl.list[c0 + ia / f] * f + ia % f;
+                const float4 a = *reinterpret_cast<const float4 *>(x);
+                const float4 b = *reinterpret_cast<const float4 *>(x + 4);
+                const bool in = i0 < n;
+                v[p][0] = in ? a.x : 0.0f; v[p][1] = in ? a.y : 0.0f; v[p][2] = in ? a.z : 0.0f; v[p][3] = in ? a.w : 0.0f;
+                v[p][4] = in ? b.x : 0.0f; v[p][5] = in ? b.y : 0.0f; v[p][6] = in ? b.z : 0.0f; v[p][7] = in ? b.w : 0.0f;
+            }
+#pragma unroll
+            for (int p = 0; p < NG; p++) {
+                const int i0 = ((p0 + p) * bd + tid) * 8;
+                if ((p0 + p) * bd * 8 < n) quantize8<QT>(v[p], i0, i0 < n, xs, xd, xb);
+            }
+        }
         __syncthreads();
         for (int tc = 0; tc < nt; tc++) {
             float acc = 0.0f;
