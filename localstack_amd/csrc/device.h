@@ -704,6 +704,16 @@ __device__ __forceinline__ float dot_sb_kq8(const uint4 (&w)[kChunksKQ8], const 
     return acc;
 }
 
+// Marks a super-block's weight registers as rewritten (an empty asm statement: no instruction), so that
+// what dot_sb derives from them (masked nibbles, scales, fp16 factors) is formed again at each call in a
+// loop over tokens instead of being held in registers across the loop: the raw chunks stay the only live
+// copy, which keeps multi-token expert kernels at more wavefronts per SIMD. Values are unchanged.
+template <int C>
+__device__ __forceinline__ void rederive(uint4 (&w)[C]) {
+#pragma unroll
+    for (int c = 0; c < C; c++) asm volatile("" : "+v"(w[c].x), "+v"(w[c].y), "+v"(w[c].z), "+v"(w[c].w));
+}
+
 template <int WT>
 __device__ __forceinline__ float dot_sb(const uint4 (&w)[chunks_of(WT)], const int8_t *x, const float *xd,
                                         const int *xb, float acc) {
