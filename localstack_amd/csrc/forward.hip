@@ -888,22 +888,22 @@ __global__ __launch_bounds__(kAtBlock) void attn_kernel(AttnParams P) {
 
 // ------------------------------------------------------------------------------------------------
 // Single-token attention at head size 128 with RoPE inside (grp <= 16 query heads per KV head): each
-// wavefront runs its own 16 cells of the work-group's 64-cell chunk from registers to registers, so
+// wavefront runs its own 16 cells of the work-group's chunk (16 cells per wavefront) from registers to registers, so
 // the pass has no barrier and no LDS round trip. With the K fragments as the A operand and the query
 // rows as the B operand the product comes out transposed, S^T [cell][row]: lane (row j, quad q) holds
 // cells 4q .. 4q + 3 of row j, which is exactly the B operand of O^T = V^T P^T (and the V fragments
 // of the cache are the A operand as they stand). A row's softmax state and output stay in the lanes
 // of that row; the row's max over its 16 cells takes two lane exchanges (quads 0-3). At the end the
-// four wavefronts' (max, sum, output) rows are merged through LDS, and the merged row is the chunk's
+// wavefronts' (max, sum, output) rows are merged through LDS, and the merged row is the chunk's
 // partial (or, with one chunk, the output). Probabilities enter the product as fp16 hi + lo parts
 // (p = hi + lo to 2^-22), Q and K as fp16, all accumulation in f32, as in attn_kernel.
 // ------------------------------------------------------------------------------------------------
-constexpr int kA1Cells = 16; // cells per wavefront
-static_assert(kA1Cells * (kAtBlock / kWave) == kFaCells, "a work-group covers one 64-cell chunk");
+constexpr int kA1Cells = 16; // cells per wavefront; a work-group of NW = 4, 5 or 6 wavefronts covers a chunk of 16 NW cells
 __device__ __forceinline__ float xor_lanes(float v, int m) { return __shfl_xor(v, m, kWave); }
 
-__global__ __launch_bounds__(kAtBlock) void attn1_kernel(AttnParams P) {
-    constexpr int HD = 128, NK = HD / 16, NW = kAtBlock / kWave, RS = HD + 4;
+template <int NW>
+__global__ __launch_bounds__(NW *kWave) void attn1_kernel(AttnParams P) {
+    constexpr int HD = 128, NK = HD / 16, RS = HD + 4;
     __shared__ float s_q[16 * HD];
     __shared__ __align__(8) uint16_t s_kv[2 * HD];
     __shared__ __align__(16) float s_o[NW][16][RS];
@@ -928,7 +928,10 @@ __global__ __launch_bounds__(kAtBlock) void attn1_kernel(AttnParams P) {
         cseq = *reinterpret_cast<const int4 *>(P.cell_seq + cv);
         cpos = *reinterpret_cast<const int4 *>(P.cell_pos + cv);
     };
-    rope_token_128(P.rope, g, grp, owner, s_q, s_kv, loads);
+    // wavefronts 0-3 rotate the query rows (heads w, w + 4, ...; K / V of the owner's token by 0 and 1);
+    // any further ones only issue their loads
+    if (w < 4) rope_token_128(P.rope, g, grp, owner, s_q, s_kv, loads);
+    else loads();
     __syncthreads();
     // B operand of S^T: query row lr (zero past grp), dims ks*16 + 4 lq .. +3
     half4v qb[NK];
@@ -990,7 +993,7 @@ __global__ __launch_bounds__(kAtBlock) void attn1_kernel(AttnParams P) {
     for (int dt = 0; dt < NK; dt++) *reinterpret_cast<f32x4v *>(&s_o[w][lr][dt * 16 + 4 * lq]) = o[dt];
     __syncthreads();
     // merge the wavefronts: thread (row r, dims 4 dq .. +3)
-    for (int i = tid; i < grp * (HD / 4); i += kAtBlock) {
+    for (int i = tid; i < grp * (HD / 4); i += NW * kWave) {
         const int r = i / (HD / 4), dq = i % (HD / 4), h = g * grp + r;
         float M = s_m[0][r];
 #pragma unroll
@@ -1336,6 +1339,7 @@ bool attn_supported(int hd) { return hd == 64 || hd == 128 || hd == 256; }
 // cells at 32 query heads, 32768 at 64): the RoPE prologue has only been run with single-pass chunks on
 // the device. Past that, rope_in is cleared (the caller runs rope_kernel) and chunks take several passes.
 constexpr int kAttnTarget = 512;
+constexpr int kAttn1Wgs = 256; // one work-group per CU of MI355X
 void attn_plan(AttnParams &P) {
     const int rows = P.T * (P.n_head / P.n_kv);
     P.rb_rows = rows <= 16 ? 16 : rows <= 32 ? 32 : 64;
@@ -1343,8 +1347,23 @@ void attn_plan(AttnParams &P) {
     const int passes = (P.n_cells - P.cell_begin + kFaCells - 1) / kFaCells;
     if (P.rope_in) {
         if ((long) P.n_head * passes <= 32768) {
-            P.chunk = kFaCells;
-            P.n_chunk = passes;
+            // one pass per chunk. attn1_kernel (head size 128, up to 16 query heads per KV head) takes 16
+            // cells per wavefront: 4 wavefronts (64-cell chunks), or 5 or 6 (80, 96) when that keeps the
+            // launch at one work-group per CU where 64-cell chunks would not. At 4352 cells 272 work-groups
+            // of 64 cells put 16 of them on a CU with another: the launch's last one ended 6.1 us after the
+            // first began, against 4.6 us with 256 (work-groups measured with s_memrealtime on MI355X).
+            const int cells = P.n_cells - P.cell_begin;
+            int chunk = kFaCells;
+            if (P.hd == 128 && P.n_head / P.n_kv <= 4 * kRopeMaxQ && (long) P.n_kv * passes > kAttn1Wgs) {
+                for (int nw = 5; nw <= 6; nw++) {
+                    if ((long) P.n_kv * ((cells + nw * kA1Cells - 1) / (nw * kA1Cells)) <= kAttn1Wgs) {
+                        chunk = nw * kA1Cells;
+                        break;
+                    }
+                }
+            }
+            P.chunk = chunk;
+            P.n_chunk = (cells + chunk - 1) / chunk;
             return;
         }
         P.rope_in = 0;
@@ -1477,8 +1496,11 @@ template <int HD>
 hipError_t launch_attn_hd(const AttnParams &P, hipStream_t st, const LaunchTiming *tm) {
     const dim3 grid(P.n_kv * P.n_chunk * P.n_rowblk), block(kAtBlock);
     if constexpr (HD == 128) {
-        if (P.rb_rows == 16 && P.rope_in && P.n_head / P.n_kv <= 4 * kRopeMaxQ && P.rope.cs && P.chunk == kFaCells)
-            return launch(attn1_kernel, grid, block, 0, st, tm, P);
+        if (P.rb_rows == 16 && P.rope_in && P.n_head / P.n_kv <= 4 * kRopeMaxQ && P.rope.cs) {
+            if (P.chunk == 4 * kA1Cells) return launch(attn1_kernel<4>, grid, dim3(4 * kWave), 0, st, tm, P);
+            if (P.chunk == 5 * kA1Cells) return launch(attn1_kernel<5>, grid, dim3(5 * kWave), 0, st, tm, P);
+            if (P.chunk == 6 * kA1Cells) return launch(attn1_kernel<6>, grid, dim3(6 * kWave), 0, st, tm, P);
+        }
     }
     // 64-row blocks: each wavefront on its own 16 rows (head sizes 64 and 128; 256 would need 128 KB of
     // fragments per block)

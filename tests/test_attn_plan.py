@@ -19,9 +19,10 @@ AT_BLOCK = 256      # kAtBlock: 4 wavefronts
 MAX_PASSES = 2048   # kAttnMaxPasses: passes per chunk the skip map of many-token steps covers
 BLOCK = 256         # kBlock (attn_combine_kernel)
 LDS_MAX = 65536
+A1_WGS = 256        # kAttn1Wgs: one work-group per CU
 
 
-def plan(T, n_head, n_kv, n_cells, target=512, rope_in=False, cell_begin=0):
+def plan(T, n_head, n_kv, n_cells, target=512, rope_in=False, cell_begin=0, hd=128):
     """attn_plan (forward.hip): rows per work-group, row blocks, chunk (cells), chunks; rope_in kept or not.
     The attended cells are [cell_begin, n_cells)."""
     rows = T * (n_head // n_kv)
@@ -30,7 +31,15 @@ def plan(T, n_head, n_kv, n_cells, target=512, rope_in=False, cell_begin=0):
     passes = (n_cells - cell_begin + FA_CELLS - 1) // FA_CELLS
     if rope_in:
         if n_head * passes <= 32768:
-            return rb_rows, n_rowblk, FA_CELLS, passes, True
+            # one pass per chunk; attn1_kernel's chunks (16 cells per wavefront, 4 to 6 wavefronts) widen
+            # to 80 or 96 cells when that keeps the launch within 256 work-groups and 64 would not
+            cells, chunk = n_cells - cell_begin, FA_CELLS
+            if hd == 128 and n_head // n_kv <= 16 and n_kv * passes > A1_WGS:
+                for nw in (5, 6):
+                    if n_kv * -(-cells // (16 * nw)) <= A1_WGS:
+                        chunk = 16 * nw
+                        break
+            return rb_rows, n_rowblk, chunk, -(-cells // chunk), True
         rope_in = False
     if T > 1 and n_rowblk == 1:  # a few tokens in one row block: half the target
         target //= 2
@@ -52,7 +61,7 @@ def check_launch(T, n_head, n_kv, hd, kv_size, n_cells, n_batch, target, rope_in
     assert 1 <= T <= n_batch and 1 <= n_cells <= kv_size and kv_size % 32 == 0
     assert 0 <= cell_begin < n_cells and cell_begin % 64 == 0
     grp = n_head // n_kv
-    rb_rows, n_rowblk, chunk, n_chunk, rope_in = plan(T, n_head, n_kv, n_cells, target, rope_in, cell_begin)
+    rb_rows, n_rowblk, chunk, n_chunk, rope_in = plan(T, n_head, n_kv, n_cells, target, rope_in, cell_begin, hd)
     NRT = rb_rows // 16
     RB, NK = 16 * NRT, hd // 16
     DT = NK // 4
@@ -95,16 +104,19 @@ def check_launch(T, n_head, n_kv, hd, kv_size, n_cells, n_batch, target, rope_in
         assert cc.max() < kv_size and ki_max < kv_elems
     skip = T >= 64 and not rope_in
     if rope_in and hd == 128:
-        # attn1_kernel (launch_attn_hd's single-token case): wavefront w of a work-group runs cells
-        # wb = begin + 16 w .. + 15; its cell-table entries are one int4 load at cv = min(wb + 4 lq,
-        # kv_size - 4), 16-byte aligned; LDS: s_q [16][128] f32, s_kv [256] u16, s_o [4][16][132] f32,
-        # s_m / s_l [4][16] f32
-        assert chunk == FA_CELLS and grp <= 16
-        wb = begin[:, None] + 16 * np.arange(4)[None, :]
+        # attn1_kernel<NW> (launch_attn_hd's single-token case, NW = chunk / 16 wavefronts): wavefront w
+        # of a work-group runs cells wb = begin + 16 w .. + 15, K of cell min(wb + lr, kv_size - 1); its
+        # V fragments and cell-table entries are loads at cv = min(wb + 4 lq, kv_size - 4), 16-byte
+        # aligned; LDS: s_q [16][128] f32, s_kv [256] u16, s_o [NW][16][132] f32, s_m / s_l [NW][16] f32
+        assert chunk in (64, 80, 96) and grp <= 16
+        NW = chunk // 16
+        wb = begin[:, None] + 16 * np.arange(NW)[None, :]
+        ck = np.minimum(wb[:, :, None] + np.arange(16)[None, None, :], kv_size - 1)
         cv = np.minimum(wb[:, :, None] + 4 * np.arange(4)[None, None, :], kv_size - 4)
+        assert ck.min() >= 0 and ck.max() < kv_size
         assert (cv % 4 == 0).all() and cv.min() >= 0 and cv.max() + 3 < kv_size
-        lds = 16 * 128 * 4 + 2 * 128 * 2 + 4 * 16 * 132 * 4 + 2 * 4 * 16 * 4
-        assert lds == 43008 and lds <= LDS_MAX
+        lds = 16 * 128 * 4 + 2 * 128 * 2 + NW * 16 * 132 * 4 + 2 * NW * 16 * 4
+        assert lds == {4: 43008, 5: 51584, 6: 60160}[NW] and lds <= LDS_MAX  # the compiler's figures
     elif rb_rows == 64 and hd <= 128:
         # attn_rows_kernel: wavefront w fetches K of cell b0 + 16 w + lr, V of cells b0 + 16 w + 4 lq ..
         # + 3 and the cell tables of cell b0 + 16 w + (lane & 15), clamped to the cache; partial rows and
@@ -153,11 +165,11 @@ def test_replayed_plan_is_the_library_plan(lstk):
     for n_head, n_kv, hd in SHAPES.values():
         grp = n_head // n_kv
         for kv_size in (96, 288, 1000 // 32 * 32, 1024, 4608, 4352 + 32, 65536, 65600, 131072):
-            for n_cells in sorted({min(kv_size, c) for c in (1, 64, 256, 300, 4352, 8192, 65536, 65600, 131072)}):
+            for n_cells in sorted({min(kv_size, c) for c in (1, 64, 256, 300, 4160, 4352, 5632, 6144, 6200, 8192, 65536, 65600, 131072)}):
                 for cell_begin in sorted({0, (n_cells - 1) // 2 // 64 * 64, (n_cells - 1) // 64 * 64}):
                     for T in (1, 2, 8, 32, 64, 256, 512):
                         for rope in ((False, True) if T == 1 and grp <= 16 else (False,)):
-                            want = plan(T, n_head, n_kv, n_cells, 512, rope, cell_begin)
+                            want = plan(T, n_head, n_kv, n_cells, 512, rope, cell_begin, hd)
                             got = lstk.attn_plan(T, n_head, n_kv, hd, kv_size, n_cells, cell_begin, rope)
                             assert got[:5] == want, (n_head, kv_size, n_cells, cell_begin, T, rope)
                             assert got[5] == n_kv * want[1] * want[3]
@@ -170,7 +182,7 @@ def test_replayed_plan_is_the_library_plan(lstk):
 
 
 SHAPES = {"tiny": (4, 2, 64), "30b": (32, 4, 128), "235b": (64, 4, 128)}
-CELLS = [256, 300, 512, 4352, 8192, 8256, 16384, 32768, 65536, 65600, 131072]
+CELLS = [256, 300, 512, 4160, 4352, 5632, 6144, 6200, 8192, 8256, 16384, 32768, 65536, 65600, 131072]
 
 
 @pytest.mark.parametrize("target", [512, 256, 128])
@@ -206,8 +218,13 @@ def check_cells(n_head, n_kv, hd, grp, n_cells, kv_size, target):
 
 
 def test_rope_in_keeps_single_pass_chunks():
-    # one token at the 30B shape: one pass per chunk up to 65536 cells, then RoPE leaves the launch
-    assert plan(1, 32, 4, 4352, rope_in=True)[2:] == (64, 68, True)
+    # one token at the 30B shape: one pass per chunk up to 65536 cells, then RoPE leaves the launch; chunks
+    # of 80 or 96 cells keep 4097 .. 6144 cells within 256 work-groups
+    assert plan(1, 32, 4, 4096, rope_in=True)[2:] == (64, 64, True)
+    assert plan(1, 32, 4, 4352, rope_in=True)[2:] == (80, 55, True)
+    assert plan(1, 32, 4, 5632, rope_in=True)[2:] == (96, 59, True)
+    assert plan(1, 32, 4, 8192, rope_in=True)[2:] == (64, 128, True)
+    assert plan(1, 32, 4, 4352, rope_in=True, hd=64)[2:] == (64, 68, True)
     assert plan(1, 32, 4, 65536, rope_in=True)[2:] == (64, 1024, True)
     rb, nrb, chunk, n_chunk, rope = plan(1, 32, 4, 65600, rope_in=True)
     assert not rope and chunk > 64

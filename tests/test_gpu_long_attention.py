@@ -12,7 +12,8 @@ token (8 heads of the group):
   * an 8-token step at 4352 cells: 68 one-pass chunks and the combine;
   * a 32-token step at 4352 cells: 23 chunks of 3 passes (the multi-pass online softmax) and the combine,
     the plan of the whole-model benchmark's 32-token steps at a 4096-token context;
-  * single-token steps: RoPE inside the attention launch, one-pass chunks;
+  * single-token steps: RoPE inside the attention launch, one-pass chunks (of 80 or 96 cells where that keeps
+    the launch within 256 work-groups: 4097 ... 6144 cells);
   * a 512-token prompt placed high in the cache past another sequence's cells: the range starts at its
     lowest block (cell 512), one chunk of 12 passes per row block, the other sequence's 4 passes skipped.
 
@@ -173,11 +174,12 @@ def synthetic_kv(seed, layer, pos0, n, n_kv, hd):
 
 
 def test_single_token_long_context(lstk, dev, mid):
-    """Single-token steps after 4351, 16383, 32767 and 65535 positions of synthetic context (seeded K / V
+    """Single-token steps after 4351, 5631, 16383, 32767 and 65535 positions of synthetic context (seeded K / V
     written by lstk_model_fill_context, the same values given to the oracle with set_kv), each run with both
     plans on the same cache (the step truncated away in between): the default one, RoPE and the new cell's
-    K / V store inside the attention launch with one-pass chunks (68 ... 1024 per KV head, then the combine
-    over them), and RoPE in a launch of its own with 128 chunks of 1 ... 8 passes (lstk_model_debug_options).
+    K / V store inside the attention launch with one-pass chunks (55 of 80 cells, 59 of 96, then 256 ... 1024
+    of 64 per KV head, then the combine over them), and RoPE in a launch of its own with 128 chunks of
+    1 ... 8 passes (lstk_model_debug_options).
     Both are held to the oracle layer by layer, as the steps above."""
     hp, w = mid
     seed = 99
@@ -185,7 +187,7 @@ def test_single_token_long_context(lstk, dev, mid):
     hk = hp["n_head_kv"] * hp["head_dim"]
     done = 0
     rng = np.random.default_rng(65536)
-    for cells in (4352, 16384, 32768, 65536):
+    for cells in (4352, 5632, 16384, 32768, 65536):
         n = cells - 1 - done
         chk.model.fill_context(0, n, seed=seed)
         for l in range(hp["n_layer"]):
