@@ -235,8 +235,8 @@ __device__ __forceinline__ void quantize_row(const float *__restrict__ x, int n,
 }
 
 // quantize_row for n <= NP * 8 * blockDim.x with every load issued before the first pass is
-// quantized (one memory round trip instead of one per pass).
-// Split form: quantize_row_load issues the loads into v, quantize_row_store quantizes v.
+// quantized (one memory round trip instead of one per pass), in two calls:
+// quantize_row_load issues the loads into v, quantize_row_store quantizes v.
 // Every load is unconditional (addresses clamped into [0, n), n >= 8), so no branch separates them
 // from the caller's next loads.
 template <int NP>
@@ -254,29 +254,6 @@ __device__ __forceinline__ void quantize_row_load(const float *__restrict__ x, i
 }
 template <int QT, int NP>
 __device__ __forceinline__ void quantize_row_store(const float (&v)[NP][8], int n, int8_t *qs, float *d, int32_t *bs) {
-#pragma unroll
-    for (int p = 0; p < NP; p++) {
-        const int i0 = (p * blockDim.x + threadIdx.x) * 8;
-        if (p * (int) blockDim.x * 8 < n) quantize8<QT>(v[p], i0, i0 < n, qs, d, bs);
-    }
-}
-
-template <int QT, int NP>
-__device__ __forceinline__ void quantize_row_pre(const float *__restrict__ x, int n, int8_t *qs, float *d, int32_t *bs) {
-    float v[NP][8];
-#pragma unroll
-    for (int p = 0; p < NP; p++) {
-        const int i0 = (p * blockDim.x + threadIdx.x) * 8;
-        if (i0 < n) {
-            const float4 a = *reinterpret_cast<const float4 *>(x + i0);
-            const float4 b = *reinterpret_cast<const float4 *>(x + i0 + 4);
-            v[p][0] = a.x; v[p][1] = a.y; v[p][2] = a.z; v[p][3] = a.w;
-            v[p][4] = b.x; v[p][5] = b.y; v[p][6] = b.z; v[p][7] = b.w;
-        } else {
-#pragma unroll
-            for (int j = 0; j < 8; j++) v[p][j] = 0.0f;
-        }
-    }
 #pragma unroll
     for (int p = 0; p < NP; p++) {
         const int i0 = (p * blockDim.x + threadIdx.x) * 8;
@@ -445,55 +422,12 @@ __device__ __forceinline__ bool rank_token(const float *__restrict__ l_row, int 
     return true;
 }
 
-// Order key of a logit for the selection rounds: monotone in the value, -0 and +0 equal, every real
-// logit > 0 (0 marks an expert that is out of range or already selected).
+// Order key of a logit: monotone in the value, -0 and +0 equal, every real logit's key > 0 (route_one
+// places it above the expert's id, so the keys are unique and 0 marks an expert past E).
 __device__ __forceinline__ unsigned select_key(float v) {
     unsigned u = __float_as_uint(v);
     if (v == 0.0f) u = 0u;
     return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
-}
-
-__device__ __forceinline__ unsigned wave_max_u32(unsigned v) {
-    v = max(v, (unsigned) __builtin_amdgcn_update_dpp(0, (int) v, 0xB1, 0xF, 0xF, false));
-    v = max(v, (unsigned) __builtin_amdgcn_update_dpp(0, (int) v, 0x4E, 0xF, 0xF, false));
-    v = max(v, (unsigned) __builtin_amdgcn_update_dpp(0, (int) v, 0x141, 0xF, 0xF, false));
-    v = max(v, (unsigned) __builtin_amdgcn_update_dpp(0, (int) v, 0x140, 0xF, 0xF, false));
-    return max(max((unsigned) __builtin_amdgcn_readlane((int) v, 0), (unsigned) __builtin_amdgcn_readlane((int) v, 16)),
-               max((unsigned) __builtin_amdgcn_readlane((int) v, 32), (unsigned) __builtin_amdgcn_readlane((int) v, 48)));
-}
-
-// Top-k of one token's row by one wavefront, no LDS and no barrier: k rounds, each taking the
-// largest remaining key and, among equal keys, the lowest expert id (expert lane + 64 i, searched
-// i = 0 first, lowest lane first), so the selection is largest first with ties to the lower id, the
-// order rank_token computes. rank[i] = the round that took expert lane + 64 i, INT_MAX if none.
-template <int EPL>
-__device__ __forceinline__ void select_topk(const float (&l)[EPL], const bool (&valid)[EPL], int k, int (&rank)[EPL]) {
-    const int lane = threadIdx.x % kWave;
-    unsigned key[EPL];
-#pragma unroll
-    for (int i = 0; i < EPL; i++) {
-        key[i] = valid[i] ? select_key(l[i]) : 0u;
-        rank[i] = INT_MAX;
-    }
-    for (int r = 0; r < k; r++) {
-        unsigned m = key[0];
-#pragma unroll
-        for (int i = 1; i < EPL; i++) m = max(m, key[i]);
-        m = wave_max_u32(m);
-        int sel = -1;
-#pragma unroll
-        for (int i = 0; i < EPL; i++) {
-            const unsigned long long b = __ballot(key[i] == m && m != 0u);
-            if (sel < 0 && b) sel = kWave * i + __ffsll((long long) b) - 1;
-        }
-#pragma unroll
-        for (int i = 0; i < EPL; i++) {
-            if (lane + kWave * i == sel) {
-                rank[i] = r;
-                key[i] = 0u;
-            }
-        }
-    }
 }
 
 // Softmax, renormalisation and output of one token whose ranks rank_token found (part 0 only).
