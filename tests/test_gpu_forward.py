@@ -310,6 +310,35 @@ def test_30b_shaped_layers(lstk, dev):
         feed = np.array([np.argmax(rl)], np.int32)
 
 
+@pytest.mark.parametrize("n_kv,tiles", [(8, 3), (32, 4)])
+def test_wide_qkv_projection_tiles(lstk, dev, n_kv, tiles):
+    """h 2048 with 64 query heads of 128 and 8 or 32 KV heads: the joined Q/K/V rows (10240, 16384) spread
+    over 256 work-groups of the few-token projection take 40 and 64 rows each, three and four 16-row tiles
+    (with 40, the last tile's rows past the work-group's are neither loaded nor stored); steps of 8 and 16
+    tokens take it, then single tokens. One layer, 8 Q8_0 experts top-2. Held to BIG_TOL: the o-proj sums
+    8192 columns, as at the 235B attention shape (measured 2.8e-3 .. 5.2e-3)."""
+    n_head = 64
+    hp = dict(n_layer=1, n_embd=2048, n_head=n_head, n_head_kv=n_kv, head_dim=128, n_vocab=1024, n_expert=8,
+              n_expert_used=2, n_ff_exp=512, n_ctx_train=1024, rms_eps=1e-6, rope_freq_base=1000000.0)
+    rows = (n_head + 2 * n_kv) * 128
+    rw = next(r for r in range(-(-rows // 256), 65) if rows % r == 0)  # gemm16_rows_per_wg at 2048 columns
+    assert -(-rw // 16) == tiles
+    w = synth.qwen3_weights(np.random.default_rng(40 + tiles), hp, wtype=8)
+    _, model = build(lstk, dev, hp, w, n_batch=16, kv_size=512)
+    ref = oracle.Qwen3(hp, w, 64)
+    feeds = [prompt(50 + tiles, 8, hp["n_vocab"]), prompt(60 + tiles, 16, hp["n_vocab"])]
+    for step in range(4):
+        feed = feeds[step] if step < len(feeds) else np.array([np.argmax(rl)], np.int32)
+        rl, rt = ref.decode(feed, want_trace=True)
+        gl, gt = run(model, 0, feed, hp, dev)
+        err, rms, _, _ = oracle.diff_logits(rl, gl)
+        print(f"[wide q/k/v {n_head} / {n_kv} heads, {tiles} tiles, step {step} T={len(feed)}] max|dlogit| {err:.2e} "
+              f"rms {rms:.2e} (logit std {np.std(rl):.3f})", flush=True)
+        assert err <= BIG_TOL and rms <= BIG_RMS_TOL
+        assert np.argmax(gl) == np.argmax(rl)
+        np.testing.assert_array_equal(gt, rt)
+
+
 def test_235b_attention_shape(lstk, dev):
     """h 4096 and 64 / 4 heads: single-token GEMVs over 4096 and 8192 columns, 16-row query tiles per
     KV head, two row blocks at 8 tokens."""
