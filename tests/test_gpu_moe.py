@@ -50,6 +50,10 @@ def model(name):
         "q2": dict(h=2048, f=768, E=32, k=8, types=(Q2_K, Q2_K, Q3_K), n_layer=1, n_batch=64),
         # the 235B shape with k-quants in both kernels (two super-blocks per thread in gate/up)
         "235b_q6": dict(h=4096, f=1536, E=16, k=8, types=(Q6_K, Q6_K, Q5_K), n_layer=1, n_batch=64),
+        # long SwiGLU rows (f 2560: ten super-blocks, two per thread in the multi-token down kernel, whose
+        # eight-pair chunks then take eight one-row passes of the quantizer)
+        "f2560_q8": dict(h=256, f=2560, E=8, k=2, types=(Q8_0,) * 3, n_layer=1, n_batch=64),
+        "f2560_q4": dict(h=256, f=2560, E=8, k=2, types=(Q4_K,) * 3, n_layer=1, n_batch=64),
     }[name]
     rng = np.random.default_rng(sum(map(ord, name)))
     layers = [layer_bytes(rng, cfg["types"], cfg["E"], cfg["h"], cfg["f"]) for _ in range(cfg["n_layer"])]
@@ -113,7 +117,9 @@ def test_route_f32_weights_and_zipf(orc, lstk, dev):
                                     ("30b_q4", 1), ("30b_q4", 8), ("30b_q4", 64), ("mixed", 5), ("235b_q4", 1),
                                     ("235b_q4", 8), ("235b_q4", 64), ("q4km", 1), ("q4km", 8), ("q4km", 64),
                                     ("q5km", 1), ("q5km", 16), ("q3", 1), ("q3", 8), ("q2", 1), ("q2", 8),
-                                    ("235b_q6", 1), ("235b_q6", 8), ("235b_q8", 1), ("235b_q8", 8)])
+                                    ("235b_q6", 1), ("235b_q6", 8), ("235b_q8", 1), ("235b_q8", 8),
+                                    ("f2560_q8", 1), ("f2560_q8", 16), ("f2560_q8", 40), ("f2560_q4", 8),
+                                    ("f2560_q4", 40)])
 def test_ffn_matches_oracle(orc, lstk, dev, name, T):
     import torch
     cfg, layers, routers, store = model(name)
